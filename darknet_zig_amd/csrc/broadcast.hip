@@ -1,0 +1,218 @@
+// broadcast.hip -- ops that combine every element of an NCHW tensor with a
+// per-channel (or per-row) constant: add_bias, scale_bias, normalize,
+// normalize_delta (src/gpu.zig:527-537, 573-608) and backward_avgpool
+// (gpu.zig:765-767).
+//
+// Element e of a [batch, filters, spatial] tensor belongs to row r = e / spatial
+// and channel f = r % filters (blas.zig:51); both divisions are multiply-high
+// by launch constants. The tensor streams through in float4s exactly as in
+// elementwise.hip; when spatial % 4 == 0 a float4 never straddles a row, so
+// its channel constants are looked up (and derived, e.g. normalize's
+// reciprocal) once per float4.
+#include "dkz_device.hpp"
+#include "dkz_internal.hpp"
+
+namespace dkz {
+namespace {
+
+constexpr int kUnroll = 4;
+
+struct ChanGeom {
+    FastDiv spatial;
+    FastDiv filters;
+};
+
+// ROWWISE: the constant is per row r (backward_avgpool), not per channel.
+template <bool ROWWISE>
+__device__ __forceinline__ uint32_t channel_of(uint32_t e, const ChanGeom &g) {
+    const uint32_t r = fdiv(e, g.spatial);
+    if constexpr (ROWWISE) return r;
+    else return r - fdiv(r, g.filters) * g.filters.d;
+}
+
+template <class Op, bool TWO, bool ROWWISE, bool S4>
+__device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io, float4 a,
+                                            const ChanGeom &g) {
+    if constexpr (S4) {
+        const auto p = op.param(channel_of<ROWWISE>(v << 2, g));
+        io.x = op(io.x, a.x, p);
+        io.y = op(io.y, a.y, p);
+        io.z = op(io.z, a.z, p);
+        io.w = op(io.w, a.w, p);
+    } else {
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const auto p = op.param(channel_of<ROWWISE>((v << 2) + l, g));
+            lane(io, l) = op(lane(io, l), lane(a, l), p);
+        }
+    }
+    return io;
+}
+
+template <class Op, bool TWO, bool ROWWISE, bool S4>
+__global__ __launch_bounds__(kBlock) void bcast_vec_kernel(Op op, float *io, const float *a, ChanGeom g,
+                                                           uint32_t n) {
+    const uint32_t nv = n >> 2;
+    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    if (base + (kUnroll - 1) * kBlock < nv) {
+        float4 x[kUnroll], y[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            x[u] = ld4(io, base + u * kBlock);
+            if constexpr (TWO) y[u] = ld4(a, base + u * kBlock);
+            else y[u] = x[u];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+            st4(io, base + u * kBlock, bcast_vec<Op, TWO, ROWWISE, S4>(op, base + u * kBlock, x[u], y[u], g));
+    } else {
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t v = base + u * kBlock;
+            if (v < nv) {
+                const float4 x = ld4(io, v);
+                const float4 y = TWO ? ld4(a, v) : x;
+                st4(io, v, bcast_vec<Op, TWO, ROWWISE, S4>(op, v, x, y, g));
+            }
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3u)) {
+        const uint32_t e = (nv << 2) + threadIdx.x;
+        io[e] = op(io[e], TWO ? a[e] : 0.0f, op.param(channel_of<ROWWISE>(e, g)));
+    }
+}
+
+template <class Op, bool TWO, bool ROWWISE>
+__global__ __launch_bounds__(kBlock) void bcast_scalar_kernel(Op op, float *io, const float *a,
+                                                              ChanGeom g, uint32_t n) {
+    for (uint32_t e = blockIdx.x * kBlock + threadIdx.x; e < n; e += gridDim.x * kBlock)
+        io[e] = op(io[e], TWO ? a[e] : 0.0f, op.param(channel_of<ROWWISE>(e, g)));
+}
+
+// batch, filters, spatial already validated as non-negative ints.
+template <class Op, bool TWO, bool ROWWISE = false>
+int run_bcast(const char *name, const Op &op, float *io, const float *a, int batch, int filters,
+              int spatial) {
+    const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
+    if (n64 == 0) return 0;
+    DKZ_REQUIRE(n64 <= kMaxElems);
+    const uint32_t n = (uint32_t)n64;
+    const ChanGeom g{make_fastdiv((uint32_t)spatial), make_fastdiv((uint32_t)filters)};
+    if (aligned16(io) && (!TWO || aligned16(a))) {
+        const uint32_t nv = n >> 2;
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
+        if (spatial % 4 == 0)
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true>, dim3(grid), dim3(kBlock), op, io,
+                          a, g, n);
+        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false>, dim3(grid), dim3(kBlock), op, io, a,
+                      g, n);
+    }
+    const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
+    return launch(name, bcast_scalar_kernel<Op, TWO, ROWWISE>, dim3(grid), dim3(kBlock), op, io, a, g, n);
+}
+
+// ---- ops ------------------------------------------------------------------
+
+struct AddBiasOp {  // blas.zig:53-61
+    const float *biases;
+    __device__ float param(uint32_t f) const { return biases[f]; }
+    __device__ float operator()(float v, float, float b) const { return v + b; }
+};
+
+struct ScaleBiasOp {  // blas.zig:63-71
+    const float *scales;
+    __device__ float param(uint32_t f) const { return scales[f]; }
+    __device__ float operator()(float v, float, float s) const { return v * s; }
+};
+
+struct NormParam {
+    float m, inv;
+};
+struct NormalizeOp {  // blas.zig:137-146
+    const float *mean, *variance;
+    __device__ NormParam param(uint32_t f) const {
+        return {mean[f], 1.0f / (sqrtf(variance[f]) + 1e-6f)};
+    }
+    __device__ float operator()(float v, float, NormParam p) const { return (v - p.m) * p.inv; }
+};
+
+struct NormDeltaParam {
+    float m, inv, vd2, md_over_n;
+};
+// blas.zig:180-204: dv*inv + vd*2*(xv-m)/denom + md/denom, left to right.
+// vd*2 is exact, and md/denom is the same value for every element of f.
+struct NormalizeDeltaOp {
+    const float *mean, *variance, *mean_delta, *variance_delta;
+    float denom;
+    __device__ NormDeltaParam param(uint32_t f) const {
+        return {mean[f], 1.0f / sqrtf(variance[f] + 1e-5f), variance_delta[f] * 2.0f, mean_delta[f] / denom};
+    }
+    __device__ float operator()(float dv, float xv, NormDeltaParam p) const {
+        return (dv * p.inv + (p.vd2 * (xv - p.m)) / denom) + p.md_over_n;
+    }
+};
+
+struct AvgpoolBackOp {  // pooling.zig:160-172: d = out_delta[r] / S, added to the row
+    const float *out_delta;
+    float denom;
+    __device__ float param(uint32_t r) const { return out_delta[r] / denom; }
+    __device__ float operator()(float v, float, float d) const { return v + d; }
+};
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+#define DKZ_REQUIRE_SHAPE(b, f, s) DKZ_REQUIRE((b) >= 0 && (f) >= 0 && (s) >= 0)
+#define DKZ_EMPTY(b, f, s) ((b) == 0 || (f) == 0 || (s) == 0)
+
+extern "C" {
+
+int dkz_add_bias(float *output, const float *biases, int batch, int filters, int spatial) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (DKZ_EMPTY(batch, filters, spatial)) return 0;
+    DKZ_REQUIRE(output && biases);
+    return run_bcast<AddBiasOp, false>("add_bias", AddBiasOp{biases}, output, nullptr, batch, filters,
+                                       spatial);
+}
+
+int dkz_scale_bias(float *output, const float *scales, int batch, int filters, int spatial) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (DKZ_EMPTY(batch, filters, spatial)) return 0;
+    DKZ_REQUIRE(output && scales);
+    return run_bcast<ScaleBiasOp, false>("scale_bias", ScaleBiasOp{scales}, output, nullptr, batch,
+                                         filters, spatial);
+}
+
+int dkz_normalize(float *x, const float *mean, const float *variance, int batch, int filters,
+                  int spatial) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (DKZ_EMPTY(batch, filters, spatial)) return 0;
+    DKZ_REQUIRE(x && mean && variance);
+    return run_bcast<NormalizeOp, false>("normalize", NormalizeOp{mean, variance}, x, nullptr, batch,
+                                         filters, spatial);
+}
+
+int dkz_normalize_delta(const float *x, const float *mean, const float *variance,
+                        const float *mean_delta, const float *variance_delta, int batch, int filters,
+                        int spatial, float *delta) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (DKZ_EMPTY(batch, filters, spatial)) return 0;
+    DKZ_REQUIRE(x && mean && variance && mean_delta && variance_delta && delta);
+    const float denom = (float)((uint64_t)spatial * (uint64_t)batch);  // blas.zig:191
+    const NormalizeDeltaOp op{mean, variance, mean_delta, variance_delta, denom};
+    return run_bcast<NormalizeDeltaOp, true>("normalize_delta", op, delta, x, batch, filters, spatial);
+}
+
+int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const float *out_delta) {
+    DKZ_REQUIRE(n >= 0 && w >= 0 && h >= 0 && c >= 0);
+    const uint64_t spatial = (uint64_t)w * (uint64_t)h;
+    if (n == 0 || spatial == 0) return 0;
+    DKZ_REQUIRE(spatial <= kMaxElems);
+    DKZ_REQUIRE(in_delta && out_delta);
+    const AvgpoolBackOp op{out_delta, (float)spatial};
+    return run_bcast<AvgpoolBackOp, false, true>("backward_avgpool", op, in_delta, nullptr, n, 1,
+                                                 (int)spatial);
+}
+
+}  // extern "C"

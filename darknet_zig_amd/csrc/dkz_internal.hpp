@@ -1,0 +1,64 @@
+// dkz_internal.hpp -- host-side plumbing shared by the op sources: the current
+// stream, argument checks, the launch helper with sync-after-launch, and the
+// per-device reduction scratch. Not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dkz_ops.h"
+
+namespace dkz {
+
+// Stream every op and copy is issued on (the null stream by default).
+hipStream_t current_stream();
+
+// Records "what failed" for dkz_last_error_context on this host thread.
+void set_error_context(const char *fmt, ...);
+
+// Called right after a kernel launch: reports a launch error, and under
+// sync-after-launch waits for the kernel and reports its fault. `name` and the
+// launch shape go into the error context (gpu.zig:445-462).
+int after_launch(const char *name, dim3 grid, dim3 block);
+
+template <typename Kernel, typename... Args>
+inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args... args) {
+    (void)hipGetLastError();  // a stale error from the caller's own calls is not ours
+    hipLaunchKernelGGL(kernel, grid, block, 0, current_stream(), args...);
+    return after_launch(name, grid, block);
+}
+
+// Reduction scratch of the current device: completion counters followed by
+// double partials. Allocated by dkz_init (or on first use), zero-filled once;
+// every kernel that bumps a counter returns it to zero before it exits.
+struct Scratch {
+    uint32_t *counters;
+    double *partials;
+};
+constexpr uint32_t kScratchCounters = 1u << 14;  // channels that may split
+constexpr uint32_t kScratchPartials = 1u << 18;  // channels * chunks
+int device_scratch(Scratch *out);
+
+// Largest element count any op indexes with 32-bit arithmetic, as the
+// reference's kernels do (int global_index(), darknet_kernels.hip:40-42).
+constexpr uint64_t kMaxElems = 0x7fffffffull;
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+}  // namespace dkz
+
+#define DKZ_REQUIRE(cond)                                                    \
+    do {                                                                     \
+        if (!(cond)) {                                                       \
+            ::dkz::set_error_context("%s: invalid argument (%s)", __func__, #cond); \
+            return (int)hipErrorInvalidValue;                                \
+        }                                                                    \
+    } while (0)
+
+#define DKZ_TRY(expr)                    \
+    do {                                 \
+        const int dkz_rc_ = (expr);      \
+        if (dkz_rc_ != 0) return dkz_rc_; \
+    } while (0)

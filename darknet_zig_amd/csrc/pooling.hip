@@ -1,0 +1,242 @@
+// pooling.hip -- max pooling forward/backward (src/gpu.zig:725-759, CPU twin
+// layers/pooling.zig:59-103). Global average pooling lives in reduce.hip
+// (forward) and broadcast.hip (backward).
+//
+// Forward: out_w = (in_w + pad - size)/stride + 1 (pooling.zig:33-34), the
+// window starts at -pad/2, out-of-range taps are skipped, and the first
+// maximum under strict '>' wins, starting from -FLT_MAX with index -1. The
+// index is the absolute flat index into the batched input.
+//
+// Backward: the twin scatters prev_delta[idx[o]] += delta[o] over ascending o.
+// Here each input element gathers instead: it visits the outputs whose window
+// covers it in ascending o and adds delta[o] whenever idx[o] names it, so an
+// element with several contributors receives them in the twin's order and the
+// result is bit-exact with no atomics. Elements with no contributor are not
+// written (0 + -0 would otherwise flip a sign).
+//
+// Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
+// a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
+// two adjacent outputs and their 2x4 input patch, read and written as two
+// float4s.
+#include <float.h>
+
+#include "dkz_device.hpp"
+#include "dkz_internal.hpp"
+
+namespace dkz {
+namespace {
+
+struct PoolGeom {
+    uint32_t h, w, c, oh, ow, size, stride, half_pad;  // window offset is -half_pad
+    FastDiv div_w, div_h, div_ow, div_oh;
+};
+
+// ---- generic ----------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g,
+                                                             uint32_t out_n) {
+    const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
+    if (o >= out_n) return;
+    uint32_t t = fdiv(o, g.div_ow);
+    const uint32_t j = o - t * g.ow;
+    uint32_t t2 = fdiv(t, g.div_oh);
+    const uint32_t i = t - t2 * g.oh;
+    const uint32_t plane = t2;  // k + b*c
+    float mx = -FLT_MAX;
+    int mi = -1;
+    for (uint32_t n = 0; n < g.size; ++n) {
+        const int ch = (int)(i * g.stride + n) - (int)g.half_pad;
+        if (ch < 0 || ch >= (int)g.h) continue;
+        for (uint32_t m = 0; m < g.size; ++m) {
+            const int cw = (int)(j * g.stride + m) - (int)g.half_pad;
+            if (cw < 0 || cw >= (int)g.w) continue;
+            const uint32_t index = (uint32_t)cw + g.w * ((uint32_t)ch + g.h * plane);
+            const float val = in[index];
+            if (val > mx) {
+                mx = val;
+                mi = (int)index;
+            }
+        }
+    }
+    out[o] = mx;
+    idx[o] = mi;
+}
+
+__global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta, float *prev, const int *idx,
+                                                             PoolGeom g, uint32_t in_n) {
+    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+    if (e >= in_n) return;
+    uint32_t t = fdiv(e, g.div_w);
+    const uint32_t x = e - t * g.w;
+    const uint32_t t2 = fdiv(t, g.div_h);
+    const uint32_t y = t - t2 * g.h;
+    const uint32_t plane = t2;
+    // Outputs i with i*stride + n - half_pad == y for some n in [0, size).
+    const int yp = (int)(y + g.half_pad), xp = (int)(x + g.half_pad);
+    const int s = (int)g.stride, sz = (int)g.size;
+    const int ilo = yp - sz + 1 <= 0 ? 0 : (yp - sz + 1 + s - 1) / s;
+    const int jlo = xp - sz + 1 <= 0 ? 0 : (xp - sz + 1 + s - 1) / s;
+    const int ihi = min(yp / s, (int)g.oh - 1);
+    const int jhi = min(xp / s, (int)g.ow - 1);
+    if (ilo > ihi || jlo > jhi) return;
+    float v = 0.0f;
+    bool touched = false;
+    for (int i = ilo; i <= ihi; ++i) {
+        for (int j = jlo; j <= jhi; ++j) {
+            const uint32_t o = (uint32_t)j + g.ow * ((uint32_t)i + g.oh * plane);
+            if (idx[o] == (int)e) {
+                if (!touched) v = prev[e];
+                touched = true;
+                v += delta[o];
+            }
+        }
+    }
+    if (touched) prev[e] = v;
+}
+
+// ---- 2x2, stride 2, offset 0 ------------------------------------------------
+
+__device__ __forceinline__ void max_tap(float val, int index, float &mx, int &mi) {
+    if (val > mx) {
+        mx = val;
+        mi = index;
+    }
+}
+
+// q indexes output pairs; ow is even so a pair never straddles a row.
+__global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, float *out, int *idx,
+                                                              PoolGeom g, uint32_t pairs) {
+    const uint32_t q = blockIdx.x * kBlock + threadIdx.x;
+    if (q >= pairs) return;
+    const uint32_t o = 2 * q;
+    const uint32_t t = fdiv(o, g.div_ow);
+    const uint32_t j = o - t * g.ow;
+    const uint32_t plane = fdiv(t, g.div_oh);
+    const uint32_t i = t - plane * g.oh;
+    const uint32_t r0 = (plane * g.h + 2 * i) * g.w + 2 * j;  // first tap of output j
+    const uint32_t r1 = r0 + g.w;
+    const float4 a = ld4(in, r0 >> 2);
+    const float4 b = ld4(in, r1 >> 2);
+    float m0 = -FLT_MAX, m1 = -FLT_MAX;
+    int i0 = -1, i1 = -1;
+    max_tap(a.x, (int)r0, m0, i0);
+    max_tap(a.y, (int)r0 + 1, m0, i0);
+    max_tap(b.x, (int)r1, m0, i0);
+    max_tap(b.y, (int)r1 + 1, m0, i0);
+    max_tap(a.z, (int)r0 + 2, m1, i1);
+    max_tap(a.w, (int)r0 + 3, m1, i1);
+    max_tap(b.z, (int)r1 + 2, m1, i1);
+    max_tap(b.w, (int)r1 + 3, m1, i1);
+    reinterpret_cast<float2 *>(out)[q] = make_float2(m0, m1);
+    reinterpret_cast<int2 *>(idx)[q] = make_int2(i0, i1);
+}
+
+__device__ __forceinline__ float add_if(float p, int want, int have, float d) {
+    return have == want ? p + d : p;
+}
+
+__global__ __launch_bounds__(kBlock) void maxpool2_bwd_kernel(const float *delta, float *prev, const int *idx,
+                                                              PoolGeom g, uint32_t pairs) {
+    const uint32_t q = blockIdx.x * kBlock + threadIdx.x;
+    if (q >= pairs) return;
+    const uint32_t o = 2 * q;
+    const uint32_t t = fdiv(o, g.div_ow);
+    const uint32_t j = o - t * g.ow;
+    const uint32_t plane = fdiv(t, g.div_oh);
+    const uint32_t i = t - plane * g.oh;
+    const uint32_t r0 = (plane * g.h + 2 * i) * g.w + 2 * j;
+    const uint32_t r1 = r0 + g.w;
+    const float2 d = reinterpret_cast<const float2 *>(delta)[q];
+    const int2 k = reinterpret_cast<const int2 *>(idx)[q];
+    float4 a = ld4(prev, r0 >> 2);
+    float4 b = ld4(prev, r1 >> 2);
+    // Each input of the patch has exactly one candidate output: j for the
+    // first two columns, j+1 for the last two.
+    a.x = add_if(a.x, (int)r0, k.x, d.x);
+    a.y = add_if(a.y, (int)r0 + 1, k.x, d.x);
+    b.x = add_if(b.x, (int)r1, k.x, d.x);
+    b.y = add_if(b.y, (int)r1 + 1, k.x, d.x);
+    a.z = add_if(a.z, (int)r0 + 2, k.y, d.y);
+    a.w = add_if(a.w, (int)r0 + 3, k.y, d.y);
+    b.z = add_if(b.z, (int)r1 + 2, k.y, d.y);
+    b.w = add_if(b.w, (int)r1 + 3, k.y, d.y);
+    st4(prev, r0 >> 2, a);
+    st4(prev, r1 >> 2, b);
+}
+
+// Validates the gpu.zig arguments and derives the geometry. `n` is out_n
+// (forward) or in_n (backward); the batch follows from it.
+int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, PoolGeom *g, uint64_t *planes,
+                  bool *fast) {
+    DKZ_REQUIRE(in_h >= 0 && in_w >= 0 && in_c >= 0 && pad >= 0);
+    DKZ_REQUIRE(stride >= 1 && size >= 1);
+    DKZ_REQUIRE((int64_t)in_w + pad >= size && (int64_t)in_h + pad >= size);  // pooling.zig:33-34
+    g->h = (uint32_t)in_h;
+    g->w = (uint32_t)in_w;
+    g->c = (uint32_t)in_c;
+    g->size = (uint32_t)size;
+    g->stride = (uint32_t)stride;
+    g->half_pad = (uint32_t)(pad / 2);
+    g->ow = (uint32_t)((in_w + pad - size) / stride + 1);
+    g->oh = (uint32_t)((in_h + pad - size) / stride + 1);
+    g->div_w = make_fastdiv(g->w ? g->w : 1);
+    g->div_h = make_fastdiv(g->h ? g->h : 1);
+    g->div_ow = make_fastdiv(g->ow);
+    g->div_oh = make_fastdiv(g->oh);
+    *planes = 0;
+    *fast = size == 2 && stride == 2 && pad / 2 == 0 && in_w % 4 == 0 && in_h % 2 == 0 && in_w > 0 && in_h > 0;
+    return 0;
+}
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+extern "C" {
+
+int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int size, int pad,
+                        const float *input, float *output, int *indexes) {
+    DKZ_REQUIRE(out_n >= 0);
+    if (out_n == 0) return 0;
+    PoolGeom g;
+    uint64_t planes;
+    bool fast;
+    DKZ_TRY(pool_geometry(in_h, in_w, in_c, stride, size, pad, &g, &planes, &fast));
+    const uint64_t per_plane = (uint64_t)g.oh * g.ow;
+    DKZ_REQUIRE(per_plane > 0 && (uint64_t)out_n % per_plane == 0);
+    planes = (uint64_t)out_n / per_plane;  // c * batch
+    DKZ_REQUIRE(planes * g.h * g.w <= kMaxElems);
+    DKZ_REQUIRE(input && output && indexes);
+    if (fast && aligned16(input) && ((uintptr_t)output & 7u) == 0 && ((uintptr_t)indexes & 7u) == 0) {
+        const uint32_t pairs = (uint32_t)out_n / 2;
+        return launch("forward_maxpool_2x2", maxpool2_fwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
+                      input, output, indexes, g, pairs);
+    }
+    return launch("forward_maxpool", maxpool_fwd_kernel, dim3(div_up((uint32_t)out_n, kBlock)), dim3(kBlock),
+                  input, output, indexes, g, (uint32_t)out_n);
+}
+
+int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int size, int pad,
+                         const float *delta, float *prev_delta, const int *indexes) {
+    DKZ_REQUIRE(in_n >= 0);
+    if (in_n == 0) return 0;
+    PoolGeom g;
+    uint64_t planes;
+    bool fast;
+    DKZ_TRY(pool_geometry(in_h, in_w, in_c, stride, size, pad, &g, &planes, &fast));
+    const uint64_t per_plane = (uint64_t)g.h * g.w;
+    DKZ_REQUIRE(per_plane > 0 && (uint64_t)in_n % per_plane == 0);
+    planes = (uint64_t)in_n / per_plane;
+    DKZ_REQUIRE(planes * g.oh * g.ow <= kMaxElems);
+    DKZ_REQUIRE(delta && prev_delta && indexes);
+    if (fast && aligned16(prev_delta) && ((uintptr_t)delta & 7u) == 0 && ((uintptr_t)indexes & 7u) == 0) {
+        const uint32_t pairs = (uint32_t)(planes * g.oh * g.ow / 2);
+        return launch("backward_maxpool_2x2", maxpool2_bwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
+                      delta, prev_delta, indexes, g, pairs);
+    }
+    return launch("backward_maxpool", maxpool_bwd_kernel, dim3(div_up((uint32_t)in_n, kBlock)), dim3(kBlock),
+                  delta, prev_delta, indexes, g, (uint32_t)in_n);
+}
+
+}  // extern "C"

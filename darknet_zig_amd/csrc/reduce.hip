@@ -1,0 +1,355 @@
+// reduce.hip -- per-channel reductions over N*H*W (mean, variance, mean_delta,
+// variance_delta, backward_bias, backward_scale: src/gpu.zig:539-590) and the
+// per-row reduction of global average pooling (gpu.zig:761-763).
+//
+// Channel reductions, one launch each:
+//   * The grid is filters x K workgroups; workgroup (f, k) owns the k-th
+//     contiguous chunk of channel f's batch*spatial elements. K is picked from
+//     the shape only, so a shape always reduces in the same order on any GPU.
+//   * Each lane computes the CPU twin's per-element term in f32 -- x, (x-m)^2,
+//     delta*x_norm, delta*(x-m), rounded exactly as blas.zig rounds them -- and
+//     accumulates it in f64. A chunk is then summed by wave64 DPP reductions
+//     and a 4-entry LDS step (dkz_device.hpp).
+//   * With K > 1 each workgroup stores its f64 partial, and the workgroup that
+//     completes a channel (an acq_rel counter per channel) adds the K partials
+//     in index order and applies the finalisation. There are no float atomics:
+//     the result is deterministic, and it is the exact sum to within f64
+//     rounding, so its distance to the CPU twin's sequential f32 sum is that
+//     sum's own rounding error.
+//   * The finalisation repeats blas.zig's f32 arithmetic on the f32-rounded
+//     total: sum * (1/(B*S)), sum * (-1/sqrt(v+1e-5)), updates[f] += sum, ...
+#include "dkz_device.hpp"
+#include "dkz_internal.hpp"
+
+namespace dkz {
+namespace {
+
+constexpr int kUnroll = 4;
+
+struct RedGeom {
+    uint32_t spatial;
+    uint32_t chan_len;   // batch * spatial
+    uint32_t chunk;      // elements per workgroup (multiple of 4 on the float4 path)
+    uint32_t K;          // workgroups per channel
+    uint32_t row_extra;  // (filters - 1) * spatial
+    FastDiv div_k;
+    FastDiv div_spatial;
+};
+
+// Element j of channel f lives at ((b*F + f)*S + s) = f*S + j + b*(F-1)*S.
+__device__ __forceinline__ uint32_t chan_addr(uint32_t fbase, uint32_t j, const RedGeom &g) {
+    return fbase + j + fdiv(j, g.div_spatial) * g.row_extra;
+}
+
+template <class Term>
+__device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
+    double s = (double)t(a.x, b.x);
+    s += (double)t(a.y, b.y);
+    s += (double)t(a.z, b.z);
+    s += (double)t(a.w, b.w);
+    return s;
+}
+
+// T::at(f) gives the per-element term of channel f; Fin(f, total) writes the
+// channel's result. p1 is read only when TWO.
+template <class T, class Fin, bool TWO, bool VEC>
+__global__ __launch_bounds__(kBlock) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1,
+                                                             RedGeom g, uint32_t *counters,
+                                                             double *partials) {
+    __shared__ double lds[kBlock / kWave];
+    __shared__ int is_last;
+    const uint32_t f = fdiv(blockIdx.x, g.div_k);
+    const uint32_t k = blockIdx.x - f * g.K;
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const auto term = t.at(f);
+    double acc = 0.0;
+    if constexpr (VEC) {
+        constexpr uint32_t kStep = 4 * kBlock;
+        uint32_t j = j0 + 4 * threadIdx.x;
+        for (; j + kStep * (kUnroll - 1) < j1; j += kStep * kUnroll) {
+            float4 a[kUnroll], b[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint32_t v = chan_addr(fbase, j + u * kStep, g) >> 2;
+                a[u] = ld4(p0, v);
+                if constexpr (TWO) b[u] = ld4(p1, v);
+                else b[u] = a[u];
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) acc += term4(term, a[u], b[u]);
+        }
+        for (; j < j1; j += kStep) {
+            const uint32_t v = chan_addr(fbase, j, g) >> 2;
+            const float4 a = ld4(p0, v);
+            const float4 b = TWO ? ld4(p1, v) : a;
+            acc += term4(term, a, b);
+        }
+    } else {
+        for (uint32_t j = j0 + threadIdx.x; j < j1; j += kBlock) {
+            const uint32_t e = chan_addr(fbase, j, g);
+            acc += (double)term(p0[e], TWO ? p1[e] : 0.0f);
+        }
+    }
+    const double total = block_sum(acc, lds);
+    if (g.K == 1) {
+        if (threadIdx.x == 0) fin(f, total);
+        return;
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&partials[f * g.K + k], total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t done =
+            __hip_atomic_fetch_add(&counters[f], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = done == g.K - 1;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    if (threadIdx.x < kWave) {
+        double s = 0.0;
+        for (uint32_t i = threadIdx.x; i < g.K; i += kWave)
+            s += __hip_atomic_load(&partials[f * g.K + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s = wave_sum(s);
+        if (threadIdx.x == 0) {
+            fin(f, s);
+            __hip_atomic_store(&counters[f], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Workgroups per channel: about 2048 over the launch, each with at least 4096
+// elements, within the scratch's capacity. Depends on the shape only.
+uint32_t pick_split(uint32_t filters, uint32_t chan_len) {
+    if (filters > kScratchCounters) return 1;
+    uint32_t k = div_up(2048, filters);
+    const uint32_t kmax = chan_len / 4096 > 1 ? chan_len / 4096 : 1;
+    if (k > kmax) k = kmax;
+    while (k > 1 && (uint64_t)filters * k > kScratchPartials) --k;
+    return k < 1 ? 1 : k;
+}
+
+template <class T, class Fin, bool TWO>
+int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p0, const float *p1,
+                    int batch, int filters, int spatial) {
+    const uint64_t chan_len64 = (uint64_t)batch * (uint64_t)spatial;
+    DKZ_REQUIRE(chan_len64 * (uint64_t)filters <= kMaxElems);
+    const uint32_t F = (uint32_t)filters, S = (uint32_t)spatial, L = (uint32_t)chan_len64;
+    const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
+    uint32_t K = pick_split(F, L);
+    uint32_t chunk = L == 0 ? 0 : div_up(L, K);
+    if (vec) chunk = (chunk + 3) & ~3u;
+    K = chunk > 0 ? div_up(L, chunk) : 1;
+    const RedGeom g{S, L, chunk, K, (F - 1) * S, make_fastdiv(K), make_fastdiv(S == 0 ? 1 : S)};
+    Scratch sc{nullptr, nullptr};
+    if (K > 1) DKZ_TRY(device_scratch(&sc));
+    const dim3 grid(F * K), block(kBlock);
+    if (vec)
+        return launch(name, chan_reduce_kernel<T, Fin, TWO, true>, grid, block, t, fin, p0, p1, g, sc.counters,
+                      sc.partials);
+    return launch(name, chan_reduce_kernel<T, Fin, TWO, false>, grid, block, t, fin, p0, p1, g, sc.counters,
+                  sc.partials);
+}
+
+// ---- per-element terms (f32, rounded as the CPU twin rounds them) ---------
+
+struct Value {  // sum += v (blas.zig:78, 112, 153)
+    __device__ float operator()(float v, float) const { return v; }
+};
+struct SumValue {
+    __device__ Value at(uint32_t) const { return {}; }
+};
+
+struct SqDev {  // d = v - m; sum += d*d (blas.zig:128-131)
+    float m;
+    __device__ float operator()(float v, float) const {
+        const float d = v - m;
+        return d * d;
+    }
+};
+struct SumSqDev {
+    const float *mean;
+    __device__ SqDev at(uint32_t f) const { return {mean[f]}; }
+};
+
+struct Prod {  // sum += dv * xv (blas.zig:96), p0 = delta, p1 = x_norm
+    __device__ float operator()(float d, float x) const { return d * x; }
+};
+struct SumProd {
+    __device__ Prod at(uint32_t) const { return {}; }
+};
+
+struct ProdDev {  // sum += dv * (xv - m) (blas.zig:174), p0 = delta, p1 = x
+    float m;
+    __device__ float operator()(float d, float x) const { return d * (x - m); }
+};
+struct SumProdDev {
+    const float *mean;
+    __device__ ProdDev at(uint32_t f) const { return {mean[f]}; }
+};
+
+// ---- finalisations ----------------------------------------------------------
+
+struct FinScale {  // out[f] = sum * scale_f (blas.zig:114, 133)
+    float *out;
+    float scale;
+    __device__ void operator()(uint32_t f, double s) const { out[f] = (float)s * scale; }
+};
+struct FinMeanDelta {  // blas.zig:155
+    float *out;
+    const float *variance;
+    __device__ void operator()(uint32_t f, double s) const {
+        out[f] = (float)s * (-1.0f / sqrtf(variance[f] + 1e-5f));
+    }
+};
+// v^-1.5 as 1/(v*sqrt(v)) in f64, rounded once. std.math.pow(f32, v, -1.5)
+// (blas.zig:176) goes through f32 exp and log and lands within a few ulps.
+__device__ __forceinline__ float pow_m1p5(float v) {
+    const double d = (double)v;
+    return (float)(1.0 / (d * sqrt(d)));
+}
+struct FinVarianceDelta {  // blas.zig:176: (sum * -0.5) * pow(v + 1e-5, -1.5)
+    float *out;
+    const float *variance;
+    __device__ void operator()(uint32_t f, double s) const {
+        out[f] = ((float)s * -0.5f) * pow_m1p5(variance[f] + 1e-5f);
+    }
+};
+struct FinAccumulate {  // updates[f] += sum (blas.zig:79, 98)
+    float *updates;
+    __device__ void operator()(uint32_t f, double s) const { updates[f] = updates[f] + (float)s; }
+};
+
+// backward_bias with spatial == 1 (gpu.zig:540-543): one lane per filter walks
+// the batch in order, adding each row's one-element sum (0 + delta) to the
+// update exactly as blas.zig:73-82 does -- bit-exact, and coalesced across f.
+__global__ __launch_bounds__(kBlock) void backward_bias_conn_kernel(float *updates, const float *delta,
+                                                                    uint32_t batch, uint32_t filters) {
+    const uint32_t f = blockIdx.x * kBlock + threadIdx.x;
+    if (f >= filters) return;
+    float u = updates[f];
+    for (uint32_t b = 0; b < batch; ++b) u += 0.0f + delta[b * filters + f];
+    updates[f] = u;
+}
+
+// ---- global average pooling forward: one wave per row ----------------------
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void avgpool_rows_kernel(const float *x, float *out, uint32_t rows,
+                                                              uint32_t S, float denom) {
+    const uint32_t row = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;  // whole waves leave together
+    const uint32_t l = threadIdx.x & (kWave - 1);
+    double acc = 0.0;
+    if constexpr (VEC) {
+        const uint32_t S4 = S >> 2;
+        const uint32_t v0 = row * S4;
+        uint32_t i = l;
+        for (; i + 3 * kWave < S4; i += 4 * kWave) {
+            float4 a[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[u] = ld4(x, v0 + i + u * kWave);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += term4(Value{}, a[u], a[u]);
+        }
+        for (; i < S4; i += kWave) {
+            const float4 a = ld4(x, v0 + i);
+            acc += term4(Value{}, a, a);
+        }
+    } else {
+        const uint32_t e0 = row * S;
+        for (uint32_t i = l; i < S; i += kWave) acc += (double)x[e0 + i];
+    }
+    acc = wave_sum(acc);
+    if (l == 0) out[row] = (float)acc / denom;  // pooling.zig:155: sum / denom
+}
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+#define DKZ_REQUIRE_SHAPE(b, f, s) DKZ_REQUIRE((b) >= 0 && (f) >= 0 && (s) >= 0)
+
+extern "C" {
+
+int dkz_mean(const float *x, int batch, int filters, int spatial, float *out) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(out && (x || (uint64_t)batch * spatial == 0));
+    const float scale = 1.0f / (float)((uint64_t)batch * (uint64_t)spatial);  // blas.zig:107
+    return run_chan_reduce<SumValue, FinScale, false>("mean", SumValue{}, FinScale{out, scale}, x, nullptr,
+                                                      batch, filters, spatial);
+}
+
+int dkz_variance(const float *x, const float *mean, int batch, int filters, int spatial, float *out) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(out && mean && (x || (uint64_t)batch * spatial == 0));
+    // blas.zig:122, usize arithmetic: batch*spatial - 1 wraps when the product is 0.
+    const float scale = 1.0f / (float)((uint64_t)batch * (uint64_t)spatial - 1u);
+    return run_chan_reduce<SumSqDev, FinScale, false>("variance", SumSqDev{mean}, FinScale{out, scale}, x,
+                                                      nullptr, batch, filters, spatial);
+}
+
+int dkz_mean_delta(const float *delta, const float *variance, int batch, int filters, int spatial,
+                   float *out) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(out && variance && (delta || (uint64_t)batch * spatial == 0));
+    return run_chan_reduce<SumValue, FinMeanDelta, false>("mean_delta", SumValue{},
+                                                          FinMeanDelta{out, variance}, delta, nullptr,
+                                                          batch, filters, spatial);
+}
+
+int dkz_variance_delta(const float *x, const float *delta, const float *mean, const float *variance,
+                       int batch, int filters, int spatial, float *out) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(out && mean && variance && ((x && delta) || (uint64_t)batch * spatial == 0));
+    return run_chan_reduce<SumProdDev, FinVarianceDelta, true>("variance_delta", SumProdDev{mean},
+                                                               FinVarianceDelta{out, variance}, delta, x,
+                                                               batch, filters, spatial);
+}
+
+int dkz_backward_bias(float *bias_updates, const float *delta, int batch, int filters, int spatial) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    // blas.zig:73-82 adds one row sum per batch item: nothing at all when batch == 0.
+    if (filters == 0 || batch == 0) return 0;
+    DKZ_REQUIRE(bias_updates && (delta || spatial == 0));
+    if (spatial == 1) {
+        DKZ_REQUIRE((uint64_t)batch * (uint64_t)filters <= kMaxElems);
+        return launch("backward_bias_conn", backward_bias_conn_kernel, dim3(div_up((uint32_t)filters, kBlock)),
+                      dim3(kBlock), bias_updates, delta, (uint32_t)batch, (uint32_t)filters);
+    }
+    return run_chan_reduce<SumValue, FinAccumulate, false>("backward_bias", SumValue{},
+                                                           FinAccumulate{bias_updates}, delta, nullptr, batch,
+                                                           filters, spatial);
+}
+
+int dkz_backward_scale(const float *x_norm, const float *delta, int batch, int filters, int spatial,
+                       float *scale_updates) {
+    DKZ_REQUIRE_SHAPE(batch, filters, spatial);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(scale_updates && ((x_norm && delta) || (uint64_t)batch * spatial == 0));
+    return run_chan_reduce<SumProd, FinAccumulate, true>("backward_scale", SumProd{},
+                                                         FinAccumulate{scale_updates}, delta, x_norm, batch,
+                                                         filters, spatial);
+}
+
+int dkz_forward_avgpool(int n, int w, int h, int c, const float *input, float *output) {
+    DKZ_REQUIRE(n >= 0 && w >= 0 && h >= 0 && c >= 0);
+    if (n == 0) return 0;
+    const uint64_t S = (uint64_t)w * (uint64_t)h;
+    DKZ_REQUIRE(S * (uint64_t)n <= kMaxElems);
+    DKZ_REQUIRE(output && (input || S == 0));
+    const float denom = (float)S;  // pooling.zig:148
+    const uint32_t rows = (uint32_t)n;
+    const dim3 grid(div_up(rows, kBlock / kWave)), block(kBlock);
+    if (S % 4 == 0 && aligned16(input))
+        return launch("forward_avgpool", avgpool_rows_kernel<true>, grid, block, input, output, rows,
+                      (uint32_t)S, denom);
+    return launch("forward_avgpool", avgpool_rows_kernel<false>, grid, block, input, output, rows, (uint32_t)S,
+                  denom);
+}
+
+}  // extern "C"

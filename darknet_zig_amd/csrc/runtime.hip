@@ -1,0 +1,215 @@
+// runtime.hip -- device and memory glue of the C ABI. Replaces the HIP backend
+// interface of src/hip/hip.zig:60-135 and the device/memory half of
+// src/gpu.zig (init 259-347, alloc/free/push/pull/sync 362-410).
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "dkz_internal.hpp"
+
+namespace dkz {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+    void *scratch = nullptr;
+};
+
+DeviceState g_devices[kMaxDevices];
+std::mutex g_mutex;
+hipStream_t g_stream = nullptr;
+bool g_sync_after_launch = false;
+thread_local char g_context[512] = "";
+
+bool env_flag(const char *name) {
+    const char *v = getenv(name);
+    return v != nullptr && v[0] != '\0' && v[0] != '0';
+}
+
+// One allocation per device: counters first (kept 256-byte aligned), then
+// the double partials.
+constexpr size_t kCounterBytes = ((kScratchCounters * sizeof(uint32_t)) + 255) & ~size_t(255);
+constexpr size_t kScratchBytes = kCounterBytes + kScratchPartials * sizeof(double);
+
+int ensure_scratch(int dev) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_devices[dev].scratch != nullptr) return 0;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, kScratchBytes);
+    if (e != hipSuccess) {
+        set_error_context("allocating the reduction scratch (%zu bytes)", kScratchBytes);
+        return (int)e;
+    }
+    e = hipMemset(p, 0, kScratchBytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        set_error_context("zeroing the reduction scratch");
+        return (int)e;
+    }
+    g_devices[dev].scratch = p;
+    return 0;
+}
+
+}  // namespace
+
+hipStream_t current_stream() { return g_stream; }
+
+void set_error_context(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_context, sizeof g_context, fmt, ap);
+    va_end(ap);
+}
+
+int after_launch(const char *name, dim3 grid, dim3 block) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error_context("HIP: launching %s <<<(%u,%u),(%u,%u)>>> failed: %s", name, grid.x, grid.y,
+                          block.x, block.y, hipGetErrorString(e));
+        return (int)e;
+    }
+    if (g_sync_after_launch) {
+        e = hipStreamSynchronize(g_stream);
+        if (e != hipSuccess) {
+            set_error_context("HIP: %s <<<(%u,%u),(%u,%u)>>> faulted: %s", name, grid.x, grid.y,
+                              block.x, block.y, hipGetErrorString(e));
+            return (int)e;
+        }
+    }
+    return 0;
+}
+
+int device_scratch(Scratch *out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    if (g_devices[dev].scratch == nullptr) DKZ_TRY(ensure_scratch(dev));
+    char *base = static_cast<char *>(g_devices[dev].scratch);
+    out->counters = reinterpret_cast<uint32_t *>(base);
+    out->partials = reinterpret_cast<double *>(base + kCounterBytes);
+    return 0;
+}
+
+}  // namespace dkz
+
+using namespace dkz;
+
+extern "C" {
+
+int dkz_device_count(int *count) {
+    DKZ_REQUIRE(count != nullptr);
+    return (int)hipGetDeviceCount(count);
+}
+
+int dkz_init(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) {
+        set_error_context("querying device count");
+        return (int)e;
+    }
+    if (device < 0 || device >= count || device >= 64) {
+        set_error_context("Requested GPU %d but only %d HIP device(s) present", device, count);
+        return (int)hipErrorInvalidDevice;
+    }
+    e = hipSetDevice(device);
+    if (e != hipSuccess) {
+        set_error_context("selecting the device");
+        return (int)e;
+    }
+    if (env_flag("DARKNET_GPU_SYNC") || env_flag("DARKNET_HIP_SYNC")) g_sync_after_launch = true;
+    return ensure_scratch(device);
+}
+
+int dkz_device_name(int device, char *buf, int len) {
+    DKZ_REQUIRE(buf != nullptr && len > 0);
+    buf[0] = '\0';
+    hipDevice_t dev;
+    hipError_t e = hipDeviceGet(&dev, device);
+    if (e != hipSuccess) return (int)e;
+    return (int)hipDeviceGetName(buf, len - 1 > 0 ? len - 1 : 1, dev);
+}
+
+int dkz_mem_info(size_t *free_bytes, size_t *total_bytes) {
+    DKZ_REQUIRE(free_bytes != nullptr && total_bytes != nullptr);
+    return (int)hipMemGetInfo(free_bytes, total_bytes);
+}
+
+int dkz_malloc(void **ptr, size_t bytes) {
+    DKZ_REQUIRE(ptr != nullptr);
+    *ptr = nullptr;
+    if (bytes == 0) return 0;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        set_error_context("device allocation of %zu bytes", bytes);
+        *ptr = nullptr;
+        return (int)e;
+    }
+    e = hipMemsetAsync(*ptr, 0, bytes, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        set_error_context("zeroing device memory");
+        (void)hipFree(*ptr);
+        *ptr = nullptr;
+    }
+    return (int)e;
+}
+
+int dkz_free(void *ptr) {
+    if (ptr == nullptr) return 0;
+    return (int)hipFree(ptr);
+}
+
+int dkz_memset_zero(void *ptr, size_t bytes) {
+    if (bytes == 0) return 0;
+    DKZ_REQUIRE(ptr != nullptr);
+    return (int)hipMemsetAsync(ptr, 0, bytes, g_stream);
+}
+
+int dkz_copy_to_device(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return 0;
+    DKZ_REQUIRE(dst != nullptr && src != nullptr);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) set_error_context("copy host to device");
+    return (int)e;
+}
+
+int dkz_copy_to_host(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return 0;
+    DKZ_REQUIRE(dst != nullptr && src != nullptr);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) set_error_context("copy device to host");
+    return (int)e;
+}
+
+int dkz_synchronize(void) {
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) set_error_context("device synchronise");
+    return (int)e;
+}
+
+const char *dkz_error_string(int err) { return hipGetErrorString((hipError_t)err); }
+
+void dkz_set_sync_after_launch(int on) { g_sync_after_launch = on != 0; }
+
+int dkz_get_sync_after_launch(void) { return g_sync_after_launch ? 1 : 0; }
+
+const char *dkz_last_error_context(void) { return g_context; }
+
+int dkz_set_stream(void *stream) {
+    g_stream = static_cast<hipStream_t>(stream);
+    return 0;
+}
+
+void *dkz_get_stream(void) { return g_stream; }
+
+}  // extern "C"

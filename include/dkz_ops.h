@@ -1,0 +1,271 @@
+/*
+ * dkz_ops.h -- C ABI of the MI355X (gfx950) tensor-op layer for darknet-zig.
+ *
+ * This header is the whole drop-in boundary. It replaces two things in the
+ * reference (Eightscer/darknet_zig):
+ *
+ *   - the HIP backend glue src/hip/hip.zig:60-135 (device, memory, sync), and
+ *   - the launch half of src/gpu.zig: the 37-kernel registry (gpu.zig:188-233),
+ *     code-object loading (gpu.zig:240-257, 283-319), launchDims/launch1d/
+ *     launchPerFilter (gpu.zig:427-477) and each op wrapper's argument
+ *     marshalling (gpu.zig:483-800).
+ *
+ * Every op keeps the argument order and meaning of its gpu.zig wrapper: device
+ * pointers where gpu.zig passes a Buf's .ptr, `int` where gpu.zig casts a usize
+ * with ci() (gpu.zig:416-418), `float` scalars and the activation code as an
+ * int (src/activations.zig:11-27). Kernels are private to the library; no
+ * module, function or launch symbol is exported.
+ *
+ * Conventions shared by every entry point:
+ *   - Return value: 0 on success, otherwise a hipError_t value (decode it with
+ *     dkz_error_string). gpu.zig's must() turns a nonzero value into a panic
+ *     (gpu.zig:51-55); callers that want that behaviour do the same.
+ *   - A negative size or a null pointer where elements must be touched returns
+ *     hipErrorInvalidValue (1) and launches nothing.
+ *   - n == 0 / filters == 0 / batch == 0 is a silent no-op, as launch1d and
+ *     launchPerFilter make it (gpu.zig:468, 475).
+ *   - Work is issued, in call order, on the library's current stream (the null
+ *     stream unless dkz_set_stream chose another), asynchronously to the host,
+ *     as the reference issues everything on the null stream (hip.zig:134).
+ *     dkz_copy_to_host blocks until earlier work on that stream is done.
+ *   - With sync-after-launch on (dkz_set_sync_after_launch, or the environment
+ *     variable DARKNET_GPU_SYNC / DARKNET_HIP_SYNC read by dkz_init) each op
+ *     waits for its kernels and returns the fault, and dkz_last_error_context
+ *     names the kernel (gpu.zig:173-183, 321-327, 456-464).
+ *   - Layout is NCHW: element (b, f, s) of a [batch, filters, spatial] tensor is
+ *     at ((b * filters) + f) * spatial + s (src/blas.zig:51).
+ *   - Results follow the CPU twins in src/blas.zig, src/activations.zig and
+ *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
+ *     per-channel and per-row reductions and softmax within 1e-5 relative,
+ *     maxpool indices bit-exact.
+ *   - The library owns one scratch buffer per device for reduction partials
+ *     and their completion counters, allocated by dkz_init. Ops never
+ *     allocate. Reductions issued concurrently on two streams of one device
+ *     share that buffer and race; issue them on one stream.
+ */
+#ifndef DKZ_OPS_H
+#define DKZ_OPS_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Activation codes: the enum values of src/activations.zig:11-27. */
+enum dkz_activation {
+    DKZ_LOGISTIC = 0,
+    DKZ_RELU = 1,
+    DKZ_RELIE = 2,
+    DKZ_LINEAR = 3,
+    DKZ_RAMP = 4,
+    DKZ_TANH = 5,
+    DKZ_PLSE = 6,
+    DKZ_LEAKY = 7,
+    DKZ_ELU = 8,
+    DKZ_LOGGY = 9,
+    DKZ_STAIR = 10,
+    DKZ_HARDTAN = 11,
+    DKZ_LHTAN = 12,
+    DKZ_SELU = 13
+};
+
+/* ------------------------------------------------------------------------ */
+/* Device and memory glue                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:259-347 init(): select `device`, read DARKNET_GPU_SYNC, allocate the
+ * device's reduction scratch. Returns hipErrorInvalidDevice (101) when
+ * `device` is out of range (gpu.zig:274-277 NoSuchDevice). */
+int dkz_init(int device);
+
+/* hip.zig:69-71 deviceCount. */
+int dkz_device_count(int *count);
+
+/* hip.zig:77-81 deviceName; writes at most len-1 bytes plus a NUL. */
+int dkz_device_name(int device, char *buf, int len);
+
+/* hip.zig:83-85 memInfo. */
+int dkz_mem_info(size_t *free_bytes, size_t *total_bytes);
+
+/* gpu.zig:362-369 alloc(): hipMalloc followed by zero fill. bytes == 0 gives
+ * *ptr = NULL and success, as alloc(0) returns a null Buf. */
+int dkz_malloc(void **ptr, size_t bytes);
+
+/* gpu.zig:384-387 free(); NULL is a no-op. */
+int dkz_free(void *ptr);
+
+/* hip.zig:95-97 memsetZero. Ordered on the current stream. */
+int dkz_memset_zero(void *ptr, size_t bytes);
+
+/* gpu.zig:389-393 push() / hip.zig:99-101 copyToDevice. Blocking. */
+int dkz_copy_to_device(void *dst, const void *src, size_t bytes);
+
+/* gpu.zig:395-405 pull()/pullInts() / hip.zig:103-105 copyToHost. Blocking,
+ * after all earlier work on the current stream. */
+int dkz_copy_to_host(void *dst, const void *src, size_t bytes);
+
+/* gpu.zig:407-410 sync() / hip.zig:107-109 synchronize. */
+int dkz_synchronize(void);
+
+/* hip.zig:60-62 errorString. */
+const char *dkz_error_string(int err);
+
+/* gpu.zig:181-183 setSyncAfterLaunch. */
+void dkz_set_sync_after_launch(int on);
+int dkz_get_sync_after_launch(void);
+
+/* Name of the kernel (and launch shape) behind the last nonzero return on
+ * this host thread, or "" -- the text of gpu.zig:445-462's panic messages. */
+const char *dkz_last_error_context(void);
+
+/* No counterpart in the reference, which always uses the null stream: choose
+ * the hipStream_t (passed as void*) that later ops and copies are issued on.
+ * NULL selects the null stream again. */
+int dkz_set_stream(void *stream);
+void *dkz_get_stream(void);
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise ops (gpu.zig:483-521; CPU twins blas.zig:13-46,              */
+/* activations.zig:107-143)                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:483 fill(x, n, alpha): x[i] = alpha.            blas.zig:13 */
+int dkz_fill(float *x, int n, float alpha);
+
+/* gpu.zig:487 copy(n, x, y): y[i] = x[i].                 blas.zig:17 */
+int dkz_copy(int n, const float *x, float *y);
+
+/* gpu.zig:491 axpy(n, alpha, x, y): y[i] = fmaf(alpha, x[i], y[i]) -- one
+ * rounding, as blas.zig:21-24 contracts under @setFloatMode(.optimized). */
+int dkz_axpy(int n, float alpha, const float *x, float *y);
+
+/* gpu.zig:495 scal(n, alpha, x): x[i] *= alpha.           blas.zig:26 */
+int dkz_scal(int n, float alpha, float *x);
+
+/* gpu.zig:499 mul(n, x, y): y[i] *= x[i].                 blas.zig:31 */
+int dkz_mul(int n, const float *x, float *y);
+
+/* gpu.zig:507 constrainArray(n, alpha, x): clamp to [-alpha, alpha]; NaN
+ * becomes +alpha as std.math.clamp does (blas.zig:44-46). */
+int dkz_constrain(int n, float alpha, float *x);
+
+/* gpu.zig:515 activateArray(x, n, a): x[i] = act(x[i]) (activations.zig:58-81,
+ * 107-125). Exp-based activations use a bit-exact restatement of the host
+ * libm expf. */
+int dkz_activate_array(float *x, int n, int a);
+
+/* gpu.zig:519 gradientArray(x, n, a, delta): delta[i] *= grad(x[i]), where x is
+ * the activation's output (activations.zig:85-104, 127-143). */
+int dkz_gradient_array(const float *x, int n, int a, float *delta);
+
+/* ------------------------------------------------------------------------ */
+/* Bias / scale broadcasts and their reductions (gpu.zig:527-555,           */
+/* blas.zig:53-100)                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:527 addBias: output[b,f,s] += biases[f].         blas.zig:53 */
+int dkz_add_bias(float *output, const float *biases, int batch, int filters, int spatial);
+
+/* gpu.zig:533 scaleBias: output[b,f,s] *= scales[f].       blas.zig:63 */
+int dkz_scale_bias(float *output, const float *scales, int batch, int filters, int spatial);
+
+/* gpu.zig:539-549 backwardBias: bias_updates[f] += sum over b,s of delta.
+ * spatial == 1 takes gpu.zig:540-543's per-filter path. blas.zig:73 */
+int dkz_backward_bias(float *bias_updates, const float *delta, int batch, int filters, int spatial);
+
+/* gpu.zig:551 backwardScale: scale_updates[f] += sum of delta*x_norm.
+ * blas.zig:84-100 */
+int dkz_backward_scale(const float *x_norm, const float *delta, int batch, int filters, int spatial,
+                       float *scale_updates);
+
+/* ------------------------------------------------------------------------ */
+/* Batch normalisation (gpu.zig:561-608, blas.zig:106-204)                   */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:561 mean: out[f] = (sum of x) * (1/(batch*spatial)).   blas.zig:106 */
+int dkz_mean(const float *x, int batch, int filters, int spatial, float *out);
+
+/* gpu.zig:567 variance: out[f] = (sum of (x-m)^2) * (1/(batch*spatial-1)).
+ * blas.zig:121-135 */
+int dkz_variance(const float *x, const float *mean, int batch, int filters, int spatial, float *out);
+
+/* gpu.zig:573 normalize: x = (x - m) * (1/(sqrt(v) + 1e-6)).  blas.zig:137-146 */
+int dkz_normalize(float *x, const float *mean, const float *variance, int batch, int filters,
+                  int spatial);
+
+/* gpu.zig:580 meanDelta: out[f] = (sum of delta) * (-1/sqrt(v + 1e-5)).
+ * blas.zig:148-157 */
+int dkz_mean_delta(const float *delta, const float *variance, int batch, int filters, int spatial,
+                   float *out);
+
+/* gpu.zig:586 varianceDelta: out[f] = (sum of delta*(x-m)) * -0.5 * (v+1e-5)^-1.5.
+ * blas.zig:159-178 */
+int dkz_variance_delta(const float *x, const float *delta, const float *mean, const float *variance,
+                       int batch, int filters, int spatial, float *out);
+
+/* gpu.zig:592-608 normalizeDelta: delta = delta*inv + vd*2*(x-m)/N + md/N.
+ * blas.zig:180-204 */
+int dkz_normalize_delta(const float *x, const float *mean, const float *variance,
+                        const float *mean_delta, const float *variance_delta, int batch, int filters,
+                        int spatial, float *delta);
+
+/* ------------------------------------------------------------------------ */
+/* Softmax and losses (gpu.zig:614-645, blas.zig:213-282)                    */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:614-629 softmax: per (b, g) group at b*batch_offset + g*group_offset,
+ * n elements `stride` apart; max, exp(x/T - max/T), sum, divide.
+ * blas.zig:213-242 */
+int dkz_softmax(const float *input, int n, int batch, int batch_offset, int groups, int group_offset,
+                int stride, float temp, float *output);
+
+/* gpu.zig:631 softmaxCrossEntropy: err = t != 0 ? -log(p) : 0; delta = t - p.
+ * blas.zig:247-252 */
+int dkz_softmax_cross_entropy(int n, const float *pred, const float *truth, float *delta, float *err);
+
+/* gpu.zig:635 l2 / 639 l1 / 643 smoothL1.                 blas.zig:254-282 */
+int dkz_l2(int n, const float *pred, const float *truth, float *delta, float *err);
+int dkz_l1(int n, const float *pred, const float *truth, float *delta, float *err);
+int dkz_smooth_l1(int n, const float *pred, const float *truth, float *delta, float *err);
+
+/* ------------------------------------------------------------------------ */
+/* Pooling and shortcut (gpu.zig:725-800, pooling.zig:59-172,               */
+/* blas.zig:290-322)                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:725-741 forwardMaxpool, called from pooling.zig:105-108 with
+ * out_n = out_h*out_w*c*batch; out_w = (in_w + pad - size)/stride + 1.
+ * Window offset -pad/2; first maximum under strict '>'; indexes holds the
+ * absolute flat input index, -1 for a window with no valid tap.
+ * pooling.zig:59-93 */
+int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int size, int pad,
+                        const float *input, float *output, int *indexes);
+
+/* gpu.zig:743-759 backwardMaxpool, called from pooling.zig:110-114 with
+ * in_n = h*w*c*batch: prev_delta[indexes[o]] += delta[o], contributions to one
+ * element added in ascending o. indexes must come from dkz_forward_maxpool
+ * with the same geometry. pooling.zig:95-103 */
+int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int size, int pad,
+                         const float *delta, float *prev_delta, const int *indexes);
+
+/* gpu.zig:761 forwardAvgpool(n = c*batch, w, h, c): out[r] = (sum of the
+ * row's w*h inputs) / (w*h).                              pooling.zig:146-158 */
+int dkz_forward_avgpool(int n, int w, int h, int c, const float *input, float *output);
+
+/* gpu.zig:765 backwardAvgpool(n = c*batch, w, h, c, in_delta, out_delta):
+ * in_delta[r, s] += out_delta[r] / (w*h).                 pooling.zig:160-172 */
+int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const float *out_delta);
+
+/* gpu.zig:773-800 shortcut: out = s1*out + s2*add over the overlapping
+ * region, with stride = w1/w2 and sample = w2/w1 (each at least 1) computed
+ * here as gpu.zig:786-793 does. Two products, then a sum; no fma.
+ * blas.zig:290-322 */
+int dkz_shortcut(int batch, int w1, int h1, int c1, const float *add, int w2, int h2, int c2,
+                 float s1, float s2, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DKZ_OPS_H */

@@ -1,0 +1,81 @@
+"""Shared helpers: seeded inputs, device round trips and the parity rules.
+
+Parity rules (north star):
+  * elementwise, broadcast and index results: bit-exact (NaNs compare equal
+    to each other whatever their payload);
+  * reductions and softmax-derived losses: an element passes when
+    |gpu - cpu| <= 1e-5 * |cpu|, or when the GPU value is at least as close to
+    an f64 evaluation of the same formula as the CPU twin's is. The second
+    clause covers ill-conditioned sums (a channel mean of N(0,1) data is ~0),
+    where the twin's own sequential f32 rounding error exceeds 1e-5 relative.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from darknet_zig_amd import gpu
+
+RTOL = 1e-5
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def uniform(r: np.random.Generator, shape, lo=-1.0, hi=1.0) -> np.ndarray:
+    return r.uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def normal(r: np.random.Generator, shape, mu=0.0, sigma=1.0) -> np.ndarray:
+    return r.normal(mu, sigma, size=shape).astype(np.float32)
+
+
+def up(a: np.ndarray) -> gpu.Buf:
+    return gpu.make(np.ascontiguousarray(a))
+
+
+def down(b: gpu.Buf, like: np.ndarray) -> np.ndarray:
+    out = np.empty_like(like)
+    gpu.pull(b, out)
+    return out
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(a).view(np.uint32).copy()
+    nan = np.isnan(a.astype(np.float32, copy=False)) if a.dtype == np.float32 else np.zeros(a.shape, bool)
+    u[nan] = 0x7FC00000
+    return u
+
+
+def assert_bitexact(got: np.ndarray, want: np.ndarray, name: str) -> None:
+    assert got.shape == want.shape and got.dtype == want.dtype, (name, got.shape, want.shape)
+    g, w = bits(got).ravel(), bits(want).ravel()
+    bad = np.nonzero(g != w)[0]
+    if bad.size:
+        i = bad[:5]
+        raise AssertionError(
+            f"{name}: {bad.size} of {g.size} elements differ; first at {i.tolist()}: "
+            f"gpu={got.ravel()[i].tolist()} cpu={want.ravel()[i].tolist()}"
+        )
+
+
+def assert_r5(got: np.ndarray, cpu: np.ndarray, ref64: np.ndarray, name: str) -> dict:
+    """The reduction rule above; returns error statistics for reporting."""
+    got64, cpu64, ref = got.astype(np.float64), cpu.astype(np.float64), ref64.astype(np.float64)
+    d = np.abs(got64 - cpu64)
+    ok = (d <= RTOL * np.abs(cpu64)) | (np.abs(got64 - ref) <= np.abs(cpu64 - ref))
+    ok |= (np.isnan(got64) & np.isnan(cpu64)) | (got64 == cpu64)
+    if not ok.all():
+        i = np.nonzero(~ok)[0][:5]
+        raise AssertionError(
+            f"{name}: {int((~ok).sum())} of {ok.size} outside 1e-5 of the CPU twin and farther from f64; "
+            f"first {i.tolist()}: gpu={got.ravel()[i].tolist()} cpu={cpu.ravel()[i].tolist()} "
+            f"f64={ref.ravel()[i].tolist()}"
+        )
+    scale = np.maximum(np.abs(ref), 1e-30)
+    return {
+        "max_rel_gpu_vs_cpu": float(np.max(d / np.maximum(np.abs(cpu64), 1e-30))),
+        "max_rel_gpu_vs_f64": float(np.max(np.abs(got64 - ref) / scale)),
+        "max_rel_cpu_vs_f64": float(np.max(np.abs(cpu64 - ref) / scale)),
+    }

@@ -1,0 +1,180 @@
+"""GPU parity of softmax, max/avg pooling and the shortcut.
+
+Softmax: gputest's 8x137 (gputest.zig:252-279) and config 3 ([256,1000],
+logits ~N(0,4)) are bit-exact (sequential-sum path); strided groups (spatial
+softmax) are bit-exact; rows longer than the LDS stage are held to 1e-5.
+Maxpool: output bit-exact, indexes bit-exact (IX), backward bit-exact.
+Avgpool: forward within 1e-5 (row sums), backward bit-exact. Shortcut:
+bit-exact on the same-shape, stride, upsample and channel-mismatch paths.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from darknet_zig_amd import gpu
+from oracle import ref
+from tests.helpers import assert_bitexact, assert_r5, down, normal, rng, uniform, up
+
+pytestmark = pytest.mark.gpu
+
+
+def _softmax_case(x, n, batch, batch_offset, groups, group_offset, stride, temp):
+    cpu = np.zeros_like(x)
+    ref.softmax(x, n, batch, batch_offset, groups, group_offset, stride, temp, cpu)
+    dx, dout = up(x), up(np.zeros_like(x))
+    gpu.softmax(dx, n, batch, batch_offset, groups, group_offset, stride, temp, dout)
+    got = down(dout, x)
+    gpu.free(dx)
+    gpu.free(dout)
+    return got, cpu
+
+
+@pytest.mark.parametrize(
+    "batch, classes, sigma, temp",
+    [(8, 137, 1.0, 1.0), (256, 1000, 4.0, 1.0), (3, 33, 10.0, 0.5), (5, 8192, 2.0, 1.0), (17, 1, 1.0, 1.0),
+     (4, 5, 1.0, 2.0)],
+)
+def test_softmax_rows_bitexact(dev, batch, classes, sigma, temp):
+    x = normal(rng(classes + batch), batch * classes, 0, sigma)
+    got, cpu = _softmax_case(x, classes, batch, classes, 1, classes, 1, temp)
+    assert_bitexact(got, cpu, f"softmax {batch}x{classes}")
+    np.testing.assert_allclose(got.reshape(batch, classes).sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_softmax_long_rows(dev):
+    batch, classes = 3, 20000
+    x = normal(rng(5), batch * classes, 0, 3.0)
+    got, cpu = _softmax_case(x, classes, batch, classes, 1, classes, 1, 1.0)
+    x64 = x.astype(np.float64).reshape(batch, classes)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    assert_r5(got, cpu, (e / e.sum(axis=1, keepdims=True)).ravel(), "softmax long rows")
+
+
+def test_softmax_spatial_groups(dev):
+    # Spatial softmax: groups = positions, elements `spatial` apart
+    # (n = channels, batch_offset = c*s, groups = s, group_offset = 1, stride = s).
+    b, c, s = 2, 11, 49
+    x = normal(rng(11), b * c * s, 0, 2.0)
+    got, cpu = _softmax_case(x, c, b, c * s, s, 1, s, 1.0)
+    assert_bitexact(got, cpu, "spatial softmax")
+    np.testing.assert_allclose(got.reshape(b, c, s).sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_softmax_then_xent_config3(dev):
+    """Config 3: logits [256,1000] ~N(0,4), one-hot labels; p then
+    softmax_x_ent's delta = t - p is bit-exact and sums to 0 per row."""
+    batch, classes = 256, 1000
+    r = rng(3)
+    x = normal(r, batch * classes, 0, 4.0)
+    truth = np.zeros(batch * classes, np.float32)
+    truth[np.arange(batch) * classes + r.integers(0, classes, batch)] = 1.0
+    got, cpu = _softmax_case(x, classes, batch, classes, 1, classes, 1, 1.0)
+    assert_bitexact(got, cpu, "softmax cfg3")
+    d_c, e_c = np.empty_like(x), np.empty_like(x)
+    ref.softmaxCrossEntropy(cpu, truth, d_c, e_c)
+    dp, dt, dd, de = up(got), up(truth), gpu.alloc(x.size), gpu.alloc(x.size)
+    gpu.softmaxCrossEntropy(x.size, dp, dt, dd, de)
+    d = down(dd, x)
+    assert_bitexact(d, d_c, "xent delta")
+    np.testing.assert_allclose(d.reshape(batch, classes).sum(axis=1), 0.0, atol=1e-5)
+    np.testing.assert_allclose(down(de, x), e_c, rtol=1e-5)
+    for bb in (dp, dt, dd, de):
+        gpu.free(bb)
+
+
+MAXPOOL_CASES = [
+    # batch, c, h, w, size, stride, pad
+    (3, 6, 14, 14, 2, 2, 1),      # gputest.zig:393-399 (generic path: w % 4 != 0)
+    (2, 3, 8, 8, 2, 2, 1),        # 2x2 fast path
+    (2, 3, 8, 8, 2, 2, 0),        # fast path, pad 0
+    (2, 4, 13, 13, 2, 2, 1),      # odd input: last column dropped
+    (2, 3, 9, 11, 3, 2, 2),       # overlapping windows, several contributors
+    (1, 2, 7, 7, 3, 1, 2),        # darknet size=3 stride=1 (default pad size-1)
+    (2, 2, 6, 10, 5, 3, 4),
+    (256, 512, 28, 28, 2, 2, 1),  # config 5
+]
+
+
+@pytest.mark.parametrize("case", MAXPOOL_CASES, ids=str)
+def test_maxpool(dev, case):
+    batch, c, h, w, size, stride, pad = case
+    oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
+    r = rng(sum(case))
+    x = uniform(r, batch * c * h * w)
+    if batch * c * h * w < 10000:
+        x[::7] = np.float32(0.25)  # ties: the first maximum must win
+        x[3] = np.nan
+        x[5] = -np.inf
+    out_n = batch * c * oh * ow
+    out_c, idx_c = np.empty(out_n, np.float32), np.empty(out_n, np.int32)
+    ref.forwardMaxpool(batch, h, w, c, size, stride, pad, x, out_c, idx_c)
+    dx, dout, didx = up(x), gpu.alloc(out_n), gpu.allocInts(out_n)
+    gpu.forwardMaxpool(out_n, h, w, c, stride, size, pad, dx, dout, didx)
+    assert_bitexact(down(dout, out_c), out_c, f"maxpool fwd {case}")
+    assert_bitexact(down(didx, idx_c), idx_c, f"maxpool idx {case}")
+
+    delta = uniform(r, out_n)
+    prev = uniform(r, x.size) if x.size < 10**6 else np.zeros_like(x)
+    prev_c = prev.copy()
+    ref.backwardMaxpool(idx_c, delta, prev_c)
+    dd, dprev = up(delta), up(prev)
+    gpu.backwardMaxpool(x.size, h, w, c, stride, size, pad, dd, dprev, didx)
+    got = down(dprev, prev)
+    assert_bitexact(got, prev_c, f"maxpool bwd {case}")
+    if stride >= size:  # at most one contributor per input: the delta is conserved
+        np.testing.assert_allclose(got.astype(np.float64).sum() - prev.astype(np.float64).sum(),
+                                   delta[idx_c >= 0].astype(np.float64).sum(), rtol=1e-4, atol=1e-3)
+    for b in (dx, dout, didx, dd, dprev):
+        gpu.free(b)
+
+
+@pytest.mark.parametrize("batch, c, h, w", [(3, 6, 14, 14), (2, 5, 7, 7), (4, 3, 1, 1), (256, 512, 28, 28)])
+def test_avgpool(dev, batch, c, h, w):
+    r = rng(batch * c + h)
+    x = uniform(r, batch * c * h * w)
+    n = batch * c
+    out_c = np.empty(n, np.float32)
+    ref.forwardAvgpool(batch, w, h, c, x, out_c)
+    dx, dout = up(x), gpu.alloc(n)
+    gpu.forwardAvgpool(n, w, h, c, dx, dout)
+    x64 = x.astype(np.float64).reshape(n, h * w)
+    assert_r5(down(dout, out_c), out_c, x64.sum(axis=1) / (h * w), f"avgpool fwd {(batch, c, h, w)}")
+
+    od = uniform(r, n)
+    prev = uniform(r, x.size)
+    prev_c = prev.copy()
+    ref.backwardAvgpool(batch, w, h, c, od, prev_c)
+    dod, dprev = up(od), up(prev)
+    gpu.backwardAvgpool(n, w, h, c, dprev, dod)
+    assert_bitexact(down(dprev, prev), prev_c, f"avgpool bwd {(batch, c, h, w)}")
+    for b in (dx, dout, dod, dprev):
+        gpu.free(b)
+
+
+SHORTCUT_CASES = [
+    # batch, w1, h1, c1 (add), w2, h2, c2 (out), s1, s2
+    (2, 8, 8, 4, 8, 8, 4, 1.0, 1.0),          # gputest.zig:453-480
+    (64, 28, 28, 256, 14, 14, 512, 1.0, 1.0), # config 4: stride 2, channel mismatch
+    (3, 14, 14, 8, 7, 7, 8, 0.5, 2.0),        # stride 2, odd output width (generic)
+    (2, 7, 7, 6, 14, 14, 3, 1.0, -0.75),      # upsample: sample 2
+    (2, 9, 9, 5, 4, 4, 5, 0.9, 1.1),          # w1/w2 = 2 with remainder
+    (1, 5, 5, 3, 5, 5, 9, 2.0, 1.0),          # channel mismatch only
+]
+
+
+@pytest.mark.parametrize("case", SHORTCUT_CASES, ids=str)
+def test_shortcut(dev, case):
+    batch, w1, h1, c1, w2, h2, c2, s1, s2 = case
+    r = rng(sum(case[:7]))
+    add, out = normal(r, batch * c1 * h1 * w1, 0, 0.05), normal(r, batch * c2 * h2 * w2, 0, 0.05)
+    cpu = out.copy()
+    ref.shortcut(batch, w1, h1, c1, add, w2, h2, c2, s1, s2, cpu)
+    da, do = up(add), up(out)
+    gpu.shortcut(batch, w1, h1, c1, da, w2, h2, c2, s1, s2, do)
+    assert_bitexact(down(do, out), cpu, f"shortcut {case}")
+    if case[1:4] == case[4:7] and s1 == s2 == 1.0:  # same shape: exact addition
+        assert_bitexact(cpu, (out + add).astype(np.float32), "shortcut == add")
+    gpu.free(da)
+    gpu.free(do)
