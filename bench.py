@@ -1,0 +1,506 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 tensor-op layer on BASELINE.json's workload.
+
+Headline (the one JSON line on stdout): configs[1], the batch-norm backward
+layer step of darknet-zig at [64,128,56,56] fp32 -- gradient (leaky),
+backward_bias, backward_scale, scale_bias(delta), mean_delta, variance_delta,
+normalize_delta (convolutional.zig:280-286 + batchnorm.zig:155-174), run
+through the C ABI exactly as the layer issues it. One step = one such pass
+over one batch; inputs are resident in HBM and rotate over three buffer sets
+(1.2 GB) so no step starts from data the 256 MB Infinity Cache still holds.
+
+  value        algorithmic bytes of the 7-op chain x steps / wall time of the
+               timed region (HIP events on the library's stream), in GB/s
+  roofline     the chain's longest kernel: its algorithmic bytes / its mean
+               duration from per-kernel HIP events over the same steps,
+               against MI355X's 8 TB/s HBM peak
+  per_op       every op of BASELINE.json's five configs timed on its own,
+               cold (rotated buffers, >= 512 MB per rotation), in GB/s and as
+               a fraction of 8 TB/s
+  bn_act_gelem_s  config 1 elements / sum of config 1 op times (forward) and
+               config 2 elements / sum of config 2 op times (backward)
+  cpu_baseline the CPU twins' C restatement (oracle/) on the same inputs on
+               this host, one thread, median of 3 full config-2 chains
+
+Algorithmic bytes count every logical fp32/int32 element read or written once
+(4 B); per-channel vectors are not counted (BASELINE.md's accounting).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
+METRIC = "achieved HBM GB/s (% of MI355X peak) per op; BN+act fwd+bwd GElem/s"
+
+
+# ---------------------------------------------------------------------------
+# HIP events (the library issues on the null stream unless told otherwise)
+# ---------------------------------------------------------------------------
+
+
+class Hip:
+    def __init__(self):
+        self.lib = C.CDLL("libamdhip64.so")
+        for name, args in {
+            "hipEventCreate": [C.POINTER(C.c_void_p)],
+            "hipEventRecord": [C.c_void_p, C.c_void_p],
+            "hipEventSynchronize": [C.c_void_p],
+            "hipEventElapsedTime": [C.POINTER(C.c_float), C.c_void_p, C.c_void_p],
+            "hipEventDestroy": [C.c_void_p],
+            "hipDeviceSynchronize": [],
+        }.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+
+    def event(self) -> C.c_void_p:
+        e = C.c_void_p()
+        assert self.lib.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream) -> None:
+        assert self.lib.hipEventRecord(e, stream) == 0
+
+    def ms(self, a, b) -> float:
+        assert self.lib.hipEventSynchronize(b) == 0
+        out = C.c_float()
+        assert self.lib.hipEventElapsedTime(C.byref(out), a, b) == 0
+        return float(out.value)
+
+    def sync(self) -> None:
+        assert self.lib.hipDeviceSynchronize() == 0
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+
+def gen(seed: int):
+    return np.random.default_rng(seed)
+
+
+class Device:
+    """Device buffers of one run, uploaded once and freed at exit."""
+
+    def __init__(self, gpu):
+        self.gpu = gpu
+        self.bufs = []
+
+    def up(self, a: np.ndarray):
+        b = self.gpu.make(np.ascontiguousarray(a))
+        self.bufs.append(b)
+        return b
+
+    def zeros(self, n: int):
+        b = self.gpu.alloc(n)
+        self.bufs.append(b)
+        return b
+
+    def clone(self, b, n: int, k: int):
+        """k copies of b made on the device (copy kernel)."""
+        out = [b]
+        for _ in range(k - 1):
+            c = self.zeros(n)
+            self.gpu.copy(n, b, c)
+            out.append(c)
+        return out
+
+    def free(self):
+        for b in self.bufs:
+            self.gpu.free(b)
+        self.bufs = []
+
+
+def rotations(bytes_per_set: int, min_total: int = 512 << 20, lo: int = 2) -> int:
+    return max(lo, -(-min_total // max(bytes_per_set, 1)))
+
+
+def config2_host(seed=2):
+    B, F, S = 64, 128, 56 * 56
+    n = B * F * S
+    r = gen(seed)
+    y = r.normal(0, 1, n).astype(np.float32)
+    y = np.where(y > 0, y, np.float32(0.1) * y).astype(np.float32)  # leaky output
+    delta = r.normal(0, 1, n).astype(np.float32)
+    x = r.normal(0, 1, n).astype(np.float32)
+    x_norm = r.normal(0, 1, n).astype(np.float32)
+    scales = r.uniform(0.5, 1.5, F).astype(np.float32)
+    xm = x.reshape(B, F, S).astype(np.float64)
+    mean = xm.mean(axis=(0, 2)).astype(np.float32)
+    var = xm.var(axis=(0, 2), ddof=1).astype(np.float32)
+    return dict(B=B, F=F, S=S, n=n, y=y, delta=delta, x=x, x_norm=x_norm, scales=scales, mean=mean, var=var)
+
+
+def config2_chain_ops(gpu, d, h):
+    """The 7 ops of one BN backward step on device set d; (name, bytes, fn)."""
+    from darknet_zig_amd.activations import Activation
+
+    B, F, S, n = h["B"], h["F"], h["S"], h["n"]
+    E = 4 * n
+    return [
+        ("gradient_array(leaky)", 3 * E, lambda: gpu.gradientArray(d["y"], n, Activation.leaky, d["delta"])),
+        ("backward_bias", E, lambda: gpu.backwardBias(d["bu"], d["delta"], B, F, S)),
+        ("backward_scale", 2 * E, lambda: gpu.backwardScale(d["x_norm"], d["delta"], B, F, S, d["su"])),
+        ("scale_bias(delta)", 2 * E, lambda: gpu.scaleBias(d["delta"], d["scales"], B, F, S)),
+        ("mean_delta", E, lambda: gpu.meanDelta(d["delta"], d["var"], B, F, S, d["md"])),
+        ("variance_delta", 2 * E, lambda: gpu.varianceDelta(d["x"], d["delta"], d["mean"], d["var"], B, F, S, d["vd"])),
+        ("normalize_delta", 3 * E,
+         lambda: gpu.normalizeDelta(d["x"], d["mean"], d["var"], d["md"], d["vd"], B, F, S, d["delta"])),
+    ]
+
+
+def upload_config2(dev, h, sets: int):
+    F, n = h["F"], h["n"]
+    big = {k: dev.up(h[k]) for k in ("y", "delta", "x", "x_norm")}
+    small = {k: dev.up(h[k]) for k in ("scales", "mean", "var")}
+    out = []
+    clones = {k: dev.clone(v, n, sets) for k, v in big.items()}
+    for s in range(sets):
+        d = {k: clones[k][s] for k in big}
+        d.update(small)
+        d.update(bu=dev.zeros(F), su=dev.zeros(F), md=dev.zeros(F), vd=dev.zeros(F))
+        out.append(d)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# timing
+# ---------------------------------------------------------------------------
+
+
+def time_chain(hip, stream, chains, steps, warmup):
+    """Clean timed region: `steps` chain passes, events only at its ends."""
+    for k in range(warmup):
+        for _, _, fn in chains[k % len(chains)]:
+            fn()
+    hip.sync()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for k in range(steps):
+        for _, _, fn in chains[k % len(chains)]:
+            fn()
+    hip.record(b, stream)
+    ms = hip.ms(a, b)
+    hip.sync()
+    return ms
+
+
+def time_chain_per_kernel(hip, stream, chains, steps):
+    """Per-kernel HIP events around every launch of `steps` chain passes."""
+    nops = len(chains[0])
+    evs = [(hip.event(), hip.event()) for _ in range(steps * nops)]
+    hip.sync()
+    i = 0
+    for k in range(steps):
+        for _, _, fn in chains[k % len(chains)]:
+            hip.record(evs[i][0], stream)
+            fn()
+            hip.record(evs[i][1], stream)
+            i += 1
+    hip.sync()
+    per = [[] for _ in range(nops)]
+    for j, (a, b) in enumerate(evs):
+        per[j % nops].append(hip.ms(a, b))
+    return [statistics.mean(p) for p in per]
+
+
+def time_op(hip, stream, fns, launches, warmup=3):
+    """Mean per-launch time (ms) of an op cycling over rotated inputs."""
+    for k in range(warmup):
+        fns[k % len(fns)]()
+    hip.sync()
+    evs = [(hip.event(), hip.event()) for _ in range(launches)]
+    for k in range(launches):
+        hip.record(evs[k][0], stream)
+        fns[k % len(fns)]()
+        hip.record(evs[k][1], stream)
+    hip.sync()
+    return statistics.mean(hip.ms(a, b) for a, b in evs)
+
+
+def gbs(nbytes: int, ms: float) -> float:
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+# ---------------------------------------------------------------------------
+# per-op table over the five configs
+# ---------------------------------------------------------------------------
+
+
+def per_op_table(gpu, hip, stream, launches: int):
+    from darknet_zig_amd.activations import Activation
+
+    rows = {}
+
+    def add(cfg, name, nbytes, fns, elems=None):
+        ms = time_op(hip, stream, fns, max(launches, len(fns)))
+        g = gbs(nbytes, ms)
+        rows[f"{cfg}/{name}"] = {"us": round(ms * 1e3, 3), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4),
+                                 "bytes": nbytes}
+
+    # -- config 1: BN forward + leaky, [128,32,32,32], x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1)
+    dev = Device(gpu)
+    B, F, S = 128, 32, 1024
+    n = B * F * S
+    E = 4 * n
+    r = gen(1)
+    x = r.normal(0, 1, n).astype(np.float32)
+    R = rotations(E)
+    xs = dev.clone(dev.up(x), n, R)
+    gam, bet = dev.up(r.uniform(0.5, 1.5, F).astype(np.float32)), dev.up(r.normal(0, 0.1, F).astype(np.float32))
+    m, v = dev.zeros(F), dev.zeros(F)
+    gpu.mean(xs[0], B, F, S, m)
+    gpu.variance(xs[0], m, B, F, S, v)
+    cfg = "cfg1_bn_fwd[128,32,32,32]"
+    add(cfg, "mean", E, [lambda b=b: gpu.mean(b, B, F, S, m) for b in xs])
+    add(cfg, "variance", E, [lambda b=b: gpu.variance(b, m, B, F, S, v) for b in xs])
+    add(cfg, "normalize", 2 * E, [lambda b=b: gpu.normalize(b, m, v, B, F, S) for b in xs])
+    add(cfg, "scale_bias", 2 * E, [lambda b=b: gpu.scaleBias(b, gam, B, F, S) for b in xs])
+    add(cfg, "add_bias", 2 * E, [lambda b=b: gpu.addBias(b, bet, B, F, S) for b in xs])
+    add(cfg, "activate(leaky)", 2 * E, [lambda b=b: gpu.activateArray(b, n, Activation.leaky) for b in xs])
+    ys = [dev.zeros(n) for _ in range(R)]
+    add(cfg, "copy (x, x_norm)", 2 * E, [lambda a=a, b=b: gpu.copy(n, a, b) for a, b in zip(xs, ys)])
+    rm, rv = dev.zeros(F), dev.zeros(F)
+    add(cfg, "ema scal+axpy (C floats)", 4 * 3 * F,
+        [lambda: (gpu.scal(F, 0.99, rm), gpu.axpy(F, 0.01, m, rm), gpu.scal(F, 0.99, rv), gpu.axpy(F, 0.01, v, rv))])
+    dev.free()
+
+    # -- config 2: BN backward ops on their own
+    h = config2_host()
+    dev = Device(gpu)
+    sets = upload_config2(dev, h, 3)
+    chains = [config2_chain_ops(gpu, d, h) for d in sets]
+    for j, (name, nbytes, _) in enumerate(chains[0]):
+        add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
+    dev.free()
+
+    # -- config 3: softmax + cross-entropy delta, [256,1000], logits ~N(0,4)
+    dev = Device(gpu)
+    b3, c3 = 256, 1000
+    n3 = b3 * c3
+    r = gen(3)
+    logits = r.normal(0, 4.0, n3).astype(np.float32)
+    truth = np.zeros(n3, np.float32)
+    truth[np.arange(b3) * c3 + r.integers(0, c3, b3)] = 1.0
+    R = rotations(4 * 4 * n3)
+    ls = dev.clone(dev.up(logits), n3, R)
+    ps = [dev.zeros(n3) for _ in range(R)]
+    ts = dev.clone(dev.up(truth), n3, R)
+    ds_ = [dev.zeros(n3) for _ in range(R)]
+    es = [dev.zeros(n3) for _ in range(R)]
+    cfg = "cfg3_softmax[256,1000]"
+    add(cfg, "softmax", 2 * 4 * n3, [lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)])
+    add(cfg, "softmax_x_ent", 4 * 4 * n3,
+        [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)])
+    dev.free()
+
+    # -- config 4: SGD over 25e6 floats ~N(0,0.05), and the stride-2 shortcut
+    dev = Device(gpu)
+    n4 = 25_000_000
+    r = gen(4)
+    R = rotations(2 * 4 * n4)
+    ws = dev.clone(dev.up(r.normal(0, 0.05, n4).astype(np.float32)), n4, R)
+    dws = dev.clone(dev.up(r.normal(0, 0.05, n4).astype(np.float32)), n4, R)
+    batch, lr, decay, momentum = 64, 0.1, 0.0005, 0.9
+    cfg = "cfg4_sgd[25e6]"
+    add(cfg, "axpy(-decay*batch, w, dw)", 3 * 4 * n4,
+        [lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d) for w, d in zip(ws, dws)])
+    add(cfg, "axpy(lr/batch, dw, w)", 3 * 4 * n4, [lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w) for w, d in zip(ws, dws)])
+    add(cfg, "scal(momentum, dw)", 2 * 4 * n4, [lambda d=d: gpu.scal(n4, momentum, d) for d in dws])
+    dev.free()
+    dev = Device(gpu)
+    sb, w1, c1, w2, c2 = 64, 28, 256, 14, 512
+    na, no = sb * c1 * w1 * w1, sb * c2 * w2 * w2
+    s4 = sb * c1 * w2 * w2
+    R = rotations(4 * (na + no))
+    adds = dev.clone(dev.up(r.normal(0, 0.05, na).astype(np.float32)), na, R)
+    outs = dev.clone(dev.up(r.normal(0, 0.05, no).astype(np.float32)), no, R)
+    add("cfg4_shortcut[64,256,28,28]->[64,512,14,14]", "shortcut", 3 * 4 * s4,
+        [lambda a=a, o=o: gpu.shortcut(sb, w1, w1, c1, a, w2, w2, c2, 1.0, 1.0, o) for a, o in zip(adds, outs)])
+    dev.free()
+
+    # -- config 5: pooling at [256,512,28,28], inputs ~U(-1,1)
+    dev = Device(gpu)
+    pb, pc, ph = 256, 512, 28
+    nin = pb * pc * ph * ph
+    oh = (ph + 1 - 2) // 2 + 1
+    nout = pb * pc * oh * oh
+    r = gen(5)
+    R = 2
+    ins = dev.clone(dev.up(r.uniform(-1, 1, nin).astype(np.float32)), nin, R)
+    outs = [dev.zeros(nout) for _ in range(R)]
+    idxs = [dev.zeros(nout) for _ in range(R)]
+    dls = dev.clone(dev.up(r.uniform(-1, 1, nout).astype(np.float32)), nout, R)
+    cfg = "cfg5_pool[256,512,28,28]"
+    add(cfg, "maxpool_fwd 2x2/s2", 4 * (nin + 2 * nout),
+        [lambda i=i, o=o, x=x: gpu.forwardMaxpool(nout, ph, ph, pc, 2, 2, 1, i, o, x) for i, o, x in zip(ins, outs, idxs)])
+    add(cfg, "maxpool_bwd", 4 * (2 * nout + 2 * nin),
+        [lambda d=d, p=p, x=x: gpu.backwardMaxpool(nin, ph, ph, pc, 2, 2, 1, d, p, x) for d, p, x in zip(dls, ins, idxs)])
+    rows_ = pb * pc
+    avg = [dev.zeros(rows_) for _ in range(R)]
+    add(cfg, "avgpool_fwd (global)", 4 * (nin + rows_),
+        [lambda i=i, a=a: gpu.forwardAvgpool(rows_, ph, ph, pc, i, a) for i, a in zip(ins, avg)])
+    add(cfg, "avgpool_bwd (global)", 4 * (2 * nin + rows_),
+        [lambda i=i, a=a: gpu.backwardAvgpool(rows_, ph, ph, pc, i, a) for i, a in zip(ins, avg)])
+    dev.free()
+    return rows
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the CPU twins (C restatement) on the same config-2 inputs
+# ---------------------------------------------------------------------------
+
+
+def cpu_baseline(h, repeats=3):
+    from darknet_zig_amd.activations import Activation
+    from oracle import ref
+
+    B, F, S = h["B"], h["F"], h["S"]
+    chain_bytes = 14 * 4 * h["n"]
+    times = []
+    for _ in range(repeats):
+        d = h["delta"].copy()
+        bu, su = np.zeros(F, np.float32), np.zeros(F, np.float32)
+        md, vd = np.empty(F, np.float32), np.empty(F, np.float32)
+        t0 = time.perf_counter()
+        ref.gradientArray(h["y"], Activation.leaky, d)
+        ref.backwardBias(bu, d, B, F, S)
+        ref.backwardScale(h["x_norm"], d, B, F, S, su)
+        ref.scaleBias(d, h["scales"], B, F, S)
+        ref.meanDelta(d, h["var"], B, F, S, md)
+        ref.varianceDelta(h["x"], d, h["mean"], h["var"], B, F, S, vd)
+        ref.normalizeDelta(h["x"], h["mean"], h["var"], md, vd, B, F, S, d)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(chain_bytes / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"full config-2 chain (7 ops over [64,128,56,56]) on the same inputs, median of {repeats} runs, "
+                   f"{t * 1e3:.1f} ms per chain, 1 thread of {os.cpu_count()} ({model}); C restatement of the Zig "
+                   "CPU twins built -O3 -march=x86-64-v3 -ffp-contract=off"),
+    }
+
+
+# ---------------------------------------------------------------------------
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--op-launches", type=int, default=24, help="timed launches per op in the per-op table")
+    ap.add_argument("--no-per-op", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every op runs on one device's share); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from darknet_zig_amd import gpu
+
+    gpu.init(0)
+    hip = Hip()
+    stream = C.c_void_p(None)  # the library's stream: the null stream
+
+    h = config2_host()
+    dev = Device(gpu)
+    sets = upload_config2(dev, h, 3)
+    chains = [config2_chain_ops(gpu, d, h) for d in sets]
+    chain_bytes = sum(b for _, b, _ in chains[0])
+    hip.sync()
+    ms = time_chain(hip, stream, chains, args.steps, args.warmup)
+    per_kernel_ms = time_chain_per_kernel(hip, stream, chains, args.steps)
+    dev.free()
+
+    names = [nm for nm, _, _ in chains[0]]
+    byts = [b for _, b, _ in chains[0]]
+    dom = max(range(len(names)), key=lambda j: per_kernel_ms[j])
+    achieved = gbs(byts[dom], per_kernel_ms[dom])
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_bn_backward.txt"
+    if tfile.exists():
+        for line in tfile.read_text().splitlines():
+            if line.startswith(f"{names[dom]}:"):
+                try:
+                    traffic = int(line.split(":", 1)[1].split()[0])
+                except ValueError:
+                    traffic = None
+
+    chain_kernels = {names[j]: {"us": round(per_kernel_ms[j] * 1e3, 2),
+                                "GB/s": round(gbs(byts[j], per_kernel_ms[j]), 1)} for j in range(len(names))}
+    result = {
+        "metric": METRIC,
+        "value": round(gbs(chain_bytes * args.steps, ms), 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy: y=leaky(N(0,1)), delta/x/x_norm ~N(0,1), gamma ~U(0.5,1.5))",
+        "config": {
+            "workload": "configs[1]: BN backward layer step (gradient leaky, backward_bias, backward_scale, "
+                        "scale_bias, mean_delta, variance_delta, normalize_delta), fp32 NCHW",
+            "batch": 64, "channels": 128, "height": 56, "width": 56,
+            "bytes_per_step": chain_bytes, "buffer_sets_rotated": 3,
+            "parallelism": "1 GPU",
+        },
+        "roofline": {
+            "kernel": names[dom],
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "chain_kernels": chain_kernels,
+    }
+    if not args.no_per_op:
+        table = per_op_table(gpu, hip, stream, args.op_launches)
+        result["per_op"] = table
+        fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and "copy" not in k and "ema" not in k)
+        bwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg2"))
+        e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
+        result["bn_act_gelem_s"] = {
+            "fwd_cfg1_per_op_sum": round(e1 / (fwd * 1e-6) / 1e9, 2),
+            "bwd_cfg2_per_op_sum": round(e2 / (bwd * 1e-6) / 1e9, 2),
+            "bwd_cfg2_chained": round(e2 / (ms / args.steps * 1e-3) / 1e9, 2),
+        }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(h)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

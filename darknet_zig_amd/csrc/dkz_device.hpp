@@ -206,7 +206,7 @@ __host__ __device__ __forceinline__ float expf_libm(float x) {
 // ---------------------------------------------------------------------------
 // Activations (src/activations.zig:11-27 codes, 58-104 maths). Selects, not
 // multiplies, where the Zig code selects; literals are the f32 roundings of
-// the Zig comptime values (1.0507 * 1.6732 folds to 1.75803324f).
+// the Zig comptime values (1.0507 * 1.6732 folds to 1.75803124f).
 // ---------------------------------------------------------------------------
 enum Act : int {
     kLogistic = 0, kRelu = 1, kRelie = 2, kLinear = 3, kRamp = 4, kTanh = 5, kPlse = 6,
@@ -221,7 +221,7 @@ __device__ __forceinline__ float activate(float x) {
     else if constexpr (A == kLoggy) return 2.0f / (1.0f + expf_libm(-x)) - 1.0f;
     else if constexpr (A == kRelu) return x > 0.0f ? x : 0.0f;
     else if constexpr (A == kElu) return x >= 0.0f ? x : expf_libm(x) - 1.0f;
-    else if constexpr (A == kSelu) return x >= 0.0f ? 1.0507f * x : 1.75803324f * (expf_libm(x) - 1.0f);
+    else if constexpr (A == kSelu) return x >= 0.0f ? 1.0507f * x : 1.75803124f * (expf_libm(x) - 1.0f);
     else if constexpr (A == kRelie) return x > 0.0f ? x : 0.01f * x;
     else if constexpr (A == kRamp) return (x > 0.0f ? x : 0.0f) + 0.1f * x;
     else if constexpr (A == kLeaky) return x > 0.0f ? x : 0.1f * x;
@@ -251,7 +251,7 @@ __device__ __forceinline__ float gradient(float y) {
         return (2.0f * (1.0f - t)) * t;
     } else if constexpr (A == kRelu) return y > 0.0f ? 1.0f : 0.0f;
     else if constexpr (A == kElu) return y >= 0.0f ? 1.0f : y + 1.0f;
-    else if constexpr (A == kSelu) return y >= 0.0f ? 1.0507f : y + 1.75803324f;
+    else if constexpr (A == kSelu) return y >= 0.0f ? 1.0507f : y + 1.75803124f;
     else if constexpr (A == kRelie) return y > 0.0f ? 1.0f : 0.01f;
     else if constexpr (A == kRamp) return (y > 0.0f ? 1.0f : 0.0f) + 0.1f;
     else if constexpr (A == kLeaky) return y > 0.0f ? 1.0f : 0.1f;

@@ -28,14 +28,12 @@ inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args..
     return after_launch(name, grid, block);
 }
 
-// Reduction scratch of the current device: completion counters followed by
-// double partials. Allocated by dkz_init (or on first use), zero-filled once;
-// every kernel that bumps a counter returns it to zero before it exits.
+// Reduction scratch of the current device: the f64 partial sums one split
+// reduction hands from its first launch to its second. Allocated by dkz_init
+// (or on first use); every split reduction writes all the partials it reads.
 struct Scratch {
-    uint32_t *counters;
     double *partials;
 };
-constexpr uint32_t kScratchCounters = 1u << 14;  // channels that may split
 constexpr uint32_t kScratchPartials = 1u << 18;  // channels * chunks
 int device_scratch(Scratch *out);
 

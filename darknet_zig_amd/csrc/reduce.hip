@@ -2,7 +2,7 @@
 // variance_delta, backward_bias, backward_scale: src/gpu.zig:539-590) and the
 // per-row reduction of global average pooling (gpu.zig:761-763).
 //
-// Channel reductions, one launch each:
+// Channel reductions:
 //   * The grid is filters x K workgroups; workgroup (f, k) owns the k-th
 //     contiguous chunk of channel f's batch*spatial elements. K is picked from
 //     the shape only, so a shape always reduces in the same order on any GPU.
@@ -10,12 +10,14 @@
 //     delta*x_norm, delta*(x-m), rounded exactly as blas.zig rounds them -- and
 //     accumulates it in f64. A chunk is then summed by wave64 DPP reductions
 //     and a 4-entry LDS step (dkz_device.hpp).
-//   * With K > 1 each workgroup stores its f64 partial, and the workgroup that
-//     completes a channel (an acq_rel counter per channel) adds the K partials
-//     in index order and applies the finalisation. There are no float atomics:
-//     the result is deterministic, and it is the exact sum to within f64
-//     rounding, so its distance to the CPU twin's sequential f32 sum is that
-//     sum's own rounding error.
+//   * K == 1: the workgroup finalises its channel itself (one launch).
+//     K > 1: each workgroup stores its f64 partial, and a second, tiny launch
+//     (one wave per channel) adds the K partials in index order and
+//     finalises. The kernel boundary orders the two passes, so no workgroup
+//     needs a device-scope fence (which on gfx950 writes back and invalidates
+//     the whole XCD L2) and nothing uses atomics: the result is deterministic,
+//     and it is the exact sum to within f64 rounding, so its distance to the
+//     CPU twin's sequential f32 sum is that sum's own rounding error.
 //   * The finalisation repeats blas.zig's f32 arithmetic on the f32-rounded
 //     total: sum * (1/(B*S)), sum * (-1/sqrt(v+1e-5)), updates[f] += sum, ...
 #include "dkz_device.hpp"
@@ -43,28 +45,19 @@ __device__ __forceinline__ uint32_t chan_addr(uint32_t fbase, uint32_t j, const 
 
 template <class Term>
 __device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
-    double s = (double)t(a.x, b.x);
-    s += (double)t(a.y, b.y);
-    s += (double)t(a.z, b.z);
-    s += (double)t(a.w, b.w);
-    return s;
+    return ((double)t(a.x, b.x) + (double)t(a.y, b.y)) + ((double)t(a.z, b.z) + (double)t(a.w, b.w));
 }
 
-// T::at(f) gives the per-element term of channel f; Fin(f, total) writes the
-// channel's result. p1 is read only when TWO.
-template <class T, class Fin, bool TWO, bool VEC>
-__global__ __launch_bounds__(kBlock) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1,
-                                                             RedGeom g, uint32_t *counters,
-                                                             double *partials) {
-    __shared__ double lds[kBlock / kWave];
-    __shared__ int is_last;
-    const uint32_t f = fdiv(blockIdx.x, g.div_k);
-    const uint32_t k = blockIdx.x - f * g.K;
+// Sum of this workgroup's chunk of channel f (all threads return it).
+// T::at(f) gives the per-element term of channel f; p1 is read only when TWO.
+template <class T, bool TWO, bool VEC>
+__device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const float *p1, const RedGeom &g,
+                                            uint32_t f, uint32_t k, double *lds) {
     const uint32_t j0 = k * g.chunk;
     const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
     const uint32_t fbase = f * g.spatial;
     const auto term = t.at(f);
-    double acc = 0.0;
+    double acc0 = 0.0, acc1 = 0.0;
     if constexpr (VEC) {
         constexpr uint32_t kStep = 4 * kBlock;
         uint32_t j = j0 + 4 * threadIdx.x;
@@ -78,49 +71,61 @@ __global__ __launch_bounds__(kBlock) void chan_reduce_kernel(T t, Fin fin, const
                 else b[u] = a[u];
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) acc += term4(term, a[u], b[u]);
+            for (int u = 0; u < kUnroll; u += 2) {
+                acc0 += term4(term, a[u], b[u]);
+                acc1 += term4(term, a[u + 1], b[u + 1]);
+            }
         }
         for (; j < j1; j += kStep) {
             const uint32_t v = chan_addr(fbase, j, g) >> 2;
             const float4 a = ld4(p0, v);
             const float4 b = TWO ? ld4(p1, v) : a;
-            acc += term4(term, a, b);
+            acc0 += term4(term, a, b);
         }
     } else {
         for (uint32_t j = j0 + threadIdx.x; j < j1; j += kBlock) {
             const uint32_t e = chan_addr(fbase, j, g);
-            acc += (double)term(p0[e], TWO ? p1[e] : 0.0f);
+            acc0 += (double)term(p0[e], TWO ? p1[e] : 0.0f);
         }
     }
-    const double total = block_sum(acc, lds);
-    if (g.K == 1) {
-        if (threadIdx.x == 0) fin(f, total);
-        return;
-    }
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(&partials[f * g.K + k], total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t done =
-            __hip_atomic_fetch_add(&counters[f], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = done == g.K - 1;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    if (threadIdx.x < kWave) {
-        double s = 0.0;
-        for (uint32_t i = threadIdx.x; i < g.K; i += kWave)
-            s += __hip_atomic_load(&partials[f * g.K + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s = wave_sum(s);
-        if (threadIdx.x == 0) {
-            fin(f, s);
-            __hip_atomic_store(&counters[f], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    return block_sum(acc0 + acc1, lds);
+}
+
+// K == 1: one workgroup per channel, finalised in place.
+template <class T, class Fin, bool TWO, bool VEC>
+__global__ __launch_bounds__(kBlock) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1,
+                                                             RedGeom g) {
+    __shared__ double lds[kBlock / kWave];
+    const double total = chunk_sum<T, TWO, VEC>(t, p0, p1, g, blockIdx.x, 0, lds);
+    if (threadIdx.x == 0) fin(blockIdx.x, total);
+}
+
+// K > 1, pass 1: workgroup (f, k) stores its partial at partials[f*K + k].
+template <class T, bool TWO, bool VEC>
+__global__ __launch_bounds__(kBlock) void chan_partial_kernel(T t, const float *p0, const float *p1, RedGeom g,
+                                                              double *partials) {
+    __shared__ double lds[kBlock / kWave];
+    const uint32_t f = fdiv(blockIdx.x, g.div_k);
+    const uint32_t k = blockIdx.x - f * g.K;
+    const double total = chunk_sum<T, TWO, VEC>(t, p0, p1, g, f, k, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = total;
+}
+
+// K > 1, pass 2: one wave per channel adds its K partials in a fixed order.
+template <class Fin>
+__global__ __launch_bounds__(kBlock) void chan_finalize_kernel(Fin fin, const double *partials, uint32_t F,
+                                                               uint32_t K) {
+    const uint32_t f = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (f >= F) return;  // whole waves leave together
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x & (kWave - 1); i < K; i += kWave) s += partials[f * K + i];
+    s = wave_sum(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s);
 }
 
 // Workgroups per channel: about 2048 over the launch, each with at least 4096
 // elements, within the scratch's capacity. Depends on the shape only.
 uint32_t pick_split(uint32_t filters, uint32_t chan_len) {
-    if (filters > kScratchCounters) return 1;
     uint32_t k = div_up(2048, filters);
     const uint32_t kmax = chan_len / 4096 > 1 ? chan_len / 4096 : 1;
     if (k > kmax) k = kmax;
@@ -140,14 +145,19 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     if (vec) chunk = (chunk + 3) & ~3u;
     K = chunk > 0 ? div_up(L, chunk) : 1;
     const RedGeom g{S, L, chunk, K, (F - 1) * S, make_fastdiv(K), make_fastdiv(S == 0 ? 1 : S)};
-    Scratch sc{nullptr, nullptr};
-    if (K > 1) DKZ_TRY(device_scratch(&sc));
-    const dim3 grid(F * K), block(kBlock);
+    const dim3 block(kBlock);
+    if (K == 1) {
+        if (vec) return launch(name, chan_reduce_kernel<T, Fin, TWO, true>, dim3(F), block, t, fin, p0, p1, g);
+        return launch(name, chan_reduce_kernel<T, Fin, TWO, false>, dim3(F), block, t, fin, p0, p1, g);
+    }
+    Scratch sc{nullptr};
+    DKZ_TRY(device_scratch(&sc));
     if (vec)
-        return launch(name, chan_reduce_kernel<T, Fin, TWO, true>, grid, block, t, fin, p0, p1, g, sc.counters,
-                      sc.partials);
-    return launch(name, chan_reduce_kernel<T, Fin, TWO, false>, grid, block, t, fin, p0, p1, g, sc.counters,
-                  sc.partials);
+        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, true>, dim3(F * K), block, t, p0, p1, g, sc.partials));
+    else
+        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, false>, dim3(F * K), block, t, p0, p1, g, sc.partials));
+    return launch(name, chan_finalize_kernel<Fin>, dim3(div_up(F, kBlock / kWave)), block, fin,
+                  (const double *)sc.partials, F, K);
 }
 
 // ---- per-element terms (f32, rounded as the CPU twin rounds them) ---------

@@ -30,10 +30,7 @@ bool env_flag(const char *name) {
     return v != nullptr && v[0] != '\0' && v[0] != '0';
 }
 
-// One allocation per device: counters first (kept 256-byte aligned), then
-// the double partials.
-constexpr size_t kCounterBytes = ((kScratchCounters * sizeof(uint32_t)) + 255) & ~size_t(255);
-constexpr size_t kScratchBytes = kCounterBytes + kScratchPartials * sizeof(double);
+constexpr size_t kScratchBytes = kScratchPartials * sizeof(double);
 
 int ensure_scratch(int dev) {
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -90,9 +87,7 @@ int device_scratch(Scratch *out) {
     if (e != hipSuccess) return (int)e;
     if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
     if (g_devices[dev].scratch == nullptr) DKZ_TRY(ensure_scratch(dev));
-    char *base = static_cast<char *>(g_devices[dev].scratch);
-    out->counters = reinterpret_cast<uint32_t *>(base);
-    out->partials = reinterpret_cast<double *>(base + kCounterBytes);
+    out->partials = static_cast<double *>(g_devices[dev].scratch);
     return 0;
 }
 

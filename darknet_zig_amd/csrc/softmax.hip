@@ -61,14 +61,20 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
         for (uint32_t i = threadIdx.x; i < n; i += kBlock) e_lds[i] = expf_libm(x[i] / G.temp - mt);
         __syncthreads();
         if (threadIdx.x == 0) {
+            // The one sequential part: 8 LDS reads in flight ahead of the adds.
             float s = 0.0f;
             uint32_t i = 0;
-            for (; i + 4 <= n; i += 4) {
-                const float4 v = e_lds4[i >> 2];
-                s += v.x;
-                s += v.y;
-                s += v.z;
-                s += v.w;
+            for (; i + 32 <= n; i += 32) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = e_lds4[(i >> 2) + u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    s += v[u].x;
+                    s += v[u].y;
+                    s += v[u].z;
+                    s += v[u].w;
+                }
             }
             for (; i < n; ++i) s += e_lds[i];
             sum_sh = s;

@@ -38,10 +38,11 @@
  *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
- *   - The library owns one scratch buffer per device for reduction partials
- *     and their completion counters, allocated by dkz_init. Ops never
- *     allocate. Reductions issued concurrently on two streams of one device
- *     share that buffer and race; issue them on one stream.
+ *   - The library owns one scratch buffer per device (2 MiB) for the f64
+ *     partial sums a per-channel reduction passes from its first launch to
+ *     its second; dkz_init allocates it. Ops never allocate. Reductions
+ *     issued concurrently on two streams of one device share that buffer and
+ *     race; issue them on one stream.
  */
 #ifndef DKZ_OPS_H
 #define DKZ_OPS_H

@@ -15,7 +15,7 @@
  *   - Zig float literals are comptime values coerced to f32 at the point of
  *     use, so 0.1 is 0.1f, 0.000001 is 1e-6f and 0.00001 is 1e-5f. A product
  *     of two literals is folded at comptime before the coercion (selu's
- *     1.0507 * 1.6732 becomes the single f32 constant 1.75803324f).
+ *     1.0507 * 1.6732 becomes the single f32 constant 1.75803124f).
  *   - @exp and @log on f32 lower to the C library's expf/logf; @sqrt is the
  *     correctly rounded square root; @max/@min ignore a NaN operand like
  *     fmaxf/fminf; @rem is C's %.
@@ -320,7 +320,7 @@ float ref_activate(float x, int a) {
     case A_LOGGY: return 2.0f / (1.0f + expf(-x)) - 1.0f;
     case A_RELU: return (x > 0.0f) ? x : 0.0f;
     case A_ELU: return (x >= 0.0f) ? x : expf(x) - 1.0f;
-    case A_SELU: return (x >= 0.0f) ? 1.0507f * x : 1.75803324f * (expf(x) - 1.0f);
+    case A_SELU: return (x >= 0.0f) ? 1.0507f * x : 1.75803124f * (expf(x) - 1.0f);
     case A_RELIE: return (x > 0.0f) ? x : 0.01f * x;
     case A_RAMP: return ((x > 0.0f) ? x : 0.0f) + 0.1f * x;
     case A_LEAKY: return (x > 0.0f) ? x : 0.1f * x;
@@ -358,7 +358,7 @@ float ref_gradient(float y, int a) {
     }
     case A_RELU: return (y > 0.0f) ? 1.0f : 0.0f;
     case A_ELU: return (y >= 0.0f) ? 1.0f : y + 1.0f;
-    case A_SELU: return (y >= 0.0f) ? 1.0507f : y + 1.75803324f;
+    case A_SELU: return (y >= 0.0f) ? 1.0507f : y + 1.75803124f;
     case A_RELIE: return (y > 0.0f) ? 1.0f : 0.01f;
     case A_RAMP: return ((y > 0.0f) ? 1.0f : 0.0f) + 0.1f;
     case A_LEAKY: return (y > 0.0f) ? 1.0f : 0.1f;

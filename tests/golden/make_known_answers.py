@@ -1,0 +1,70 @@
+"""Writes reference_known_answers.json: the known answers held by the
+reference's own tests for the tensor-op path, as data.
+
+Each entry records the inputs, the call, the expected values and the tolerance
+the reference test uses, with the file:line it comes from. The reference
+stores no fixture files and its gputest pins nothing bit-level
+(gputest.zig:27-52, 1e-3 either-abs-or-rel), so these test-block values are
+all the golden data it has for this path. Values are transcribed; nothing
+from the reference is executed.
+
+Usage: python tests/golden/make_known_answers.py
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+OUT = Path(__file__).resolve().parent / "reference_known_answers.json"
+
+CASES = [
+    {
+        "source": "src/blas.zig:324-332",
+        "name": "softmax sums to one and cross entropy matches",
+        "op": "softmax",
+        "args": {"input": [1.0, 2.0, 3.0, 4.0], "n": 4, "batch": 1, "batch_offset": 4, "groups": 1,
+                 "group_offset": 4, "stride": 1, "temp": 1.0},
+        "expect": {"sum": 1.0, "sum_abs_tol": 1e-6, "output3_gt_output0": True},
+    },
+    {
+        "source": "src/blas.zig:334-346",
+        "name": "normalize then denormalize round trips",
+        "op": "mean_variance_normalize",
+        "args": {"x": [1, 2, 3, 4, 5, 6, 7, 8], "batch": 1, "filters": 2, "spatial": 4},
+        "expect": {"mean": [2.5, 6.5], "mean_abs_tol": 1e-6, "normalized_channel0_sum": 0.0,
+                   "normalized_sum_abs_tol": 1e-5},
+    },
+    {
+        "source": "src/activations.zig:145-150",
+        "name": "leaky activation and its gradient agree with darknet",
+        "op": "leaky",
+        "args": {"activate": [2.0, -2.0], "gradient": [2.0, -0.2]},
+        "expect": {"activate": [2.0, -0.2], "gradient": [1.0, 0.1], "abs_tol": 1e-6},
+    },
+    {
+        "source": "src/smoke_test.zig:229-274",
+        "name": "batch norm rolling statistics follow darknet's 0.99 EMA",
+        "op": "bn_rolling_ema",
+        "args": {"batch": 4, "w": 3, "h": 3, "c": 2, "input_uniform": [-2.0, 2.0], "steps": 200,
+                 "momentum": 0.99},
+        "expect": {"rolling_over_batch_stat": "1 - 0.99**steps", "rel_tol": 1e-3,
+                   "fraction_range": [0.86, 0.88]},
+    },
+    {
+        "source": "src/smoke_test.zig:276-308",
+        "name": "flat-index decomposition covers every output element exactly once",
+        "op": "nchw_bijection",
+        "args": {"batch": 3, "n": 5, "size": 7},
+        "expect": {"each_index_hit": 1},
+    },
+]
+
+
+def main() -> None:
+    OUT.write_text(json.dumps({"reference": "Eightscer/darknet_zig", "cases": CASES}, indent=2) + "\n")
+    print(OUT)
+
+
+if __name__ == "__main__":
+    main()

@@ -8,9 +8,11 @@ from __future__ import annotations
 
 import os
 import subprocess
+import sys
 from pathlib import Path
 
-from darknet_zig_amd import build as pkg_build
+sys.path.insert(0, str(Path(__file__).resolve().parents[2]))
+from darknet_zig_amd import build as pkg_build  # noqa: E402
 
 HERE = Path(__file__).resolve().parent
 SRC = HERE / "dkz_checks.hip"

@@ -1,0 +1,81 @@
+"""Host-side checks of two pieces of the device header (dkz_device.hpp),
+compiled for the host from the same source (tests/native/dkz_checks.hip):
+
+* expf_libm, the exp behind every exp-based activation and softmax, against
+  the host C library's expf over all 2^32 float inputs (the GPU-side twin of
+  this check is tests/test_gpu_expf.py);
+* its 2^(i/32) table, against 2^(i/32) computed to 60 digits and rounded to
+  double;
+* the launch-constant division against Python's integer division.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import struct
+from decimal import Decimal, getcontext
+
+import numpy as np
+import pytest
+
+from tests.native import build as native_build
+
+
+def lib():
+    L = C.CDLL(str(native_build.LIB))
+    L.chk_fastdiv.restype = C.c_uint32
+    L.chk_fastdiv.argtypes = [C.c_uint32, C.c_uint32]
+    L.chk_exp2f_tab.restype = C.c_uint64
+    L.chk_exp2f_tab.argtypes = [C.c_uint32]
+    L.chk_expf_restated.restype = C.c_float
+    L.chk_expf_restated.argtypes = [C.c_float]
+    L.chk_expf_host_mismatches.restype = C.c_uint64
+    L.chk_expf_host_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+    return L
+
+
+def double_bits(x: float) -> int:
+    return struct.unpack("<Q", struct.pack("<d", x))[0]
+
+
+def test_exp2_table_is_2_pow_i_over_32():
+    getcontext().prec = 60
+    L = lib()
+    for i in range(32):
+        exact = Decimal(2) ** (Decimal(i) / Decimal(32))
+        nearest = float(exact)  # Decimal -> float rounds correctly to nearest
+        assert L.chk_exp2f_tab(i) == double_bits(nearest) - (i << 47), i
+
+
+def test_expf_special_values():
+    L = lib()
+    assert L.chk_expf_restated(0.0) == 1.0
+    assert L.chk_expf_restated(float("-inf")) == 0.0
+    assert L.chk_expf_restated(float("inf")) == float("inf")
+    assert np.isnan(L.chk_expf_restated(float("nan")))
+    assert L.chk_expf_restated(89.0) == float("inf")
+    assert L.chk_expf_restated(-104.0) == 0.0
+    assert L.chk_expf_restated(1.0) == np.float32(np.e)
+
+
+def test_expf_matches_libm_on_every_float():
+    threads = min(os.cpu_count() or 4, 16)
+    assert lib().chk_expf_host_mismatches(0, 1 << 32, threads) == 0
+
+
+DIVISORS = sorted({1, 2, 3, 5, 7, 13, 14, 28, 49, 53, 196, 784, 1024, 3136, 4096, 12544, 65535, 65536, 65537,
+                   1000003, (1 << 20) - 1, (1 << 30) + 1, (1 << 31) - 1} | {(1 << k) + d for k in range(1, 31)
+                                                                           for d in (-1, 0, 1)})
+
+
+@pytest.mark.parametrize("d", DIVISORS)
+def test_fastdiv(d):
+    L = lib()
+    g = np.random.default_rng(d)
+    ns = {0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d, (1 << 31) - 1, (1 << 31) - 2, ((1 << 31) - 1) // d * d,
+          ((1 << 31) - 1) // d * d - 1}
+    ns |= set(int(v) for v in g.integers(0, 1 << 31, 2000))
+    for n in ns:
+        if 0 <= n < (1 << 31):
+            assert L.chk_fastdiv(n, d) == n // d, (n, d)
