@@ -416,6 +416,11 @@ def main() -> int:
     ap.add_argument("--op-launches", type=int, default=24, help="timed launches per op in the per-op table")
     ap.add_argument("--no-per-op", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--per-op-only", action="store_true",
+                    help="only run the per-op table (for a kernel trace without the chain's launches)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run dkz_copy over MIB MiB (x4 launches, rotated): the known-size kernel "
+                         "that scales rocprofv3's FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -427,6 +432,22 @@ def main() -> int:
     gpu.init(0)
     hip = Hip()
     stream = C.c_void_p(None)  # the library's stream: the null stream
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 18  # floats
+        dev = Device(gpu)
+        src = [dev.zeros(n) for _ in range(2)]
+        dst = [dev.zeros(n) for _ in range(2)]
+        fns = [lambda a=a, b=b: gpu.copy(n, a, b) for a, b in zip(src, dst)]
+        ms = time_op(hip, stream, fns, 4, warmup=0)
+        dev.free()
+        print(json.dumps({"copy_calibration": {"bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 4,
+                                               "us": round(ms * 1e3, 2)}}), flush=True)
+        return 0
+
+    if args.per_op_only:
+        print(json.dumps({"per_op": per_op_table(gpu, hip, stream, args.op_launches)}), flush=True)
+        return 0
 
     h = config2_host()
     dev = Device(gpu)

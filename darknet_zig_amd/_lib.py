@@ -11,6 +11,7 @@ be loaded), load() raises and nothing runs.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libdkz.so"
@@ -72,11 +73,16 @@ _LIB: C.CDLL | None = None
 
 
 def load(path: Path | str | None = None) -> C.CDLL:
-    """Loads libdkz.so (once) and declares every signature. Raises if absent."""
+    """Loads libdkz.so (once) and declares every signature. Raises if absent.
+
+    $DKZ_LIBRARY names another build of the library, as $DARKNET_KERNELS names
+    another code object in the reference (gpu.zig:240-244).
+    """
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
-    p = Path(path) if path is not None else LIB_PATH
+    env = os.environ.get("DKZ_LIBRARY")
+    p = Path(path) if path is not None else Path(env) if env else LIB_PATH
     if not p.exists():
         raise ImportError(
             f"{p} is not built; the HIP tensor-op library is required "

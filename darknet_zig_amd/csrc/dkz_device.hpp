@@ -54,14 +54,71 @@ __host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) 
 }
 
 // ---------------------------------------------------------------------------
-// 128-bit global accesses.
+// Streaming global accesses: 128-bit (and 64-bit) loads and stores, with the
+// nontemporal hint selected by DKZ_STREAM_HINTS (bit 0: loads, bit 1: stores).
+// Measured on MI355X: on data that is cold in HBM, nontemporal loads and
+// stores together lift a 2-read/1-write stream from 5.5 to 6.5 TB/s; but a
+// nontemporal load also keeps the line out of the 256 MB Infinity Cache, and
+// in darknet's layer step the next op usually re-reads the same delta, so the
+// batch-norm backward step runs fastest with nontemporal stores only. Small
+// per-channel vectors use ordinary loads.
 // ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+#ifndef DKZ_STREAM_HINTS
+#define DKZ_STREAM_HINTS 2
+#endif
 __device__ __forceinline__ float4 ld4(const float *p, uint32_t v) {
+#if DKZ_STREAM_HINTS & 1
+    const f32x4 r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + v);
+    return make_float4(r.x, r.y, r.z, r.w);
+#else
     return reinterpret_cast<const float4 *>(p)[v];
+#endif
 }
 __device__ __forceinline__ void st4(float *p, uint32_t v, float4 x) {
+#if DKZ_STREAM_HINTS & 2
+    const f32x4 w = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p) + v);
+#else
     reinterpret_cast<float4 *>(p)[v] = x;
+#endif
 }
+__device__ __forceinline__ float2 ld2(const float *p, uint32_t v) {
+#if DKZ_STREAM_HINTS & 1
+    const f32x2 r = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p) + v);
+    return make_float2(r.x, r.y);
+#else
+    return reinterpret_cast<const float2 *>(p)[v];
+#endif
+}
+__device__ __forceinline__ void st2(float *p, uint32_t v, float2 x) {
+#if DKZ_STREAM_HINTS & 2
+    const f32x2 w = {x.x, x.y};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x2 *>(p) + v);
+#else
+    reinterpret_cast<float2 *>(p)[v] = x;
+#endif
+}
+__device__ __forceinline__ int2 ld2i(const int *p, uint32_t v) {
+#if DKZ_STREAM_HINTS & 1
+    const i32x2 r = __builtin_nontemporal_load(reinterpret_cast<const i32x2 *>(p) + v);
+    return make_int2(r.x, r.y);
+#else
+    return reinterpret_cast<const int2 *>(p)[v];
+#endif
+}
+__device__ __forceinline__ void st2i(int *p, uint32_t v, int2 x) {
+#if DKZ_STREAM_HINTS & 2
+    const i32x2 w = {x.x, x.y};
+    __builtin_nontemporal_store(w, reinterpret_cast<i32x2 *>(p) + v);
+#else
+    reinterpret_cast<int2 *>(p)[v] = x;
+#endif
+}
+
 __device__ __forceinline__ float &lane(float4 &v, int k) {
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }

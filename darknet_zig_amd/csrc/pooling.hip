@@ -17,7 +17,7 @@
 // Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
 // a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
 // two adjacent outputs and their 2x4 input patch, read and written as two
-// float4s.
+// float4s (outputs and indexes as float2/int2), all with streaming hints.
 #include <float.h>
 
 #include "dkz_device.hpp"
@@ -127,8 +127,8 @@ __global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, f
     max_tap(a.w, (int)r0 + 3, m1, i1);
     max_tap(b.z, (int)r1 + 2, m1, i1);
     max_tap(b.w, (int)r1 + 3, m1, i1);
-    reinterpret_cast<float2 *>(out)[q] = make_float2(m0, m1);
-    reinterpret_cast<int2 *>(idx)[q] = make_int2(i0, i1);
+    st2(out, q, make_float2(m0, m1));
+    st2i(idx, q, make_int2(i0, i1));
 }
 
 __device__ __forceinline__ float add_if(float p, int want, int have, float d) {
@@ -146,8 +146,8 @@ __global__ __launch_bounds__(kBlock) void maxpool2_bwd_kernel(const float *delta
     const uint32_t i = t - plane * g.oh;
     const uint32_t r0 = (plane * g.h + 2 * i) * g.w + 2 * j;
     const uint32_t r1 = r0 + g.w;
-    const float2 d = reinterpret_cast<const float2 *>(delta)[q];
-    const int2 k = reinterpret_cast<const int2 *>(idx)[q];
+    const float2 d = ld2(delta, q);
+    const int2 k = ld2i(idx, q);
     float4 a = ld4(prev, r0 >> 2);
     float4 b = ld4(prev, r1 >> 2);
     // Each input of the patch has exactly one candidate output: j for the

@@ -53,11 +53,11 @@ __global__ __launch_bounds__(kBlock) void shortcut2_kernel(const float *add, flo
     shortcut_coords(2 * q, g, i, j, k, b);
     const uint32_t oi = i + g.w2 * (j + g.h2 * (k + g.c2 * b));
     const uint32_t ai = 2 * i + g.w1 * (2 * j + g.h1 * (k + g.c1 * b));
-    float2 o = *reinterpret_cast<const float2 *>(out + oi);
+    float2 o = ld2(out, oi >> 1);
     const float4 a = ld4(add, ai >> 2);
     o.x = g.s1 * o.x + g.s2 * a.x;
     o.y = g.s1 * o.y + g.s2 * a.z;
-    *reinterpret_cast<float2 *>(out + oi) = o;
+    st2(out, oi >> 1, o);
 }
 
 }  // namespace

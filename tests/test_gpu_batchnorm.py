@@ -153,19 +153,42 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
         gpu.free(b)
 
 
-def test_reductions_deterministic(dev):
-    """Same input, same bits: the split reduction has a fixed order."""
-    B, F, S = CONFIG2
-    x = normal(rng(9), B * F * S)
-    dx, dm = up(x), gpu.alloc(F)
-    outs = []
-    for _ in range(3):
-        gpu.mean(dx, B, F, S, dm)
-        outs.append(down(dm, np.empty(F, np.float32)))
-    for o in outs[1:]:
-        assert_bitexact(o, outs[0], "mean repeat")
-    gpu.free(dx)
-    gpu.free(dm)
+@pytest.mark.parametrize("shape", [CONFIG1, CONFIG2, (16, 64, 3136)], ids=str)
+def test_reductions_deterministic(dev, shape):
+    """Same input, same bits, every time: the split reductions hand partials
+    between workgroups through device-coherent stores and a counter, and add
+    them in a fixed order. 200 repeats of each op at shapes that split."""
+    B, F, S = shape
+    r = rng(9)
+    x, d = normal(r, B * F * S), normal(r, B * F * S)
+    m, v = _stats(x, shape)
+    dx, dd, dm, dv, out = up(x), up(d), up(m), up(v), gpu.alloc(F)
+    ops = {
+        "mean": lambda: gpu.mean(dx, B, F, S, out),
+        "variance": lambda: gpu.variance(dx, dm, B, F, S, out),
+        "variance_delta": lambda: gpu.varianceDelta(dx, dd, dm, dv, B, F, S, out),
+    }
+    for name, op in ops.items():
+        first = None
+        for _ in range(200):
+            op()
+            got = down(out, np.empty(F, np.float32))
+            if first is None:
+                first = got
+            else:
+                assert_bitexact(got, first, f"{name} repeat {shape}")
+    zero = up(np.zeros(F, np.float32))
+    for _ in range(50):  # accumulate: each call adds the same bits
+        gpu.backwardBias(zero, dd, B, F, S)
+    single = up(np.zeros(F, np.float32))
+    gpu.backwardBias(single, dd, B, F, S)
+    s1 = down(single, np.empty(F, np.float32))
+    want = np.zeros(F, np.float32)
+    for _ in range(50):
+        want = want + s1
+    assert_bitexact(down(zero, want), want, f"backward_bias x50 {shape}")
+    for b in (dx, dd, dm, dv, out, zero, single):
+        gpu.free(b)
 
 
 def _bn_forward_cpu(x, scales, biases, roll_m, roll_v, shape):
