@@ -12,8 +12,11 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
   value        algorithmic bytes of the 7-op chain x steps / wall time of the
                timed region (HIP events on the library's stream), in GB/s
   roofline     the chain's longest kernel: its algorithmic bytes / its mean
-               duration from per-kernel HIP events over the same steps,
-               against MI355X's 8 TB/s HBM peak
+               duration from per-kernel HIP events over the same steps (less
+               the event-pair overhead: the per-step excess of the event-timed
+               steps over the clean ones, spread over the 7 pairs), against
+               MI355X's 8 TB/s HBM peak; traffic from the committed counter
+               summary profiles/traffic_bn_backward.txt
   per_op       every op of BASELINE.json's five configs timed on its own,
                cold (rotated buffers, >= 512 MB per rotation), in GB/s and as
                a fraction of 8 TB/s
@@ -218,6 +221,23 @@ def time_chain_per_kernel(hip, stream, chains, steps):
     return [statistics.mean(p) for p in per]
 
 
+def time_seq(hip, stream, seqs, steps, warmup=3):
+    """Mean time (ms) of one pass of an op sequence, cycling over rotated sets."""
+    for k in range(warmup):
+        for fn in seqs[k % len(seqs)]:
+            fn()
+    hip.sync()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for k in range(steps):
+        for fn in seqs[k % len(seqs)]:
+            fn()
+    hip.record(b, stream)
+    ms = hip.ms(a, b)
+    hip.sync()
+    return ms / steps
+
+
 def time_op(hip, stream, fns, launches, warmup=3):
     """Mean per-launch time (ms) of an op cycling over rotated inputs."""
     for k in range(warmup):
@@ -274,6 +294,15 @@ def per_op_table(gpu, hip, stream, launches: int):
     add(cfg, "activate(leaky)", 2 * E, [lambda b=b: gpu.activateArray(b, n, Activation.leaky) for b in xs])
     ys = [dev.zeros(n) for _ in range(R)]
     add(cfg, "copy (x, x_norm)", 2 * E, [lambda a=a, b=b: gpu.copy(n, a, b) for a, b in zip(xs, ys)])
+    # the named ops in the layer's order on one tensor (batchnorm.zig:137-152 + activate)
+    seqs = [[lambda b=b: gpu.mean(b, B, F, S, m), lambda b=b: gpu.variance(b, m, B, F, S, v),
+             lambda b=b: gpu.normalize(b, m, v, B, F, S), lambda b=b: gpu.scaleBias(b, gam, B, F, S),
+             lambda b=b: gpu.addBias(b, bet, B, F, S), lambda b=b: gpu.activateArray(b, n, Activation.leaky)]
+            for b in xs]
+    ms = time_seq(hip, stream, seqs, max(launches, R))
+    rows[f"{cfg}/chain: mean,variance,normalize,scale_bias,add_bias,leaky"] = {
+        "us": round(ms * 1e3, 3), "GB/s": round(gbs(10 * E, ms), 1), "frac": round(gbs(10 * E, ms) / PEAK_GBS, 4),
+        "bytes": 10 * E}
     rm, rv = dev.zeros(F), dev.zeros(F)
     add(cfg, "ema scal+axpy (C floats)", 4 * 3 * F,
         [lambda: (gpu.scal(F, 0.99, rm), gpu.axpy(F, 0.01, m, rm), gpu.scal(F, 0.99, rv), gpu.axpy(F, 0.01, v, rv))])
@@ -321,6 +350,12 @@ def per_op_table(gpu, hip, stream, launches: int):
         [lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d) for w, d in zip(ws, dws)])
     add(cfg, "axpy(lr/batch, dw, w)", 3 * 4 * n4, [lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w) for w, d in zip(ws, dws)])
     add(cfg, "scal(momentum, dw)", 2 * 4 * n4, [lambda d=d: gpu.scal(n4, momentum, d) for d in dws])
+    seqs = [[lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d), lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w),
+             lambda d=d: gpu.scal(n4, momentum, d)] for w, d in zip(ws, dws)]
+    ms = time_seq(hip, stream, seqs, max(launches, R))
+    rows[f"{cfg}/chain: axpy,axpy,scal (one SGD step)"] = {
+        "us": round(ms * 1e3, 3), "GB/s": round(gbs(8 * 4 * n4, ms), 1),
+        "frac": round(gbs(8 * 4 * n4, ms) / PEAK_GBS, 4), "bytes": 8 * 4 * n4}
     dev.free()
     dev = Device(gpu)
     sb, w1, c1, w2, c2 = 64, 28, 256, 14, 512
@@ -461,8 +496,14 @@ def main() -> int:
 
     names = [nm for nm, _, _ in chains[0]]
     byts = [b for _, b, _ in chains[0]]
-    dom = max(range(len(names)), key=lambda j: per_kernel_ms[j])
-    achieved = gbs(byts[dom], per_kernel_ms[dom])
+    # A HIP event pair around a launch also times the dispatch and completion
+    # latency that back-to-back launches hide. The clean region runs the same
+    # kernels without inner events, so the per-pair overhead is the difference
+    # of the two per-step times spread over the pairs of a step.
+    overhead_ms = max(0.0, (sum(per_kernel_ms) - ms / args.steps) / len(names))
+    kernel_ms = [t - overhead_ms for t in per_kernel_ms]
+    dom = max(range(len(names)), key=lambda j: kernel_ms[j])
+    achieved = gbs(byts[dom], kernel_ms[dom])
     traffic = None
     tfile = ROOT / "profiles" / "traffic_bn_backward.txt"
     if tfile.exists():
@@ -473,8 +514,8 @@ def main() -> int:
                 except ValueError:
                     traffic = None
 
-    chain_kernels = {names[j]: {"us": round(per_kernel_ms[j] * 1e3, 2),
-                                "GB/s": round(gbs(byts[j], per_kernel_ms[j]), 1)} for j in range(len(names))}
+    chain_kernels = {names[j]: {"us": round(kernel_ms[j] * 1e3, 2), "GB/s": round(gbs(byts[j], kernel_ms[j]), 1),
+                                "event_pair_us": round(per_kernel_ms[j] * 1e3, 2)} for j in range(len(names))}
     result = {
         "metric": METRIC,
         "value": round(gbs(chain_bytes * args.steps, ms), 1),
@@ -503,19 +544,24 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic,
+            "duration_us": round(kernel_ms[dom] * 1e3, 2),
+            "event_pair_overhead_us": round(overhead_ms * 1e3, 2),
         },
         "chain_kernels": chain_kernels,
     }
     if not args.no_per_op:
         table = per_op_table(gpu, hip, stream, args.op_launches)
         result["per_op"] = table
-        fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and "copy" not in k and "ema" not in k)
+        named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
+        fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and k.split("/", 1)[1] in named)
+        fwd_chain = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/chain" in k)
         bwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg2"))
         e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
         result["bn_act_gelem_s"] = {
+            "fwd_cfg1_chained": round(e1 / (fwd_chain * 1e-6) / 1e9, 2),
+            "bwd_cfg2_chained": round(e2 / (ms / args.steps * 1e-3) / 1e9, 2),
             "fwd_cfg1_per_op_sum": round(e1 / (fwd * 1e-6) / 1e9, 2),
             "bwd_cfg2_per_op_sum": round(e2 / (bwd * 1e-6) / 1e9, 2),
-            "bwd_cfg2_chained": round(e2 / (ms / args.steps * 1e-3) / 1e9, 2),
         }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(h)

@@ -10,6 +10,7 @@
 // its channel constants are looked up (and derived, e.g. normalize's
 // reciprocal) once per float4.
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -49,29 +50,31 @@ __device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io,
     return io;
 }
 
-template <class Op, bool TWO, bool ROWWISE, bool S4>
+// H: bit 0 = nontemporal io loads, bit 1 = io stores, bit 2 = loads of a.
+template <class Op, bool TWO, bool ROWWISE, bool S4, int H>
 __global__ __launch_bounds__(kBlock) void bcast_vec_kernel(Op op, float *io, const float *a, ChanGeom g,
                                                            uint32_t n) {
+    constexpr bool kNtIo = (H & 1) != 0, kNtOut = (H & 2) != 0, kNtA = (H & 4) != 0;
     const uint32_t nv = n >> 2;
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
     if (base + (kUnroll - 1) * kBlock < nv) {
         float4 x[kUnroll], y[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            x[u] = ld4(io, base + u * kBlock);
-            if constexpr (TWO) y[u] = ld4(a, base + u * kBlock);
+            x[u] = ld4<kNtIo>(io, base + u * kBlock);
+            if constexpr (TWO) y[u] = ld4<kNtA>(a, base + u * kBlock);
             else y[u] = x[u];
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
-            st4(io, base + u * kBlock, bcast_vec<Op, TWO, ROWWISE, S4>(op, base + u * kBlock, x[u], y[u], g));
+            st4<kNtOut>(io, base + u * kBlock, bcast_vec<Op, TWO, ROWWISE, S4>(op, base + u * kBlock, x[u], y[u], g));
     } else {
         for (int u = 0; u < kUnroll; ++u) {
             const uint32_t v = base + u * kBlock;
             if (v < nv) {
-                const float4 x = ld4(io, v);
-                const float4 y = TWO ? ld4(a, v) : x;
-                st4(io, v, bcast_vec<Op, TWO, ROWWISE, S4>(op, v, x, y, g));
+                const float4 x = ld4<kNtIo>(io, v);
+                const float4 y = TWO ? ld4<kNtA>(a, v) : x;
+                st4<kNtOut>(io, v, bcast_vec<Op, TWO, ROWWISE, S4>(op, v, x, y, g));
             }
         }
     }
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(kBlock) void bcast_scalar_kernel(Op op, float *io, 
 }
 
 // batch, filters, spatial already validated as non-negative ints.
-template <class Op, bool TWO, bool ROWWISE = false>
+template <int H, class Op, bool TWO, bool ROWWISE = false>
 int run_bcast(const char *name, const Op &op, float *io, const float *a, int batch, int filters,
               int spatial) {
     const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
@@ -101,9 +104,9 @@ int run_bcast(const char *name, const Op &op, float *io, const float *a, int bat
         const uint32_t nv = n >> 2;
         const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
         if (spatial % 4 == 0)
-            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true>, dim3(grid), dim3(kBlock), op, io,
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H>, dim3(grid), dim3(kBlock), op, io,
                           a, g, n);
-        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false>, dim3(grid), dim3(kBlock), op, io, a,
+        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H>, dim3(grid), dim3(kBlock), op, io, a,
                       g, n);
     }
     const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
@@ -172,7 +175,7 @@ int dkz_add_bias(float *output, const float *biases, int batch, int filters, int
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (DKZ_EMPTY(batch, filters, spatial)) return 0;
     DKZ_REQUIRE(output && biases);
-    return run_bcast<AddBiasOp, false>("add_bias", AddBiasOp{biases}, output, nullptr, batch, filters,
+    return run_bcast<DKZ_HINT_ADD_BIAS, AddBiasOp, false>("add_bias", AddBiasOp{biases}, output, nullptr, batch, filters,
                                        spatial);
 }
 
@@ -180,7 +183,7 @@ int dkz_scale_bias(float *output, const float *scales, int batch, int filters, i
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (DKZ_EMPTY(batch, filters, spatial)) return 0;
     DKZ_REQUIRE(output && scales);
-    return run_bcast<ScaleBiasOp, false>("scale_bias", ScaleBiasOp{scales}, output, nullptr, batch,
+    return run_bcast<DKZ_HINT_SCALE_BIAS, ScaleBiasOp, false>("scale_bias", ScaleBiasOp{scales}, output, nullptr, batch,
                                          filters, spatial);
 }
 
@@ -189,7 +192,7 @@ int dkz_normalize(float *x, const float *mean, const float *variance, int batch,
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (DKZ_EMPTY(batch, filters, spatial)) return 0;
     DKZ_REQUIRE(x && mean && variance);
-    return run_bcast<NormalizeOp, false>("normalize", NormalizeOp{mean, variance}, x, nullptr, batch,
+    return run_bcast<DKZ_HINT_NORMALIZE, NormalizeOp, false>("normalize", NormalizeOp{mean, variance}, x, nullptr, batch,
                                          filters, spatial);
 }
 
@@ -201,7 +204,7 @@ int dkz_normalize_delta(const float *x, const float *mean, const float *variance
     DKZ_REQUIRE(x && mean && variance && mean_delta && variance_delta && delta);
     const float denom = (float)((uint64_t)spatial * (uint64_t)batch);  // blas.zig:191
     const NormalizeDeltaOp op{mean, variance, mean_delta, variance_delta, denom};
-    return run_bcast<NormalizeDeltaOp, true>("normalize_delta", op, delta, x, batch, filters, spatial);
+    return run_bcast<DKZ_HINT_NORMALIZE_DELTA, NormalizeDeltaOp, true>("normalize_delta", op, delta, x, batch, filters, spatial);
 }
 
 int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const float *out_delta) {
@@ -211,7 +214,7 @@ int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const floa
     DKZ_REQUIRE(spatial <= kMaxElems);
     DKZ_REQUIRE(in_delta && out_delta);
     const AvgpoolBackOp op{out_delta, (float)spatial};
-    return run_bcast<AvgpoolBackOp, false, true>("backward_avgpool", op, in_delta, nullptr, n, 1,
+    return run_bcast<DKZ_HINT_AVGPOOL_BWD, AvgpoolBackOp, false, true>("backward_avgpool", op, in_delta, nullptr, n, 1,
                                                  (int)spatial);
 }
 

@@ -54,69 +54,68 @@ __host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) 
 }
 
 // ---------------------------------------------------------------------------
-// Streaming global accesses: 128-bit (and 64-bit) loads and stores, with the
-// nontemporal hint selected by DKZ_STREAM_HINTS (bit 0: loads, bit 1: stores).
-// Measured on MI355X: on data that is cold in HBM, nontemporal loads and
-// stores together lift a 2-read/1-write stream from 5.5 to 6.5 TB/s; but a
-// nontemporal load also keeps the line out of the 256 MB Infinity Cache, and
-// in darknet's layer step the next op usually re-reads the same delta, so the
-// batch-norm backward step runs fastest with nontemporal stores only. Small
-// per-channel vectors use ordinary loads.
+// Global accesses of the tensors: 128-bit (and 64-bit) loads and stores, with
+// or without the nontemporal hint (NT). Which operand of which op carries the
+// hint is decided per op in dkz_hints.hpp. Small per-channel vectors use
+// ordinary loads.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef DKZ_STREAM_HINTS
-#define DKZ_STREAM_HINTS 2
-#endif
+template <bool NT>
 __device__ __forceinline__ float4 ld4(const float *p, uint32_t v) {
-#if DKZ_STREAM_HINTS & 1
-    const f32x4 r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + v);
-    return make_float4(r.x, r.y, r.z, r.w);
-#else
-    return reinterpret_cast<const float4 *>(p)[v];
-#endif
+    if constexpr (NT) {
+        const f32x4 r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + v);
+        return make_float4(r.x, r.y, r.z, r.w);
+    } else {
+        return reinterpret_cast<const float4 *>(p)[v];
+    }
 }
+template <bool NT>
 __device__ __forceinline__ void st4(float *p, uint32_t v, float4 x) {
-#if DKZ_STREAM_HINTS & 2
-    const f32x4 w = {x.x, x.y, x.z, x.w};
-    __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p) + v);
-#else
-    reinterpret_cast<float4 *>(p)[v] = x;
-#endif
+    if constexpr (NT) {
+        const f32x4 w = {x.x, x.y, x.z, x.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p) + v);
+    } else {
+        reinterpret_cast<float4 *>(p)[v] = x;
+    }
 }
+template <bool NT>
 __device__ __forceinline__ float2 ld2(const float *p, uint32_t v) {
-#if DKZ_STREAM_HINTS & 1
-    const f32x2 r = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p) + v);
-    return make_float2(r.x, r.y);
-#else
-    return reinterpret_cast<const float2 *>(p)[v];
-#endif
+    if constexpr (NT) {
+        const f32x2 r = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p) + v);
+        return make_float2(r.x, r.y);
+    } else {
+        return reinterpret_cast<const float2 *>(p)[v];
+    }
 }
+template <bool NT>
 __device__ __forceinline__ void st2(float *p, uint32_t v, float2 x) {
-#if DKZ_STREAM_HINTS & 2
-    const f32x2 w = {x.x, x.y};
-    __builtin_nontemporal_store(w, reinterpret_cast<f32x2 *>(p) + v);
-#else
-    reinterpret_cast<float2 *>(p)[v] = x;
-#endif
+    if constexpr (NT) {
+        const f32x2 w = {x.x, x.y};
+        __builtin_nontemporal_store(w, reinterpret_cast<f32x2 *>(p) + v);
+    } else {
+        reinterpret_cast<float2 *>(p)[v] = x;
+    }
 }
+template <bool NT>
 __device__ __forceinline__ int2 ld2i(const int *p, uint32_t v) {
-#if DKZ_STREAM_HINTS & 1
-    const i32x2 r = __builtin_nontemporal_load(reinterpret_cast<const i32x2 *>(p) + v);
-    return make_int2(r.x, r.y);
-#else
-    return reinterpret_cast<const int2 *>(p)[v];
-#endif
+    if constexpr (NT) {
+        const i32x2 r = __builtin_nontemporal_load(reinterpret_cast<const i32x2 *>(p) + v);
+        return make_int2(r.x, r.y);
+    } else {
+        return reinterpret_cast<const int2 *>(p)[v];
+    }
 }
+template <bool NT>
 __device__ __forceinline__ void st2i(int *p, uint32_t v, int2 x) {
-#if DKZ_STREAM_HINTS & 2
-    const i32x2 w = {x.x, x.y};
-    __builtin_nontemporal_store(w, reinterpret_cast<i32x2 *>(p) + v);
-#else
-    reinterpret_cast<int2 *>(p)[v] = x;
-#endif
+    if constexpr (NT) {
+        const i32x2 w = {x.x, x.y};
+        __builtin_nontemporal_store(w, reinterpret_cast<i32x2 *>(p) + v);
+    } else {
+        reinterpret_cast<int2 *>(p)[v] = x;
+    }
 }
 
 __device__ __forceinline__ float &lane(float4 &v, int k) {
@@ -182,14 +181,18 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
-// Sum over a 256-thread block; every thread returns the same value. `lds`
-// holds kBlock/kWave doubles. Contains barriers: call from all threads.
+// Sum over a BS-thread workgroup; every thread returns the same value, added
+// over the waves in index order. `lds` holds BS/64 doubles. Contains barriers:
+// call from all threads.
+template <int BS = kBlock>
 __device__ __forceinline__ double block_sum(double v, double *lds) {
     v = wave_sum(v);
     const int w = threadIdx.x / kWave;
     if ((threadIdx.x & (kWave - 1)) == 0) lds[w] = v;
     __syncthreads();
-    const double t = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+    double t = lds[0];
+#pragma unroll
+    for (int i = 1; i < BS / kWave; ++i) t += lds[i];
     __syncthreads();
     return t;
 }

@@ -1,0 +1,99 @@
+// dkz_hints.hpp -- which operands of each op stream past the caches.
+//
+// A nontemporal (NT) access keeps a line out of the caches' normal
+// replacement order. Measured on MI355X, NT loads and stores make every op
+// faster when its operands are cold in HBM (a 2-read/1-write stream: 5.5 ->
+// 6.5 TB/s), and also in two of the three op sequences of BASELINE.json's
+// configs -- the SGD step (axpy, axpy, scal over 2 x 100 MB: 6.27 -> 6.48 TB/s)
+// and the batch-norm forward + leaky sequence (4.09 -> 4.46 TB/s). The
+// exception is the batch-norm backward sequence: all seven ops read the same
+// delta, which then stays in the 256 MB Infinity Cache between them, so delta
+// and the ops that only touch delta keep ordinary accesses (an NT scale_bias
+// there costs mean_delta 18 -> 26 us), and only the operands the sequence
+// reads once (the activation output y, x_norm, x in variance_delta) are NT.
+//
+// Bit i of an op's mask marks its operand i; the operand order of each mask is
+// given beside it. Every mask can be overridden at build time (-D...).
+#pragma once
+
+// elementwise.hip: bit k = input stream k (load), bit 4 = the outputs (store)
+#ifndef DKZ_HINT_FILL
+#define DKZ_HINT_FILL 0          // out: delta zeroed before accumulation, or a GEMM output
+#endif
+#ifndef DKZ_HINT_COPY
+#define DKZ_HINT_COPY 16         // x (live), y (a backup read in the backward pass): NT store
+#endif
+#ifndef DKZ_HINT_AXPY
+#define DKZ_HINT_AXPY 19         // x, y loads; y store
+#endif
+#ifndef DKZ_HINT_SCAL
+#define DKZ_HINT_SCAL 17         // x load and store
+#endif
+#ifndef DKZ_HINT_MUL
+#define DKZ_HINT_MUL 0           // x, y
+#endif
+#ifndef DKZ_HINT_CONSTRAIN
+#define DKZ_HINT_CONSTRAIN 0     // x
+#endif
+#ifndef DKZ_HINT_ACTIVATE
+#define DKZ_HINT_ACTIVATE 17     // x load and store
+#endif
+#ifndef DKZ_HINT_GRADIENT
+#define DKZ_HINT_GRADIENT 17     // y (read once) and the delta store; the delta load stays cached
+#endif
+#ifndef DKZ_HINT_LOSS
+#define DKZ_HINT_LOSS 0          // pred, truth; delta, err
+#endif
+
+// broadcast.hip: bit 0 = io load, bit 1 = io store, bit 2 = the read-only operand
+#ifndef DKZ_HINT_ADD_BIAS
+#define DKZ_HINT_ADD_BIAS 3
+#endif
+#ifndef DKZ_HINT_SCALE_BIAS
+#define DKZ_HINT_SCALE_BIAS 0    // also runs on delta inside the backward sequence
+#endif
+#ifndef DKZ_HINT_NORMALIZE
+#define DKZ_HINT_NORMALIZE 3
+#endif
+#ifndef DKZ_HINT_NORMALIZE_DELTA
+#define DKZ_HINT_NORMALIZE_DELTA 4  // x (its last read); delta stays cached
+#endif
+#ifndef DKZ_HINT_AVGPOOL_BWD
+#define DKZ_HINT_AVGPOOL_BWD 3
+#endif
+
+// reduce.hip: bit 0 = first stream, bit 1 = second stream
+#ifndef DKZ_HINT_MEAN
+#define DKZ_HINT_MEAN 1            // x
+#endif
+#ifndef DKZ_HINT_VARIANCE
+#define DKZ_HINT_VARIANCE 1        // x
+#endif
+#ifndef DKZ_HINT_MEAN_DELTA
+#define DKZ_HINT_MEAN_DELTA 0      // delta
+#endif
+#ifndef DKZ_HINT_VARIANCE_DELTA
+#define DKZ_HINT_VARIANCE_DELTA 2  // x; delta stays cached
+#endif
+#ifndef DKZ_HINT_BACKWARD_BIAS
+#define DKZ_HINT_BACKWARD_BIAS 0   // delta
+#endif
+#ifndef DKZ_HINT_BACKWARD_SCALE
+#define DKZ_HINT_BACKWARD_SCALE 2  // x_norm (read once); delta stays cached
+#endif
+#ifndef DKZ_HINT_AVGPOOL_FWD
+#define DKZ_HINT_AVGPOOL_FWD 1     // input, read once
+#endif
+
+// pooling.hip forward: bit 0 = input load, bit 1 = output store, bit 2 = index store
+#ifndef DKZ_HINT_MAXPOOL_FWD
+#define DKZ_HINT_MAXPOOL_FWD 0
+#endif
+// pooling.hip backward: bit 0 = delta and index loads, bit 1 = prev load, bit 2 = prev store
+#ifndef DKZ_HINT_MAXPOOL_BWD
+#define DKZ_HINT_MAXPOOL_BWD 1
+#endif
+// shortcut.hip: bit 0 = add load, bit 1 = out load, bit 2 = out store
+#ifndef DKZ_HINT_SHORTCUT
+#define DKZ_HINT_SHORTCUT 1
+#endif

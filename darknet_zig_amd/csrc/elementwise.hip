@@ -9,6 +9,7 @@
 // (a Buf.offset() view, gpu.zig:128-133) take a one-element-per-thread
 // grid-stride kernel with the same arithmetic.
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -34,7 +35,14 @@ __device__ __forceinline__ void apply_one(const Op &op, const Streams<NI, NO> &s
     for (int k = 0; k < NO; ++k) s.out[k][i] = r[k];
 }
 
-template <int NI, int NO, class Op>
+// H: bit k marks input stream k for nontemporal loads, bit 4 the outputs'
+// stores (dkz_hints.hpp).
+template <int H>
+__device__ __forceinline__ float4 ld4_in(int k, const float *p, uint32_t v) {
+    return ((H >> k) & 1) ? ld4<true>(p, v) : ld4<false>(p, v);
+}
+
+template <int NI, int NO, int H, class Op>
 __device__ __forceinline__ void apply_vec(const Op &op, const Streams<NI, NO> &s, uint32_t v,
                                           const float4 (&in)[NI > 0 ? NI : 1]) {
     float4 out[NO];
@@ -49,10 +57,10 @@ __device__ __forceinline__ void apply_vec(const Op &op, const Streams<NI, NO> &s
         for (int k = 0; k < NO; ++k) lane(out[k], l) = r[k];
     }
 #pragma unroll
-    for (int k = 0; k < NO; ++k) st4(s.out[k], v, out[k]);
+    for (int k = 0; k < NO; ++k) st4<(H & 16) != 0>(s.out[k], v, out[k]);
 }
 
-template <int NI, int NO, class Op>
+template <int NI, int NO, int H, class Op>
 __global__ __launch_bounds__(kBlock) void ew_vec_kernel(Op op, Streams<NI, NO> s, uint32_t n) {
     const uint32_t nv = n >> 2;
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
@@ -62,17 +70,17 @@ __global__ __launch_bounds__(kBlock) void ew_vec_kernel(Op op, Streams<NI, NO> s
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-            for (int k = 0; k < NI; ++k) in[u][k] = ld4(s.in[k], base + u * kBlock);
+            for (int k = 0; k < NI; ++k) in[u][k] = ld4_in<H>(k, s.in[k], base + u * kBlock);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) apply_vec<NI, NO>(op, s, base + u * kBlock, in[u]);
+        for (int u = 0; u < kUnroll; ++u) apply_vec<NI, NO, H>(op, s, base + u * kBlock, in[u]);
     } else {
         for (int u = 0; u < kUnroll; ++u) {
             const uint32_t v = base + u * kBlock;
             if (v < nv) {
                 float4 in[NI > 0 ? NI : 1];
 #pragma unroll
-                for (int k = 0; k < NI; ++k) in[k] = ld4(s.in[k], v);
-                apply_vec<NI, NO>(op, s, v, in);
+                for (int k = 0; k < NI; ++k) in[k] = ld4_in<H>(k, s.in[k], v);
+                apply_vec<NI, NO, H>(op, s, v, in);
             }
         }
     }
@@ -85,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void ew_scalar_kernel(Op op, Streams<NI, NO
         apply_one<NI, NO>(op, s, i);
 }
 
-template <int NI, int NO, class Op>
+template <int H, int NI, int NO, class Op>
 int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
     if (n == 0) return 0;
     bool vec = true;
@@ -95,7 +103,7 @@ int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
     if (vec) {
         const uint32_t nv = un >> 2;
         const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
-        return launch(name, ew_vec_kernel<NI, NO, Op>, dim3(grid), dim3(kBlock), op, s, un);
+        return launch(name, ew_vec_kernel<NI, NO, H, Op>, dim3(grid), dim3(kBlock), op, s, un);
     }
     const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
     return launch(name, ew_scalar_kernel<NI, NO, Op>, dim3(grid), dim3(kBlock), op, s, un);
@@ -178,13 +186,13 @@ struct SmoothL1Op {  // blas.zig:270-282
 template <int A>
 int activate_dispatch(float *x, int n) {
     Streams<1, 1> s{{x}, {x}};
-    return run_ew("activate_array", ActivateOp<A>{}, s, n);
+    return run_ew<DKZ_HINT_ACTIVATE>("activate_array", ActivateOp<A>{}, s, n);
 }
 
 template <int A>
 int gradient_dispatch(const float *y, int n, float *delta) {
     Streams<2, 1> s{{y, delta}, {delta}};
-    return run_ew("gradient_array", GradientOp<A>{}, s, n);
+    return run_ew<DKZ_HINT_GRADIENT>("gradient_array", GradientOp<A>{}, s, n);
 }
 
 typedef int (*ActFn)(float *, int);
@@ -203,7 +211,7 @@ int run_loss(const char *name, int n, const float *pred, const float *truth, flo
     if (n == 0) return 0;
     DKZ_REQUIRE(pred && truth && delta && err);
     Streams<2, 2> s{{pred, truth}, {delta, err}};
-    return run_ew(name, Op{}, s, n);
+    return run_ew<DKZ_HINT_LOSS>(name, Op{}, s, n);
 }
 
 }  // namespace
@@ -218,7 +226,7 @@ int dkz_fill(float *x, int n, float alpha) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr);
     Streams<0, 1> s{{nullptr}, {x}};
-    return run_ew("fill", FillOp{alpha}, s, n);
+    return run_ew<DKZ_HINT_FILL>("fill", FillOp{alpha}, s, n);
 }
 
 int dkz_copy(int n, const float *x, float *y) {
@@ -226,7 +234,7 @@ int dkz_copy(int n, const float *x, float *y) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr && y != nullptr);
     Streams<1, 1> s{{x}, {y}};
-    return run_ew("copy", CopyOp{}, s, n);
+    return run_ew<DKZ_HINT_COPY>("copy", CopyOp{}, s, n);
 }
 
 int dkz_axpy(int n, float alpha, const float *x, float *y) {
@@ -234,7 +242,7 @@ int dkz_axpy(int n, float alpha, const float *x, float *y) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr && y != nullptr);
     Streams<2, 1> s{{x, y}, {y}};
-    return run_ew("axpy", AxpyOp{alpha}, s, n);
+    return run_ew<DKZ_HINT_AXPY>("axpy", AxpyOp{alpha}, s, n);
 }
 
 int dkz_scal(int n, float alpha, float *x) {
@@ -242,7 +250,7 @@ int dkz_scal(int n, float alpha, float *x) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr);
     Streams<1, 1> s{{x}, {x}};
-    return run_ew("scal", ScalOp{alpha}, s, n);
+    return run_ew<DKZ_HINT_SCAL>("scal", ScalOp{alpha}, s, n);
 }
 
 int dkz_mul(int n, const float *x, float *y) {
@@ -250,7 +258,7 @@ int dkz_mul(int n, const float *x, float *y) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr && y != nullptr);
     Streams<2, 1> s{{x, y}, {y}};
-    return run_ew("mul", MulOp{}, s, n);
+    return run_ew<DKZ_HINT_MUL>("mul", MulOp{}, s, n);
 }
 
 int dkz_constrain(int n, float alpha, float *x) {
@@ -258,7 +266,7 @@ int dkz_constrain(int n, float alpha, float *x) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr);
     Streams<1, 1> s{{x}, {x}};
-    return run_ew("constrain", ConstrainOp{alpha}, s, n);
+    return run_ew<DKZ_HINT_CONSTRAIN>("constrain", ConstrainOp{alpha}, s, n);
 }
 
 int dkz_activate_array(float *x, int n, int a) {

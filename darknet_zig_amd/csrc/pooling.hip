@@ -21,6 +21,7 @@
 #include <float.h>
 
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -104,6 +105,9 @@ __device__ __forceinline__ void max_tap(float val, int index, float &mx, int &mi
 }
 
 // q indexes output pairs; ow is even so a pair never straddles a row.
+// Nontemporal accesses per DKZ_HINT_MAXPOOL_FWD / _BWD (dkz_hints.hpp).
+constexpr int kHf = DKZ_HINT_MAXPOOL_FWD, kHb = DKZ_HINT_MAXPOOL_BWD;
+
 __global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, float *out, int *idx,
                                                               PoolGeom g, uint32_t pairs) {
     const uint32_t q = blockIdx.x * kBlock + threadIdx.x;
@@ -115,8 +119,8 @@ __global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, f
     const uint32_t i = t - plane * g.oh;
     const uint32_t r0 = (plane * g.h + 2 * i) * g.w + 2 * j;  // first tap of output j
     const uint32_t r1 = r0 + g.w;
-    const float4 a = ld4(in, r0 >> 2);
-    const float4 b = ld4(in, r1 >> 2);
+    const float4 a = ld4<(kHf & 1) != 0>(in, r0 >> 2);
+    const float4 b = ld4<(kHf & 1) != 0>(in, r1 >> 2);
     float m0 = -FLT_MAX, m1 = -FLT_MAX;
     int i0 = -1, i1 = -1;
     max_tap(a.x, (int)r0, m0, i0);
@@ -127,8 +131,8 @@ __global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, f
     max_tap(a.w, (int)r0 + 3, m1, i1);
     max_tap(b.z, (int)r1 + 2, m1, i1);
     max_tap(b.w, (int)r1 + 3, m1, i1);
-    st2(out, q, make_float2(m0, m1));
-    st2i(idx, q, make_int2(i0, i1));
+    st2<(kHf & 2) != 0>(out, q, make_float2(m0, m1));
+    st2i<(kHf & 4) != 0>(idx, q, make_int2(i0, i1));
 }
 
 __device__ __forceinline__ float add_if(float p, int want, int have, float d) {
@@ -146,10 +150,10 @@ __global__ __launch_bounds__(kBlock) void maxpool2_bwd_kernel(const float *delta
     const uint32_t i = t - plane * g.oh;
     const uint32_t r0 = (plane * g.h + 2 * i) * g.w + 2 * j;
     const uint32_t r1 = r0 + g.w;
-    const float2 d = ld2(delta, q);
-    const int2 k = ld2i(idx, q);
-    float4 a = ld4(prev, r0 >> 2);
-    float4 b = ld4(prev, r1 >> 2);
+    const float2 d = ld2<(kHb & 1) != 0>(delta, q);
+    const int2 k = ld2i<(kHb & 1) != 0>(idx, q);
+    float4 a = ld4<(kHb & 2) != 0>(prev, r0 >> 2);
+    float4 b = ld4<(kHb & 2) != 0>(prev, r1 >> 2);
     // Each input of the patch has exactly one candidate output: j for the
     // first two columns, j+1 for the last two.
     a.x = add_if(a.x, (int)r0, k.x, d.x);
@@ -160,8 +164,8 @@ __global__ __launch_bounds__(kBlock) void maxpool2_bwd_kernel(const float *delta
     a.w = add_if(a.w, (int)r0 + 3, k.y, d.y);
     b.z = add_if(b.z, (int)r1 + 2, k.y, d.y);
     b.w = add_if(b.w, (int)r1 + 3, k.y, d.y);
-    st4(prev, r0 >> 2, a);
-    st4(prev, r1 >> 2, b);
+    st4<(kHb & 4) != 0>(prev, r0 >> 2, a);
+    st4<(kHb & 4) != 0>(prev, r1 >> 2, b);
 }
 
 // Validates the gpu.zig arguments and derives the geometry. `n` is out_n

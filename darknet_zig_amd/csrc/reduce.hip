@@ -10,7 +10,9 @@
 //     delta*x_norm, delta*(x-m), rounded exactly as blas.zig rounds them -- and
 //     accumulates it in f64. A chunk is then summed by wave64 DPP reductions
 //     and a 4-entry LDS step (dkz_device.hpp).
-//   * K == 1: the workgroup finalises its channel itself (one launch).
+//   * K == 1 (enough channels to fill the GPU, see pick_split): the
+//     workgroup, 1024 threads wide for long channels, finalises its channel
+//     itself (one launch).
 //     K > 1: each workgroup stores its f64 partial, and a second, tiny launch
 //     (one wave per channel) adds the K partials in index order and
 //     finalises. The kernel boundary orders the two passes, so no workgroup
@@ -21,6 +23,7 @@
 //   * The finalisation repeats blas.zig's f32 arithmetic on the f32-rounded
 //     total: sum * (1/(B*S)), sum * (-1/sqrt(v+1e-5)), updates[f] += sum, ...
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -50,7 +53,8 @@ __device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
 
 // Sum of this workgroup's chunk of channel f (all threads return it).
 // T::at(f) gives the per-element term of channel f; p1 is read only when TWO.
-template <class T, bool TWO, bool VEC>
+// H: bit 0 / bit 1 = nontemporal loads of p0 / p1 (dkz_hints.hpp).
+template <class T, bool TWO, bool VEC, int H, int BS>
 __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const float *p1, const RedGeom &g,
                                             uint32_t f, uint32_t k, double *lds) {
     const uint32_t j0 = k * g.chunk;
@@ -59,15 +63,15 @@ __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const f
     const auto term = t.at(f);
     double acc0 = 0.0, acc1 = 0.0;
     if constexpr (VEC) {
-        constexpr uint32_t kStep = 4 * kBlock;
+        constexpr uint32_t kStep = 4 * BS;
         uint32_t j = j0 + 4 * threadIdx.x;
         for (; j + kStep * (kUnroll - 1) < j1; j += kStep * kUnroll) {
             float4 a[kUnroll], b[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 const uint32_t v = chan_addr(fbase, j + u * kStep, g) >> 2;
-                a[u] = ld4(p0, v);
-                if constexpr (TWO) b[u] = ld4(p1, v);
+                a[u] = ld4<(H & 1) != 0>(p0, v);
+                if constexpr (TWO) b[u] = ld4<(H & 2) != 0>(p1, v);
                 else b[u] = a[u];
             }
 #pragma unroll
@@ -78,36 +82,35 @@ __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const f
         }
         for (; j < j1; j += kStep) {
             const uint32_t v = chan_addr(fbase, j, g) >> 2;
-            const float4 a = ld4(p0, v);
-            const float4 b = TWO ? ld4(p1, v) : a;
+            const float4 a = ld4<(H & 1) != 0>(p0, v);
+            const float4 b = TWO ? ld4<(H & 2) != 0>(p1, v) : a;
             acc0 += term4(term, a, b);
         }
     } else {
-        for (uint32_t j = j0 + threadIdx.x; j < j1; j += kBlock) {
+        for (uint32_t j = j0 + threadIdx.x; j < j1; j += BS) {
             const uint32_t e = chan_addr(fbase, j, g);
             acc0 += (double)term(p0[e], TWO ? p1[e] : 0.0f);
         }
     }
-    return block_sum(acc0 + acc1, lds);
+    return block_sum<BS>(acc0 + acc1, lds);
 }
 
-// K == 1: one workgroup per channel, finalised in place.
-template <class T, class Fin, bool TWO, bool VEC>
-__global__ __launch_bounds__(kBlock) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1,
-                                                             RedGeom g) {
-    __shared__ double lds[kBlock / kWave];
-    const double total = chunk_sum<T, TWO, VEC>(t, p0, p1, g, blockIdx.x, 0, lds);
+// K == 1: one workgroup of BS threads per channel, finalised in place.
+template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
+__global__ __launch_bounds__(BS) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g) {
+    __shared__ double lds[BS / kWave];
+    const double total = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, blockIdx.x, 0, lds);
     if (threadIdx.x == 0) fin(blockIdx.x, total);
 }
 
 // K > 1, pass 1: workgroup (f, k) stores its partial at partials[f*K + k].
-template <class T, bool TWO, bool VEC>
+template <class T, bool TWO, bool VEC, int H>
 __global__ __launch_bounds__(kBlock) void chan_partial_kernel(T t, const float *p0, const float *p1, RedGeom g,
                                                               double *partials) {
     __shared__ double lds[kBlock / kWave];
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
-    const double total = chunk_sum<T, TWO, VEC>(t, p0, p1, g, f, k, lds);
+    const double total = chunk_sum<T, TWO, VEC, H, kBlock>(t, p0, p1, g, f, k, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
@@ -123,9 +126,20 @@ __global__ __launch_bounds__(kBlock) void chan_finalize_kernel(Fin fin, const do
     if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s);
 }
 
-// Workgroups per channel: about 2048 over the launch, each with at least 4096
-// elements, within the scratch's capacity. Depends on the shape only.
-uint32_t pick_split(uint32_t filters, uint32_t chan_len) {
+// How a channel reduction is split, from the shape only. A workgroup streams
+// at most ~43 GB/s, so one 1024-thread workgroup per channel reaches
+// ~5.5 TB/s with 128 channels and ~6.4 TB/s with 256; splitting each channel
+// over ~2048 workgroups reaches ~6.4 TB/s but costs a second (finalize)
+// launch of ~4 us. Hence:
+//  * filters >= 256, or filters >= 128 with at most 160 MB to read: one
+//    workgroup per channel and one launch (1024 threads for long channels);
+//  * otherwise about 2048 workgroups of >= 4096 elements, then the finalize
+//    launch (within the scratch's capacity).
+constexpr uint32_t kWideBlock = 1024;
+
+uint32_t pick_split(uint32_t filters, uint32_t chan_len, uint32_t streams) {
+    const uint64_t bytes = (uint64_t)4 * streams * filters * chan_len;
+    if (filters >= 256 || (filters >= 128 && bytes <= 160000000ull)) return 1;
     uint32_t k = div_up(2048, filters);
     const uint32_t kmax = chan_len / 4096 > 1 ? chan_len / 4096 : 1;
     if (k > kmax) k = kmax;
@@ -133,29 +147,35 @@ uint32_t pick_split(uint32_t filters, uint32_t chan_len) {
     return k < 1 ? 1 : k;
 }
 
-template <class T, class Fin, bool TWO>
+template <int H, class T, class Fin, bool TWO>
 int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p0, const float *p1,
                     int batch, int filters, int spatial) {
     const uint64_t chan_len64 = (uint64_t)batch * (uint64_t)spatial;
     DKZ_REQUIRE(chan_len64 * (uint64_t)filters <= kMaxElems);
     const uint32_t F = (uint32_t)filters, S = (uint32_t)spatial, L = (uint32_t)chan_len64;
     const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
-    uint32_t K = pick_split(F, L);
+    uint32_t K = pick_split(F, L, TWO ? 2 : 1);
     uint32_t chunk = L == 0 ? 0 : div_up(L, K);
     if (vec) chunk = (chunk + 3) & ~3u;
     K = chunk > 0 ? div_up(L, chunk) : 1;
     const RedGeom g{S, L, chunk, K, (F - 1) * S, make_fastdiv(K), make_fastdiv(S == 0 ? 1 : S)};
-    const dim3 block(kBlock);
     if (K == 1) {
-        if (vec) return launch(name, chan_reduce_kernel<T, Fin, TWO, true>, dim3(F), block, t, fin, p0, p1, g);
-        return launch(name, chan_reduce_kernel<T, Fin, TWO, false>, dim3(F), block, t, fin, p0, p1, g);
+        if (L >= 16 * kWideBlock) {
+            const dim3 block(kWideBlock);
+            if (vec) return launch(name, chan_reduce_kernel<T, Fin, TWO, true, H, kWideBlock>, dim3(F), block, t, fin, p0, p1, g);
+            return launch(name, chan_reduce_kernel<T, Fin, TWO, false, H, kWideBlock>, dim3(F), block, t, fin, p0, p1, g);
+        }
+        const dim3 block(kBlock);
+        if (vec) return launch(name, chan_reduce_kernel<T, Fin, TWO, true, H, kBlock>, dim3(F), block, t, fin, p0, p1, g);
+        return launch(name, chan_reduce_kernel<T, Fin, TWO, false, H, kBlock>, dim3(F), block, t, fin, p0, p1, g);
     }
+    const dim3 block(kBlock);
     Scratch sc{nullptr};
     DKZ_TRY(device_scratch(&sc));
     if (vec)
-        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, true>, dim3(F * K), block, t, p0, p1, g, sc.partials));
+        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, true, H>, dim3(F * K), block, t, p0, p1, g, sc.partials));
     else
-        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, false>, dim3(F * K), block, t, p0, p1, g, sc.partials));
+        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, false, H>, dim3(F * K), block, t, p0, p1, g, sc.partials));
     return launch(name, chan_finalize_kernel<Fin>, dim3(div_up(F, kBlock / kWave)), block, fin,
                   (const double *)sc.partials, F, K);
 }
@@ -257,12 +277,12 @@ __global__ __launch_bounds__(kBlock) void avgpool_rows_kernel(const float *x, fl
         for (; i + 3 * kWave < S4; i += 4 * kWave) {
             float4 a[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) a[u] = ld4(x, v0 + i + u * kWave);
+            for (int u = 0; u < 4; ++u) a[u] = ld4<(DKZ_HINT_AVGPOOL_FWD & 1) != 0>(x, v0 + i + u * kWave);
 #pragma unroll
             for (int u = 0; u < 4; ++u) acc += term4(Value{}, a[u], a[u]);
         }
         for (; i < S4; i += kWave) {
-            const float4 a = ld4(x, v0 + i);
+            const float4 a = ld4<(DKZ_HINT_AVGPOOL_FWD & 1) != 0>(x, v0 + i);
             acc += term4(Value{}, a, a);
         }
     } else {
@@ -287,7 +307,7 @@ int dkz_mean(const float *x, int batch, int filters, int spatial, float *out) {
     if (filters == 0) return 0;
     DKZ_REQUIRE(out && (x || (uint64_t)batch * spatial == 0));
     const float scale = 1.0f / (float)((uint64_t)batch * (uint64_t)spatial);  // blas.zig:107
-    return run_chan_reduce<SumValue, FinScale, false>("mean", SumValue{}, FinScale{out, scale}, x, nullptr,
+    return run_chan_reduce<DKZ_HINT_MEAN, SumValue, FinScale, false>("mean", SumValue{}, FinScale{out, scale}, x, nullptr,
                                                       batch, filters, spatial);
 }
 
@@ -297,7 +317,7 @@ int dkz_variance(const float *x, const float *mean, int batch, int filters, int 
     DKZ_REQUIRE(out && mean && (x || (uint64_t)batch * spatial == 0));
     // blas.zig:122, usize arithmetic: batch*spatial - 1 wraps when the product is 0.
     const float scale = 1.0f / (float)((uint64_t)batch * (uint64_t)spatial - 1u);
-    return run_chan_reduce<SumSqDev, FinScale, false>("variance", SumSqDev{mean}, FinScale{out, scale}, x,
+    return run_chan_reduce<DKZ_HINT_VARIANCE, SumSqDev, FinScale, false>("variance", SumSqDev{mean}, FinScale{out, scale}, x,
                                                       nullptr, batch, filters, spatial);
 }
 
@@ -306,7 +326,7 @@ int dkz_mean_delta(const float *delta, const float *variance, int batch, int fil
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (filters == 0) return 0;
     DKZ_REQUIRE(out && variance && (delta || (uint64_t)batch * spatial == 0));
-    return run_chan_reduce<SumValue, FinMeanDelta, false>("mean_delta", SumValue{},
+    return run_chan_reduce<DKZ_HINT_MEAN_DELTA, SumValue, FinMeanDelta, false>("mean_delta", SumValue{},
                                                           FinMeanDelta{out, variance}, delta, nullptr,
                                                           batch, filters, spatial);
 }
@@ -316,7 +336,7 @@ int dkz_variance_delta(const float *x, const float *delta, const float *mean, co
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (filters == 0) return 0;
     DKZ_REQUIRE(out && mean && variance && ((x && delta) || (uint64_t)batch * spatial == 0));
-    return run_chan_reduce<SumProdDev, FinVarianceDelta, true>("variance_delta", SumProdDev{mean},
+    return run_chan_reduce<DKZ_HINT_VARIANCE_DELTA, SumProdDev, FinVarianceDelta, true>("variance_delta", SumProdDev{mean},
                                                                FinVarianceDelta{out, variance}, delta, x,
                                                                batch, filters, spatial);
 }
@@ -331,7 +351,7 @@ int dkz_backward_bias(float *bias_updates, const float *delta, int batch, int fi
         return launch("backward_bias_conn", backward_bias_conn_kernel, dim3(div_up((uint32_t)filters, kBlock)),
                       dim3(kBlock), bias_updates, delta, (uint32_t)batch, (uint32_t)filters);
     }
-    return run_chan_reduce<SumValue, FinAccumulate, false>("backward_bias", SumValue{},
+    return run_chan_reduce<DKZ_HINT_BACKWARD_BIAS, SumValue, FinAccumulate, false>("backward_bias", SumValue{},
                                                            FinAccumulate{bias_updates}, delta, nullptr, batch,
                                                            filters, spatial);
 }
@@ -341,7 +361,7 @@ int dkz_backward_scale(const float *x_norm, const float *delta, int batch, int f
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (filters == 0) return 0;
     DKZ_REQUIRE(scale_updates && ((x_norm && delta) || (uint64_t)batch * spatial == 0));
-    return run_chan_reduce<SumProd, FinAccumulate, true>("backward_scale", SumProd{},
+    return run_chan_reduce<DKZ_HINT_BACKWARD_SCALE, SumProd, FinAccumulate, true>("backward_scale", SumProd{},
                                                          FinAccumulate{scale_updates}, delta, x_norm, batch,
                                                          filters, spatial);
 }

@@ -12,6 +12,7 @@
 // fast path: a lane owns two adjacent outputs, reads them as a float2 and the
 // four add values around their sources as one float4.
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -53,11 +54,12 @@ __global__ __launch_bounds__(kBlock) void shortcut2_kernel(const float *add, flo
     shortcut_coords(2 * q, g, i, j, k, b);
     const uint32_t oi = i + g.w2 * (j + g.h2 * (k + g.c2 * b));
     const uint32_t ai = 2 * i + g.w1 * (2 * j + g.h1 * (k + g.c1 * b));
-    float2 o = ld2(out, oi >> 1);
-    const float4 a = ld4(add, ai >> 2);
+    constexpr int H = DKZ_HINT_SHORTCUT;  // bit 0: add loads, 1: out loads, 2: out stores
+    float2 o = ld2<(H & 2) != 0>(out, oi >> 1);
+    const float4 a = ld4<(H & 1) != 0>(add, ai >> 2);
     o.x = g.s1 * o.x + g.s2 * a.x;
     o.y = g.s1 * o.y + g.s2 * a.z;
-    st2(out, oi >> 1, o);
+    st2<(H & 4) != 0>(out, oi >> 1, o);
 }
 
 }  // namespace
