@@ -20,8 +20,12 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
   per_op       every op of BASELINE.json's five configs timed on its own,
                cold (rotated buffers, >= 512 MB per rotation), in GB/s and as
                a fraction of 8 TB/s
-  bn_act_gelem_s  config 1 elements / sum of config 1 op times (forward) and
-               config 2 elements / sum of config 2 op times (backward)
+  fused_bwd    the same step through dkz_batchnorm_backward (one reduction
+               pass and one apply pass, 32 B/elem instead of 56)
+  bn_act_gelem_s  config 1 elements / config 1 forward time and config 2
+               elements / config 2 backward time: per-op (chained, and the sum
+               of single-op times), the whole per-op layer forward with its
+               copies and EMA, and the fused entry points
   cpu_baseline the CPU twins' C restatement (oracle/) on the same inputs on
                this host, one thread, median of 3 full config-2 chains
 
@@ -166,6 +170,15 @@ def config2_chain_ops(gpu, d, h):
     ]
 
 
+def fused_backward(gpu, d, h):
+    """The same layer step through the fused entry point (one reduction pass
+    over y, delta, x_norm, x; one apply pass over y, delta, x): 32 B/elem."""
+    from darknet_zig_amd.activations import Activation
+
+    gpu.batchnormBackward(h["B"], h["F"], h["S"], Activation.leaky, d["y"], d["delta"], d["x"], d["x_norm"],
+                          d["mean"], d["var"], d["scales"], d["bu"], d["su"], d["md"], d["vd"])
+
+
 def upload_config2(dev, h, sets: int):
     F, n = h["F"], h["n"]
     big = {k: dev.up(h[k]) for k in ("y", "delta", "x", "x_norm")}
@@ -266,11 +279,19 @@ def per_op_table(gpu, hip, stream, launches: int):
 
     rows = {}
 
-    def add(cfg, name, nbytes, fns, elems=None):
-        ms = time_op(hip, stream, fns, max(launches, len(fns)))
+    def row(cfg, name, nbytes, ms):
         g = gbs(nbytes, ms)
         rows[f"{cfg}/{name}"] = {"us": round(ms * 1e3, 3), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4),
                                  "bytes": nbytes}
+
+    def add(cfg, name, nbytes, fns):
+        """One op, HIP events around each launch."""
+        row(cfg, name, nbytes, time_op(hip, stream, fns, max(launches, len(fns))))
+
+    def add_seq(cfg, name, nbytes, seqs):
+        """A call sequence (or a multi-launch entry point), events only around
+        the whole timed region, as a layer would issue it back to back."""
+        row(cfg, name, nbytes, time_seq(hip, stream, seqs, max(launches, len(seqs))))
 
     # -- config 1: BN forward + leaky, [128,32,32,32], x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1)
     dev = Device(gpu)
@@ -299,13 +320,29 @@ def per_op_table(gpu, hip, stream, launches: int):
              lambda b=b: gpu.normalize(b, m, v, B, F, S), lambda b=b: gpu.scaleBias(b, gam, B, F, S),
              lambda b=b: gpu.addBias(b, bet, B, F, S), lambda b=b: gpu.activateArray(b, n, Activation.leaky)]
             for b in xs]
-    ms = time_seq(hip, stream, seqs, max(launches, R))
-    rows[f"{cfg}/chain: mean,variance,normalize,scale_bias,add_bias,leaky"] = {
-        "us": round(ms * 1e3, 3), "GB/s": round(gbs(10 * E, ms), 1), "frac": round(gbs(10 * E, ms) / PEAK_GBS, 4),
-        "bytes": 10 * E}
+    add_seq(cfg, "chain: mean,variance,normalize,scale_bias,add_bias,leaky", 10 * E, seqs)
     rm, rv = dev.zeros(F), dev.zeros(F)
-    add(cfg, "ema scal+axpy (C floats)", 4 * 3 * F,
-        [lambda: (gpu.scal(F, 0.99, rm), gpu.axpy(F, 0.01, m, rm), gpu.scal(F, 0.99, rv), gpu.axpy(F, 0.01, v, rv))])
+    mom, alpha = 0.99, float(np.float32(1) - np.float32(0.99))  # batchnorm.zig:16, :141
+
+    def ema():
+        gpu.scal(F, mom, rm)
+        gpu.axpy(F, alpha, m, rm)
+        gpu.scal(F, mom, rv)
+        gpu.axpy(F, alpha, v, rv)
+
+    add(cfg, "ema scal+axpy (C floats)", 4 * 3 * F, [ema])
+    # the whole layer forward as batchnorm.zig:129-153 issues it (copies and
+    # EMA included) and then the activation, against the fused entry point
+    xcs, xns = [dev.zeros(n) for _ in range(R)], [dev.zeros(n) for _ in range(R)]
+    seqs = [[lambda b=b, c=c: gpu.copy(n, b, c), lambda b=b: gpu.mean(b, B, F, S, m),
+             lambda b=b: gpu.variance(b, m, B, F, S, v), ema, lambda b=b: gpu.normalize(b, m, v, B, F, S),
+             lambda b=b, c=c: gpu.copy(n, b, c), lambda b=b: gpu.scaleBias(b, gam, B, F, S),
+             lambda b=b: gpu.addBias(b, bet, B, F, S), lambda b=b: gpu.activateArray(b, n, Activation.leaky)]
+            for b, c in zip(xs, xcs)]
+    add_seq(cfg, "layer sequence: copy,mean,variance,ema,normalize,copy,scale_bias,add_bias,leaky", 14 * E, seqs)
+    add_seq("fused", "cfg1 batchnorm_forward(train, leaky): stats + apply", 5 * E,
+            [[lambda b=b, c=c, xn=xn: gpu.batchnormForward(B, F, S, Activation.leaky, True, b, b, c, xn, m, v, rm, rv,
+                                                           gam, bet)] for b, c, xn in zip(xs, xcs, xns)])
     dev.free()
 
     # -- config 2: BN backward ops on their own
@@ -315,6 +352,8 @@ def per_op_table(gpu, hip, stream, launches: int):
     chains = [config2_chain_ops(gpu, d, h) for d in sets]
     for j, (name, nbytes, _) in enumerate(chains[0]):
         add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
+    add_seq("fused", "cfg2 batchnorm_backward(leaky): sums + apply", 8 * 4 * h["n"],
+            [[lambda d=d: fused_backward(gpu, d, h)] for d in sets])
     dev.free()
 
     # -- config 3: softmax + cross-entropy delta, [256,1000], logits ~N(0,4)
@@ -352,10 +391,7 @@ def per_op_table(gpu, hip, stream, launches: int):
     add(cfg, "scal(momentum, dw)", 2 * 4 * n4, [lambda d=d: gpu.scal(n4, momentum, d) for d in dws])
     seqs = [[lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d), lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w),
              lambda d=d: gpu.scal(n4, momentum, d)] for w, d in zip(ws, dws)]
-    ms = time_seq(hip, stream, seqs, max(launches, R))
-    rows[f"{cfg}/chain: axpy,axpy,scal (one SGD step)"] = {
-        "us": round(ms * 1e3, 3), "GB/s": round(gbs(8 * 4 * n4, ms), 1),
-        "frac": round(gbs(8 * 4 * n4, ms) / PEAK_GBS, 4), "bytes": 8 * 4 * n4}
+    add_seq(cfg, "chain: axpy,axpy,scal (one SGD step)", 8 * 4 * n4, seqs)
     dev.free()
     dev = Device(gpu)
     sb, w1, c1, w2, c2 = 64, 28, 256, 14, 512
@@ -492,6 +528,8 @@ def main() -> int:
     hip.sync()
     ms = time_chain(hip, stream, chains, args.steps, args.warmup)
     per_kernel_ms = time_chain_per_kernel(hip, stream, chains, args.steps)
+    fused_ms = time_seq(hip, stream, [[lambda d=d: fused_backward(gpu, d, h)] for d in sets], args.steps,
+                        args.warmup)
     dev.free()
 
     names = [nm for nm, _, _ in chains[0]]
@@ -548,6 +586,14 @@ def main() -> int:
             "event_pair_overhead_us": round(overhead_ms * 1e3, 2),
         },
         "chain_kernels": chain_kernels,
+        "fused_bwd": {
+            "entry": "dkz_batchnorm_backward (same step, same buffers: one sums pass + one apply pass)",
+            "us": round(fused_ms * 1e3, 2),
+            "bytes": 8 * 4 * h["n"],
+            "GB/s": round(gbs(8 * 4 * h["n"], fused_ms), 1),
+            "GElem/s": round(h["n"] / (fused_ms * 1e-3) / 1e9, 2),
+            "speedup_vs_per_op_chain": round((ms / args.steps) / fused_ms, 3),
+        },
     }
     if not args.no_per_op:
         table = per_op_table(gpu, hip, stream, args.op_launches)
@@ -555,6 +601,9 @@ def main() -> int:
         named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
         fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and k.split("/", 1)[1] in named)
         fwd_chain = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/chain" in k)
+        fwd_layer = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/layer sequence" in k)
+        fwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg1"))
+        bwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg2"))
         bwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg2"))
         e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
         result["bn_act_gelem_s"] = {
@@ -562,6 +611,9 @@ def main() -> int:
             "bwd_cfg2_chained": round(e2 / (ms / args.steps * 1e-3) / 1e9, 2),
             "fwd_cfg1_per_op_sum": round(e1 / (fwd * 1e-6) / 1e9, 2),
             "bwd_cfg2_per_op_sum": round(e2 / (bwd * 1e-6) / 1e9, 2),
+            "fwd_cfg1_layer_sequence": round(e1 / (fwd_layer * 1e-6) / 1e9, 2),
+            "fwd_cfg1_fused": round(e1 / (fwd_fused * 1e-6) / 1e9, 2),
+            "bwd_cfg2_fused": round(e2 / (bwd_fused * 1e-6) / 1e9, 2),
         }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(h)

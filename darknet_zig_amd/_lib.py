@@ -67,6 +67,8 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_forward_avgpool": (_i, [_i, _i, _i, _i, _p, _p]),
     "dkz_backward_avgpool": (_i, [_i, _i, _i, _i, _p, _p]),
     "dkz_shortcut": (_i, [_i, _i, _i, _i, _p, _i, _i, _i, _f, _f, _p]),
+    "dkz_batchnorm_forward": (_i, [_i, _i, _i, _i, _i] + [_p] * 10),
+    "dkz_batchnorm_backward": (_i, [_i, _i, _i, _i] + [_p] * 11),
 }
 
 _LIB: C.CDLL | None = None

@@ -1,0 +1,547 @@
+// batchnorm.hip -- the batch-norm layer step as fused passes over the tensor.
+//
+// The reference issues the layer as a sequence of per-op launches, each
+// streaming the whole tensor (layers/batchnorm.zig:129-174, plus the
+// activation of convolutional.zig:269 and its gradient at :280):
+//   forward (train):  copy->x, mean, variance, 4 x EMA, normalize,
+//                     copy->x_norm, scale_bias, add_bias, activate
+//                     = 56 bytes/element with the copies;
+//   backward:         gradient, backward_bias, backward_scale, scale_bias,
+//                     mean_delta, variance_delta, normalize_delta
+//                     = 56 bytes/element.
+// Here each direction is one reduction pass, a tiny per-channel finalise,
+// and one apply pass:
+//   forward:  stats (read input: 4 B/elem) -> finalise (mean, variance, EMA)
+//             -> apply (read input; write x, x_norm, output: 16 B/elem);
+//   backward: sums (read y, delta, x_norm, x: 16 B/elem) -> finalise
+//             (bias/scale updates, mean_delta, variance_delta) -> apply
+//             (read y, delta, x; write delta: 16 B/elem).
+// Element results are the per-op sequence's, bit for bit, given the same
+// per-channel values: every element expression below is the one of the
+// corresponding op (broadcast.hip, elementwise.hip), in the same order.
+//
+// Forward statistics. The per-op path makes two passes (mean, then the sum
+// of squared deviations from it). The fused pass reads the input once and
+// accumulates, in f64, s1 = sum(x - c) and s2 = sum((x - c)^2) about a
+// per-channel shift c = the channel's first element (x - c is exact in f64).
+// Then sum(x) = n*c + s1, and the sum of squared deviations from any f32
+// mean m is s2 - s1^2/n + n*(c + s1/n - m)^2. Shifting by a sample of the
+// channel keeps the cancellation in s2 - s1^2/n to the factor
+// 1 + ((c - mean)/stddev)^2, so the result stays within a few f64 ulps of the
+// exact sum unless c is an outlier by ~10^4 standard deviations. The twin
+// (blas.zig:121-135) sums f32-rounded (x - m)^2 terms sequentially in f32, so
+// the two agree to within the twin's own rounding error.
+//
+// The fast path needs spatial % 4 == 0, 16-byte aligned tensors and a
+// non-empty tensor; any other call runs the per-op sequence, which handles
+// every shape (and edge case) exactly as the individual entry points do.
+#include "dkz_channel.hpp"
+#include "dkz_hints.hpp"
+
+namespace dkz {
+namespace {
+
+constexpr int kUnroll = 4;
+constexpr float kMomentum = 0.99f;          // rolling_momentum, batchnorm.zig:16 (f32)
+constexpr float kAlpha = 1.0f - kMomentum;  // batchnorm.zig:141: an f32 subtraction, exact
+
+template <int NS>
+struct Sums {
+    double s[NS];
+};
+
+// Workgroup of a reduction pass: chunk k of channel f. Consecutive
+// workgroups take the same chunk of consecutive channels, so the grid
+// sweeps the tensor roughly in address order.
+__device__ __forceinline__ void red_coords(const RedGeom &g, uint32_t &f, uint32_t &k) {
+    k = fdiv(blockIdx.x, g.div_filters);
+    f = blockIdx.x - k * g.div_filters.d;
+}
+
+// NS sums over a BS-thread workgroup; the result is valid in wave 0. Each
+// wave's sums go through LDS (lds holds NS * BS/64 doubles) and wave 0 adds
+// them with one more DPP reduction, so the order is fixed by the shape.
+template <int NS, int BS>
+__device__ __forceinline__ Sums<NS> block_sums(const double (&a)[NS], double *lds) {
+    constexpr int W = BS / kWave;
+    const int w = threadIdx.x / kWave, l = threadIdx.x & (kWave - 1);
+    Sums<NS> r;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const double v = wave_sum(a[q]);
+        if (l == 0) lds[q * W + w] = v;
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int q = 0; q < NS; ++q) r.s[q] = wave_sum(l < W ? lds[q * W + l] : 0.0);
+    }
+    return r;
+}
+
+// Partial sums of workgroup (f, k) go to partials[(q*F + f)*K + k].
+template <int NS, int BS>
+__device__ __forceinline__ void store_partials(const Sums<NS> &r, const RedGeom &g, uint32_t f, uint32_t k,
+                                               double *partials) {
+    if (threadIdx.x == 0) {
+        const uint32_t F = g.div_filters.d;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) partials[((uint32_t)q * F + f) * g.K + k] = r.s[q];
+    }
+}
+
+// Second launch: one wave per channel adds its K partials of each sum in
+// index order, then finalises.
+template <int NS, class Fin>
+__global__ __launch_bounds__(kBlock) void bn_finalize_kernel(Fin fin, const double *partials, uint32_t F,
+                                                             uint32_t K) {
+    const uint32_t f = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (f >= F) return;  // whole waves leave together
+    const uint32_t l = threadIdx.x & (kWave - 1);
+    Sums<NS> r;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const double *p = partials + ((uint64_t)q * F + f) * K;
+        double s = 0.0;
+        for (uint32_t i = l; i < K; i += kWave) s += p[i];
+        r.s[q] = wave_sum(s);
+    }
+    if (l == 0) fin(f, r);
+}
+
+// ---- forward ----------------------------------------------------------------
+
+// mean, variance and the rolling averages of channel f from s1 = sum(x - c),
+// s2 = sum((x - c)^2) over its n elements.
+struct FwdFin {
+    const float *input;
+    float *mean, *variance, *rolling_mean, *rolling_variance;
+    uint32_t spatial;
+    double n;
+    float mean_scale;  // 1/(B*S) in f32 (blas.zig:107)
+    float var_scale;   // 1/(B*S - 1) in f32 (blas.zig:122)
+    __device__ void operator()(uint32_t f, const Sums<2> &r) const {
+        const double s1 = r.s[0], s2 = r.s[1];
+        const double c = (double)input[f * spatial];
+        const float m = (float)(n * c + s1) * mean_scale;  // blas.zig:114: sum * (1/(B*S))
+        const double dm = (c + s1 / n) - (double)m;
+        double m2 = s2 - s1 * (s1 / n);
+        m2 = m2 > 0.0 ? m2 : 0.0;
+        const float v = (float)(m2 + n * dm * dm) * var_scale;  // blas.zig:133
+        mean[f] = m;
+        variance[f] = v;
+        // batchnorm.zig:140-143: scal(0.99) then axpy(1 - 0.99) -- axpy is an fma (blas.zig:22)
+        rolling_mean[f] = __builtin_fmaf(kAlpha, m, rolling_mean[f] * kMomentum);
+        rolling_variance[f] = __builtin_fmaf(kAlpha, v, rolling_variance[f] * kMomentum);
+    }
+};
+
+__device__ __forceinline__ void acc_shifted(float4 v, double c, double &a1, double &a2) {
+    const double d0 = (double)v.x - c, d1 = (double)v.y - c, d2 = (double)v.z - c, d3 = (double)v.w - c;
+    a1 += (d0 + d1) + (d2 + d3);
+    a2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+}
+
+// FIN: the channel is one workgroup (K == 1), which finalises it itself.
+template <int H, int BS, bool FIN>
+__global__ __launch_bounds__(BS) void bn_stats_kernel(const float *input, RedGeom g, FwdFin fin, double *partials) {
+    __shared__ double lds[2 * (BS / kWave)];
+    uint32_t f, k;
+    red_coords(g, f, k);
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const double c = (double)input[fbase];
+    double a[2] = {0.0, 0.0}, b[2] = {0.0, 0.0};
+    constexpr uint32_t kStep = 4 * BS;
+    uint32_t j = j0 + 4 * threadIdx.x;
+    for (; j + kStep * (kUnroll - 1) < j1; j += kStep * kUnroll) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = ld4<(H & 1) != 0>(input, chan_addr(fbase, j + u * kStep, g) >> 2);
+#pragma unroll
+        for (int u = 0; u < kUnroll; u += 2) {
+            acc_shifted(v[u], c, a[0], a[1]);
+            acc_shifted(v[u + 1], c, b[0], b[1]);
+        }
+    }
+    for (; j < j1; j += kStep) acc_shifted(ld4<(H & 1) != 0>(input, chan_addr(fbase, j, g) >> 2), c, a[0], a[1]);
+    const double t[2] = {a[0] + b[0], a[1] + b[1]};
+    const Sums<2> r = block_sums<2, BS>(t, lds);
+    if constexpr (FIN) {
+        if (threadIdx.x == 0) fin(f, r);
+    } else {
+        store_partials<2, BS>(r, g, f, k, partials);
+    }
+}
+
+struct FwdParams {
+    const float *mean, *variance, *scales, *biases;
+};
+
+// x = input; x_norm = (input - m) * (1/(sqrt(v) + 1e-6)) (blas.zig:137-146);
+// output = act(x_norm * scale + bias) (blas.zig:63-71, 53-61;
+// activations.zig:107-125). TRAIN: x_norm is stored (batchnorm.zig:146).
+template <int A, bool TRAIN>
+__device__ __forceinline__ void fwd_elem(float4 v, const FwdParams &p, uint32_t f, float4 &xn, float4 &o) {
+    const float m = p.mean[f];
+    const float inv = 1.0f / (sqrtf(p.variance[f]) + 1e-6f);
+    const float gam = p.scales[f], bet = p.biases[f];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const float t = (lane(v, l) - m) * inv;
+        lane(xn, l) = t;
+        lane(o, l) = activate<A>(t * gam + bet);
+    }
+}
+
+// H: bit 0 = input load, bit 1 = x store, bit 2 = x_norm store, bit 3 = output store.
+template <int A, bool TRAIN, int H, bool REV>
+__global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input, float *output, float *x,
+                                                              float *x_norm, FwdParams p, ChanGeom g,
+                                                              uint32_t nv) {
+    constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
+    const uint32_t tile = REV ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+    const uint32_t base = tile * (kBlock * kUnroll) + threadIdx.x;
+    if (base + (kUnroll - 1) * kBlock < nv) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = ld4<kNtIn>(input, base + u * kBlock);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t i = base + u * kBlock;
+            float4 xn, o;
+            fwd_elem<A, TRAIN>(v[u], p, channel_of<false>(i << 2, g), xn, o);
+            st4<kNtX>(x, i, v[u]);
+            if constexpr (TRAIN) st4<kNtXn>(x_norm, i, xn);
+            st4<kNtOut>(output, i, o);
+        }
+    } else {
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t i = base + u * kBlock;
+            if (i < nv) {
+                const float4 v = ld4<kNtIn>(input, i);
+                float4 xn, o;
+                fwd_elem<A, TRAIN>(v, p, channel_of<false>(i << 2, g), xn, o);
+                st4<kNtX>(x, i, v);
+                if constexpr (TRAIN) st4<kNtXn>(x_norm, i, xn);
+                st4<kNtOut>(output, i, o);
+            }
+        }
+    }
+}
+
+// ---- backward -----------------------------------------------------------------
+
+// Per channel: s0 = sum(d1), s1 = sum(d1 * x_norm), s2 = sum(d2),
+// s3 = sum(d2 * (x - m)), where d1 = delta * gradient(y) (activations.zig:
+// 127-143) and d2 = d1 * scale (the scale_bias on delta, batchnorm.zig:165).
+struct BwdFin {
+    const float *variance;
+    float *bias_updates, *scale_updates, *mean_delta, *variance_delta;
+    __device__ void operator()(uint32_t f, const Sums<4> &r) const {
+        const float v = variance[f];
+        bias_updates[f] = bias_updates[f] + (float)r.s[0];             // blas.zig:79
+        scale_updates[f] = scale_updates[f] + (float)r.s[1];           // blas.zig:98
+        mean_delta[f] = (float)r.s[2] * (-1.0f / sqrtf(v + 1e-5f));    // blas.zig:155
+        variance_delta[f] = ((float)r.s[3] * -0.5f) * pow_m1p5(v + 1e-5f);  // blas.zig:176
+    }
+};
+
+template <int A>
+__device__ __forceinline__ float grad_delta(float d, float y) {
+    if constexpr (A == kLinear) return d;  // activations.zig:129: linear leaves delta alone
+    else return d * gradient<A>(y);
+}
+
+template <int A>
+__device__ __forceinline__ void acc_bwd(float4 y, float4 d, float4 xn, float4 x, float m, float gam,
+                                        double (&a)[4]) {
+    double t[4][4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const float d1 = grad_delta<A>(lane(d, l), lane(y, l));
+        const float d2 = d1 * gam;
+        t[0][l] = (double)d1;
+        t[1][l] = (double)(d1 * lane(xn, l));         // blas.zig:96
+        t[2][l] = (double)d2;
+        t[3][l] = (double)(d2 * (lane(x, l) - m));    // blas.zig:174
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] += (t[q][0] + t[q][1]) + (t[q][2] + t[q][3]);
+}
+
+// H: bit 0 = y, bit 1 = delta, bit 2 = x_norm, bit 3 = x loads.
+template <int A, int H, int BS, bool FIN>
+__global__ __launch_bounds__(BS) void bn_bwd_sums_kernel(const float *y, const float *delta, const float *x_norm,
+                                                         const float *x, const float *mean, const float *scales,
+                                                         RedGeom g, BwdFin fin, double *partials) {
+    constexpr bool kLin = A == kLinear;
+    __shared__ double lds[4 * (BS / kWave)];
+    uint32_t f, k;
+    red_coords(g, f, k);
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const float m = mean[f], gam = scales[f];
+    double a[4] = {0.0, 0.0, 0.0, 0.0};
+    constexpr int kU = 2;  // four streams: 2 float4s each in flight per lane
+    constexpr uint32_t kStep = 4 * BS;
+    uint32_t j = j0 + 4 * threadIdx.x;
+    for (; j + kStep * (kU - 1) < j1; j += kStep * kU) {
+        float4 vy[kU], vd[kU], vn[kU], vx[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const uint32_t i = chan_addr(fbase, j + u * kStep, g) >> 2;
+            vd[u] = ld4<(H & 2) != 0>(delta, i);
+            if constexpr (!kLin) vy[u] = ld4<(H & 1) != 0>(y, i);
+            else vy[u] = vd[u];
+            vn[u] = ld4<(H & 4) != 0>(x_norm, i);
+            vx[u] = ld4<(H & 8) != 0>(x, i);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) acc_bwd<A>(vy[u], vd[u], vn[u], vx[u], m, gam, a);
+    }
+    for (; j < j1; j += kStep) {
+        const uint32_t i = chan_addr(fbase, j, g) >> 2;
+        const float4 vd = ld4<(H & 2) != 0>(delta, i);
+        const float4 vy = kLin ? vd : ld4<(H & 1) != 0>(y, i);
+        acc_bwd<A>(vy, vd, ld4<(H & 4) != 0>(x_norm, i), ld4<(H & 8) != 0>(x, i), m, gam, a);
+    }
+    const Sums<4> r = block_sums<4, BS>(a, lds);
+    if constexpr (FIN) {
+        if (threadIdx.x == 0) fin(f, r);
+    } else {
+        store_partials<4, BS>(r, g, f, k, partials);
+    }
+}
+
+struct BwdParams {
+    const float *mean, *variance, *mean_delta, *variance_delta, *scales;
+    float denom;  // f32(spatial * batch), blas.zig:191
+};
+
+// delta = d2 * inv + ((vd * 2) * (x - m)) / N + md / N (blas.zig:180-204) on
+// d2 = delta * gradient(y) * scale.
+template <int A>
+__device__ __forceinline__ float4 bwd_elem(float4 y, float4 d, float4 x, const BwdParams &p, uint32_t f) {
+    const float m = p.mean[f];
+    const float inv = 1.0f / sqrtf(p.variance[f] + 1e-5f);
+    const float vd2 = p.variance_delta[f] * 2.0f;
+    const float mdn = p.mean_delta[f] / p.denom;
+    const float gam = p.scales[f];
+    float4 o;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const float d2 = grad_delta<A>(lane(d, l), lane(y, l)) * gam;
+        lane(o, l) = (d2 * inv + (vd2 * (lane(x, l) - m)) / p.denom) + mdn;
+    }
+    return o;
+}
+
+// H: bit 0 = y, bit 1 = delta, bit 2 = x loads, bit 3 = delta store.
+template <int A, int H, bool REV>
+__global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, float *delta, const float *x,
+                                                              BwdParams p, ChanGeom g, uint32_t nv) {
+    constexpr bool kLin = A == kLinear;
+    constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtX = (H & 4) != 0, kNtOut = (H & 8) != 0;
+    const uint32_t tile = REV ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+    const uint32_t base = tile * (kBlock * kUnroll) + threadIdx.x;
+    if (base + (kUnroll - 1) * kBlock < nv) {
+        float4 vy[kUnroll], vd[kUnroll], vx[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t i = base + u * kBlock;
+            vd[u] = ld4<kNtD>(delta, i);
+            if constexpr (!kLin) vy[u] = ld4<kNtY>(y, i);
+            else vy[u] = vd[u];
+            vx[u] = ld4<kNtX>(x, i);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t i = base + u * kBlock;
+            st4<kNtOut>(delta, i, bwd_elem<A>(vy[u], vd[u], vx[u], p, channel_of<false>(i << 2, g)));
+        }
+    } else {
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t i = base + u * kBlock;
+            if (i < nv) {
+                const float4 vd = ld4<kNtD>(delta, i);
+                const float4 vy = kLin ? vd : ld4<kNtY>(y, i);
+                const float4 vx = ld4<kNtX>(x, i);
+                st4<kNtOut>(delta, i, bwd_elem<A>(vy, vd, vx, p, channel_of<false>(i << 2, g)));
+            }
+        }
+    }
+}
+
+// ---- host ---------------------------------------------------------------------
+
+struct Shape {
+    uint32_t B, F, S, n;
+};
+
+struct FwdArgs {
+    Shape sh;
+    bool train;
+    const float *input;
+    float *output, *x, *x_norm, *mean, *variance, *rolling_mean, *rolling_variance;
+    const float *scales, *biases;
+};
+
+struct BwdArgs {
+    Shape sh;
+    const float *y;
+    float *delta;
+    const float *x, *x_norm, *mean, *variance, *scales;
+    float *bias_updates, *scale_updates, *mean_delta, *variance_delta;
+};
+
+// Launches a channel reduction pass (NS sums) through `kern_fin` (K == 1,
+// block BS) or `kern_part` + the finalize launch (K > 1).
+template <int NS, class Fin, class KFin1024, class KFin256, class KPart, class... Args>
+int run_sums(const char *name, uint32_t streams, const Shape &sh, const Fin &fin, KFin1024 kfin_wide,
+             KFin256 kfin, KPart kpart, Args... args) {
+    const uint32_t L = sh.B * sh.S;
+    const RedGeom g = make_red_geom(sh.F, sh.S, L, pick_split(sh.F, L, streams, NS), true);
+    if (g.K == 1) {
+        if (L >= 16 * kWideBlock)
+            return launch(name, kfin_wide, dim3(sh.F), dim3(kWideBlock), args..., g, fin, (double *)nullptr);
+        return launch(name, kfin, dim3(sh.F), dim3(kBlock), args..., g, fin, (double *)nullptr);
+    }
+    Scratch sc{nullptr};
+    DKZ_TRY(device_scratch(&sc));
+    DKZ_TRY(launch(name, kpart, dim3(sh.F * g.K), dim3(kBlock), args..., g, fin, sc.partials));
+    return launch(name, bn_finalize_kernel<NS, Fin>, dim3(div_up(sh.F, kBlock / kWave)), dim3(kBlock), fin,
+                  (const double *)sc.partials, sh.F, g.K);
+}
+
+constexpr bool kRev = DKZ_BN_APPLY_REVERSE != 0;
+
+template <int A>
+int bn_forward_fused(const FwdArgs &a) {
+    const Shape &sh = a.sh;
+    const ChanGeom cg{make_fastdiv(sh.S), make_fastdiv(sh.F)};
+    const uint32_t nv = sh.n >> 2;
+    const dim3 grid(div_up(nv, (uint64_t)kBlock * kUnroll)), block(kBlock);
+    if (!a.train) {
+        const FwdParams p{a.rolling_mean, a.rolling_variance, a.scales, a.biases};
+        return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, false, DKZ_HINT_BN_FWD_APPLY, kRev>, grid,
+                      block, a.input, a.output, a.x, a.x_norm, p, cg, nv);
+    }
+    const uint64_t L = (uint64_t)sh.B * sh.S;
+    const FwdFin fin{a.input, a.mean, a.variance, a.rolling_mean, a.rolling_variance, sh.S, (double)L,
+                     1.0f / (float)L, 1.0f / (float)(L - 1u)};
+    DKZ_TRY(run_sums<2>("batchnorm_forward_stats", 1, sh, fin, bn_stats_kernel<DKZ_HINT_BN_STATS, kWideBlock, true>,
+                        bn_stats_kernel<DKZ_HINT_BN_STATS, kBlock, true>,
+                        bn_stats_kernel<DKZ_HINT_BN_STATS, kBlock, false>, a.input));
+    const FwdParams p{a.mean, a.variance, a.scales, a.biases};
+    return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, true, DKZ_HINT_BN_FWD_APPLY, kRev>, grid, block,
+                  a.input, a.output, a.x, a.x_norm, p, cg, nv);
+}
+
+template <int A>
+int bn_backward_fused(const BwdArgs &a) {
+    const Shape &sh = a.sh;
+    const BwdFin fin{a.variance, a.bias_updates, a.scale_updates, a.mean_delta, a.variance_delta};
+    constexpr int H = DKZ_HINT_BN_BWD_SUMS;
+    DKZ_TRY(run_sums<4>("batchnorm_backward_sums", A == kLinear ? 3 : 4, sh, fin,
+                        bn_bwd_sums_kernel<A, H, kWideBlock, true>, bn_bwd_sums_kernel<A, H, kBlock, true>,
+                        bn_bwd_sums_kernel<A, H, kBlock, false>, a.y, (const float *)a.delta, a.x_norm, a.x,
+                        a.mean, a.scales));
+    const ChanGeom cg{make_fastdiv(sh.S), make_fastdiv(sh.F)};
+    const uint32_t nv = sh.n >> 2;
+    const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
+                      (float)((uint64_t)sh.S * (uint64_t)sh.B)};
+    return launch("batchnorm_backward_apply", bn_bwd_apply_kernel<A, DKZ_HINT_BN_BWD_APPLY, kRev>,
+                  dim3(div_up(nv, (uint64_t)kBlock * kUnroll)), dim3(kBlock), a.y, a.delta, a.x, p, cg, nv);
+}
+
+typedef int (*FwdFn)(const FwdArgs &);
+typedef int (*BwdFn)(const BwdArgs &);
+template <int... As>
+struct BnTables {
+    static constexpr FwdFn fwd[] = {bn_forward_fused<As>...};
+    static constexpr BwdFn bwd[] = {bn_backward_fused<As>...};
+};
+using Tables = BnTables<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13>;
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+extern "C" {
+
+int dkz_batchnorm_forward(int batch, int filters, int spatial, int activation, int train, const float *input,
+                          float *output, float *x, float *x_norm, float *mean, float *variance,
+                          float *rolling_mean, float *rolling_variance, const float *scales,
+                          const float *biases) {
+    DKZ_REQUIRE(batch >= 0 && filters >= 0 && spatial >= 0);
+    DKZ_REQUIRE(activation >= 0 && activation < kActCount);
+    const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
+    DKZ_REQUIRE(n64 <= kMaxElems);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(scales && biases && rolling_mean && rolling_variance);
+    DKZ_REQUIRE(!train || (mean && variance));
+    DKZ_REQUIRE(n64 == 0 || (input && output && x && (!train || x_norm)));
+    const int n = (int)n64;
+    const bool fast = n64 > 0 && spatial % 4 == 0 && aligned16(input) && aligned16(output) && aligned16(x) &&
+                      (!train || aligned16(x_norm));
+    if (fast) {
+        const FwdArgs a{{(uint32_t)batch, (uint32_t)filters, (uint32_t)spatial, (uint32_t)n},
+                        train != 0, input, output, x, x_norm, mean, variance, rolling_mean, rolling_variance,
+                        scales, biases};
+        return Tables::fwd[activation](a);
+    }
+    // The per-op sequence of batchnorm.zig:129-153 and convolutional.zig:269.
+    if (input != output) DKZ_TRY(dkz_copy(n, input, output));
+    DKZ_TRY(dkz_copy(n, output, x));
+    if (train) {
+        DKZ_TRY(dkz_mean(output, batch, filters, spatial, mean));
+        DKZ_TRY(dkz_variance(output, mean, batch, filters, spatial, variance));
+        DKZ_TRY(dkz_scal(filters, kMomentum, rolling_mean));
+        DKZ_TRY(dkz_axpy(filters, kAlpha, mean, rolling_mean));
+        DKZ_TRY(dkz_scal(filters, kMomentum, rolling_variance));
+        DKZ_TRY(dkz_axpy(filters, kAlpha, variance, rolling_variance));
+        DKZ_TRY(dkz_normalize(output, mean, variance, batch, filters, spatial));
+        DKZ_TRY(dkz_copy(n, output, x_norm));
+    } else {
+        DKZ_TRY(dkz_normalize(output, rolling_mean, rolling_variance, batch, filters, spatial));
+    }
+    DKZ_TRY(dkz_scale_bias(output, scales, batch, filters, spatial));
+    DKZ_TRY(dkz_add_bias(output, biases, batch, filters, spatial));
+    return dkz_activate_array(output, n, activation);
+}
+
+int dkz_batchnorm_backward(int batch, int filters, int spatial, int activation, const float *output,
+                           float *delta, const float *x, const float *x_norm, const float *mean,
+                           const float *variance, const float *scales, float *bias_updates,
+                           float *scale_updates, float *mean_delta, float *variance_delta) {
+    DKZ_REQUIRE(batch >= 0 && filters >= 0 && spatial >= 0);
+    DKZ_REQUIRE(activation >= 0 && activation < kActCount);
+    const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
+    DKZ_REQUIRE(n64 <= kMaxElems);
+    if (filters == 0) return 0;
+    DKZ_REQUIRE(mean && variance && scales && bias_updates && scale_updates && mean_delta && variance_delta);
+    DKZ_REQUIRE(n64 == 0 || (delta && x && x_norm && (activation == kLinear || output)));
+    const int n = (int)n64;
+    const bool fast = n64 > 0 && spatial % 4 == 0 && aligned16(delta) && aligned16(x) && aligned16(x_norm) &&
+                      (activation == kLinear || aligned16(output));
+    if (fast) {
+        const BwdArgs a{{(uint32_t)batch, (uint32_t)filters, (uint32_t)spatial, (uint32_t)n},
+                        output, delta, x, x_norm, mean, variance, scales,
+                        bias_updates, scale_updates, mean_delta, variance_delta};
+        return Tables::bwd[activation](a);
+    }
+    // convolutional.zig:280 and the per-op sequence of batchnorm.zig:155-174.
+    DKZ_TRY(dkz_gradient_array(output, n, activation, delta));
+    DKZ_TRY(dkz_backward_bias(bias_updates, delta, batch, filters, spatial));
+    DKZ_TRY(dkz_backward_scale(x_norm, delta, batch, filters, spatial, scale_updates));
+    DKZ_TRY(dkz_scale_bias(delta, scales, batch, filters, spatial));
+    DKZ_TRY(dkz_mean_delta(delta, variance, batch, filters, spatial, mean_delta));
+    DKZ_TRY(dkz_variance_delta(x, delta, mean, variance, batch, filters, spatial, variance_delta));
+    return dkz_normalize_delta(x, mean, variance, mean_delta, variance_delta, batch, filters, spatial, delta);
+}
+
+}  // extern "C"

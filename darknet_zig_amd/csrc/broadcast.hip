@@ -9,27 +9,13 @@
 // elementwise.hip; when spatial % 4 == 0 a float4 never straddles a row, so
 // its channel constants are looked up (and derived, e.g. normalize's
 // reciprocal) once per float4.
-#include "dkz_device.hpp"
+#include "dkz_channel.hpp"
 #include "dkz_hints.hpp"
-#include "dkz_internal.hpp"
 
 namespace dkz {
 namespace {
 
 constexpr int kUnroll = 4;
-
-struct ChanGeom {
-    FastDiv spatial;
-    FastDiv filters;
-};
-
-// ROWWISE: the constant is per row r (backward_avgpool), not per channel.
-template <bool ROWWISE>
-__device__ __forceinline__ uint32_t channel_of(uint32_t e, const ChanGeom &g) {
-    const uint32_t r = fdiv(e, g.spatial);
-    if constexpr (ROWWISE) return r;
-    else return r - fdiv(r, g.filters) * g.filters.d;
-}
 
 template <class Op, bool TWO, bool ROWWISE, bool S4>
 __device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io, float4 a,

@@ -263,6 +263,14 @@ __host__ __device__ __forceinline__ float expf_libm(float x) {
     return (float)(y * s);
 }
 
+// v^-1.5 as 1/(v*sqrt(v)) in f64, rounded once: the factor of variance_delta.
+// std.math.pow(f32, v, -1.5) (blas.zig:176) goes through f32 exp and log and
+// lands within a few ulps of it.
+__device__ __forceinline__ float pow_m1p5(float v) {
+    const double d = (double)v;
+    return (float)(1.0 / (d * sqrt(d)));
+}
+
 // ---------------------------------------------------------------------------
 // Activations (src/activations.zig:11-27 codes, 58-104 maths). Selects, not
 // multiplies, where the Zig code selects; literals are the f32 roundings of

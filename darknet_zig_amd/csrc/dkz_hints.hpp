@@ -97,3 +97,31 @@
 #ifndef DKZ_HINT_SHORTCUT
 #define DKZ_HINT_SHORTCUT 1
 #endif
+
+// batchnorm.hip, the fused layer passes. The statistics / sums pass and the
+// apply pass read the same tensors, so the first pass keeps its loads cached
+// (a layer at config sizes then finds much of it in the Infinity Cache) and
+// the apply pass, their last reader, streams them.
+// forward statistics: bit 0 = input load
+#ifndef DKZ_HINT_BN_STATS
+#define DKZ_HINT_BN_STATS 0
+#endif
+// forward apply: bit 0 = input load, bit 1 = x store, bit 2 = x_norm store,
+// bit 3 = output store (x and x_norm are next read by the backward pass; the
+// output by the next layer)
+#ifndef DKZ_HINT_BN_FWD_APPLY
+#define DKZ_HINT_BN_FWD_APPLY 7
+#endif
+// backward sums: bit 0 = y, bit 1 = delta, bit 2 = x_norm, bit 3 = x loads
+#ifndef DKZ_HINT_BN_BWD_SUMS
+#define DKZ_HINT_BN_BWD_SUMS 4
+#endif
+// backward apply: bit 0 = y, bit 1 = delta, bit 2 = x loads, bit 3 = delta store
+#ifndef DKZ_HINT_BN_BWD_APPLY
+#define DKZ_HINT_BN_BWD_APPLY 7
+#endif
+// Apply passes walk their tiles last-to-first, starting where the first pass
+// ended, i.e. on the lines most likely still in the Infinity Cache.
+#ifndef DKZ_BN_APPLY_REVERSE
+#define DKZ_BN_APPLY_REVERSE 1
+#endif

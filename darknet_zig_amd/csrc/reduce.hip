@@ -22,29 +22,13 @@
 //     CPU twin's sequential f32 sum is that sum's own rounding error.
 //   * The finalisation repeats blas.zig's f32 arithmetic on the f32-rounded
 //     total: sum * (1/(B*S)), sum * (-1/sqrt(v+1e-5)), updates[f] += sum, ...
-#include "dkz_device.hpp"
+#include "dkz_channel.hpp"
 #include "dkz_hints.hpp"
-#include "dkz_internal.hpp"
 
 namespace dkz {
 namespace {
 
 constexpr int kUnroll = 4;
-
-struct RedGeom {
-    uint32_t spatial;
-    uint32_t chan_len;   // batch * spatial
-    uint32_t chunk;      // elements per workgroup (multiple of 4 on the float4 path)
-    uint32_t K;          // workgroups per channel
-    uint32_t row_extra;  // (filters - 1) * spatial
-    FastDiv div_k;
-    FastDiv div_spatial;
-};
-
-// Element j of channel f lives at ((b*F + f)*S + s) = f*S + j + b*(F-1)*S.
-__device__ __forceinline__ uint32_t chan_addr(uint32_t fbase, uint32_t j, const RedGeom &g) {
-    return fbase + j + fdiv(j, g.div_spatial) * g.row_extra;
-}
 
 template <class Term>
 __device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
@@ -126,27 +110,6 @@ __global__ __launch_bounds__(kBlock) void chan_finalize_kernel(Fin fin, const do
     if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s);
 }
 
-// How a channel reduction is split, from the shape only. A workgroup streams
-// at most ~43 GB/s, so one 1024-thread workgroup per channel reaches
-// ~5.5 TB/s with 128 channels and ~6.4 TB/s with 256; splitting each channel
-// over ~2048 workgroups reaches ~6.4 TB/s but costs a second (finalize)
-// launch of ~4 us. Hence:
-//  * filters >= 256, or filters >= 128 with at most 160 MB to read: one
-//    workgroup per channel and one launch (1024 threads for long channels);
-//  * otherwise about 2048 workgroups of >= 4096 elements, then the finalize
-//    launch (within the scratch's capacity).
-constexpr uint32_t kWideBlock = 1024;
-
-uint32_t pick_split(uint32_t filters, uint32_t chan_len, uint32_t streams) {
-    const uint64_t bytes = (uint64_t)4 * streams * filters * chan_len;
-    if (filters >= 256 || (filters >= 128 && bytes <= 160000000ull)) return 1;
-    uint32_t k = div_up(2048, filters);
-    const uint32_t kmax = chan_len / 4096 > 1 ? chan_len / 4096 : 1;
-    if (k > kmax) k = kmax;
-    while (k > 1 && (uint64_t)filters * k > kScratchPartials) --k;
-    return k < 1 ? 1 : k;
-}
-
 template <int H, class T, class Fin, bool TWO>
 int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p0, const float *p1,
                     int batch, int filters, int spatial) {
@@ -154,11 +117,8 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     DKZ_REQUIRE(chan_len64 * (uint64_t)filters <= kMaxElems);
     const uint32_t F = (uint32_t)filters, S = (uint32_t)spatial, L = (uint32_t)chan_len64;
     const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
-    uint32_t K = pick_split(F, L, TWO ? 2 : 1);
-    uint32_t chunk = L == 0 ? 0 : div_up(L, K);
-    if (vec) chunk = (chunk + 3) & ~3u;
-    K = chunk > 0 ? div_up(L, chunk) : 1;
-    const RedGeom g{S, L, chunk, K, (F - 1) * S, make_fastdiv(K), make_fastdiv(S == 0 ? 1 : S)};
+    const RedGeom g = make_red_geom(F, S, L, pick_split(F, L, TWO ? 2 : 1), vec);
+    const uint32_t K = g.K;
     if (K == 1) {
         if (L >= 16 * kWideBlock) {
             const dim3 block(kWideBlock);
@@ -231,12 +191,6 @@ struct FinMeanDelta {  // blas.zig:155
         out[f] = (float)s * (-1.0f / sqrtf(variance[f] + 1e-5f));
     }
 };
-// v^-1.5 as 1/(v*sqrt(v)) in f64, rounded once. std.math.pow(f32, v, -1.5)
-// (blas.zig:176) goes through f32 exp and log and lands within a few ulps.
-__device__ __forceinline__ float pow_m1p5(float v) {
-    const double d = (double)v;
-    return (float)(1.0 / (d * sqrt(d)));
-}
 struct FinVarianceDelta {  // blas.zig:176: (sum * -0.5) * pow(v + 1e-5, -1.5)
     float *out;
     const float *variance;

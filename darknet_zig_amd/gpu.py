@@ -343,3 +343,60 @@ def shortcut(
     batch: int, w1: int, h1: int, c1: int, add: Buf, w2: int, h2: int, c2: int, s1: float, s2: float, out: Buf
 ) -> None:
     _must(_lib.load().dkz_shortcut(batch, w1, h1, c1, _p(add), w2, h2, c2, s1, s2, _p(out)), "shortcut")
+
+
+# ---- fused batch-norm layer passes (no single gpu.zig counterpart: each
+# replaces the call sequence of layers/batchnorm.zig forwardGpu / backwardGpu
+# together with the activation calls of convolutional.zig:269 and :280) ----
+
+
+def batchnormForward(
+    batch: int,
+    filters: int,
+    spatial: int,
+    activation: int,
+    train: bool,
+    input: Buf,
+    output: Buf,
+    x: Buf,
+    x_norm: Buf | None,
+    mean: Buf | None,
+    variance: Buf | None,
+    rolling_mean: Buf,
+    rolling_variance: Buf,
+    scales: Buf,
+    biases: Buf,
+) -> None:
+    _must(
+        _lib.load().dkz_batchnorm_forward(
+            batch, filters, spatial, int(activation), 1 if train else 0, _p(input), _p(output), _p(x),
+            _p(x_norm), _p(mean), _p(variance), _p(rolling_mean), _p(rolling_variance), _p(scales), _p(biases),
+        ),
+        "batchnorm_forward",
+    )
+
+
+def batchnormBackward(
+    batch: int,
+    filters: int,
+    spatial: int,
+    activation: int,
+    output: Buf | None,
+    delta: Buf,
+    x: Buf,
+    x_norm: Buf,
+    mean: Buf,
+    variance: Buf,
+    scales: Buf,
+    bias_updates: Buf,
+    scale_updates: Buf,
+    mean_delta: Buf,
+    variance_delta: Buf,
+) -> None:
+    _must(
+        _lib.load().dkz_batchnorm_backward(
+            batch, filters, spatial, int(activation), _p(output), _p(delta), _p(x), _p(x_norm), _p(mean),
+            _p(variance), _p(scales), _p(bias_updates), _p(scale_updates), _p(mean_delta), _p(variance_delta),
+        ),
+        "batchnorm_backward",
+    )

@@ -265,6 +265,48 @@ int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const floa
 int dkz_shortcut(int batch, int w1, int h1, int c1, const float *add, int w2, int h2, int c2,
                  float s1, float s2, float *out);
 
+/* ---- fused batch-norm layer passes ------------------------------------------
+ * Each replaces a sequence of the calls above that the layers issue; the
+ * per-op entry points stay. Results equal the sequence's: every element
+ * expression is the same op's, in the same order, given the same per-channel
+ * values; the per-channel sums are the channel reductions' (within 1e-5 of
+ * the CPU twin, or closer to the exact value). Shapes with spatial % 4 != 0,
+ * empty tensors or tensors not 16-byte aligned run the per-op sequence. */
+
+/* Forward of a batch-normalised layer and its activation: the sequence of
+ * layers/batchnorm.zig:129-153 (forwardGpu) followed by
+ * convolutional.zig:269 (activateArray(output, n, activation)), for a tensor
+ * of batch*filters*spatial floats.
+ *   input != output: output = input first (the standalone batchnorm layer,
+ *   batchnorm.zig:133); input == output: in place (a convolutional layer).
+ *   x = the input (batchnorm.zig:134).
+ *   train: mean, variance of the input per channel (blas.zig:106-135);
+ *     rolling_mean = rolling_mean*0.99 + 0.01*mean, likewise rolling_variance
+ *     (scal, then axpy: batchnorm.zig:140-143);
+ *     x_norm = (input - mean) * (1/(sqrt(variance) + 1e-6)) (blas.zig:137-146);
+ *   not train: normalised with rolling_mean / rolling_variance; mean,
+ *     variance and x_norm are not touched (may be NULL).
+ *   output = act(x_norm * scales + biases)   (blas.zig:53-71, activations.zig)
+ * The statistics are one pass over the input: f64 sums of (x - c) and
+ * (x - c)^2 about the channel's first element c. */
+int dkz_batchnorm_forward(int batch, int filters, int spatial, int activation, int train,
+                          const float *input, float *output, float *x, float *x_norm, float *mean,
+                          float *variance, float *rolling_mean, float *rolling_variance,
+                          const float *scales, const float *biases);
+
+/* Backward of a batch-normalised layer and its activation: convolutional.zig:280
+ * (gradientArray(output, n, activation, delta)) followed by
+ * layers/batchnorm.zig:155-174 (backwardGpu): backward_bias, backward_scale,
+ * scale_bias(delta), mean_delta, variance_delta, normalize_delta. mean and
+ * variance are the statistics the forward normalised with (the batch ones
+ * when training, the rolling ones otherwise, batchnorm.zig:159-160).
+ * bias_updates and scale_updates accumulate; mean_delta, variance_delta and
+ * delta are overwritten. output may be NULL when activation is linear. */
+int dkz_batchnorm_backward(int batch, int filters, int spatial, int activation, const float *output,
+                           float *delta, const float *x, const float *x_norm, const float *mean,
+                           const float *variance, const float *scales, float *bias_updates,
+                           float *scale_updates, float *mean_delta, float *variance_delta);
+
 #ifdef __cplusplus
 }
 #endif

@@ -234,3 +234,50 @@ def pow_f32(x: float, y: float) -> float:
 
 def expf(x: float) -> float:
     return lib().ref_expf(x)
+
+
+# ---- layers/batchnorm.zig: the layer sequences over the twins above ---------
+
+ROLLING_MOMENTUM = np.float32(0.99)  # batchnorm.zig:16, an f32 constant
+EMA_ALPHA = np.float32(1) - ROLLING_MOMENTUM  # batchnorm.zig:87: 1 - rolling_momentum, in f32
+
+
+def batchnormForward(batch, filters, spatial, activation, train, input, output, x, x_norm, mean_out, variance_out,
+                     rolling_mean, rolling_variance, scales, biases) -> None:
+    """layers/batchnorm.zig:74-99 (forward, CPU), then the activation the
+    convolutional layer applies to its output (convolutional.zig:173).
+    input is copied to output first unless it is the same array (the
+    standalone batchnorm layer, batchnorm.zig:78)."""
+    n = batch * filters * spatial
+    if input is not output:
+        copy(input[:n], output[:n])
+    copy(output[:n], x[:n])
+    if train:
+        mean(output[:n], batch, filters, spatial, mean_out)
+        variance(output[:n], mean_out, batch, filters, spatial, variance_out)
+        scal(ROLLING_MOMENTUM, rolling_mean)
+        axpy(EMA_ALPHA, mean_out, rolling_mean)
+        scal(ROLLING_MOMENTUM, rolling_variance)
+        axpy(EMA_ALPHA, variance_out, rolling_variance)
+        normalize(output[:n], mean_out, variance_out, batch, filters, spatial)
+        copy(output[:n], x_norm[:n])
+    else:
+        normalize(output[:n], rolling_mean, rolling_variance, batch, filters, spatial)
+    scaleBias(output[:n], scales, batch, filters, spatial)
+    addBias(output[:n], biases, batch, filters, spatial)
+    activateArray(output[:n], activation)
+
+
+def batchnormBackward(batch, filters, spatial, activation, output, delta, x, x_norm, mean_in, variance_in, scales,
+                      bias_updates, scale_updates, mean_delta_out, variance_delta_out) -> None:
+    """The activation gradient of convolutional.zig:184, then
+    layers/batchnorm.zig:101-123 (backward, CPU). mean_in / variance_in are
+    the statistics the forward normalised with (batchnorm.zig:108-109)."""
+    n = batch * filters * spatial
+    gradientArray(output[:n], activation, delta[:n])
+    backwardBias(bias_updates, delta[:n], batch, filters, spatial)
+    backwardScale(x_norm[:n], delta[:n], batch, filters, spatial, scale_updates)
+    scaleBias(delta[:n], scales, batch, filters, spatial)
+    meanDelta(delta[:n], variance_in, batch, filters, spatial, mean_delta_out)
+    varianceDelta(x[:n], delta[:n], mean_in, variance_in, batch, filters, spatial, variance_delta_out)
+    normalizeDelta(x[:n], mean_in, variance_in, mean_delta_out, variance_delta_out, batch, filters, spatial, delta[:n])

@@ -45,7 +45,7 @@ def exported_symbols() -> set[str]:
 
 def test_header_exports_and_binding_agree():
     declared = header_symbols()
-    assert len(declared) == len(set(declared)) == 44
+    assert len(declared) == len(set(declared)) == 46
     assert set(declared) == exported_symbols()
     assert list(_lib.SIGNATURES) == declared  # same set, same order as the header
 
@@ -113,6 +113,16 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_backward_avgpool(6, 7, 7, 3, None, P), INVALID),
         (lambda L: L.dkz_shortcut(2, 8, 8, 0, None, 8, 8, 4, 1.0, 1.0, None), 0),  # min channels 0
         (lambda L: L.dkz_shortcut(2, 8, 8, 4, None, 8, 8, 4, 1.0, 1.0, P), INVALID),
+        (lambda L: L.dkz_batchnorm_forward(2, 3, 4, 14, 1, P, P, P, P, P, P, P, P, P, P), INVALID),
+        (lambda L: L.dkz_batchnorm_forward(2, -3, 4, 7, 1, P, P, P, P, P, P, P, P, P, P), INVALID),
+        (lambda L: L.dkz_batchnorm_forward(2, 0, 4, 7, 1, *[None] * 10), 0),  # filters 0: nothing to do
+        (lambda L: L.dkz_batchnorm_forward(2, 3, 4, 7, 1, P, P, P, None, P, P, P, P, P, P), INVALID),  # x_norm
+        (lambda L: L.dkz_batchnorm_forward(2, 3, 4, 7, 0, P, P, P, P, P, P, None, P, P, P), INVALID),  # rolling
+        (lambda L: L.dkz_batchnorm_forward(65536, 65536, 4, 7, 1, P, P, P, P, P, P, P, P, P, P), INVALID),
+        (lambda L: L.dkz_batchnorm_backward(2, 3, 4, -1, P, P, P, P, P, P, P, P, P, P, P), INVALID),
+        (lambda L: L.dkz_batchnorm_backward(2, 3, 4, 7, None, P, P, P, P, P, P, P, P, P, P), INVALID),  # y
+        (lambda L: L.dkz_batchnorm_backward(2, 3, 4, 7, P, P, P, P, P, P, P, P, P, None, P), INVALID),
+        (lambda L: L.dkz_batchnorm_backward(0, 0, 4, 7, *[None] * 11), 0),
         (lambda L: L.dkz_malloc(None, 4), INVALID),
         (lambda L: L.dkz_free(None), 0),
         (lambda L: L.dkz_copy_to_host(None, None, 0), 0),

@@ -1,0 +1,287 @@
+"""GPU parity of the fused batch-norm layer entry points
+(dkz_batchnorm_forward / dkz_batchnorm_backward) against the CPU twins run
+as the layer runs them (oracle.ref.batchnormForward / batchnormBackward:
+layers/batchnorm.zig:74-123 with the activation calls of
+convolutional.zig:173 and :184).
+
+The per-channel values (mean, variance, the bias/scale updates, mean_delta,
+variance_delta) are reductions and follow the 1e-5 rule of tests/helpers.py
+against f64 evaluations. Every element result is then held to bit-exactness
+against the twins fed the GPU's own per-channel values: the fused passes
+must repeat the per-op element arithmetic exactly. Shapes cover the fused
+fast path (spatial % 4 == 0) with split (K > 1) and one-workgroup-per-channel
+reductions, and the per-op fallback (spatial % 4 != 0, spatial == 1).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from darknet_zig_amd import gpu
+from darknet_zig_amd.activations import Activation
+from oracle import ref
+from tests.helpers import assert_bitexact, assert_r5, down, normal, rng, uniform, up
+
+pytestmark = pytest.mark.gpu
+
+FAST = [
+    (4, 17, 52),      # split reduction, small
+    (5, 33, 196),
+    (3, 128, 64),     # filters 128, few bytes: one 256-thread workgroup per channel
+    (4, 256, 4096),   # filters 256, long channels: one 1024-thread workgroup per channel
+    (2, 8, 20000),    # few channels, long: split with a ragged last chunk
+    (128, 32, 1024),
+]
+FALLBACK = [
+    (4, 17, 53),      # gputest's shape: spatial % 4 != 0
+    (3, 5, 7),
+    (6, 10, 1),       # spatial 1 (a connected layer)
+]
+CONFIG2 = (64, 128, 3136)
+
+
+def _chan64(a, shape):
+    B, F, S = shape
+    return a.astype(np.float64).reshape(B, F, S)
+
+
+def _free(*bufs):
+    for b in bufs:
+        gpu.free(b)
+
+
+def _forward_case(shape, act, train, inplace, seed):
+    B, F, S = shape
+    n = B * F * S
+    r = rng(seed)
+    inp = normal(r, n, 0.25, 1.0)
+    scales, biases = uniform(r, F, 0.5, 1.5), normal(r, F, 0, 0.1)
+    rm0, rv0 = normal(r, F, 0, 0.1), uniform(r, F, 0.5, 1.5)
+    sentinel = np.full(F, 7.0, np.float32)
+
+    d_in = up(inp)
+    d_out = d_in if inplace else gpu.alloc(n)
+    d_x, d_xn = gpu.alloc(n), up(np.full(n, 3.0, np.float32))
+    d_m, d_v, d_rm, d_rv = up(sentinel), up(sentinel), up(rm0), up(rv0)
+    d_s, d_b = up(scales), up(biases)
+    gpu.batchnormForward(B, F, S, act, train, d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    out, x, xn = down(d_out, inp), down(d_x, inp), down(d_xn, inp)
+    g_m, g_v, g_rm, g_rv = down(d_m, sentinel), down(d_v, sentinel), down(d_rm, rm0), down(d_rv, rv0)
+    _free(d_in, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b, *([] if inplace else [d_out]))
+
+    assert_bitexact(x, inp, f"x {shape}")
+    if train:
+        # the twins' statistics, and f64 evaluations of the same formulas
+        c_m, c_v = np.empty(F, np.float32), np.empty(F, np.float32)
+        ref.mean(inp, B, F, S, c_m)
+        ref.variance(inp, c_m, B, F, S, c_v)
+        x64 = _chan64(inp, shape)
+        assert_r5(g_m, c_m, x64.sum(axis=(0, 2)) * np.float64(np.float32(1) / np.float32(B * S)), f"mean {shape}")
+        if B * S > 1:
+            dev64 = ((x64 - c_m.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2))
+            assert_r5(g_v, c_v, dev64 * np.float64(np.float32(1) / np.float32(B * S - 1)), f"variance {shape}")
+        # the rolling averages from the GPU statistics: scal then axpy, bit-exact
+        want_rm, want_rv = rm0.copy(), rv0.copy()
+        ref.scal(ref.ROLLING_MOMENTUM, want_rm)
+        ref.axpy(ref.EMA_ALPHA, g_m, want_rm)
+        ref.scal(ref.ROLLING_MOMENTUM, want_rv)
+        ref.axpy(ref.EMA_ALPHA, g_v, want_rv)
+        assert_bitexact(g_rm, want_rm, f"rolling_mean {shape}")
+        assert_bitexact(g_rv, want_rv, f"rolling_variance {shape}")
+        stat_m, stat_v = g_m, g_v
+    else:
+        assert_bitexact(g_m, sentinel, "mean untouched in inference")
+        assert_bitexact(g_v, sentinel, "variance untouched in inference")
+        assert_bitexact(g_rm, rm0, "rolling_mean untouched in inference")
+        assert_bitexact(g_rv, rv0, "rolling_variance untouched in inference")
+        stat_m, stat_v = rm0, rv0
+    # element results: the twins on the statistics the GPU normalised with
+    want = inp.copy()
+    ref.normalize(want, stat_m, stat_v, B, F, S)
+    if train:
+        assert_bitexact(xn, want, f"x_norm {shape} act={act}")
+    else:
+        assert_bitexact(xn, np.full(n, 3.0, np.float32), "x_norm untouched in inference")
+    ref.scaleBias(want, scales, B, F, S)
+    ref.addBias(want, biases, B, F, S)
+    ref.activateArray(want, act)
+    assert_bitexact(out, want, f"output {shape} act={act}")
+    return stat_m, stat_v
+
+
+@pytest.mark.parametrize("shape", FAST + FALLBACK, ids=str)
+def test_forward_train(dev, shape):
+    _forward_case(shape, Activation.leaky, True, inplace=True, seed=sum(shape))
+
+
+@pytest.mark.parametrize("shape", [(4, 17, 52), (4, 17, 53)], ids=str)
+def test_forward_standalone_layer_copies_input(dev, shape):
+    """input != output: the standalone batchnorm layer (batchnorm.zig:78)."""
+    _forward_case(shape, Activation.linear, True, inplace=False, seed=11)
+
+
+@pytest.mark.parametrize("shape", [(4, 17, 52), (4, 17, 53), (128, 32, 1024)], ids=str)
+def test_forward_inference(dev, shape):
+    _forward_case(shape, Activation.leaky, False, inplace=True, seed=12)
+
+
+@pytest.mark.parametrize("act", list(Activation), ids=lambda a: a.name)
+def test_forward_every_activation(dev, act):
+    _forward_case((4, 12, 64), act, True, inplace=True, seed=100 + int(act))
+
+
+def test_forward_matches_oracle_layer_sequence(dev):
+    """The whole oracle layer sequence at config 1, compared end to end: the
+    statistics by the 1e-5 rule, everything downstream of them to 1e-4
+    (they carry the statistics' last-bit differences)."""
+    B, F, S = 128, 32, 1024
+    n = B * F * S
+    r = rng(21)
+    inp = normal(r, n)
+    scales, biases = uniform(r, F, 0.5, 1.5), normal(r, F, 0, 0.1)
+    rm0, rv0 = normal(r, F, 0, 0.1), uniform(r, F, 0.5, 1.5)
+    c_out, c_x, c_xn = inp.copy(), np.empty(n, np.float32), np.empty(n, np.float32)
+    c_m, c_v, c_rm, c_rv = np.empty(F, np.float32), np.empty(F, np.float32), rm0.copy(), rv0.copy()
+    ref.batchnormForward(B, F, S, Activation.leaky, True, c_out, c_out, c_x, c_xn, c_m, c_v, c_rm, c_rv, scales,
+                         biases)
+    d_io, d_x, d_xn = up(inp), gpu.alloc(n), gpu.alloc(n)
+    d_m, d_v, d_rm, d_rv, d_s, d_b = gpu.alloc(F), gpu.alloc(F), up(rm0), up(rv0), up(scales), up(biases)
+    gpu.batchnormForward(B, F, S, Activation.leaky, True, d_io, d_io, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    np.testing.assert_allclose(down(d_io, inp), c_out, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(down(d_xn, inp), c_xn, rtol=1e-4, atol=1e-5)
+    assert_bitexact(down(d_x, inp), c_x, "x")
+    np.testing.assert_allclose(down(d_rm, rm0), c_rm, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(down(d_rv, rv0), c_rv, rtol=1e-5, atol=1e-7)
+    _free(d_io, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+
+
+def _backward_case(shape, act, seed, with_y=True):
+    B, F, S = shape
+    n = B * F * S
+    r = rng(seed)
+    y, delta, x = normal(r, n), normal(r, n), normal(r, n, 0.2, 1.0)
+    ref.activateArray(y, act)  # y is an activation output, as gradient() expects
+    scales = uniform(r, F, 0.5, 1.5)
+    m, v = np.empty(F, np.float32), np.empty(F, np.float32)
+    ref.mean(x, B, F, S, m)
+    ref.variance(x, m, B, F, S, v)
+    x_norm = x.copy()
+    ref.normalize(x_norm, m, v, B, F, S)
+    bu0, su0 = normal(r, F, 0, 1), normal(r, F, 0, 1)
+
+    # the twins' layer sequence
+    c_d, c_bu, c_su = delta.copy(), bu0.copy(), su0.copy()
+    c_md, c_vd = np.empty(F, np.float32), np.empty(F, np.float32)
+    ref.batchnormBackward(B, F, S, act, y, c_d, x, x_norm, m, v, scales, c_bu, c_su, c_md, c_vd)
+
+    d_y = up(y) if with_y else gpu.Buf()
+    d_d, d_x, d_xn, d_m, d_v, d_s = up(delta), up(x), up(x_norm), up(m), up(v), up(scales)
+    d_bu, d_su, d_md, d_vd = up(bu0), up(su0), gpu.alloc(F), gpu.alloc(F)
+    gpu.batchnormBackward(B, F, S, act, d_y, d_d, d_x, d_xn, d_m, d_v, d_s, d_bu, d_su, d_md, d_vd)
+    g_d, g_bu, g_su = down(d_d, delta), down(d_bu, bu0), down(d_su, su0)
+    g_md, g_vd = down(d_md, c_md), down(d_vd, c_vd)
+    _free(*[b for b in (d_y, d_d, d_x, d_xn, d_m, d_v, d_s, d_bu, d_su, d_md, d_vd) if not b.is_null()])
+
+    # f64 evaluations on the (bit-exact) per-element terms
+    d1 = delta.copy()
+    ref.gradientArray(y, act, d1)
+    d2 = d1.copy()
+    ref.scaleBias(d2, scales, B, F, S)
+    d1_64, d2_64 = _chan64(d1, shape), _chan64(d2, shape)
+    prod = _chan64(d1 * x_norm, shape)  # f32 products, as blas.zig:96 rounds them
+    dev = _chan64(d2 * (x - np.repeat(np.tile(m, B), S)), shape)  # blas.zig:174
+    assert_r5(g_bu, c_bu, bu0.astype(np.float64) + d1_64.sum(axis=(0, 2)), f"bias_updates {shape} {act.name}")
+    assert_r5(g_su, c_su, su0.astype(np.float64) + prod.sum(axis=(0, 2)), f"scale_updates {shape} {act.name}")
+    fac = (np.float32(-1.0) / np.sqrt(v + np.float32(1e-5))).astype(np.float64)
+    assert_r5(g_md, c_md, d2_64.sum(axis=(0, 2)) * fac, f"mean_delta {shape} {act.name}")
+    v64 = (v + np.float32(1e-5)).astype(np.float64)
+    assert_r5(g_vd, c_vd, dev.sum(axis=(0, 2)) * -0.5 * v64**-1.5, f"variance_delta {shape} {act.name}")
+    # delta: normalize_delta of the twin's d2 with the GPU's mean_delta / variance_delta
+    want = d2.copy()
+    ref.normalizeDelta(x, m, v, g_md, g_vd, B, F, S, want)
+    assert_bitexact(g_d, want, f"delta {shape} {act.name}")
+    return g_d, c_d
+
+
+@pytest.mark.parametrize("shape", FAST + FALLBACK + [CONFIG2], ids=str)
+def test_backward(dev, shape):
+    g_d, c_d = _backward_case(shape, Activation.leaky, seed=40 + sum(shape))
+    np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("act", list(Activation), ids=lambda a: a.name)
+def test_backward_every_activation(dev, act):
+    _backward_case((4, 12, 64), act, seed=200 + int(act))
+
+
+def test_backward_linear_needs_no_output(dev):
+    _backward_case((4, 12, 64), Activation.linear, seed=300, with_y=False)
+    _backward_case((4, 12, 63), Activation.linear, seed=301, with_y=False)
+
+
+def test_fused_deterministic(dev):
+    """Repeated calls on the same inputs give the same bits (fixed split and
+    summation order), at config 2 for the backward and config 1 forward."""
+    B, F, S = CONFIG2
+    n = B * F * S
+    r = rng(5)
+    y, delta, x, xn = normal(r, n), normal(r, n), normal(r, n), normal(r, n)
+    m, v, s = normal(r, F, 0, 0.1), uniform(r, F, 0.5, 1.5), uniform(r, F, 0.5, 1.5)
+    d_y, d_x, d_xn, d_m, d_v, d_s = up(y), up(x), up(xn), up(m), up(v), up(s)
+    d_d = gpu.alloc(n)
+    outs = [gpu.alloc(F) for _ in range(4)]
+    first = None
+    for _ in range(10):
+        gpu.push(d_d, delta)
+        for o in outs[:2]:
+            gpu.fill(o, F, 0.0)
+        gpu.batchnormBackward(B, F, S, Activation.leaky, d_y, d_d, d_x, d_xn, d_m, d_v, d_s, *outs)
+        got = [down(o, m) for o in outs] + [down(d_d, delta)]
+        if first is None:
+            first = got
+        else:
+            for i, (a, b) in enumerate(zip(got, first)):
+                assert_bitexact(a, b, f"backward repeat output {i}")
+    _free(d_y, d_x, d_xn, d_m, d_v, d_s, d_d, *outs)
+
+    B, F, S = 128, 32, 1024
+    n = B * F * S
+    inp = normal(r, n)
+    d_in, d_out, d_x, d_xn = up(inp), gpu.alloc(n), gpu.alloc(n), gpu.alloc(n)
+    d_s, d_b = up(uniform(r, F, 0.5, 1.5)), up(normal(r, F, 0, 0.1))
+    stats = [gpu.alloc(F) for _ in range(4)]
+    first = None
+    for _ in range(10):
+        gpu.fill(stats[2], F, 0.0)
+        gpu.fill(stats[3], F, 1.0)
+        gpu.batchnormForward(B, F, S, Activation.leaky, True, d_in, d_out, d_x, d_xn, *stats, d_s, d_b)
+        got = [down(b, np.empty(F, np.float32)) for b in stats] + [down(d_out, inp)]
+        if first is None:
+            first = got
+        else:
+            for i, (a, b) in enumerate(zip(got, first)):
+                assert_bitexact(a, b, f"forward repeat output {i}")
+    _free(d_in, d_out, d_x, d_xn, d_s, d_b, *stats)
+
+
+def test_empty_batch_follows_the_sequence(dev):
+    """batch == 0 takes the per-op sequence: mean = 0 * (1/0) = NaN, variance
+    0, the rolling averages move toward them (blas.zig:106-135); the backward
+    adds nothing to the updates (blas.zig:73-82)."""
+    F = 3
+    d_m, d_v, d_rm, d_rv = gpu.alloc(F), gpu.alloc(F), up(np.ones(F, np.float32)), up(np.ones(F, np.float32))
+    d_s, d_b = up(np.ones(F, np.float32)), up(np.zeros(F, np.float32))
+    e = gpu.Buf()
+    gpu.batchnormForward(0, F, 16, Activation.leaky, True, e, e, e, e, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    assert np.isnan(down(d_m, np.empty(F, np.float32))).all()
+    assert_bitexact(down(d_v, np.empty(F, np.float32)), np.zeros(F, np.float32), "variance of nothing")
+    c_rv = np.ones(F, np.float32)
+    ref.scal(ref.ROLLING_MOMENTUM, c_rv)
+    ref.axpy(ref.EMA_ALPHA, np.zeros(F, np.float32), c_rv)
+    assert_bitexact(down(d_rv, c_rv), c_rv, "rolling_variance toward 0")
+    d_bu = up(np.full(F, 2.0, np.float32))
+    d_md, d_vd = gpu.alloc(F), gpu.alloc(F)
+    gpu.batchnormBackward(0, F, 16, Activation.leaky, e, e, e, e, d_m, d_v, d_s, d_bu, d_b, d_md, d_vd)
+    assert_bitexact(down(d_bu, np.empty(F, np.float32)), np.full(F, 2.0, np.float32), "no batch, no update")
+    _free(d_m, d_v, d_rm, d_rv, d_s, d_b, d_bu, d_md, d_vd)
