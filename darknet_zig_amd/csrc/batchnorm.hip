@@ -50,12 +50,43 @@ struct Sums {
     double s[NS];
 };
 
-// Workgroup of a reduction pass: chunk k of channel f. Consecutive
+// Workgroup of a reduction pass: chunk k of channel f. KMAJOR: consecutive
 // workgroups take the same chunk of consecutive channels, so the grid
-// sweeps the tensor roughly in address order.
+// sweeps the tensor roughly in address order; otherwise consecutive chunks
+// of one channel.
+// Launch shape of the reduction passes, measured on MI355X (config 2
+// backward, config 1 forward):
+//  * the backward sums grid is chunk-major (workgroup i takes chunk i / F of
+//    channel i % F): 138 us against 147 us channel-major; the forward
+//    statistics grid is channel-major: 23.6 us against 25.2 us;
+//  * about 8192 workgroups of >= 4096 elements (partials permitting): 138 us
+//    against 142 us with 2048 (a smoother tail);
+//  * two float4s of each of the four streams in flight per lane (1 or 4:
+//    no difference).
+#ifndef DKZ_BN_KMAJOR
+#define DKZ_BN_KMAJOR 1
+#endif
+#ifndef DKZ_BN_STATS_KMAJOR
+#define DKZ_BN_STATS_KMAJOR 0
+#endif
+#ifndef DKZ_BN_SUMS_UNROLL
+#define DKZ_BN_SUMS_UNROLL 2
+#endif
+#ifndef DKZ_BN_SPLIT_TARGET
+#define DKZ_BN_SPLIT_TARGET 8192
+#endif
+#ifndef DKZ_BN_MIN_CHUNK
+#define DKZ_BN_MIN_CHUNK 4096
+#endif
+template <bool KMAJOR>
 __device__ __forceinline__ void red_coords(const RedGeom &g, uint32_t &f, uint32_t &k) {
-    k = fdiv(blockIdx.x, g.div_filters);
-    f = blockIdx.x - k * g.div_filters.d;
+    if constexpr (KMAJOR) {
+        k = fdiv(blockIdx.x, g.div_filters);
+        f = blockIdx.x - k * g.div_filters.d;
+    } else {
+        f = fdiv(blockIdx.x, g.div_k);
+        k = blockIdx.x - f * g.K;
+    }
 }
 
 // NS sums over a BS-thread workgroup; the result is valid in wave 0. Each
@@ -112,27 +143,35 @@ __global__ __launch_bounds__(kBlock) void bn_finalize_kernel(Fin fin, const doub
 // ---- forward ----------------------------------------------------------------
 
 // mean, variance and the rolling averages of channel f from s1 = sum(x - c),
-// s2 = sum((x - c)^2) over its n elements.
+// s2 = sum((x - c)^2) over its n elements, c = the channel's first element.
+// The split statistics pass stores c beside the partials (shift[f]): the
+// apply pass may overwrite the input in place before every workgroup has
+// finalised.
 struct FwdFin {
-    const float *input;
+    const double *shift;
     float *mean, *variance, *rolling_mean, *rolling_variance;
-    uint32_t spatial;
     double n;
     float mean_scale;  // 1/(B*S) in f32 (blas.zig:107)
     float var_scale;   // 1/(B*S - 1) in f32 (blas.zig:122)
-    __device__ void operator()(uint32_t f, const Sums<2> &r) const {
+    __device__ void stats(const Sums<2> &r, double c, float &m, float &v) const {
         const double s1 = r.s[0], s2 = r.s[1];
-        const double c = (double)input[f * spatial];
-        const float m = (float)(n * c + s1) * mean_scale;  // blas.zig:114: sum * (1/(B*S))
+        m = (float)(n * c + s1) * mean_scale;  // blas.zig:114: sum * (1/(B*S))
         const double dm = (c + s1 / n) - (double)m;
         double m2 = s2 - s1 * (s1 / n);
         m2 = m2 > 0.0 ? m2 : 0.0;
-        const float v = (float)(m2 + n * dm * dm) * var_scale;  // blas.zig:133
+        v = (float)(m2 + n * dm * dm) * var_scale;  // blas.zig:133
+    }
+    __device__ void write(uint32_t f, float m, float v) const {
         mean[f] = m;
         variance[f] = v;
         // batchnorm.zig:140-143: scal(0.99) then axpy(1 - 0.99) -- axpy is an fma (blas.zig:22)
         rolling_mean[f] = __builtin_fmaf(kAlpha, m, rolling_mean[f] * kMomentum);
         rolling_variance[f] = __builtin_fmaf(kAlpha, v, rolling_variance[f] * kMomentum);
+    }
+    __device__ void operator()(uint32_t f, const Sums<2> &r) const {  // after a split pass
+        float m, v;
+        stats(r, shift[f], m, v);
+        write(f, m, v);
     }
 };
 
@@ -147,7 +186,7 @@ template <int H, int BS, bool FIN>
 __global__ __launch_bounds__(BS) void bn_stats_kernel(const float *input, RedGeom g, FwdFin fin, double *partials) {
     __shared__ double lds[2 * (BS / kWave)];
     uint32_t f, k;
-    red_coords(g, f, k);
+    red_coords<DKZ_BN_STATS_KMAJOR != 0>(g, f, k);
     const uint32_t j0 = k * g.chunk;
     const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
     const uint32_t fbase = f * g.spatial;
@@ -169,9 +208,14 @@ __global__ __launch_bounds__(BS) void bn_stats_kernel(const float *input, RedGeo
     const double t[2] = {a[0] + b[0], a[1] + b[1]};
     const Sums<2> r = block_sums<2, BS>(t, lds);
     if constexpr (FIN) {
-        if (threadIdx.x == 0) fin(f, r);
+        if (threadIdx.x == 0) {
+            float m, v;
+            fin.stats(r, c, m, v);
+            fin.write(f, m, v);
+        }
     } else {
         store_partials<2, BS>(r, g, f, k, partials);
+        if (k == 0 && threadIdx.x == 0) partials[2u * g.div_filters.d * g.K + f] = c;  // = fin.shift[f]
     }
 }
 
@@ -179,55 +223,130 @@ struct FwdParams {
     const float *mean, *variance, *scales, *biases;
 };
 
-// x = input; x_norm = (input - m) * (1/(sqrt(v) + 1e-6)) (blas.zig:137-146);
-// output = act(x_norm * scale + bias) (blas.zig:63-71, 53-61;
-// activations.zig:107-125). TRAIN: x_norm is stored (batchnorm.zig:146).
-template <int A, bool TRAIN>
-__device__ __forceinline__ void fwd_elem(float4 v, const FwdParams &p, uint32_t f, float4 &xn, float4 &o) {
-    const float m = p.mean[f];
-    const float inv = 1.0f / (sqrtf(p.variance[f]) + 1e-6f);
-    const float gam = p.scales[f], bet = p.biases[f];
+// What the forward apply pass needs of channel f.
+struct FwdChan {
+    float m, inv, gam, bet;
+};
+
+__device__ __forceinline__ FwdChan fwd_chan(float m, float v, float gam, float bet) {
+    return {m, 1.0f / (sqrtf(v) + 1e-6f), gam, bet};  // blas.zig:141-143
+}
+
+// x_norm = (input - m) * inv (blas.zig:137-146); output = act(x_norm * scale
+// + bias) (blas.zig:63-71, 53-61; activations.zig:107-125).
+template <int A>
+__device__ __forceinline__ void fwd_elem(float4 v, const FwdChan &c, float4 &xn, float4 &o) {
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const float t = (lane(v, l) - m) * inv;
+        const float t = (lane(v, l) - c.m) * c.inv;
         lane(xn, l) = t;
-        lane(o, l) = activate<A>(t * gam + bet);
+        lane(o, l) = activate<A>(t * c.gam + c.bet);
     }
 }
 
+// Whether the apply pass finalises its own channels (saves the finalize
+// launch: config 1 forward 23.6 -> 20.9 us, config 2 backward 140.7 ->
+// 139.1 us) when the split reduction leaves partials.
+#ifndef DKZ_BN_DEFER_FWD
+#define DKZ_BN_DEFER_FWD 1
+#endif
+#ifndef DKZ_BN_DEFER_BWD
+#define DKZ_BN_DEFER_BWD 1
+#endif
+// Elements of one apply workgroup, and how many channel rows it may span
+// and still finalise its channels itself.
+#ifndef DKZ_BN_APPLY_UNROLL
+#define DKZ_BN_APPLY_UNROLL 4  // 2 or 8 float4s per stream per lane: slower (config 2: +1 / +7 us)
+#endif
+constexpr int kApplyUnroll = DKZ_BN_APPLY_UNROLL;
+constexpr uint32_t kTile = kBlock * kApplyUnroll * 4;
+constexpr uint32_t kSlots = 16;
+
+// The rows [r0, r0 + nrows) of this workgroup's tile of n elements.
+__device__ __forceinline__ void tile_rows(const ChanGeom &g, uint32_t n, uint32_t &e0, uint32_t &r0,
+                                          uint32_t &nrows) {
+    e0 = blockIdx.x * kTile;
+    const uint32_t e1 = min(e0 + kTile, n) - 1;
+    r0 = fdiv(e0, g.spatial);
+    nrows = fdiv(e1, g.spatial) - r0 + 1;
+}
+
+// Adds channel f's K partials of each of NS sums, in index order, over one
+// wave (all lanes return the sums). The same code as bn_finalize_kernel,
+// so every workgroup that does this gets the same bits.
+template <int NS>
+__device__ __forceinline__ Sums<NS> wave_partials(const double *partials, uint32_t F, uint32_t K, uint32_t f) {
+    const uint32_t l = threadIdx.x & (kWave - 1);
+    Sums<NS> r;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const double *p = partials + ((uint64_t)q * F + f) * K;
+        double s = 0.0;
+        for (uint32_t i = l; i < K; i += kWave) s += p[i];
+        r.s[q] = wave_sum(s);
+    }
+    return r;
+}
+
+// Forward apply: x = input, x_norm (TRAIN), output.
+// FIN: the statistics are still K partials per channel; the workgroup adds
+// them for the (at most kSlots) rows of its tile itself, and the workgroup
+// whose tile holds a channel's first element writes that channel's mean,
+// variance and rolling averages, exactly once. Otherwise they are read
+// from p (normalised with the batch statistics, or with the rolling ones
+// when !TRAIN).
 // H: bit 0 = input load, bit 1 = x store, bit 2 = x_norm store, bit 3 = output store.
-template <int A, bool TRAIN, int H, bool REV>
+template <int A, bool TRAIN, int H, bool FIN>
 __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input, float *output, float *x,
-                                                              float *x_norm, FwdParams p, ChanGeom g,
-                                                              uint32_t nv) {
+                                                              float *x_norm, FwdParams p, ChanGeom g, uint32_t n,
+                                                              FwdFin fin, const double *partials, uint32_t K) {
     constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
-    const uint32_t tile = REV ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
-    const uint32_t base = tile * (kBlock * kUnroll) + threadIdx.x;
-    if (base + (kUnroll - 1) * kBlock < nv) {
-        float4 v[kUnroll];
+    __shared__ FwdChan slot[kSlots];
+    const uint32_t nv = n >> 2;
+    const uint32_t base = blockIdx.x * (kBlock * kApplyUnroll) + threadIdx.x;
+    const bool full = base + (kApplyUnroll - 1) * kBlock < nv;
+    float4 v[kApplyUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = ld4<kNtIn>(input, base + u * kBlock);
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t i = base + u * kBlock;
-            float4 xn, o;
-            fwd_elem<A, TRAIN>(v[u], p, channel_of<false>(i << 2, g), xn, o);
-            st4<kNtX>(x, i, v[u]);
-            if constexpr (TRAIN) st4<kNtXn>(x_norm, i, xn);
-            st4<kNtOut>(output, i, o);
-        }
-    } else {
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t i = base + u * kBlock;
-            if (i < nv) {
-                const float4 v = ld4<kNtIn>(input, i);
-                float4 xn, o;
-                fwd_elem<A, TRAIN>(v, p, channel_of<false>(i << 2, g), xn, o);
-                st4<kNtX>(x, i, v);
-                if constexpr (TRAIN) st4<kNtXn>(x_norm, i, xn);
-                st4<kNtOut>(output, i, o);
+    for (int u = 0; u < kApplyUnroll; ++u) {
+        const uint32_t i = base + u * kBlock;
+        if (full || i < nv) v[u] = ld4<kNtIn>(input, i);
+    }
+    uint32_t r0 = 0;
+    if constexpr (FIN) {
+        uint32_t e0, nrows;
+        tile_rows(g, n, e0, r0, nrows);
+        for (uint32_t s = threadIdx.x / kWave; s < nrows; s += kBlock / kWave) {
+            const uint32_t r = r0 + s;
+            const uint32_t f = r - fdiv(r, g.filters) * g.filters.d;
+            const Sums<2> sums = wave_partials<2>(partials, g.filters.d, K, f);
+            if ((threadIdx.x & (kWave - 1)) == 0) {
+                float m, var;
+                fin.stats(sums, fin.shift[f], m, var);
+                slot[s] = fwd_chan(m, var, p.scales[f], p.biases[f]);
+                // row r == f is channel f's first row (b = 0); several slots
+                // may hold one channel when the tile spans more than F rows
+                if (r == f && f * g.spatial.d >= e0) fin.write(f, m, var);
             }
         }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kApplyUnroll; ++u) {
+        const uint32_t i = base + u * kBlock;
+        if (!(full || i < nv)) continue;
+        const uint32_t r = fdiv(i << 2, g.spatial);
+        FwdChan c;
+        if constexpr (FIN) {
+            c = slot[r - r0];
+        } else {
+            const uint32_t f = r - fdiv(r, g.filters) * g.filters.d;
+            c = fwd_chan(p.mean[f], p.variance[f], p.scales[f], p.biases[f]);
+        }
+        float4 xn, o;
+        fwd_elem<A>(v[u], c, xn, o);
+        st4<kNtX>(x, i, v[u]);
+        if constexpr (TRAIN) st4<kNtXn>(x_norm, i, xn);
+        st4<kNtOut>(output, i, o);
     }
 }
 
@@ -239,12 +358,21 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 struct BwdFin {
     const float *variance;
     float *bias_updates, *scale_updates, *mean_delta, *variance_delta;
-    __device__ void operator()(uint32_t f, const Sums<4> &r) const {
+    __device__ void values(uint32_t f, const Sums<4> &r, float &md, float &vd) const {
         const float v = variance[f];
-        bias_updates[f] = bias_updates[f] + (float)r.s[0];             // blas.zig:79
-        scale_updates[f] = scale_updates[f] + (float)r.s[1];           // blas.zig:98
-        mean_delta[f] = (float)r.s[2] * (-1.0f / sqrtf(v + 1e-5f));    // blas.zig:155
-        variance_delta[f] = ((float)r.s[3] * -0.5f) * pow_m1p5(v + 1e-5f);  // blas.zig:176
+        md = (float)r.s[2] * (-1.0f / sqrtf(v + 1e-5f));            // blas.zig:155
+        vd = ((float)r.s[3] * -0.5f) * pow_m1p5(v + 1e-5f);          // blas.zig:176
+    }
+    __device__ void write(uint32_t f, const Sums<4> &r, float md, float vd) const {
+        bias_updates[f] = bias_updates[f] + (float)r.s[0];   // blas.zig:79
+        scale_updates[f] = scale_updates[f] + (float)r.s[1]; // blas.zig:98
+        mean_delta[f] = md;
+        variance_delta[f] = vd;
+    }
+    __device__ void operator()(uint32_t f, const Sums<4> &r) const {
+        float md, vd;
+        values(f, r, md, vd);
+        write(f, r, md, vd);
     }
 };
 
@@ -279,13 +407,13 @@ __global__ __launch_bounds__(BS) void bn_bwd_sums_kernel(const float *y, const f
     constexpr bool kLin = A == kLinear;
     __shared__ double lds[4 * (BS / kWave)];
     uint32_t f, k;
-    red_coords(g, f, k);
+    red_coords<DKZ_BN_KMAJOR != 0>(g, f, k);
     const uint32_t j0 = k * g.chunk;
     const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
     const uint32_t fbase = f * g.spatial;
     const float m = mean[f], gam = scales[f];
     double a[4] = {0.0, 0.0, 0.0, 0.0};
-    constexpr int kU = 2;  // four streams: 2 float4s each in flight per lane
+    constexpr int kU = DKZ_BN_SUMS_UNROLL;  // four streams: kU float4s each in flight per lane
     constexpr uint32_t kStep = 4 * BS;
     uint32_t j = j0 + 4 * threadIdx.x;
     for (; j + kStep * (kU - 1) < j1; j += kStep * kU) {
@@ -321,57 +449,83 @@ struct BwdParams {
     float denom;  // f32(spatial * batch), blas.zig:191
 };
 
+// What the backward apply pass needs of channel f.
+struct BwdChan {
+    float m, inv, vd2, mdn, gam;
+};
+
+__device__ __forceinline__ BwdChan bwd_chan(const BwdParams &p, uint32_t f, float md, float vd) {
+    return {p.mean[f], 1.0f / sqrtf(p.variance[f] + 1e-5f), vd * 2.0f, md / p.denom, p.scales[f]};
+}
+
 // delta = d2 * inv + ((vd * 2) * (x - m)) / N + md / N (blas.zig:180-204) on
 // d2 = delta * gradient(y) * scale.
 template <int A>
-__device__ __forceinline__ float4 bwd_elem(float4 y, float4 d, float4 x, const BwdParams &p, uint32_t f) {
-    const float m = p.mean[f];
-    const float inv = 1.0f / sqrtf(p.variance[f] + 1e-5f);
-    const float vd2 = p.variance_delta[f] * 2.0f;
-    const float mdn = p.mean_delta[f] / p.denom;
-    const float gam = p.scales[f];
+__device__ __forceinline__ float4 bwd_elem(float4 y, float4 d, float4 x, const BwdChan &c, float denom) {
     float4 o;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const float d2 = grad_delta<A>(lane(d, l), lane(y, l)) * gam;
-        lane(o, l) = (d2 * inv + (vd2 * (lane(x, l) - m)) / p.denom) + mdn;
+        const float d2 = grad_delta<A>(lane(d, l), lane(y, l)) * c.gam;
+        lane(o, l) = (d2 * c.inv + (c.vd2 * (lane(x, l) - c.m)) / denom) + c.mdn;
     }
     return o;
 }
 
+// Backward apply. FIN as in the forward apply: the workgroup adds the
+// partials of its tile's channels itself, and the workgroup holding a
+// channel's first element writes its updates, mean_delta and variance_delta.
 // H: bit 0 = y, bit 1 = delta, bit 2 = x loads, bit 3 = delta store.
-template <int A, int H, bool REV>
+template <int A, int H, bool FIN>
 __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, float *delta, const float *x,
-                                                              BwdParams p, ChanGeom g, uint32_t nv) {
+                                                              BwdParams p, ChanGeom g, uint32_t n, BwdFin fin,
+                                                              const double *partials, uint32_t K) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtX = (H & 4) != 0, kNtOut = (H & 8) != 0;
-    const uint32_t tile = REV ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
-    const uint32_t base = tile * (kBlock * kUnroll) + threadIdx.x;
-    if (base + (kUnroll - 1) * kBlock < nv) {
-        float4 vy[kUnroll], vd[kUnroll], vx[kUnroll];
+    __shared__ BwdChan slot[kSlots];
+    const uint32_t nv = n >> 2;
+    const uint32_t base = blockIdx.x * (kBlock * kApplyUnroll) + threadIdx.x;
+    const bool full = base + (kApplyUnroll - 1) * kBlock < nv;
+    float4 vy[kApplyUnroll], vd[kApplyUnroll], vx[kApplyUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t i = base + u * kBlock;
+    for (int u = 0; u < kApplyUnroll; ++u) {
+        const uint32_t i = base + u * kBlock;
+        if (full || i < nv) {
             vd[u] = ld4<kNtD>(delta, i);
             if constexpr (!kLin) vy[u] = ld4<kNtY>(y, i);
             else vy[u] = vd[u];
             vx[u] = ld4<kNtX>(x, i);
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t i = base + u * kBlock;
-            st4<kNtOut>(delta, i, bwd_elem<A>(vy[u], vd[u], vx[u], p, channel_of<false>(i << 2, g)));
-        }
-    } else {
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t i = base + u * kBlock;
-            if (i < nv) {
-                const float4 vd = ld4<kNtD>(delta, i);
-                const float4 vy = kLin ? vd : ld4<kNtY>(y, i);
-                const float4 vx = ld4<kNtX>(x, i);
-                st4<kNtOut>(delta, i, bwd_elem<A>(vy, vd, vx, p, channel_of<false>(i << 2, g)));
+    }
+    uint32_t r0 = 0;
+    if constexpr (FIN) {
+        uint32_t e0, nrows;
+        tile_rows(g, n, e0, r0, nrows);
+        for (uint32_t s = threadIdx.x / kWave; s < nrows; s += kBlock / kWave) {
+            const uint32_t r = r0 + s;
+            const uint32_t f = r - fdiv(r, g.filters) * g.filters.d;
+            const Sums<4> sums = wave_partials<4>(partials, g.filters.d, K, f);
+            if ((threadIdx.x & (kWave - 1)) == 0) {
+                float md, vdl;
+                fin.values(f, sums, md, vdl);
+                slot[s] = bwd_chan(p, f, md, vdl);
+                if (r == f && f * g.spatial.d >= e0) fin.write(f, sums, md, vdl);
             }
         }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kApplyUnroll; ++u) {
+        const uint32_t i = base + u * kBlock;
+        if (!(full || i < nv)) continue;
+        const uint32_t r = fdiv(i << 2, g.spatial);
+        BwdChan c;
+        if constexpr (FIN) {
+            c = slot[r - r0];
+        } else {
+            const uint32_t f = r - fdiv(r, g.filters) * g.filters.d;
+            c = bwd_chan(p, f, p.mean_delta[f], p.variance_delta[f]);
+        }
+        st4<kNtOut>(delta, i, bwd_elem<A>(vy[u], vd[u], vx[u], c, p.denom));
     }
 }
 
@@ -397,64 +551,97 @@ struct BwdArgs {
     float *bias_updates, *scale_updates, *mean_delta, *variance_delta;
 };
 
-// Launches a channel reduction pass (NS sums) through `kern_fin` (K == 1,
-// block BS) or `kern_part` + the finalize launch (K > 1).
-template <int NS, class Fin, class KFin1024, class KFin256, class KPart, class... Args>
-int run_sums(const char *name, uint32_t streams, const Shape &sh, const Fin &fin, KFin1024 kfin_wide,
-             KFin256 kfin, KPart kpart, Args... args) {
+// Split of a reduction pass over the channels of a shape.
+template <int NS>
+RedGeom sums_geom(const Shape &sh, uint32_t streams) {
     const uint32_t L = sh.B * sh.S;
-    const RedGeom g = make_red_geom(sh.F, sh.S, L, pick_split(sh.F, L, streams, NS), true);
+    return make_red_geom(sh.F, sh.S, L,
+                         pick_split(sh.F, L, streams, NS, DKZ_BN_SPLIT_TARGET, DKZ_BN_MIN_CHUNK), true);
+}
+
+// An apply workgroup's tile spans at most kSlots rows, so it can finalise
+// its own channels.
+inline bool tile_fits_slots(uint32_t S) { return (kTile - 1) / S + 2 <= kSlots; }
+
+// Launches a reduction pass. K == 1: one workgroup per channel finalises it
+// (1024 threads for long channels). K > 1: partial sums into the scratch,
+// then the finalize launch -- unless `defer`, when the apply pass finalises
+// and *partials receives the scratch.
+template <int NS, class Fin, class KWide, class KFin, class KPart, class... Args>
+int run_sums(const char *name, const RedGeom &g, const Shape &sh, const Fin &fin, bool defer,
+             const double **partials, KWide kwide, KFin kfin, KPart kpart, Args... args) {
+    *partials = nullptr;
     if (g.K == 1) {
-        if (L >= 16 * kWideBlock)
-            return launch(name, kfin_wide, dim3(sh.F), dim3(kWideBlock), args..., g, fin, (double *)nullptr);
+        if (g.chan_len >= 16 * kWideBlock)
+            return launch(name, kwide, dim3(sh.F), dim3(kWideBlock), args..., g, fin, (double *)nullptr);
         return launch(name, kfin, dim3(sh.F), dim3(kBlock), args..., g, fin, (double *)nullptr);
     }
     Scratch sc{nullptr};
     DKZ_TRY(device_scratch(&sc));
     DKZ_TRY(launch(name, kpart, dim3(sh.F * g.K), dim3(kBlock), args..., g, fin, sc.partials));
+    if (defer) {
+        *partials = sc.partials;
+        return 0;
+    }
     return launch(name, bn_finalize_kernel<NS, Fin>, dim3(div_up(sh.F, kBlock / kWave)), dim3(kBlock), fin,
                   (const double *)sc.partials, sh.F, g.K);
 }
 
-constexpr bool kRev = DKZ_BN_APPLY_REVERSE != 0;
-
 template <int A>
 int bn_forward_fused(const FwdArgs &a) {
+    constexpr int H = DKZ_HINT_BN_FWD_APPLY;
     const Shape &sh = a.sh;
     const ChanGeom cg{make_fastdiv(sh.S), make_fastdiv(sh.F)};
-    const uint32_t nv = sh.n >> 2;
-    const dim3 grid(div_up(nv, (uint64_t)kBlock * kUnroll)), block(kBlock);
+    const dim3 grid(div_up(sh.n, kTile)), block(kBlock);
+    const uint64_t L = (uint64_t)sh.B * sh.S;
+    // shift: after the 2*F*K partials of a split pass (two sums + one shift
+    // per channel fit the scratch: pick_split is asked for 3 per chunk)
+    const RedGeom g = sums_geom<3>(sh, 1);
+    Scratch sc{nullptr};
+    if (a.train && g.K > 1) DKZ_TRY(device_scratch(&sc));
+    const FwdFin fin{sc.partials ? sc.partials + 2u * sh.F * g.K : nullptr, a.mean, a.variance, a.rolling_mean,
+                     a.rolling_variance, (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
     if (!a.train) {
         const FwdParams p{a.rolling_mean, a.rolling_variance, a.scales, a.biases};
-        return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, false, DKZ_HINT_BN_FWD_APPLY, kRev>, grid,
-                      block, a.input, a.output, a.x, a.x_norm, p, cg, nv);
+        return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, false, H, false>, grid, block, a.input,
+                      a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
     }
-    const uint64_t L = (uint64_t)sh.B * sh.S;
-    const FwdFin fin{a.input, a.mean, a.variance, a.rolling_mean, a.rolling_variance, sh.S, (double)L,
-                     1.0f / (float)L, 1.0f / (float)(L - 1u)};
-    DKZ_TRY(run_sums<2>("batchnorm_forward_stats", 1, sh, fin, bn_stats_kernel<DKZ_HINT_BN_STATS, kWideBlock, true>,
+    const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && tile_fits_slots(sh.S);
+    const double *partials = nullptr;
+    DKZ_TRY(run_sums<2>("batchnorm_forward_stats", g, sh, fin, defer, &partials,
+                        bn_stats_kernel<DKZ_HINT_BN_STATS, kWideBlock, true>,
                         bn_stats_kernel<DKZ_HINT_BN_STATS, kBlock, true>,
                         bn_stats_kernel<DKZ_HINT_BN_STATS, kBlock, false>, a.input));
     const FwdParams p{a.mean, a.variance, a.scales, a.biases};
-    return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, true, DKZ_HINT_BN_FWD_APPLY, kRev>, grid, block,
-                  a.input, a.output, a.x, a.x_norm, p, cg, nv);
+    if (defer)
+        return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, true, H, true>, grid, block, a.input,
+                      a.output, a.x, a.x_norm, p, cg, sh.n, fin, partials, g.K);
+    return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, true, H, false>, grid, block, a.input,
+                  a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
 }
 
 template <int A>
 int bn_backward_fused(const BwdArgs &a) {
+    constexpr int H = DKZ_HINT_BN_BWD_APPLY;
     const Shape &sh = a.sh;
     const BwdFin fin{a.variance, a.bias_updates, a.scale_updates, a.mean_delta, a.variance_delta};
-    constexpr int H = DKZ_HINT_BN_BWD_SUMS;
-    DKZ_TRY(run_sums<4>("batchnorm_backward_sums", A == kLinear ? 3 : 4, sh, fin,
-                        bn_bwd_sums_kernel<A, H, kWideBlock, true>, bn_bwd_sums_kernel<A, H, kBlock, true>,
-                        bn_bwd_sums_kernel<A, H, kBlock, false>, a.y, (const float *)a.delta, a.x_norm, a.x,
+    const RedGeom g = sums_geom<4>(sh, A == kLinear ? 3 : 4);
+    const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && tile_fits_slots(sh.S);
+    const double *partials = nullptr;
+    constexpr int HS = DKZ_HINT_BN_BWD_SUMS;
+    DKZ_TRY(run_sums<4>("batchnorm_backward_sums", g, sh, fin, defer, &partials,
+                        bn_bwd_sums_kernel<A, HS, kWideBlock, true>, bn_bwd_sums_kernel<A, HS, kBlock, true>,
+                        bn_bwd_sums_kernel<A, HS, kBlock, false>, a.y, (const float *)a.delta, a.x_norm, a.x,
                         a.mean, a.scales));
     const ChanGeom cg{make_fastdiv(sh.S), make_fastdiv(sh.F)};
-    const uint32_t nv = sh.n >> 2;
     const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
-    return launch("batchnorm_backward_apply", bn_bwd_apply_kernel<A, DKZ_HINT_BN_BWD_APPLY, kRev>,
-                  dim3(div_up(nv, (uint64_t)kBlock * kUnroll)), dim3(kBlock), a.y, a.delta, a.x, p, cg, nv);
+    const dim3 grid(div_up(sh.n, kTile)), block(kBlock);
+    if (defer)
+        return launch("batchnorm_backward_apply", bn_bwd_apply_kernel<A, H, true>, grid, block, a.y, a.delta, a.x,
+                      p, cg, sh.n, fin, partials, g.K);
+    return launch("batchnorm_backward_apply", bn_bwd_apply_kernel<A, H, false>, grid, block, a.y, a.delta, a.x, p,
+                  cg, sh.n, fin, (const double *)nullptr, 0u);
 }
 
 typedef int (*FwdFn)(const FwdArgs &);

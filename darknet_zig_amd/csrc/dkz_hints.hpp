@@ -98,10 +98,12 @@
 #define DKZ_HINT_SHORTCUT 1
 #endif
 
-// batchnorm.hip, the fused layer passes. The statistics / sums pass and the
-// apply pass read the same tensors, so the first pass keeps its loads cached
-// (a layer at config sizes then finds much of it in the Infinity Cache) and
-// the apply pass, their last reader, streams them.
+// batchnorm.hip, the fused layer passes. The statistics pass keeps its input
+// cached for the apply pass that re-reads it (at config 1 all of it fits the
+// Infinity Cache). The backward passes stream everything: at config 2 the
+// sums pass reads 411 MB, so nothing it caches survives to the apply pass
+// (nontemporal sums loads: 138 us per step against 146 us; walking the
+// apply tiles backwards made no difference).
 // forward statistics: bit 0 = input load
 #ifndef DKZ_HINT_BN_STATS
 #define DKZ_HINT_BN_STATS 0
@@ -114,14 +116,11 @@
 #endif
 // backward sums: bit 0 = y, bit 1 = delta, bit 2 = x_norm, bit 3 = x loads
 #ifndef DKZ_HINT_BN_BWD_SUMS
-#define DKZ_HINT_BN_BWD_SUMS 4
+#define DKZ_HINT_BN_BWD_SUMS 15
 #endif
 // backward apply: bit 0 = y, bit 1 = delta, bit 2 = x loads, bit 3 = delta store
+// (all nontemporal: 135 us per config-2 step against 139 us with a cached
+// delta store)
 #ifndef DKZ_HINT_BN_BWD_APPLY
-#define DKZ_HINT_BN_BWD_APPLY 7
-#endif
-// Apply passes walk their tiles last-to-first, starting where the first pass
-// ended, i.e. on the lines most likely still in the Infinity Cache.
-#ifndef DKZ_BN_APPLY_REVERSE
-#define DKZ_BN_APPLY_REVERSE 1
+#define DKZ_HINT_BN_BWD_APPLY 15
 #endif

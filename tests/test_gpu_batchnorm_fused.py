@@ -31,6 +31,8 @@ FAST = [
     (3, 128, 64),     # filters 128, few bytes: one 256-thread workgroup per channel
     (4, 256, 4096),   # filters 256, long channels: one 1024-thread workgroup per channel
     (2, 8, 20000),    # few channels, long: split with a ragged last chunk
+    (16, 5, 600),     # split; an apply tile spans up to 8 rows, channels repeat within it
+    (8, 6, 1536),     # split; apply tiles finalise their own channels
     (128, 32, 1024),
 ]
 FALLBACK = [
@@ -129,6 +131,7 @@ def test_forward_inference(dev, shape):
 @pytest.mark.parametrize("act", list(Activation), ids=lambda a: a.name)
 def test_forward_every_activation(dev, act):
     _forward_case((4, 12, 64), act, True, inplace=True, seed=100 + int(act))
+    _forward_case((8, 6, 1536), act, True, inplace=True, seed=150 + int(act))
 
 
 def test_forward_matches_oracle_layer_sequence(dev):
@@ -213,6 +216,7 @@ def test_backward(dev, shape):
 @pytest.mark.parametrize("act", list(Activation), ids=lambda a: a.name)
 def test_backward_every_activation(dev, act):
     _backward_case((4, 12, 64), act, seed=200 + int(act))
+    _backward_case((8, 6, 1536), act, seed=250 + int(act))
 
 
 def test_backward_linear_needs_no_output(dev):
