@@ -44,7 +44,9 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_axpy": (_i, [_i, _f, _p, _p]),
     "dkz_scal": (_i, [_i, _f, _p]),
     "dkz_mul": (_i, [_i, _p, _p]),
+    "dkz_add_scalar": (_i, [_i, _f, _p]),
     "dkz_constrain": (_i, [_i, _f, _p]),
+    "dkz_rand_uniform": (_i, [_i, _p, C.c_uint]),
     "dkz_activate_array": (_i, [_p, _i, _i]),
     "dkz_gradient_array": (_i, [_p, _i, _i, _p]),
     "dkz_add_bias": (_i, [_p, _p, _i, _i, _i]),
@@ -67,6 +69,10 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_forward_avgpool": (_i, [_i, _i, _i, _i, _p, _p]),
     "dkz_backward_avgpool": (_i, [_i, _i, _i, _i, _p, _p]),
     "dkz_shortcut": (_i, [_i, _i, _i, _i, _p, _i, _i, _i, _f, _f, _p]),
+    "dkz_im2col": (_i, [_p, _i, _i, _i, _i, _i, _i, _p]),
+    "dkz_col2im": (_i, [_p, _i, _i, _i, _i, _i, _i, _p]),
+    "dkz_dropout": (_i, [_p, _i, _p, _f, _f]),
+    "dkz_adam_update": (_i, [_p, _p, _p, _p, _f, _f, _f, _f, _f, _i, _i, _i]),
     "dkz_batchnorm_forward": (_i, [_i, _i, _i, _i, _i] + [_p] * 10),
     "dkz_batchnorm_backward": (_i, [_i, _i, _i, _i] + [_p] * 11),
 }

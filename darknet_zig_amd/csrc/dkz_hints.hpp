@@ -41,6 +41,18 @@
 #ifndef DKZ_HINT_GRADIENT
 #define DKZ_HINT_GRADIENT 17     // y (read once) and the delta store; the delta load stays cached
 #endif
+#ifndef DKZ_HINT_ADD_SCALAR
+#define DKZ_HINT_ADD_SCALAR 0    // x (the truth buffer, read next by the cost op)
+#endif
+#ifndef DKZ_HINT_RAND_UNIFORM
+#define DKZ_HINT_RAND_UNIFORM 0  // out: read at once by dropout, again in the backward pass
+#endif
+#ifndef DKZ_HINT_DROPOUT
+#define DKZ_HINT_DROPOUT 0       // x (read next by the following layer), rand
+#endif
+#ifndef DKZ_HINT_ADAM
+#define DKZ_HINT_ADAM 31         // w, d, m, v: each read and written once per step
+#endif
 #ifndef DKZ_HINT_LOSS
 #define DKZ_HINT_LOSS 0          // pred, truth; delta, err
 #endif
@@ -96,6 +108,11 @@
 // shortcut.hip: bit 0 = add load, bit 1 = out load, bit 2 = out store
 #ifndef DKZ_HINT_SHORTCUT
 #define DKZ_HINT_SHORTCUT 1
+#endif
+
+// im2col.hip: bit 1 = column buffer store (the GEMM reads it next)
+#ifndef DKZ_HINT_IM2COL
+#define DKZ_HINT_IM2COL 0
 #endif
 
 // batchnorm.hip, the fused layer passes. The statistics pass keeps its input

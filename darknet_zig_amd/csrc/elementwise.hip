@@ -1,6 +1,7 @@
-// elementwise.hip -- the streaming elementwise ops of src/gpu.zig:483-521 and
-// 631-645 (fill, copy, axpy, scal, mul, constrain, activate, gradient,
-// softmax cross-entropy, l2, l1, smooth L1).
+// elementwise.hip -- the streaming elementwise ops of src/gpu.zig:483-521,
+// 631-645, 769 and 804-830 (fill, copy, axpy, scal, mul, add_scalar,
+// constrain, rand_uniform, activate, gradient, softmax cross-entropy, l2, l1,
+// smooth L1, dropout, and the Adam update as one pass).
 //
 // One kernel shape serves all of them: each thread moves kUnroll float4s per
 // stream, issuing every load before the first store, so a wave keeps
@@ -131,6 +132,10 @@ struct ScalOp {  // blas.zig:26
 struct MulOp {  // blas.zig:31: y *= x
     __device__ void operator()(const float (&a)[2], float (&r)[1]) const { r[0] = a[1] * a[0]; }
 };
+struct AddScalarOp {  // darknet_kernels.hip:150-153
+    float alpha;
+    __device__ void operator()(const float (&a)[1], float (&r)[1]) const { r[0] = a[0] + alpha; }
+};
 struct ConstrainOp {  // blas.zig:44: @max(-alpha, @min(v, alpha))
     float alpha;
     __device__ void operator()(const float (&a)[1], float (&r)[1]) const {
@@ -182,6 +187,79 @@ struct SmoothL1Op {  // blas.zig:270-282
         }
     }
 };
+
+// layers/misc.zig:105-127: in = {x, rand}
+struct DropoutOp {
+    float prob, scale;
+    __device__ void operator()(const float (&a)[2], float (&r)[1]) const {
+        r[0] = (a[1] < prob) ? 0.0f : a[0] * scale;
+    }
+};
+
+// gpu.zig:804-830 adamUpdate as one pass; in = out = {w, d, m, v}. Each
+// element goes through the wrapper's launches in their order -- scal(b1, m),
+// scal(b2, v), axpy(-decay*batch, w, d), axpy(1-b1, d, m), mul(d, d),
+// axpy(1-b2, d, v), the adam_kernel step (darknet_kernels.hip:588-595),
+// fill(d, 0) -- with the same roundings (axpy contracted, everything else
+// one rounding per operation), so the result equals the eight-launch
+// sequence bit for bit. c1 and c2 are the bias corrections 1 - b^t.
+struct AdamOp {
+    float b1, b2, neg_decay_batch, one_m_b1, one_m_b2, c1, c2, rate, eps;
+    __device__ void operator()(const float (&a)[4], float (&r)[4]) const {
+        const float m = a[2] * b1;
+        const float v = a[3] * b2;
+        const float d = __builtin_fmaf(neg_decay_batch, a[0], a[1]);
+        const float m2 = __builtin_fmaf(one_m_b1, d, m);
+        const float dd = d * d;
+        const float v2 = __builtin_fmaf(one_m_b2, dd, v);
+        const float mhat = m2 / c1;
+        const float vhat = v2 / c2;
+        r[0] = a[0] + rate * mhat / (sqrtf(vhat) + eps);
+        r[1] = 0.0f;
+        r[2] = m2;
+        r[3] = v2;
+    }
+};
+
+// darknet_kernels.hip:168-183: element i of a rand_uniform draw is the top 24
+// bits of hash(seed ^ hash(i)), scaled into [0, 1) (every value exact). The
+// hash is Wellons' "lowbias32".
+__device__ __forceinline__ uint32_t hash_u32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+__device__ __forceinline__ float uniform_at(uint32_t seed, uint32_t i) {
+    return (float)(hash_u32(seed ^ hash_u32(i)) >> 8) * (1.0f / 16777216.0f);
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void rand_vec_kernel(float *x, uint32_t seed, uint32_t n) {
+    const uint32_t nv = n >> 2;
+    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t v = base + u * kBlock;
+        if (v < nv) {
+            const uint32_t e = v << 2;
+            st4<NT>(x, v, make_float4(uniform_at(seed, e), uniform_at(seed, e + 1), uniform_at(seed, e + 2),
+                                      uniform_at(seed, e + 3)));
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3u)) {
+        const uint32_t e = (nv << 2) + threadIdx.x;
+        x[e] = uniform_at(seed, e);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void rand_scalar_kernel(float *x, uint32_t seed, uint32_t n) {
+    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) x[i] = uniform_at(seed, i);
+}
+
+inline bool disjoint(const float *a, const float *b, int n) { return a + n <= b || b + n <= a; }
 
 template <int A>
 int activate_dispatch(float *x, int n) {
@@ -259,6 +337,61 @@ int dkz_mul(int n, const float *x, float *y) {
     DKZ_REQUIRE(x != nullptr && y != nullptr);
     Streams<2, 1> s{{x, y}, {y}};
     return run_ew<DKZ_HINT_MUL>("mul", MulOp{}, s, n);
+}
+
+int dkz_add_scalar(int n, float alpha, float *x) {
+    DKZ_REQUIRE(n >= 0);
+    if (n == 0) return 0;
+    DKZ_REQUIRE(x != nullptr);
+    Streams<1, 1> s{{x}, {x}};
+    return run_ew<DKZ_HINT_ADD_SCALAR>("add_scalar", AddScalarOp{alpha}, s, n);
+}
+
+int dkz_rand_uniform(int n, float *x, unsigned int seed) {
+    DKZ_REQUIRE(n >= 0);
+    if (n == 0) return 0;
+    DKZ_REQUIRE(x != nullptr);
+    const uint32_t un = (uint32_t)n;
+    if (aligned16(x)) {
+        const uint32_t nv = un >> 2;
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
+        return launch("rand_uniform", rand_vec_kernel<(DKZ_HINT_RAND_UNIFORM & 16) != 0>, dim3(grid), dim3(kBlock),
+                      x, (uint32_t)seed, un);
+    }
+    const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
+    return launch("rand_uniform", rand_scalar_kernel, dim3(grid), dim3(kBlock), x, (uint32_t)seed, un);
+}
+
+int dkz_dropout(float *input, int size, const float *rand, float prob, float scale) {
+    DKZ_REQUIRE(size >= 0);
+    if (size == 0) return 0;
+    DKZ_REQUIRE(input != nullptr && rand != nullptr);
+    Streams<2, 1> s{{input, rand}, {input}};
+    return run_ew<DKZ_HINT_DROPOUT>("dropout", DropoutOp{prob, scale}, s, size);
+}
+
+int dkz_adam_update(float *w, float *d, float *m, float *v, float b1, float b2, float eps, float decay,
+                    float rate, int n, int batch, int t) {
+    DKZ_REQUIRE(n >= 0 && batch >= 0);
+    if (n == 0) return 0;
+    DKZ_REQUIRE(w && d && m && v);
+    DKZ_REQUIRE(disjoint(w, d, n) && disjoint(w, m, n) && disjoint(w, v, n) && disjoint(d, m, n) &&
+                disjoint(d, v, n) && disjoint(m, v, n));
+    // The wrapper's scalar arguments, formed in f32 as gpu.zig:819-825 forms
+    // them; the bias corrections as adam_kernel forms them (powf of the step
+    // count converted to float), here once on the host.
+    AdamOp op;
+    op.b1 = b1;
+    op.b2 = b2;
+    op.neg_decay_batch = -decay * (float)batch;
+    op.one_m_b1 = 1.0f - b1;
+    op.one_m_b2 = 1.0f - b2;
+    op.c1 = 1.0f - powf(b1, (float)t);
+    op.c2 = 1.0f - powf(b2, (float)t);
+    op.rate = rate;
+    op.eps = eps;
+    Streams<4, 4> s{{w, d, m, v}, {w, d, m, v}};
+    return run_ew<DKZ_HINT_ADAM>("adam_update", op, s, n);
 }
 
 int dkz_constrain(int n, float alpha, float *x) {

@@ -1,0 +1,179 @@
+// im2col.hip -- the convolution lowering of src/gpu.zig:651-669 (im2col,
+// col2im), CPU twins src/im2col.zig:13-83.
+//
+// The column buffer has channels*ksize*ksize rows of height_col*width_col;
+// row c holds, for every output position (h, w), the input tap
+// (c_im, h*stride - pad + kh, w*stride - pad + kw) with c = (c_im*ksize + kh)*ksize + kw,
+// or 0 where the tap falls in the padding.
+//
+// im2col: the column buffer is the large, contiguous stream, so a lane owns
+// float4s of it (kUnroll per lane, all gathers issued before the stores) and
+// decomposes each element's flat index with multiply-high divisions. The
+// input taps are gathers that the caches serve: each input element feeds up
+// to ksize^2 rows.
+//
+// col2im: a lane owns image elements and gathers their contributions, so
+// every image element is written once and no atomics are needed. The CPU twin
+// adds contributions in column order; for one image element those come from
+// distinct rows c, i.e. in ascending (kh, kw), which is the order used here,
+// starting from the image's current value -- the result is bit-exact.
+#include "dkz_device.hpp"
+#include "dkz_hints.hpp"
+#include "dkz_internal.hpp"
+
+namespace dkz {
+namespace {
+
+constexpr int kUnroll = 4;
+
+struct ColGeom {
+    uint32_t H, W, Ho, Wo, k, s, p;
+    FastDiv div_plane;  // Ho*Wo
+    FastDiv div_wo;
+    FastDiv div_k;
+    FastDiv div_w;
+    FastDiv div_h;
+    FastDiv div_s;
+};
+
+__device__ __forceinline__ float im2col_at(const float *__restrict__ im, uint32_t e, const ColGeom &g) {
+    const uint32_t row = fdiv(e, g.div_plane);
+    const uint32_t pix = e - row * g.div_plane.d;
+    const uint32_t h = fdiv(pix, g.div_wo);
+    const uint32_t w = pix - h * g.Wo;
+    const uint32_t t = fdiv(row, g.div_k);
+    const uint32_t kw = row - t * g.k;
+    const uint32_t c_im = fdiv(t, g.div_k);
+    const uint32_t kh = t - c_im * g.k;
+    const uint32_t y = h * g.s + kh - g.p;  // wraps above H when the tap is in the top padding
+    const uint32_t x = w * g.s + kw - g.p;
+    if (y >= g.H || x >= g.W) return 0.0f;
+    return im[(c_im * g.H + y) * g.W + x];
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void im2col_vec_kernel(const float *__restrict__ im, float *__restrict__ col,
+                                                            ColGeom g, uint32_t n) {
+    const uint32_t nv = n >> 2;
+    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q = base + u * kBlock;
+        if (q < nv) {
+            const uint32_t e = q << 2;
+            v[u] = make_float4(im2col_at(im, e, g), im2col_at(im, e + 1, g), im2col_at(im, e + 2, g),
+                               im2col_at(im, e + 3, g));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q = base + u * kBlock;
+        if (q < nv) st4<NT>(col, q, v[u]);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3u)) {
+        const uint32_t e = (nv << 2) + threadIdx.x;
+        col[e] = im2col_at(im, e, g);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void im2col_scalar_kernel(const float *__restrict__ im, float *__restrict__ col,
+                                                               ColGeom g, uint32_t n) {
+    for (uint32_t e = blockIdx.x * kBlock + threadIdx.x; e < n; e += gridDim.x * kBlock) col[e] = im2col_at(im, e, g);
+}
+
+// Image element e = (c, y, x): its value plus every column entry that im2col
+// took from it, in ascending (kh, kw).
+__device__ __forceinline__ float col2im_at(const float *__restrict__ col, float acc, uint32_t e,
+                                           const ColGeom &g) {
+    const uint32_t t = fdiv(e, g.div_w);
+    const uint32_t x = e - t * g.W;
+    const uint32_t c = fdiv(t, g.div_h);
+    const uint32_t y = t - c * g.H;
+    const uint32_t plane = g.div_plane.d;
+    for (uint32_t kh = 0; kh < g.k; ++kh) {
+        const uint32_t hy = y + g.p - kh;  // h*stride for the output row h that used this tap
+        if ((int)hy < 0) break;            // larger kh only lowers it further
+        const uint32_t h = fdiv(hy, g.div_s);
+        if (h * g.s != hy || h >= g.Ho) continue;
+        const float *rowp = col + ((c * g.k + kh) * g.k) * plane + h * g.Wo;
+        for (uint32_t kw = 0; kw < g.k; ++kw) {
+            const uint32_t wx = x + g.p - kw;
+            if ((int)wx < 0) break;
+            const uint32_t w = fdiv(wx, g.div_s);
+            if (w * g.s != wx || w >= g.Wo) continue;
+            acc += rowp[kw * plane + w];
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(kBlock) void col2im_kernel(const float *__restrict__ col, float *__restrict__ im,
+                                                        ColGeom g, uint32_t n) {
+    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+    if (e < n) im[e] = col2im_at(col, im[e], e, g);
+}
+
+// gpu.zig:652-653: height_col = (height + 2*pad - ksize)/stride + 1 in usize.
+int make_geom(int channels, int height, int width, int ksize, int stride, int pad, ColGeom *g, uint64_t *ncol,
+              uint64_t *nim) {
+    DKZ_REQUIRE(channels >= 0 && height >= 0 && width >= 0 && pad >= 0);
+    DKZ_REQUIRE(ksize >= 1 && stride >= 1);
+    DKZ_REQUIRE((int64_t)height + 2 * (int64_t)pad >= ksize && (int64_t)width + 2 * (int64_t)pad >= ksize);
+    const uint64_t ho = ((uint64_t)height + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t wo = ((uint64_t)width + 2 * (uint64_t)pad - ksize) / stride + 1;
+    *ncol = (uint64_t)channels * ksize * ksize * ho * wo;
+    *nim = (uint64_t)channels * height * width;
+    DKZ_REQUIRE(*ncol <= kMaxElems && *nim <= kMaxElems);
+    DKZ_REQUIRE(ho * stride + ksize + (uint64_t)height + 2 * (uint64_t)pad <= kMaxElems);
+    g->H = (uint32_t)height;
+    g->W = (uint32_t)width;
+    g->Ho = (uint32_t)ho;
+    g->Wo = (uint32_t)wo;
+    g->k = (uint32_t)ksize;
+    g->s = (uint32_t)stride;
+    g->p = (uint32_t)pad;
+    g->div_plane = make_fastdiv((uint32_t)(ho * wo));
+    g->div_wo = make_fastdiv((uint32_t)wo);
+    g->div_k = make_fastdiv((uint32_t)ksize);
+    g->div_w = make_fastdiv(width > 0 ? (uint32_t)width : 1u);
+    g->div_h = make_fastdiv(height > 0 ? (uint32_t)height : 1u);
+    g->div_s = make_fastdiv((uint32_t)stride);
+    return 0;
+}
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+extern "C" {
+
+int dkz_im2col(const float *im, int channels, int height, int width, int ksize, int stride, int pad, float *col) {
+    ColGeom g;
+    uint64_t ncol, nim;
+    DKZ_TRY(make_geom(channels, height, width, ksize, stride, pad, &g, &ncol, &nim));
+    if (ncol == 0) return 0;
+    DKZ_REQUIRE(im != nullptr && col != nullptr);
+    const uint32_t n = (uint32_t)ncol;
+    if (aligned16(col)) {
+        const uint32_t nv = n >> 2;
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
+        return launch("im2col", im2col_vec_kernel<(DKZ_HINT_IM2COL & 2) != 0>, dim3(grid), dim3(kBlock), im, col,
+                      g, n);
+    }
+    const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
+    return launch("im2col", im2col_scalar_kernel, dim3(grid), dim3(kBlock), im, col, g, n);
+}
+
+int dkz_col2im(const float *col, int channels, int height, int width, int ksize, int stride, int pad, float *im) {
+    ColGeom g;
+    uint64_t ncol, nim;
+    DKZ_TRY(make_geom(channels, height, width, ksize, stride, pad, &g, &ncol, &nim));
+    if (nim == 0) return 0;
+    DKZ_REQUIRE(im != nullptr && col != nullptr);
+    const uint32_t n = (uint32_t)nim;
+    return launch("col2im", col2im_kernel, dim3(div_up(n, kBlock)), dim3(kBlock), col, im, g, n);
+}
+
+}  // extern "C"

@@ -176,6 +176,14 @@ def mul(n: int, x: Buf, y: Buf) -> None:
     _must(_lib.load().dkz_mul(n, _p(x), _p(y)), "mul")
 
 
+def addScalar(n: int, alpha: float, x: Buf) -> None:  # gpu.zig:503
+    _must(_lib.load().dkz_add_scalar(n, alpha, _p(x)), "add_scalar")
+
+
+def randUniform(n: int, x: Buf, seed: int) -> None:  # gpu.zig:511 (seed: u32)
+    _must(_lib.load().dkz_rand_uniform(n, _p(x), seed & 0xFFFFFFFF), "rand_uniform")
+
+
 def constrainArray(n: int, alpha: float, x: Buf) -> None:
     _must(_lib.load().dkz_constrain(n, alpha, _p(x)), "constrain")
 
@@ -343,6 +351,31 @@ def shortcut(
     batch: int, w1: int, h1: int, c1: int, add: Buf, w2: int, h2: int, c2: int, s1: float, s2: float, out: Buf
 ) -> None:
     _must(_lib.load().dkz_shortcut(batch, w1, h1, c1, _p(add), w2, h2, c2, s1, s2, _p(out)), "shortcut")
+
+
+# ---------------------------------------------------------------------------
+# convolution helpers (gpu.zig:651-669)
+# ---------------------------------------------------------------------------
+
+
+def im2col(im: Buf, channels: int, height: int, width: int, ksize: int, stride: int, pad: int, col: Buf) -> None:
+    _must(_lib.load().dkz_im2col(_p(im), channels, height, width, ksize, stride, pad, _p(col)), "im2col")
+
+
+def col2im(col: Buf, channels: int, height: int, width: int, ksize: int, stride: int, pad: int, im: Buf) -> None:
+    _must(_lib.load().dkz_col2im(_p(col), channels, height, width, ksize, stride, pad, _p(im)), "col2im")
+
+
+def dropout(input: Buf, size: int, rand_buf: Buf, prob: float, scale: float) -> None:  # gpu.zig:769
+    _must(_lib.load().dkz_dropout(_p(input), size, _p(rand_buf), prob, scale), "dropout")
+
+
+def adamUpdate(
+    w: Buf, d: Buf, m: Buf, v: Buf, b1: float, b2: float, eps: float, decay: float, rate: float, n: int,
+    batch: int, t: int,
+) -> None:  # gpu.zig:804-830
+    _must(_lib.load().dkz_adam_update(_p(w), _p(d), _p(m), _p(v), b1, b2, eps, decay, rate, n, batch, t),
+          "adam_update")
 
 
 # ---- fused batch-norm layer passes (no single gpu.zig counterpart: each

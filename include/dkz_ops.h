@@ -147,9 +147,19 @@ int dkz_scal(int n, float alpha, float *x);
 /* gpu.zig:499 mul(n, x, y): y[i] *= x[i].                 blas.zig:31 */
 int dkz_mul(int n, const float *x, float *y);
 
+/* gpu.zig:503 addScalar(n, alpha, x): x[i] += alpha (darknet_kernels.hip:150-153;
+ * the cost layer's label smoothing, layers/misc.zig:186-188). */
+int dkz_add_scalar(int n, float alpha, float *x);
+
 /* gpu.zig:507 constrainArray(n, alpha, x): clamp to [-alpha, alpha]; NaN
  * becomes +alpha as std.math.clamp does (blas.zig:44-46). */
 int dkz_constrain(int n, float alpha, float *x);
+
+/* gpu.zig:511 randUniform(n, x, seed): x[i] = (hash(seed ^ hash(i)) >> 8) * 2^-24,
+ * a counter-based draw in [0, 1) that depends on (seed, i) only; hash is
+ * Wellons' lowbias32 (darknet_kernels.hip:168-183, the only definition: the
+ * CPU path draws from its own generator, layers/misc.zig:107). */
+int dkz_rand_uniform(int n, float *x, unsigned int seed);
 
 /* gpu.zig:515 activateArray(x, n, a): x[i] = act(x[i]) (activations.zig:58-81,
  * 107-125). Exp-based activations use a bit-exact restatement of the host
@@ -264,6 +274,41 @@ int dkz_backward_avgpool(int n, int w, int h, int c, float *in_delta, const floa
  * blas.zig:290-322 */
 int dkz_shortcut(int batch, int w1, int h1, int c1, const float *add, int w2, int h2, int c2,
                  float s1, float s2, float *out);
+
+/* ------------------------------------------------------------------------ */
+/* Convolution lowering (gpu.zig:651-669, im2col.zig:13-83)                   */
+/* ------------------------------------------------------------------------ */
+
+/* gpu.zig:651 im2col(im, channels, height, width, ksize, stride, pad, col): col
+ * is channels*ksize*ksize rows of height_col*width_col, height_col =
+ * (height + 2*pad - ksize)/stride + 1; row (c*ksize + kh)*ksize + kw holds
+ * im[c, h*stride - pad + kh, w*stride - pad + kw], 0 in the padding.
+ * ksize > height + 2*pad (or width) or stride < 1 is hipErrorInvalidValue.
+ * im2col.zig:13-49 */
+int dkz_im2col(const float *im, int channels, int height, int width, int ksize, int stride, int pad,
+               float *col);
+
+/* gpu.zig:661 col2im(col, channels, height, width, ksize, stride, pad, im): the
+ * adjoint, accumulated: every column entry is added to the image element
+ * im2col took it from, an element's contributions in column order.
+ * im2col.zig:54-83 */
+int dkz_col2im(const float *col, int channels, int height, int width, int ksize, int stride, int pad,
+               float *im);
+
+/* gpu.zig:769 dropout(input, size, rand, prob, scale): input[i] = rand[i] < prob ?
+ * 0 : input[i] * scale, the rule of layers/misc.zig:105-127 (forward after
+ * randUniform, and backward on the delta with the same draws). */
+int dkz_dropout(float *input, int size, const float *rand, float prob, float scale);
+
+/* gpu.zig:804-830 adamUpdate(w, d, m, v, b1, b2, eps, decay, rate, n, batch, t):
+ * the wrapper's eight launches -- scal(b1, m), scal(b2, v),
+ * axpy(-decay*batch, w, d), axpy(1-b1, d, m), mul(d, d), axpy(1-b2, d, v),
+ * w += rate*mhat/(sqrt(vhat)+eps) with mhat = m/(1-b1^t), vhat = v/(1-b2^t)
+ * (darknet_kernels.hip:588-595), fill(d, 0) -- as one pass over the four
+ * vectors with the same per-element roundings. w, d, m and v must not
+ * overlap (hipErrorInvalidValue otherwise); b^t is the host libm's powf. */
+int dkz_adam_update(float *w, float *d, float *m, float *v, float b1, float b2, float eps, float decay,
+                    float rate, int n, int batch, int t);
 
 /* ---- fused batch-norm layer passes ------------------------------------------
  * Each replaces a sequence of the calls above that the layers issue; the

@@ -535,3 +535,130 @@ float ref_pow_f32(float x, float y) {
     }
     return scalbnf(a1, ae);
 }
+
+/* ------------------------------------------------------------------------ */
+/* The rest of gpu.zig's op surface: ops whose only definition in the       */
+/* reference is the device kernel (no CPU twin), restated from it, and the  */
+/* CPU halves of the layers that call them.                                  */
+/* ------------------------------------------------------------------------ */
+
+/* darknet_kernels.hip:150-153 (add_scalar_kernel, behind gpu.zig:503
+ * addScalar; the cost layer's label smoothing, misc.zig:186-188). */
+void ref_add_scalar(float alpha, float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] += alpha;
+}
+
+/* darknet_kernels.hip:168-175: Chris Wellons' "lowbias32" integer hash (Hash
+ * Prospector), xorshift-multiply with two odd constants. */
+uint32_t ref_hash_u32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+/* darknet_kernels.hip:177-183 (rand_uniform_kernel, gpu.zig:511 randUniform):
+ * element i = top 24 bits of hash(seed ^ hash(i)) times 2^-24, in [0, 1). */
+void ref_rand_uniform(float *x, size_t n, uint32_t seed) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t h = ref_hash_u32(seed ^ ref_hash_u32((uint32_t)i));
+        x[i] = (float)(h >> 8) * (1.0f / 16777216.0f);
+    }
+}
+
+/* layers/misc.zig:105-127 (forwardDropout's mask step given the uniform
+ * draws, and backwardDropout): a draw below `prob` zeroes the element,
+ * otherwise it is multiplied by `scale`. gpu.zig:769 / .hip:189-192 apply the
+ * same rule on the device. */
+void ref_dropout(float *x, size_t n, const float *rand, float prob, float scale) {
+    for (size_t i = 0; i < n; ++i) {
+        if (rand[i] < prob)
+            x[i] = 0.0f;
+        else
+            x[i] *= scale;
+    }
+}
+
+/* gpu.zig:804-830 adamUpdate: the twins' scal/axpy/mul steps in the wrapper's
+ * order, then darknet_kernels.hip:588-595 (adam_kernel, no CPU twin):
+ * mhat = m / (1 - b1^t), vhat = v / (1 - b2^t), w += rate*mhat/(sqrt(vhat)+eps),
+ * and finally d = 0. The step count t reaches powf as a float. */
+void ref_adam_update(float *w, float *d, float *m, float *v, float b1, float b2, float eps,
+                     float decay, float rate, size_t n, size_t batch, size_t t) {
+    ref_scal(b1, m, n);
+    ref_scal(b2, v, n);
+    ref_axpy(-decay * (float)batch, w, d, n);
+    ref_axpy(1.0f - b1, d, m, n);
+    ref_mul(d, d, n);
+    ref_axpy(1.0f - b2, d, v, n);
+    const float c1 = 1.0f - powf(b1, (float)(int)t);
+    const float c2 = 1.0f - powf(b2, (float)(int)t);
+    for (size_t i = 0; i < n; ++i) {
+        const float mhat = m[i] / c1;
+        const float vhat = v[i] / c2;
+        w[i] = w[i] + rate * mhat / (sqrtf(vhat) + eps);
+    }
+    ref_fill(d, n, 0.0f);
+}
+
+/* ------------------------------------------------------------------------ */
+/* im2col.zig: the convolution lowering                                      */
+/* ------------------------------------------------------------------------ */
+
+/* im2col.zig:9-11 */
+size_t ref_conv_out_dim(size_t size, size_t ksize, size_t stride, size_t pad) {
+    return (size + 2 * pad - ksize) / stride + 1;
+}
+
+/* im2col.zig:13-49: column row c = (c_im, h_offset, w_offset); taps that fall
+ * in the padding are 0. */
+void ref_im2col(const float *data_im, size_t channels, size_t height, size_t width, size_t ksize,
+                size_t stride, size_t pad, float *data_col) {
+    const size_t hc = ref_conv_out_dim(height, ksize, stride, pad);
+    const size_t wc = ref_conv_out_dim(width, ksize, stride, pad);
+    const size_t cc = channels * ksize * ksize;
+    for (size_t c = 0; c < cc; ++c) {
+        const size_t w_off = c % ksize;
+        const size_t h_off = (c / ksize) % ksize;
+        const size_t c_im = c / ksize / ksize;
+        for (size_t h = 0; h < hc; ++h) {
+            const long row = (long)(h_off + h * stride) - (long)pad;
+            float *dst = data_col + (c * hc + h) * wc;
+            if (row < 0 || row >= (long)height) {
+                memset(dst, 0, wc * sizeof(float));
+                continue;
+            }
+            const float *src = data_im + (c_im * height + (size_t)row) * width;
+            for (size_t w = 0; w < wc; ++w) {
+                const long col = (long)(w_off + w * stride) - (long)pad;
+                dst[w] = (col >= 0 && col < (long)width) ? src[col] : 0.0f;
+            }
+        }
+    }
+}
+
+/* im2col.zig:54-83: the adjoint, accumulated into data_im in column order. */
+void ref_col2im(const float *data_col, size_t channels, size_t height, size_t width, size_t ksize,
+                size_t stride, size_t pad, float *data_im) {
+    const size_t hc = ref_conv_out_dim(height, ksize, stride, pad);
+    const size_t wc = ref_conv_out_dim(width, ksize, stride, pad);
+    const size_t cc = channels * ksize * ksize;
+    for (size_t c = 0; c < cc; ++c) {
+        const size_t w_off = c % ksize;
+        const size_t h_off = (c / ksize) % ksize;
+        const size_t c_im = c / ksize / ksize;
+        for (size_t h = 0; h < hc; ++h) {
+            const long row = (long)(h_off + h * stride) - (long)pad;
+            if (row < 0 || row >= (long)height) continue;
+            float *dst = data_im + (c_im * height + (size_t)row) * width;
+            const float *src = data_col + (c * hc + h) * wc;
+            for (size_t w = 0; w < wc; ++w) {
+                const long col = (long)(w_off + w * stride) - (long)pad;
+                if (col < 0 || col >= (long)width) continue;
+                dst[col] += src[w];
+            }
+        }
+    }
+}

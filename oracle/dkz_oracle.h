@@ -83,6 +83,23 @@ void ref_forward_avgpool(size_t batch, size_t w, size_t h, size_t c, const float
 void ref_backward_avgpool(size_t batch, size_t w, size_t h, size_t c, const float *out_delta,
                           float *in_delta);
 
+/* gpu.zig:503 addScalar, :511 randUniform, :769 dropout, :804-830 adamUpdate
+ * (device kernels darknet_kernels.hip:150-153, 168-192, 588-595; the dropout
+ * rule is also layers/misc.zig:105-127's CPU loop). */
+void ref_add_scalar(float alpha, float *x, size_t n);
+uint32_t ref_hash_u32(uint32_t x);
+void ref_rand_uniform(float *x, size_t n, uint32_t seed);
+void ref_dropout(float *x, size_t n, const float *rand, float prob, float scale);
+void ref_adam_update(float *w, float *d, float *m, float *v, float b1, float b2, float eps,
+                     float decay, float rate, size_t n, size_t batch, size_t t);
+
+/* im2col.zig:9-83 */
+size_t ref_conv_out_dim(size_t size, size_t ksize, size_t stride, size_t pad);
+void ref_im2col(const float *data_im, size_t channels, size_t height, size_t width, size_t ksize,
+                size_t stride, size_t pad, float *data_col);
+void ref_col2im(const float *data_col, size_t channels, size_t height, size_t width, size_t ksize,
+                size_t stride, size_t pad, float *data_im);
+
 /* Zig 0.16 std.math.pow(f32, x, y), used by blas.zig:176. */
 float ref_pow_f32(float x, float y);
 

@@ -55,6 +55,14 @@ _SIGS = {
     "ref_backward_maxpool": (None, [_sz, _P, _P, _P]),
     "ref_forward_avgpool": (None, [_sz, _sz, _sz, _sz, _P, _P]),
     "ref_backward_avgpool": (None, [_sz, _sz, _sz, _sz, _P, _P]),
+    "ref_add_scalar": (None, [_f, _P, _sz]),
+    "ref_hash_u32": (C.c_uint32, [C.c_uint32]),
+    "ref_rand_uniform": (None, [_P, _sz, C.c_uint32]),
+    "ref_dropout": (None, [_P, _sz, _P, _f, _f]),
+    "ref_adam_update": (None, [_P, _P, _P, _P, _f, _f, _f, _f, _f, _sz, _sz, _sz]),
+    "ref_conv_out_dim": (_sz, [_sz, _sz, _sz, _sz]),
+    "ref_im2col": (None, [_P, _sz, _sz, _sz, _sz, _sz, _sz, _P]),
+    "ref_col2im": (None, [_P, _sz, _sz, _sz, _sz, _sz, _sz, _P]),
     "ref_pow_f32": (_f, [_f, _f]),
     "ref_expf": (_f, [_f]),
 }
@@ -226,6 +234,44 @@ def forwardAvgpool(batch, w, h, c, input, output) -> None:
 
 def backwardAvgpool(batch, w, h, c, out_delta, in_delta) -> None:
     lib().ref_backward_avgpool(batch, w, h, c, _ptr(out_delta), _ptr(in_delta))
+
+
+# ---- the rest of gpu.zig's surface (kernel-defined ops, misc.zig dropout) ----
+
+
+def addScalar(alpha: float, x: np.ndarray) -> None:
+    lib().ref_add_scalar(alpha, _ptr(x), x.size)
+
+
+def hash_u32(x: int) -> int:
+    return lib().ref_hash_u32(x & 0xFFFFFFFF)
+
+
+def randUniform(x: np.ndarray, seed: int) -> None:
+    lib().ref_rand_uniform(_ptr(x), x.size, seed & 0xFFFFFFFF)
+
+
+def dropout(x: np.ndarray, rand: np.ndarray, prob: float, scale: float) -> None:
+    lib().ref_dropout(_ptr(x), x.size, _ptr(rand), prob, scale)
+
+
+def adamUpdate(w, d, m, v, b1, b2, eps, decay, rate, n, batch, t) -> None:
+    lib().ref_adam_update(_ptr(w), _ptr(d), _ptr(m), _ptr(v), b1, b2, eps, decay, rate, n, batch, t)
+
+
+# ---- im2col.zig ---------------------------------------------------------------
+
+
+def conv_out_dim(size, ksize, stride, pad) -> int:
+    return lib().ref_conv_out_dim(size, ksize, stride, pad)
+
+
+def im2col(im, channels, height, width, ksize, stride, pad, col) -> None:
+    lib().ref_im2col(_ptr(im), channels, height, width, ksize, stride, pad, _ptr(col))
+
+
+def col2im(col, channels, height, width, ksize, stride, pad, im) -> None:
+    lib().ref_col2im(_ptr(col), channels, height, width, ksize, stride, pad, _ptr(im))
 
 
 def pow_f32(x: float, y: float) -> float:

@@ -58,6 +58,22 @@ CASES = [
         "args": {"batch": 3, "n": 5, "size": 7},
         "expect": {"each_index_hit": 1},
     },
+    {
+        "source": "src/im2col.zig:87-95",
+        "name": "im2col of a 3x3 image with a 2x2 kernel",
+        "op": "im2col",
+        "args": {"im": [1, 2, 3, 4, 5, 6, 7, 8, 9], "channels": 1, "height": 3, "width": 3, "ksize": 2,
+                 "stride": 1, "pad": 0, "col_len": 16},
+        "expect": {"col[0:4]": [1, 2, 4, 5], "col[12:16]": [5, 6, 8, 9], "exact": True},
+    },
+    {
+        "source": "src/im2col.zig:97-104",
+        "name": "col2im accumulates overlapping contributions",
+        "op": "col2im",
+        "args": {"col_fill": 1.0, "col_len": 16, "channels": 1, "height": 3, "width": 3, "ksize": 2,
+                 "stride": 1, "pad": 0, "im_len": 9},
+        "expect": {"im[4]": 4.0, "im[0]": 1.0, "abs_tol": 1e-6},
+    },
 ]
 
 

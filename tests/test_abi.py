@@ -22,13 +22,15 @@ ROOT = _lib.LIB_PATH.parents[1]
 HEADER = ROOT / "include" / "dkz_ops.h"
 
 # The public op wrappers of src/gpu.zig:483-800 on this path, and their
-# mirror in darknet_zig_amd.gpu (addScalar, randUniform, dropout, im2col,
-# col2im, gemm and adamUpdate are outside the path).
+# mirror in darknet_zig_amd.gpu.
 GPU_ZIG_OPS = [
-    "fill", "copy", "axpy", "scal", "mul", "constrainArray", "activateArray", "gradientArray",
+    "fill", "copy", "axpy", "scal", "mul", "addScalar", "constrainArray", "randUniform", "activateArray",
+    "gradientArray",
     "addBias", "scaleBias", "backwardBias", "backwardScale", "mean", "variance", "normalize",
     "meanDelta", "varianceDelta", "normalizeDelta", "softmax", "softmaxCrossEntropy", "l2", "l1",
-    "smoothL1", "forwardMaxpool", "backwardMaxpool", "forwardAvgpool", "backwardAvgpool", "shortcut",
+    "smoothL1", "forwardMaxpool", "backwardMaxpool", "forwardAvgpool", "backwardAvgpool", "im2col", "col2im",
+    "dropout", "shortcut",
+    "adamUpdate",
 ]
 
 
@@ -45,7 +47,7 @@ def exported_symbols() -> set[str]:
 
 def test_header_exports_and_binding_agree():
     declared = header_symbols()
-    assert len(declared) == len(set(declared)) == 46
+    assert len(declared) == len(set(declared)) == 52
     assert set(declared) == exported_symbols()
     assert list(_lib.SIGNATURES) == declared  # same set, same order as the header
 
@@ -123,6 +125,25 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_batchnorm_backward(2, 3, 4, 7, None, P, P, P, P, P, P, P, P, P, P), INVALID),  # y
         (lambda L: L.dkz_batchnorm_backward(2, 3, 4, 7, P, P, P, P, P, P, P, P, P, None, P), INVALID),
         (lambda L: L.dkz_batchnorm_backward(0, 0, 4, 7, *[None] * 11), 0),
+        (lambda L: L.dkz_add_scalar(-2, 1.0, P), INVALID),
+        (lambda L: L.dkz_add_scalar(3, 1.0, None), INVALID),
+        (lambda L: L.dkz_rand_uniform(0, None, 7), 0),
+        (lambda L: L.dkz_rand_uniform(9, None, 7), INVALID),
+        (lambda L: L.dkz_dropout(P, 5, None, 0.5, 2.0), INVALID),
+        (lambda L: L.dkz_dropout(None, 0, None, 0.5, 2.0), 0),
+        (lambda L: L.dkz_adam_update(None, None, None, None, 0.9, 0.999, 1e-7, 0.0, 0.1, 0, 1, 1), 0),
+        (lambda L: L.dkz_adam_update(P, P, C.c_void_p(4096), C.c_void_p(8192), 0.9, 0.999, 1e-7, 0.0, 0.1, 4, 1,
+                                     1), INVALID),  # w and d overlap
+        (lambda L: L.dkz_adam_update(P, C.c_void_p(32), C.c_void_p(4096), C.c_void_p(8192), 0.9, 0.999, 1e-7, 0.0,
+                                     0.1, 5, 1, 1), INVALID),  # [16, 36) and [32, 52) overlap
+        (lambda L: L.dkz_adam_update(P, P, P, P, 0.9, 0.999, 1e-7, 0.0, 0.1, -1, 1, 1), INVALID),
+        (lambda L: L.dkz_im2col(P, 3, 4, 4, 7, 1, 1, P), INVALID),  # window larger than the padded image
+        (lambda L: L.dkz_im2col(P, 3, 4, 4, 3, 0, 1, P), INVALID),  # stride 0
+        (lambda L: L.dkz_im2col(P, 3, 4, 4, 0, 1, 1, P), INVALID),  # ksize 0
+        (lambda L: L.dkz_im2col(None, 0, 4, 4, 3, 1, 1, None), 0),  # no channels
+        (lambda L: L.dkz_col2im(P, 3, 4, -4, 3, 1, 1, P), INVALID),
+        (lambda L: L.dkz_col2im(P, 3, 4, 4, 3, 1, 1, None), INVALID),
+        (lambda L: L.dkz_col2im(P, 65536, 256, 256, 3, 1, 1, P), INVALID),  # beyond 32-bit indexing
         (lambda L: L.dkz_malloc(None, 4), INVALID),
         (lambda L: L.dkz_free(None), 0),
         (lambda L: L.dkz_copy_to_host(None, None, 0), 0),
