@@ -366,6 +366,14 @@ def col2im(col: Buf, channels: int, height: int, width: int, ksize: int, stride:
     _must(_lib.load().dkz_col2im(_p(col), channels, height, width, ksize, stride, pad, _p(im)), "col2im")
 
 
+def gemm(
+    ta: bool, tb: bool, m: int, n: int, k: int, alpha: float, a: Buf, lda: int, b: Buf, ldb: int, beta: float,
+    c: Buf, ldc: int,
+) -> None:  # gpu.zig:671-719
+    _must(_lib.load().dkz_gemm(1 if ta else 0, 1 if tb else 0, m, n, k, alpha, _p(a), lda, _p(b), ldb, beta, _p(c),
+                               ldc), "gemm")
+
+
 def dropout(input: Buf, size: int, rand_buf: Buf, prob: float, scale: float) -> None:  # gpu.zig:769
     _must(_lib.load().dkz_dropout(_p(input), size, _p(rand_buf), prob, scale), "dropout")
 

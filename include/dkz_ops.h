@@ -295,6 +295,17 @@ int dkz_im2col(const float *im, int channels, int height, int width, int ksize, 
 int dkz_col2im(const float *col, int channels, int height, int width, int ksize, int stride, int pad,
                float *im);
 
+/* gpu.zig:671-719 gemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
+ * C = alpha*op(A)*op(B) + beta*C, all row-major; op(A) is m x k (A is k x m
+ * with leading dimension lda when ta != 0), op(B) is k x n. beta == 0 clears
+ * C first (NaN included), beta != 1 scales it (gemm.zig:121-131). fp32
+ * products and sums on the matrix cores: results agree with the CPU twin
+ * within fp32 summation error. m == 0 or n == 0 does nothing (gpu.zig:686);
+ * a leading dimension below the row length is hipErrorInvalidValue.
+ * gemm.zig:47-278 */
+int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, int lda, const float *b,
+             int ldb, float beta, float *c, int ldc);
+
 /* gpu.zig:769 dropout(input, size, rand, prob, scale): input[i] = rand[i] < prob ?
  * 0 : input[i] * scale, the rule of layers/misc.zig:105-127 (forward after
  * randUniform, and backward on the delta with the same draws). */

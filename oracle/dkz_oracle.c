@@ -662,3 +662,70 @@ void ref_col2im(const float *data_col, size_t channels, size_t height, size_t wi
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* gemm.zig: C = alpha*op(A)*op(B) + beta*C, row-major                       */
+/* ------------------------------------------------------------------------ */
+
+/* gemm.zig:185-228 (gemmPanel, mr = 4 rows at once; the vector width only
+ * groups columns, each column's sum runs over p in order) and gemm.zig:230-244
+ * (gemmRow for the rows left over). The loops run under
+ * @setFloatMode(.optimized), so LLVM contracts the multiply-adds to fma on an
+ * FMA host and may regroup them: the accumulate steps are written with fmaf
+ * here, and any summation order within fp32 rounding error is as valid. */
+static void gemm_panel_rows(int ta, size_t i0, size_t rows, size_t n, size_t k, float alpha,
+                            const float *a, size_t lda, const float *b, size_t ldb, float *c,
+                            size_t ldc) {
+    for (size_t q = 0; q < n; ++q) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (size_t p = 0; p < k; ++p) {
+            const float bv = b[p * ldb + q];
+            for (size_t r = 0; r < rows; ++r) {
+                const float s = ta ? a[p * lda + i0 + r] : a[(i0 + r) * lda + p];
+                acc[r] = fmaf(s, bv, acc[r]);
+            }
+        }
+        for (size_t r = 0; r < rows; ++r) c[(i0 + r) * ldc + q] = fmaf(alpha, acc[r], c[(i0 + r) * ldc + q]);
+    }
+}
+
+static void gemm_row(int ta, size_t i, size_t n, size_t k, float alpha, const float *a, size_t lda,
+                     const float *b, size_t ldb, float *c, size_t ldc) {
+    for (size_t p = 0; p < k; ++p) {
+        const float scale = alpha * (ta ? a[p * lda + i] : a[i * lda + p]);
+        if (scale == 0.0f) continue;
+        for (size_t q = 0; q < n; ++q) c[i * ldc + q] = fmaf(scale, b[p * ldb + q], c[i * ldc + q]);
+    }
+}
+
+/* gemm.zig:47-141 (gemm, runJob: beta first -- 0 clears the row, anything but
+ * 1 scales it -- then the variant), :249-278 (gemmNT / gemmTT: one dot
+ * product per output element, c += alpha*sum). */
+void ref_gemm(int ta, int tb, size_t m, size_t n, size_t k, float alpha, const float *a, size_t lda,
+              const float *b, size_t ldb, float beta, float *c, size_t ldc) {
+    if (m == 0 || n == 0) return;
+    if (beta != 1.0f) {
+        for (size_t i = 0; i < m; ++i) {
+            float *row = c + i * ldc;
+            if (beta == 0.0f)
+                memset(row, 0, n * sizeof(float));
+            else
+                for (size_t q = 0; q < n; ++q) row[q] *= beta;
+        }
+    }
+    if (!tb) {
+        size_t i = 0;
+        for (; i + 4 <= m; i += 4) gemm_panel_rows(ta, i, 4, n, k, alpha, a, lda, b, ldb, c, ldc);
+        for (; i < m; ++i) gemm_row(ta, i, n, k, alpha, a, lda, b, ldb, c, ldc);
+        return;
+    }
+    for (size_t i = 0; i < m; ++i)
+        for (size_t q = 0; q < n; ++q) {
+            float sum = 0.0f;
+            for (size_t p = 0; p < k; ++p) {
+                const float av = ta ? a[i + p * lda] : a[i * lda + p];
+                sum = fmaf(av, b[q * ldb + p], sum);
+            }
+            c[i * ldc + q] = fmaf(alpha, sum, c[i * ldc + q]);
+        }
+}

@@ -100,6 +100,11 @@ void ref_im2col(const float *data_im, size_t channels, size_t height, size_t wid
 void ref_col2im(const float *data_col, size_t channels, size_t height, size_t width, size_t ksize,
                 size_t stride, size_t pad, float *data_im);
 
+/* gemm.zig:47-278: C = alpha*op(A)*op(B) + beta*C, row-major, ta/tb select
+ * the transposed operand layouts. */
+void ref_gemm(int ta, int tb, size_t m, size_t n, size_t k, float alpha, const float *a, size_t lda,
+              const float *b, size_t ldb, float beta, float *c, size_t ldc);
+
 /* Zig 0.16 std.math.pow(f32, x, y), used by blas.zig:176. */
 float ref_pow_f32(float x, float y);
 

@@ -63,6 +63,7 @@ _SIGS = {
     "ref_conv_out_dim": (_sz, [_sz, _sz, _sz, _sz]),
     "ref_im2col": (None, [_P, _sz, _sz, _sz, _sz, _sz, _sz, _P]),
     "ref_col2im": (None, [_P, _sz, _sz, _sz, _sz, _sz, _sz, _P]),
+    "ref_gemm": (None, [_i, _i, _sz, _sz, _sz, _f, _P, _sz, _P, _sz, _f, _P, _sz]),
     "ref_pow_f32": (_f, [_f, _f]),
     "ref_expf": (_f, [_f]),
 }
@@ -272,6 +273,13 @@ def im2col(im, channels, height, width, ksize, stride, pad, col) -> None:
 
 def col2im(col, channels, height, width, ksize, stride, pad, im) -> None:
     lib().ref_col2im(_ptr(col), channels, height, width, ksize, stride, pad, _ptr(im))
+
+
+# ---- gemm.zig ------------------------------------------------------------------
+
+
+def gemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc) -> None:
+    lib().ref_gemm(int(bool(ta)), int(bool(tb)), m, n, k, alpha, _ptr(a), lda, _ptr(b), ldb, beta, _ptr(c), ldc)
 
 
 def pow_f32(x: float, y: float) -> float:

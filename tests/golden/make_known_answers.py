@@ -74,6 +74,17 @@ CASES = [
                  "stride": 1, "pad": 0, "im_len": 9},
         "expect": {"im[4]": 4.0, "im[0]": 1.0, "abs_tol": 1e-6},
     },
+    {
+        "source": "src/gemm.zig:265-315",
+        "name": "gemm variants agree with a naive reference",
+        "op": "gemm",
+        "args": {"m": 5, "n": 4, "k": 3, "a": "a[i] = i % 7 over m*k, row-major m x k",
+                 "b": "b[i] = i % 5 over k*n, row-major k x n",
+                 "transposed": "at[p*m + i] = a[i*k + p], bt[q*k + p] = b[p*n + q]",
+                 "alpha": 2.0, "beta": 1.0, "c0": 0.0, "lda": "m if ta else k", "ldb": "k if tb else n",
+                 "ldc": "n", "variants": [[False, False], [True, False], [False, True], [True, True]]},
+        "expect": {"want": "want[i*n + q] = 2 * sum_p a[i*k + p] * b[p*n + q]", "abs_tol": 1e-4},
+    },
 ]
 
 

@@ -28,7 +28,7 @@ GPU_ZIG_OPS = [
     "gradientArray",
     "addBias", "scaleBias", "backwardBias", "backwardScale", "mean", "variance", "normalize",
     "meanDelta", "varianceDelta", "normalizeDelta", "softmax", "softmaxCrossEntropy", "l2", "l1",
-    "smoothL1", "forwardMaxpool", "backwardMaxpool", "forwardAvgpool", "backwardAvgpool", "im2col", "col2im",
+    "smoothL1", "forwardMaxpool", "backwardMaxpool", "forwardAvgpool", "backwardAvgpool", "im2col", "col2im", "gemm",
     "dropout", "shortcut",
     "adamUpdate",
 ]
@@ -47,7 +47,7 @@ def exported_symbols() -> set[str]:
 
 def test_header_exports_and_binding_agree():
     declared = header_symbols()
-    assert len(declared) == len(set(declared)) == 52
+    assert len(declared) == len(set(declared)) == 53
     assert set(declared) == exported_symbols()
     assert list(_lib.SIGNATURES) == declared  # same set, same order as the header
 
@@ -144,6 +144,13 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_col2im(P, 3, 4, -4, 3, 1, 1, P), INVALID),
         (lambda L: L.dkz_col2im(P, 3, 4, 4, 3, 1, 1, None), INVALID),
         (lambda L: L.dkz_col2im(P, 65536, 256, 256, 3, 1, 1, P), INVALID),  # beyond 32-bit indexing
+        (lambda L: L.dkz_gemm(0, 0, 0, 5, 5, 1.0, None, 5, None, 5, 0.0, None, 5), 0),  # m == 0
+        (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, P, 2, P, 5, 0.0, P, 5), INVALID),  # lda < k
+        (lambda L: L.dkz_gemm(1, 0, 4, 5, 3, 1.0, P, 3, P, 5, 0.0, P, 5), INVALID),  # lda < m (A transposed)
+        (lambda L: L.dkz_gemm(0, 1, 4, 5, 3, 1.0, P, 3, P, 2, 0.0, P, 5), INVALID),  # ldb < k (B transposed)
+        (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, P, 3, P, 5, 0.0, P, 4), INVALID),  # ldc < n
+        (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, None, 3, P, 5, 0.0, P, 5), INVALID),
+        (lambda L: L.dkz_gemm(0, 0, 65536, 65536, 3, 1.0, P, 3, P, 65536, 0.0, P, 65536), INVALID),  # > 2^31
         (lambda L: L.dkz_malloc(None, 4), INVALID),
         (lambda L: L.dkz_free(None), 0),
         (lambda L: L.dkz_copy_to_host(None, None, 0), 0),

@@ -1,6 +1,6 @@
 """Pinning the oracle's restatement of the rest of gpu.zig's op surface:
-add_scalar, rand_uniform (with its integer hash), dropout, the Adam update
-and im2col/col2im.
+add_scalar, rand_uniform (with its integer hash), dropout, the Adam update,
+im2col/col2im and gemm.
 
 add_scalar, rand_uniform and the last step of the Adam update have no CPU twin
 in the reference: their only definition is the device kernel
@@ -8,7 +8,9 @@ in the reference: their only definition is the device kernel
 something other than its own formula: a published inverse of the hash,
 distribution properties, the textbook form of Adam (Kingma & Ba 2015,
 Algorithm 1) in f64, numpy's independent arithmetic, the reference's own
-im2col.zig test blocks, and the adjoint identity between im2col and col2im.
+im2col.zig and gemm.zig test blocks, the adjoint identity between im2col and
+col2im, and Higham's a-priori error bound of an fp32 dot product against
+numpy's f64 matrix product.
 """
 
 from __future__ import annotations
@@ -245,3 +247,70 @@ def test_col2im_is_the_adjoint_and_matches_scatter(C, H, W, k, s, p):
     want = pad[:, p:p + H, p:p + W].reshape(-1)
     # the same contributions in the same (column) order on a zero start
     np.testing.assert_array_equal(ty, want)
+
+
+# ---------------------------------------------------------------------------
+# gemm (gemm.zig)
+# ---------------------------------------------------------------------------
+
+
+def test_known_gemm_variants():  # gemm.zig:265-315
+    c = case("gemm")
+    a_ = c["args"]
+    m, n, k = a_["m"], a_["n"], a_["k"]
+    a = (np.arange(m * k) % 7).astype(f32)
+    b = (np.arange(k * n) % 5).astype(f32)
+    at = np.ascontiguousarray(a.reshape(m, k).T).ravel()
+    bt = np.ascontiguousarray(b.reshape(k, n).T).ravel()
+    want = np.zeros(m * n, f32)
+    for i in range(m):
+        for q in range(n):
+            s = f32(0)
+            for p in range(k):
+                s = f32(s + a[i * k + p] * b[p * n + q])
+            want[i * n + q] = 2 * s
+    for ta, tb in a_["variants"]:
+        got = np.zeros(m * n, f32)
+        ref.gemm(ta, tb, m, n, k, a_["alpha"], at if ta else a, m if ta else k, bt if tb else b, k if tb else n,
+                 a_["beta"], got, n)
+        assert np.max(np.abs(got - want)) <= c["expect"]["abs_tol"], (ta, tb)
+        np.testing.assert_array_equal(got, want)  # small integers: exact in any order
+
+
+def gemm_bound(a64, b64, c64, alpha, beta, k):
+    """Higham's a-priori bound for an fp32 dot product of length k, any
+    summation order: gamma_k * sum|alpha a b|, plus the rounding of beta*c and
+    of the final add (3 more roundings)."""
+    u = 2.0 ** -24
+    g = (k + 3) * u / (1 - (k + 3) * u)
+    return g * (abs(alpha) * (np.abs(a64) @ np.abs(b64)) + abs(beta) * np.abs(c64))
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("m,n,k,alpha,beta", [(37, 29, 53, 1.5, 1.0), (8, 16, 300, -0.5, 0.0), (13, 7, 1, 1.0, 0.25),
+                                              (4, 9, 0, 2.0, 3.0)])
+def test_gemm_within_fp32_bound_of_f64(ta, tb, m, n, k, alpha, beta):
+    """gputest.zig:347-387's shapes and flags, against numpy's f64 product;
+    lda/ldb/ldc wider than the matrices (sub-matrix views)."""
+    r = rng(8)
+    A = r.uniform(-1, 1, (m, k)).astype(f32)
+    B = r.uniform(-1, 1, (k, n)).astype(f32)
+    C0 = r.uniform(-1, 1, (m, n)).astype(f32)
+    lda = (m if ta else k) + 3
+    ldb = (k if tb else n) + 2
+    ldc = n + 5
+    ga = np.zeros(((k if ta else m), lda), f32)
+    ga[:, : (m if ta else k)] = A.T if ta else A
+    gb = np.zeros(((n if tb else k), ldb), f32)
+    gb[:, : (k if tb else n)] = B.T if tb else B
+    gc = np.full((m, ldc), 7.0, f32)
+    gc[:, :n] = C0
+    if beta == 0.0:
+        gc[0, 0] = np.nan  # beta = 0 clears C, NaN included (gemm.zig:125-126)
+    ref.gemm(ta, tb, m, n, k, alpha, ga.ravel(), lda, gb.ravel(), ldb, beta, gc.reshape(-1), ldc)  # views
+    A64, B64, C64 = A.astype(np.float64), B.astype(np.float64), C0.astype(np.float64)
+    want = alpha * (A64 @ B64) + (beta * C64 if beta != 0 else 0.0)
+    bound = gemm_bound(A64, B64, C64, alpha, beta, k)
+    assert np.all(np.abs(gc[:, :n] - want) <= bound + 1e-30)
+    assert np.all(gc[:, n:] == 7.0)  # columns past n untouched
