@@ -128,7 +128,16 @@ int dkz_device_name(int device, char *buf, int len) {
     hipDevice_t dev;
     hipError_t e = hipDeviceGet(&dev, device);
     if (e != hipSuccess) return (int)e;
-    return (int)hipDeviceGetName(buf, len - 1 > 0 ? len - 1 : 1, dev);
+    e = hipDeviceGetName(buf, len - 1 > 0 ? len - 1 : 1, dev);
+    if (e != hipSuccess) return (int)e;
+    if (buf[0] == '\0') {
+        // Some boxes report no marketing name; the architecture name is there.
+        hipDeviceProp_t prop;
+        e = hipGetDeviceProperties(&prop, device);
+        if (e != hipSuccess) return (int)e;
+        snprintf(buf, (size_t)len, "%s", prop.gcnArchName);
+    }
+    return 0;
 }
 
 int dkz_mem_info(size_t *free_bytes, size_t *total_bytes) {

@@ -32,6 +32,8 @@ def _ensure_built() -> None:
         ref.build()
     if not native_build.LIB.exists():
         native_build.build()
+    if not native_build.GPUTEST.exists():
+        native_build.build_gputest()
 
 
 _ensure_built()

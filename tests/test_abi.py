@@ -197,3 +197,17 @@ def test_buf_offset():
     b = gpu.Buf(4096, 10)
     assert b.offset(3) == gpu.Buf(4096 + 12, 7)
     assert gpu.Buf().offset(2).is_null()
+
+
+def test_gputest_program_links_and_fails_loudly_without_a_gpu():
+    """The gputest harness resolves libdkz and the oracle, and without a
+    device it stops with gpu.zig's must() message instead of running."""
+    from tests.native import build as native_build
+
+    lib = _lib.load()
+    n = C.c_int(0)
+    if lib.dkz_device_count(C.byref(n)) == 0 and n.value > 0:
+        pytest.skip("a GPU is present")
+    proc = subprocess.run([str(native_build.GPUTEST)], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 2, proc.stdout + proc.stderr
+    assert "selecting the device failed" in proc.stdout
