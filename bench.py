@@ -19,7 +19,12 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                summary profiles/traffic_bn_backward.txt
   per_op       every op of BASELINE.json's five configs timed on its own,
                cold (rotated buffers, >= 512 MB per rotation), in GB/s and as
-               a fraction of 8 TB/s
+               a fraction of 8 TB/s: sustained (back-to-back launches, the
+               per-launch time of a stream of such calls) and single-launch
+               (an event pair around each launch); plus rand_uniform/dropout,
+               the one-pass Adam update and im2col/col2im
+  gemm         dkz_gemm at config 2's convolution shapes and a large square,
+               TFLOP/s against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
                pass and one apply pass, 32 B/elem instead of 56)
   bn_act_gelem_s  config 1 elements / config 1 forward time and config 2
@@ -279,14 +284,21 @@ def per_op_table(gpu, hip, stream, launches: int):
 
     rows = {}
 
-    def row(cfg, name, nbytes, ms):
+    def row(cfg, name, nbytes, ms, single_ms=None):
         g = gbs(nbytes, ms)
-        rows[f"{cfg}/{name}"] = {"us": round(ms * 1e3, 3), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4),
-                                 "bytes": nbytes}
+        rows[f"{cfg}/{name}"] = r = {"us": round(ms * 1e3, 3), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4),
+                                     "bytes": nbytes}
+        if single_ms is not None:
+            r["single_launch_us"] = round(single_ms * 1e3, 3)
+            r["single_launch_frac"] = round(gbs(nbytes, single_ms) / PEAK_GBS, 4)
 
     def add(cfg, name, nbytes, fns):
-        """One op, HIP events around each launch."""
-        row(cfg, name, nbytes, time_op(hip, stream, fns, max(launches, len(fns))))
+        """One op over rotated inputs: sustained (back-to-back launches, events
+        around the run: the per-launch figure of a stream of such calls) and
+        single-launch (an event pair around each launch, which also times
+        ~2 us of dispatch and completion)."""
+        k = max(launches, len(fns))
+        row(cfg, name, nbytes, time_seq(hip, stream, [[f] for f in fns], k), time_op(hip, stream, fns, k))
 
     def add_seq(cfg, name, nbytes, seqs):
         """A call sequence (or a multi-launch entry point), events only around
@@ -427,7 +439,69 @@ def per_op_table(gpu, hip, stream, launches: int):
         [lambda i=i, a=a: gpu.forwardAvgpool(rows_, ph, ph, pc, i, a) for i, a in zip(ins, avg)])
     add(cfg, "avgpool_bwd (global)", 4 * (2 * nin + rows_),
         [lambda i=i, a=a: gpu.backwardAvgpool(rows_, ph, ph, pc, i, a) for i, a in zip(ins, avg)])
+    # the dropout layer (misc.zig:128-141) on a config-5-sized activation
+    seeds = [1234567 + j for j in range(R)]
+    add("dropout[256,512,28,28]", "rand_uniform", 4 * nin,
+        [lambda i=i, s_=s_: gpu.randUniform(nin, i, s_) for i, s_ in zip(ins, seeds)])
+    add("dropout[256,512,28,28]", "dropout", 3 * 4 * nin,
+        [lambda i=i, o=o: gpu.dropout(i, nin, o, 0.5, 2.0) for i, o in zip(ins, ins[::-1])])
     dev.free()
+
+    # -- the Adam update (gpu.zig:804-830) over config 4's 25e6 weights, one pass
+    dev = Device(gpu)
+    r = gen(6)
+    R = rotations(4 * 4 * n4)
+    vecs = [[dev.up(r.normal(0, s_, n4).astype(np.float32)) for s_ in (0.05, 0.05, 0.01, 0.001)] for _ in range(R)]
+    add("cfg4_adam[25e6]", "adam_update (one pass over w, d, m, v)", 8 * 4 * n4,
+        [lambda v=v: gpu.adamUpdate(v[0], v[1], v[2], v[3], 0.9, 0.999, 1e-7, 0.0005, 0.001, n4, 64, 3)
+         for v in vecs])
+    dev.free()
+
+    # -- im2col / col2im of config 2's layer, one image (the layers call them per image)
+    dev = Device(gpu)
+    C2, H2, K2 = 128, 56, 3
+    ncol = C2 * K2 * K2 * H2 * H2
+    nim = C2 * H2 * H2
+    R = rotations(4 * (ncol + nim))
+    ims = [dev.up(r.uniform(-1, 1, nim).astype(np.float32)) for _ in range(R)]
+    cols = [dev.zeros(ncol) for _ in range(R)]
+    cfg = "conv[128,56,56]k3s1p1"
+    add(cfg, "im2col (one image)", 4 * (nim + ncol),
+        [lambda i=i, c=c: gpu.im2col(i, C2, H2, H2, K2, 1, 1, c) for i, c in zip(ims, cols)])
+    add(cfg, "col2im (one image)", 4 * (ncol + 2 * nim),
+        [lambda i=i, c=c: gpu.col2im(c, C2, H2, H2, K2, 1, 1, i) for i, c in zip(ims, cols)])
+    dev.free()
+    return rows
+
+
+GEMM_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
+
+
+def gemm_table(gpu, hip, stream):
+    """dkz_gemm at the shapes a convolutional layer issues for config 2's layer
+    (forward, backward data, weight gradient; one image each, as
+    convolutional.zig issues them) and at a large square size: TFLOP/s
+    against the fp32 matrix-core peak."""
+    rows = {}
+    shapes = [("conv fwd NN 128x3136x1152", False, False, 128, 3136, 1152),
+              ("conv bwd-data TN 1152x3136x128", True, False, 1152, 3136, 128),
+              ("conv weight-grad NT 128x1152x3136", False, True, 128, 1152, 3136),
+              ("square NN 4096x4096x4096", False, False, 4096, 4096, 4096),
+              ("square NN 8192x8192x4096", False, False, 8192, 8192, 4096)]
+    r = gen(7)
+    for name, ta, tb, m, n, k in shapes:
+        dev = Device(gpu)
+        a = dev.up(r.uniform(-1, 1, m * k).astype(np.float32))
+        b = dev.up(r.uniform(-1, 1, k * n).astype(np.float32))
+        c = dev.zeros(m * n)
+        lda, ldb = (m if ta else k), (k if tb else n)
+        flops = 2 * m * n * k
+        reps = max(3, min(100, int(3e11 / flops)))
+        ms = time_seq(hip, stream, [[lambda: gpu.gemm(ta, tb, m, n, k, 1.0, a, lda, b, ldb, 1.0, c, n)]], reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        rows[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / GEMM_PEAK_TFLOPS, 4),
+                      "flops": flops}
+        dev.free()
     return rows
 
 
@@ -517,7 +591,8 @@ def main() -> int:
         return 0
 
     if args.per_op_only:
-        print(json.dumps({"per_op": per_op_table(gpu, hip, stream, args.op_launches)}), flush=True)
+        print(json.dumps({"per_op": per_op_table(gpu, hip, stream, args.op_launches),
+                          "gemm": gemm_table(gpu, hip, stream)}), flush=True)
         return 0
 
     h = config2_host()
@@ -598,6 +673,7 @@ def main() -> int:
     if not args.no_per_op:
         table = per_op_table(gpu, hip, stream, args.op_launches)
         result["per_op"] = table
+        result["gemm"] = gemm_table(gpu, hip, stream)
         named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
         fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and k.split("/", 1)[1] in named)
         fwd_chain = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/chain" in k)

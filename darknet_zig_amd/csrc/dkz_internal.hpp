@@ -28,13 +28,17 @@ inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args..
     return after_launch(name, grid, block);
 }
 
-// Reduction scratch of the current device: the f64 partial sums one split
-// reduction hands from its first launch to its second. Allocated by dkz_init
-// (or on first use); every split reduction writes all the partials it reads.
+// Scratch of the current device, allocated once by dkz_init (or on first
+// use): the f64 partial sums one split channel reduction hands from its first
+// launch to its second, and the partial tiles of a split-K gemm. Every user
+// writes all the scratch it then reads.
 struct Scratch {
     double *partials;
+    float *gemm;
+    uint64_t gemm_floats;
 };
-constexpr uint32_t kScratchPartials = 1u << 18;  // channels * chunks
+constexpr uint32_t kScratchPartials = 1u << 18;    // channels * chunks (2 MiB of f64)
+constexpr uint64_t kScratchGemmFloats = 1ull << 23;  // split-K partial tiles (32 MiB)
 int device_scratch(Scratch *out);
 
 // Largest element count any op indexes with 32-bit arithmetic, as the

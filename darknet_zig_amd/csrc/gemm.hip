@@ -4,27 +4,35 @@
 // A workgroup of four wave64s owns a BM x BN tile of C; each wave a
 // (BM/2) x (BN/2) quarter of it, as (BM/64) x (BN/64) blocks of 32x32 that
 // v_mfma_f32_32x32x2_f32 accumulates two k at a time (products exact, sums
-// in fp32). K advances in steps of 16: every thread loads its share of the
-// next A and B slabs from global memory into registers while the waves run
-// the current slab's MFMAs out of LDS; the registers then go to the other
-// LDS buffer, so each step needs one barrier.
+// in fp32). K advances in slabs of 16: every thread loads its share of the
+// next A and B slabs into registers while the waves run the current slab's
+// MFMAs out of LDS; the registers then go to the other LDS buffer, so each
+// slab costs one barrier.
 //
-// LDS holds both slabs k-major (As[p][i], Bs[p][j]) whatever the operands'
-// layouts: a lane of an MFMA reads A(i0 + lane%32, kk + lane/32) and
-// B(kk + lane/32, j0 + lane%32), 32 consecutive words per half-wave; rows are
-// padded by 32 words so the two halves fall in different banks. Global loads
-// walk each operand's contiguous dimension (k for A row-major, m for A
-// transposed, likewise for B), zero-filling past m, n and k.
+// LDS keeps both slabs k-contiguous per row (As[i][k], Bs[j][k], rows padded
+// to 20 words). Within a slab the sixteen k are dealt to the MFMAs so that
+// MFMA s takes k = s from lanes 0-31 and k = 8 + s from lanes 32-63; a lane
+// therefore needs eight consecutive k of its row, which two 128-bit LDS reads
+// fetch (the 80-byte row pitch puts eight lanes' reads in distinct banks).
+// The order in which the k of one output are summed changes; any order is as
+// valid as the CPU twin's, which depends on its host's vector width.
 //
-// The epilogue follows gemm.zig:121-131 then :180-184: beta == 0 clears C
-// (NaN included), beta == 1 keeps it, anything else scales it; then
-// C += alpha*acc. Results agree with the CPU twin within fp32 summation
-// error (the twin's own order depends on its host's vector width).
+// Global loads walk each operand's contiguous dimension in float4s (k for A
+// row-major and B transposed -- stored to LDS as they are -- m or n for the
+// other layouts, scattered to four LDS rows). Rows, columns and k past the
+// matrix load as 0; a misaligned operand loads element by element.
+//
+// Small problems split K: the grid holds `splits` copies of the tile grid,
+// each summing one range of K into a partial tile in the library's scratch,
+// and a second kernel adds a tile's partials in split order and applies
+// alpha and beta -- deterministic, no atomics. The epilogue follows
+// gemm.zig:121-131 then :180-184: beta == 0 clears C (NaN included), beta == 1
+// keeps it, anything else scales it; then C += alpha*acc.
 //
 // Workgroups take tiles in groups of 8 tile-rows, so that the tiles running
 // at once share A and B panels, and neighbouring tile numbers are placed on
-// one XCD (workgroups are dealt to the 8 XCDs round robin) so that they
-// share its L2.
+// one XCD (workgroups are dealt to the 8 XCDs round robin) so that they share
+// its L2.
 #include "dkz_device.hpp"
 #include "dkz_internal.hpp"
 
@@ -34,6 +42,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 16;
+constexpr int kPitch = kBK + 4;  // LDS row pitch in words
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
@@ -41,16 +50,20 @@ struct GemmArgs {
     const float *a;
     const float *b;
     float *c;
+    float *partial;  // splits > 1: [splits][m][n] partial tiles
     uint32_t m, n, k, lda, ldb, ldc;
     float alpha, beta;
-    uint32_t tiles_m, tiles_n;
+    uint32_t tiles_m, tiles_n, splits, k_chunk;
+    uint32_t vec_a, vec_b;  // operand 16-byte aligned with a leading dimension % 4 == 0
 };
 
-template <int BM, int BN>
-__device__ __forceinline__ void tile_of(uint32_t w, const GemmArgs &g, uint32_t &tm, uint32_t &tn) {
-    const uint32_t total = g.tiles_m * g.tiles_n;
+__device__ __forceinline__ void tile_of(uint32_t w, const GemmArgs &g, uint32_t &tm, uint32_t &tn, uint32_t &split) {
+    const uint32_t tiles = g.tiles_m * g.tiles_n;
+    const uint32_t total = tiles * g.splits;
     uint32_t t = w;
     if (total % kXcds == 0) t = (w % kXcds) * (total / kXcds) + w / kXcds;
+    split = t / tiles;
+    t -= split * tiles;
     const uint32_t per_group = kGroupM * g.tiles_n;
     const uint32_t first_m = (t / per_group) * kGroupM;
     const uint32_t gsize = g.tiles_m - first_m < (uint32_t)kGroupM ? g.tiles_m - first_m : (uint32_t)kGroupM;
@@ -59,62 +72,85 @@ __device__ __forceinline__ void tile_of(uint32_t w, const GemmArgs &g, uint32_t 
     tn = in_group / gsize;
 }
 
-template <int BM, int BN, bool TA, bool TB>
-__global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmArgs g) {
-    constexpr int SA = BM + 32, SB = BN + 32;  // LDS row strides in words
-    constexpr int NA = BM * kBK / kBlock, NB = BN * kBK / kBlock;
-    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-    __shared__ float As[2][kBK * SA];
-    __shared__ float Bs[2][kBK * SB];
+// Four consecutive elements p[0..3] of a row (or column) starting at `idx`,
+// where `avail` of them exist (0..4). vec: idx is a multiple of 4 and p is
+// 16-byte aligned.
+__device__ __forceinline__ float4 load4(const float *p, uint32_t idx, uint32_t avail, bool vec) {
+    if (avail >= 4 && vec) return *reinterpret_cast<const float4 *>(p + idx);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (avail > 0) v.x = p[idx];
+    if (avail > 1) v.y = p[idx + 1];
+    if (avail > 2) v.z = p[idx + 2];
+    if (avail > 3) v.w = p[idx + 3];
+    return v;
+}
 
-    uint32_t tm, tn;
-    tile_of<BM, BN>(blockIdx.x, g, tm, tn);
+// One operand's slab loader. ROWK: the operand's rows run along the tile
+// dimension with k contiguous (A row-major, B transposed); otherwise its rows
+// run along k with the tile dimension contiguous. R rows of the tile.
+template <int R, bool ROWK>
+struct Slab {
+    static constexpr int kLoads = R * kBK / 4 / kBlock;  // float4s per thread
+    float4 v[kLoads];
+
+    // rows: tile rows available (m - m0 or n - n0); k0/kmax: the slab's first
+    // k and the end of this split's range.
+    __device__ __forceinline__ void load(const float *p, uint32_t ld, uint32_t r0, uint32_t rows, uint32_t k0,
+                                         uint32_t kend, bool vec, int tid) {
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const int f = tid + l * kBlock;  // float4 number within the slab
+            if constexpr (ROWK) {
+                const uint32_t r = f / (kBK / 4), q = f % (kBK / 4);
+                const uint32_t kk = k0 + 4 * q;
+                const uint32_t avail = (r < rows && kk < kend) ? (kend - kk < 4 ? kend - kk : 4) : 0;
+                v[l] = load4(p, (r0 + r) * ld + kk, avail, vec);
+            } else {
+                const uint32_t kr = f / (R / 4), q = f % (R / 4);
+                const uint32_t rr = 4 * q;
+                const uint32_t avail = (k0 + kr < kend && rr < rows) ? (rows - rr < 4 ? rows - rr : 4) : 0;
+                v[l] = load4(p, (k0 + kr) * ld + r0 + rr, avail, vec);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float *s, int tid) const {
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const int f = tid + l * kBlock;
+            if constexpr (ROWK) {
+                const int r = f / (kBK / 4), q = f % (kBK / 4);
+                *reinterpret_cast<float4 *>(s + r * kPitch + 4 * q) = v[l];
+            } else {
+                const int kr = f / (R / 4), q = f % (R / 4);
+                float *d = s + (4 * q) * kPitch + kr;
+                d[0] = v[l].x;
+                d[kPitch] = v[l].y;
+                d[2 * kPitch] = v[l].z;
+                d[3 * kPitch] = v[l].w;
+            }
+        }
+    }
+};
+
+template <int BM, int BN, bool TA, bool TB>
+__global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    __shared__ float As[2][BM * kPitch];
+    __shared__ float Bs[2][BN * kPitch];
+
+    uint32_t tm, tn, split;
+    tile_of(blockIdx.x, g, tm, tn, split);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t rows_a = g.m - m0, rows_b = g.n - n0;
+    const uint32_t kbeg = split * g.k_chunk;
+    const uint32_t kend = kbeg + g.k_chunk < g.k ? kbeg + g.k_chunk : g.k;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
     const int half = lane >> 5, l32 = lane & 31;
 
-    // This thread's slab coordinates: (ai[r], ap[r]) of A and (bp[r], bj[r]) of B.
-    auto a_coord = [&](int r, int &i, int &p) {
-        if constexpr (TA) { i = tid % BM; p = tid / BM + (kBlock / BM) * r; }
-        else { p = tid % kBK; i = tid / kBK + (kBlock / kBK) * r; }
-    };
-    auto b_coord = [&](int r, int &p, int &j) {
-        if constexpr (TB) { p = tid % kBK; j = tid / kBK + (kBlock / kBK) * r; }
-        else { j = tid % BN; p = tid / BN + (kBlock / BN) * r; }
-    };
-
-    float ra[NA], rb[NB];
-    auto load = [&](uint32_t k0) {
-#pragma unroll
-        for (int r = 0; r < NA; ++r) {
-            int i, p;
-            a_coord(r, i, p);
-            const uint32_t gi = m0 + i, gp = k0 + p;
-            ra[r] = (gi < g.m && gp < g.k) ? g.a[TA ? gp * g.lda + gi : gi * g.lda + gp] : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < NB; ++r) {
-            int p, j;
-            b_coord(r, p, j);
-            const uint32_t gp = k0 + p, gj = n0 + j;
-            rb[r] = (gp < g.k && gj < g.n) ? g.b[TB ? gj * g.ldb + gp : gp * g.ldb + gj] : 0.0f;
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < NA; ++r) {
-            int i, p;
-            a_coord(r, i, p);
-            As[buf][p * SA + i] = ra[r];
-        }
-#pragma unroll
-        for (int r = 0; r < NB; ++r) {
-            int p, j;
-            b_coord(r, p, j);
-            Bs[buf][p * SB + j] = rb[r];
-        }
-    };
+    Slab<BM, !TA> sa;
+    Slab<BN, TB> sb;
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -124,29 +160,48 @@ __global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[ti][tj][r] = 0.0f;
 
-    const uint32_t steps = (g.k + kBK - 1) / kBK;
-    load(0);
-    store(0);
-    __syncthreads();
+    const uint32_t steps = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
+    if (steps > 0) {
+        sa.load(g.a, g.lda, m0, rows_a, kbeg, kend, g.vec_a, tid);
+        sb.load(g.b, g.ldb, n0, rows_b, kbeg, kend, g.vec_b, tid);
+        sa.store(As[0], tid);
+        sb.store(Bs[0], tid);
+        __syncthreads();
+    }
     for (uint32_t s = 0; s < steps; ++s) {
         const int cur = s & 1;
-        if (s + 1 < steps) load((s + 1) * kBK);
-        const float *as = As[cur] + half * SA + wm0 + l32;
-        const float *bs = Bs[cur] + half * SB + wn0 + l32;
+        const bool more = s + 1 < steps;
+        if (more) {
+            const uint32_t k0 = kbeg + (s + 1) * kBK;
+            sa.load(g.a, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+            sb.load(g.b, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+        }
+        float4 af[TM][2], bf[TN][2];
 #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 2) {
-            float af[TM], bf[TN];
+        for (int ti = 0; ti < TM; ++ti) {
+            const float *p = As[cur] + (wm0 + ti * 32 + l32) * kPitch + 8 * half;
+            af[ti][0] = *reinterpret_cast<const float4 *>(p);
+            af[ti][1] = *reinterpret_cast<const float4 *>(p + 4);
+        }
 #pragma unroll
-            for (int ti = 0; ti < TM; ++ti) af[ti] = as[kk * SA + ti * 32];
+        for (int tj = 0; tj < TN; ++tj) {
+            const float *p = Bs[cur] + (wn0 + tj * 32 + l32) * kPitch + 8 * half;
+            bf[tj][0] = *reinterpret_cast<const float4 *>(p);
+            bf[tj][1] = *reinterpret_cast<const float4 *>(p + 4);
+        }
 #pragma unroll
-            for (int tj = 0; tj < TN; ++tj) bf[tj] = bs[kk * SB + tj * 32];
+        for (int q = 0; q < 8; ++q)
 #pragma unroll
             for (int ti = 0; ti < TM; ++ti)
 #pragma unroll
                 for (int tj = 0; tj < TN; ++tj)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[ti], bf[tj], acc[ti][tj], 0, 0, 0);
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(::dkz::lane(af[ti][q >> 2], q & 3),
+                                                                        ::dkz::lane(bf[tj][q >> 2], q & 3), acc[ti][tj],
+                                                                        0, 0, 0);
+        if (more) {
+            sa.store(As[cur ^ 1], tid);
+            sb.store(Bs[cur ^ 1], tid);
         }
-        if (s + 1 < steps) store(cur ^ 1);
         __syncthreads();
     }
 
@@ -161,7 +216,10 @@ __global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = m0 + wm0 + ti * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                if (i < g.m) {
+                if (i >= g.m) continue;
+                if (g.splits > 1) {
+                    g.partial[((size_t)split * g.m + i) * g.n + j] = acc[ti][tj][r];
+                } else {
                     float *cp = g.c + i * g.ldc + j;
                     float cv = 0.0f;
                     if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
@@ -171,13 +229,26 @@ __global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmArgs g) {
         }
 }
 
+// The split-K epilogue: C(i, j) = beta-applied C + alpha * (sum of the splits'
+// partials in split order).
+__global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) {
+    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t mn = g.m * g.n;
+    if (e >= mn) return;
+    const uint32_t i = e / g.n, j = e - i * g.n;
+    float s = 0.0f;
+    for (uint32_t t = 0; t < g.splits; ++t) s += g.partial[(size_t)t * mn + e];
+    float *cp = g.c + i * g.ldc + j;
+    float cv = 0.0f;
+    if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
+    *cp = cv + g.alpha * s;
+}
+
 template <int BM, int BN>
 int launch_gemm(bool ta, bool tb, GemmArgs g) {
-    g.tiles_m = div_up(g.m, BM);
-    g.tiles_n = div_up(g.n, BN);
-    const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
-    DKZ_REQUIRE(tiles <= 0x7fffffffull);
-    const dim3 grid((uint32_t)tiles), block(kBlock);
+    const uint64_t total = (uint64_t)g.tiles_m * g.tiles_n * g.splits;
+    DKZ_REQUIRE(total <= 0x7fffffffull);
+    const dim3 grid((uint32_t)total), block(kBlock);
     if (!ta && !tb) return launch("gemm_nn", gemm_mfma_kernel<BM, BN, false, false>, grid, block, g);
     if (ta && !tb) return launch("gemm_tn", gemm_mfma_kernel<BM, BN, true, false>, grid, block, g);
     if (!ta && tb) return launch("gemm_nt", gemm_mfma_kernel<BM, BN, false, true>, grid, block, g);
@@ -185,7 +256,11 @@ int launch_gemm(bool ta, bool tb, GemmArgs g) {
 }
 
 // Extent in elements of a rows x cols row-major view with leading dimension ld.
-inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) { return rows == 0 || cols == 0 ? 0 : (rows - 1) * ld + cols; }
+inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) {
+    return rows == 0 || cols == 0 ? 0 : (rows - 1) * ld + cols;
+}
+
+constexpr uint32_t kCus = 256;
 
 }  // namespace
 }  // namespace dkz
@@ -203,14 +278,61 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
     if (k > 0) {
         DKZ_REQUIRE(a != nullptr && b != nullptr);
         DKZ_REQUIRE(lda >= (ta ? m : k) && ldb >= (tb ? k : n));
-        DKZ_REQUIRE(extent(ta ? k : m, ta ? m : k, lda) <= kMaxElems);
-        DKZ_REQUIRE(extent(tb ? n : k, tb ? k : n, ldb) <= kMaxElems);
+        DKZ_REQUIRE(extent(ta ? k : m, ta ? m : k, lda) + 3 <= kMaxElems);
+        DKZ_REQUIRE(extent(tb ? n : k, tb ? k : n, ldb) + 3 <= kMaxElems);
     }
-    GemmArgs g{a, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)lda, (uint32_t)ldb, (uint32_t)ldc,
-               alpha, beta, 0, 0};
-    // 128x128 tiles once they alone give every CU a workgroup; 64x64 below.
-    const uint64_t big_tiles = (uint64_t)div_up(m, 128) * div_up(n, 128);
-    if (big_tiles >= 256) return launch_gemm<128, 128>(ta != 0, tb != 0, g);
+    GemmArgs g{};
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)n;
+    g.k = (uint32_t)k;
+    g.lda = (uint32_t)lda;
+    g.ldb = (uint32_t)ldb;
+    g.ldc = (uint32_t)ldc;
+    g.alpha = alpha;
+    g.beta = beta;
+    g.vec_a = aligned16(a) && lda % 4 == 0;
+    g.vec_b = aligned16(b) && ldb % 4 == 0;
+    g.splits = 1;
+    g.k_chunk = (uint32_t)k;
+
+    // 128x128 tiles when they give every CU two workgroups; 64x64 below, and
+    // if even those leave CUs idle and K is long, split K (ranges of >= 128)
+    // until about four workgroups per CU, within the scratch.
+    const uint64_t big = (uint64_t)div_up(m, 128) * div_up(n, 128);
+    if (big >= 2 * kCus) {
+        g.tiles_m = div_up(m, 128);
+        g.tiles_n = div_up(n, 128);
+        return launch_gemm<128, 128>(ta != 0, tb != 0, g);
+    }
+    g.tiles_m = div_up(m, 64);
+    g.tiles_n = div_up(n, 64);
+    const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
+    uint64_t splits = 1;
+    if (tiles < 2 * kCus && k >= 256) {
+        splits = div_up(4 * kCus, tiles);
+        const uint64_t by_k = (uint64_t)k / 128;
+        if (splits > by_k) splits = by_k;
+        Scratch sc;
+        DKZ_TRY(device_scratch(&sc));
+        const uint64_t cap = sc.gemm_floats / ((uint64_t)m * n);
+        if (splits > cap) splits = cap;
+    }
+    if (splits > 1) {
+        const uint32_t chunk = (uint32_t)((div_up(k, splits) + kBK - 1) / kBK * kBK);
+        g.k_chunk = chunk;
+        g.splits = div_up(k, chunk);
+    }
+    if (g.splits > 1) {
+        Scratch sc;
+        DKZ_TRY(device_scratch(&sc));
+        g.partial = sc.gemm;
+        DKZ_TRY((launch_gemm<64, 64>(ta != 0, tb != 0, g)));
+        return launch("gemm_splitk_reduce", gemm_splitk_reduce_kernel, dim3(div_up((uint64_t)m * n, kBlock)),
+                      dim3(kBlock), g);
+    }
     return launch_gemm<64, 64>(ta != 0, tb != 0, g);
 }
 

@@ -30,7 +30,7 @@ bool env_flag(const char *name) {
     return v != nullptr && v[0] != '\0' && v[0] != '0';
 }
 
-constexpr size_t kScratchBytes = kScratchPartials * sizeof(double);
+constexpr size_t kScratchBytes = kScratchPartials * sizeof(double) + kScratchGemmFloats * sizeof(float);
 
 int ensure_scratch(int dev) {
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -38,14 +38,14 @@ int ensure_scratch(int dev) {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, kScratchBytes);
     if (e != hipSuccess) {
-        set_error_context("allocating the reduction scratch (%zu bytes)", kScratchBytes);
+        set_error_context("allocating the scratch (%zu bytes)", kScratchBytes);
         return (int)e;
     }
     e = hipMemset(p, 0, kScratchBytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(p);
-        set_error_context("zeroing the reduction scratch");
+        set_error_context("zeroing the scratch");
         return (int)e;
     }
     g_devices[dev].scratch = p;
@@ -88,6 +88,8 @@ int device_scratch(Scratch *out) {
     if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
     if (g_devices[dev].scratch == nullptr) DKZ_TRY(ensure_scratch(dev));
     out->partials = static_cast<double *>(g_devices[dev].scratch);
+    out->gemm = reinterpret_cast<float *>(out->partials + kScratchPartials);
+    out->gemm_floats = kScratchGemmFloats;
     return 0;
 }
 
