@@ -38,11 +38,12 @@
  *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
- *   - The library owns one scratch buffer per device (2 MiB) for the f64
- *     partial sums a per-channel reduction passes from its first launch to
- *     its second; dkz_init allocates it. Ops never allocate. Reductions
- *     issued concurrently on two streams of one device share that buffer and
- *     race; issue them on one stream.
+ *   - The library owns one scratch buffer per device (34 MiB), allocated by
+ *     dkz_init: the f64 partial sums a per-channel reduction passes from its
+ *     first launch to its second (2 MiB) and the partial tiles of a split-K
+ *     gemm (32 MiB). Ops never allocate. Reductions or gemms issued
+ *     concurrently on two streams of one device share that buffer and race;
+ *     issue them on one stream.
  */
 #ifndef DKZ_OPS_H
 #define DKZ_OPS_H
