@@ -386,6 +386,13 @@ def per_op_table(gpu, hip, stream, launches: int):
     add(cfg, "softmax", 2 * 4 * n3, [lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)])
     add(cfg, "softmax_x_ent", 4 * 4 * n3,
         [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)])
+    add_seq(cfg, "chain: softmax, softmax_x_ent (the layer's two calls)", 6 * 4 * n3,
+            [[lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p),
+              lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e)]
+             for a, p, t, d, e in zip(ls, ps, ts, ds_, es)])
+    add("fused", "cfg3 softmax_layer_forward (softmax + loss in one pass)", 5 * 4 * n3,
+        [lambda a=a, p=p, t=t, d=d, e=e: gpu.softmaxLayerForward(b3, c3, 1, 1.0, a, t, p, d, e)
+         for a, p, t, d, e in zip(ls, ps, ts, ds_, es)])
     dev.free()
 
     # -- config 4: SGD over 25e6 floats ~N(0,0.05), and the stride-2 shortcut

@@ -60,6 +60,7 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_variance_delta": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "dkz_normalize_delta": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "dkz_softmax": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _p]),
+    "dkz_softmax_layer_forward": (_i, [_i, _i, _i, _f, _p, _p, _p, _p, _p]),
     "dkz_softmax_cross_entropy": (_i, [_i, _p, _p, _p, _p]),
     "dkz_l2": (_i, [_i, _p, _p, _p, _p]),
     "dkz_l1": (_i, [_i, _p, _p, _p, _p]),

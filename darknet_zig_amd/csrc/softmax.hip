@@ -1,5 +1,6 @@
 // softmax.hip -- grouped softmax (src/gpu.zig:614-629, CPU twin
-// blas.zig:213-242).
+// blas.zig:213-242), and the softmax layer's forward step with its
+// cross-entropy loss fused in (layers/misc.zig:63-76).
 //
 // Group (b, g) holds n elements `stride` apart starting at
 // b*batch_offset + g*group_offset. Per group the CPU twin takes the max
@@ -9,14 +10,20 @@
 // reproduce the twin bit for bit wherever they keep the sequential sum:
 //
 //  * contiguous groups (stride 1) with 32 < n <= kSeqMax: one workgroup per
-//    group; max by wave64 DPP + LDS, the exps in parallel into LDS, one lane
-//    adds them in order, then all lanes divide. Bit-exact.
+//    group; the row is read once into LDS (in float4s when aligned), max by
+//    wave64 DPP + LDS, the exps in parallel in place, one lane adds them in
+//    order, then all lanes divide. Bit-exact.
 //  * contiguous groups with n > kSeqMax: the same, but the sum is an f64
 //    tree (within 1e-5 relative of the twin) because the row no longer fits
 //    in LDS.
 //  * strided groups (spatial softmax) or n <= 32: one lane per group runs the
 //    twin's three loops; adjacent lanes are adjacent groups, so with
 //    group_offset 1 the loads coalesce. Bit-exact.
+//
+// dkz_softmax_layer_forward runs the layer's two calls (softmax, then
+// softmax_x_ent over the whole batch) as one pass where the block kernels
+// apply: the loss and delta are formed from each probability as it is
+// stored, with softmax_x_ent's expressions.
 #include <float.h>
 
 #include "dkz_device.hpp"
@@ -39,8 +46,24 @@ __device__ __forceinline__ uint32_t group_base(uint32_t r, const Groups &G) {
     return b * G.batch_offset + g * G.group_offset;
 }
 
-template <bool SEQ>
-__global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, float *out, Groups G) {
+// The cross-entropy step of the softmax layer (layers/misc.zig:70-75,
+// blas.zig:247-252), fused into the softmax pass: delta = t - p and
+// loss = t != 0 ? -log(p) : 0 on the probabilities just stored.
+struct Xent {
+    const float *truth;
+    float *delta;
+    float *loss;
+};
+
+__device__ __forceinline__ void xent1(float p, float t, float &d, float &l) {
+    l = (t != 0.0f) ? -logf(p) : 0.0f;
+    d = t - p;
+}
+
+// V4: the row is 16-byte aligned and n % 4 == 0 (every pointer too), so it
+// moves in float4s.
+template <bool SEQ, bool XENT, bool V4>
+__global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, float *out, Groups G, Xent xe) {
     extern __shared__ float4 e_lds4[];  // n floats when SEQ; float4 keeps it 16-byte aligned
     float *e_lds = reinterpret_cast<float *>(e_lds4);
     __shared__ float red_f[kBlock / kWave];
@@ -49,16 +72,40 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
     const uint32_t off = group_base(blockIdx.x, G);
     const float *x = in + off;
     float *y = out + off;
-    const uint32_t n = G.n;
+    const uint32_t n = G.n, nv = n >> 2;
 
     float mx = -FLT_MAX;
-    for (uint32_t i = threadIdx.x; i < n; i += kBlock) mx = fmaxf(mx, x[i]);
-    mx = block_max(mx, red_f);
-    const float mt = mx / G.temp;
-
     float sum;
     if constexpr (SEQ) {
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) e_lds[i] = expf_libm(x[i] / G.temp - mt);
+        // The row is read once, into LDS; the max is order-free.
+        if constexpr (V4) {
+            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
+                const float4 a = ld4<false>(x, v);
+                e_lds4[v] = a;
+                mx = fmaxf(mx, fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)));
+            }
+        } else {
+            for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
+                const float a = x[i];
+                e_lds[i] = a;
+                mx = fmaxf(mx, a);
+            }
+        }
+        mx = block_max(mx, red_f);
+        const float mt = mx / G.temp;
+        // Each lane turns the entries it loaded into exps, in place.
+        if constexpr (V4) {
+            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
+                float4 a = e_lds4[v];
+                a.x = expf_libm(a.x / G.temp - mt);
+                a.y = expf_libm(a.y / G.temp - mt);
+                a.z = expf_libm(a.z / G.temp - mt);
+                a.w = expf_libm(a.w / G.temp - mt);
+                e_lds4[v] = a;
+            }
+        } else {
+            for (uint32_t i = threadIdx.x; i < n; i += kBlock) e_lds[i] = expf_libm(e_lds[i] / G.temp - mt);
+        }
         __syncthreads();
         if (threadIdx.x == 0) {
             // The one sequential part: 8 LDS reads in flight ahead of the adds.
@@ -81,8 +128,33 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
         }
         __syncthreads();
         sum = sum_sh;
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) y[i] = e_lds[i] / sum;
+        if constexpr (V4) {
+            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
+                const float4 e = e_lds4[v];
+                const float4 p = make_float4(e.x / sum, e.y / sum, e.z / sum, e.w / sum);
+                st4<false>(y, v, p);
+                if constexpr (XENT) {
+                    const float4 t = ld4<false>(xe.truth + off, v);
+                    float4 d, l;
+                    xent1(p.x, t.x, d.x, l.x);
+                    xent1(p.y, t.y, d.y, l.y);
+                    xent1(p.z, t.z, d.z, l.z);
+                    xent1(p.w, t.w, d.w, l.w);
+                    st4<false>(xe.delta + off, v, d);
+                    st4<false>(xe.loss + off, v, l);
+                }
+            }
+        } else {
+            for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
+                const float p = e_lds[i] / sum;
+                y[i] = p;
+                if constexpr (XENT) xent1(p, xe.truth[off + i], xe.delta[off + i], xe.loss[off + i]);
+            }
+        }
     } else {
+        for (uint32_t i = threadIdx.x; i < n; i += kBlock) mx = fmaxf(mx, x[i]);
+        mx = block_max(mx, red_f);
+        const float mt = mx / G.temp;
         double acc = 0.0;
         for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
             const float e = expf_libm(x[i] / G.temp - mt);
@@ -90,7 +162,11 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
             acc += (double)e;
         }
         sum = (float)block_sum(acc, red_d);
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) y[i] = y[i] / sum;
+        for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
+            const float p = y[i] / sum;
+            y[i] = p;
+            if constexpr (XENT) xent1(p, xe.truth[off + i], xe.delta[off + i], xe.loss[off + i]);
+        }
     }
 }
 
@@ -115,15 +191,8 @@ __global__ __launch_bounds__(kBlock) void softmax_lane_kernel(const float *in, f
     for (uint32_t i = 0; i < n; ++i) y[i * st] = y[i * st] / s;
 }
 
-}  // namespace
-}  // namespace dkz
-
-using namespace dkz;
-
-extern "C" {
-
-int dkz_softmax(const float *input, int n, int batch, int batch_offset, int groups, int group_offset,
-                int stride, float temp, float *output) {
+int softmax_run(const float *input, int n, int batch, int batch_offset, int groups, int group_offset, int stride,
+                float temp, float *output, const Xent *xe) {
     DKZ_REQUIRE(n >= 0 && batch >= 0 && batch_offset >= 0 && groups >= 0 && group_offset >= 0 && stride >= 0);
     const uint64_t rows64 = (uint64_t)batch * (uint64_t)groups;
     if (rows64 == 0 || n == 0) return 0;  // gpu.zig:625 launches batch*groups lanes
@@ -135,19 +204,57 @@ int dkz_softmax(const float *input, int n, int batch, int batch_offset, int grou
     const uint32_t rows = (uint32_t)rows64;
     const Groups G{(uint32_t)n,      (uint32_t)groups, (uint32_t)batch_offset, (uint32_t)group_offset,
                    (uint32_t)stride, temp,             make_fastdiv((uint32_t)groups)};
-    if (stride == 1 && n > 32) {
-        (void)hipGetLastError();
-        if ((uint32_t)n <= kSeqMax) {
-            hipLaunchKernelGGL(softmax_block_kernel<true>, dim3(rows), dim3(kBlock), (size_t)n * sizeof(float),
-                               current_stream(), input, output, G);
-        } else {
-            hipLaunchKernelGGL(softmax_block_kernel<false>, dim3(rows), dim3(kBlock), 0, current_stream(), input,
-                               output, G);
-        }
-        return after_launch("softmax", dim3(rows), dim3(kBlock));
+    if (!(stride == 1 && n > 32)) {
+        DKZ_REQUIRE(xe == nullptr);
+        return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
+                      G, rows);
     }
-    return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
-                  G, rows);
+    const bool seq = (uint32_t)n <= kSeqMax;
+    bool v4 = n % 4 == 0 && batch_offset % 4 == 0 && group_offset % 4 == 0 && aligned16(input) && aligned16(output);
+    if (xe) v4 = v4 && aligned16(xe->truth) && aligned16(xe->delta) && aligned16(xe->loss);
+    const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
+    const size_t lds = seq ? (size_t)n * sizeof(float) : 0;
+    void (*k)(const float *, float *, Groups, Xent);
+    if (seq) {
+        if (xe) k = v4 ? softmax_block_kernel<true, true, true> : softmax_block_kernel<true, true, false>;
+        else k = v4 ? softmax_block_kernel<true, false, true> : softmax_block_kernel<true, false, false>;
+    } else {
+        k = xe ? softmax_block_kernel<false, true, false> : softmax_block_kernel<false, false, false>;
+    }
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k, dim3(rows), dim3(kBlock), lds, current_stream(), input, output, G, x);
+    return after_launch(xe ? "softmax_xent" : "softmax", dim3(rows), dim3(kBlock));
+}
+
+}  // namespace
+}  // namespace dkz
+
+using namespace dkz;
+
+extern "C" {
+
+int dkz_softmax(const float *input, int n, int batch, int batch_offset, int groups, int group_offset,
+                int stride, float temp, float *output) {
+    return softmax_run(input, n, batch, batch_offset, groups, group_offset, stride, temp, output, nullptr);
+}
+
+int dkz_softmax_layer_forward(int batch, int inputs, int groups, float temp, const float *input,
+                              const float *truth, float *output, float *delta, float *loss) {
+    DKZ_REQUIRE(inputs >= 0 && groups >= 0 && batch >= 0);
+    if (groups == 0 || batch == 0 || inputs == 0) return 0;
+    DKZ_REQUIRE(inputs % groups == 0);  // misc.zig:20
+    const int per_group = inputs / groups;
+    if (truth == nullptr)  // misc.zig:66: no truth, no loss
+        return softmax_run(input, per_group, batch, inputs, groups, per_group, 1, temp, output, nullptr);
+    DKZ_REQUIRE(delta != nullptr && loss != nullptr);
+    if (per_group > 32) {
+        const Xent xe{truth, delta, loss};
+        return softmax_run(input, per_group, batch, inputs, groups, per_group, 1, temp, output, &xe);
+    }
+    // Short groups take the one-lane-per-group kernel; the loss is its own pass.
+    DKZ_TRY(softmax_run(input, per_group, batch, inputs, groups, per_group, 1, temp, output, nullptr));
+    DKZ_REQUIRE((uint64_t)batch * inputs <= kMaxElems);
+    return dkz_softmax_cross_entropy(batch * inputs, output, truth, delta, loss);
 }
 
 }  // extern "C"

@@ -294,6 +294,16 @@ def softmax(
     )
 
 
+def softmaxLayerForward(
+    batch: int, inputs: int, groups: int, temp: float, input: Buf, truth: Buf | None, output: Buf,
+    delta: Buf | None, loss: Buf | None,
+) -> None:
+    """layers/misc.zig:63-76 (softmax, then the cross-entropy when truth is
+    given) as one call; no single gpu.zig counterpart."""
+    _must(_lib.load().dkz_softmax_layer_forward(batch, inputs, groups, temp, _p(input), _p(truth), _p(output),
+                                                _p(delta), _p(loss)), "softmax_layer_forward")
+
+
 def softmaxCrossEntropy(n: int, pred: Buf, truth: Buf, delta: Buf, err: Buf) -> None:
     _must(_lib.load().dkz_softmax_cross_entropy(n, _p(pred), _p(truth), _p(delta), _p(err)), "softmax_x_ent")
 

@@ -220,6 +220,14 @@ inline void softmax(Buf input, size_t n, size_t batch, size_t batch_offset, size
 inline void softmaxCrossEntropy(size_t n, Buf pred, Buf truth, Buf delta, Buf err) {
     must(dkz_softmax_cross_entropy(ci(n), pred.f(), truth.f(), delta.f(), err.f()), "softmax_x_ent");
 }
+// No single gpu.zig counterpart: layers/misc.zig:63-76 (softmax, then the
+// cross-entropy when truth is not null) as one call.
+inline void softmaxLayerForward(size_t batch, size_t inputs, size_t groups, float temp, Buf input, Buf truth,
+                                Buf output, Buf delta, Buf loss) {
+    must(dkz_softmax_layer_forward(ci(batch), ci(inputs), ci(groups), temp, input.f(), truth.f(), output.f(),
+                                   delta.f(), loss.f()),
+         "softmax_layer_forward");
+}
 inline void l2(size_t n, Buf pred, Buf truth, Buf delta, Buf err) {
     must(dkz_l2(ci(n), pred.f(), truth.f(), delta.f(), err.f()), "l2");
 }

@@ -232,6 +232,16 @@ int dkz_normalize_delta(const float *x, const float *mean, const float *variance
 int dkz_softmax(const float *input, int n, int batch, int batch_offset, int groups, int group_offset,
                 int stride, float temp, float *output);
 
+/* No single gpu.zig counterpart: the forward step of the softmax layer,
+ * layers/misc.zig:63-76 (forwardSoftmaxGpu), as one call --
+ * softmax(input, inputs/groups, batch, inputs, groups, inputs/groups, 1, temp,
+ * output), then, when truth is not NULL, softmaxCrossEntropy(batch*inputs,
+ * output, truth, delta, loss). Groups longer than 32 run both as one pass;
+ * results equal the two calls'. inputs % groups != 0 is hipErrorInvalidValue
+ * (misc.zig:20 asserts it). */
+int dkz_softmax_layer_forward(int batch, int inputs, int groups, float temp, const float *input,
+                              const float *truth, float *output, float *delta, float *loss);
+
 /* gpu.zig:631 softmaxCrossEntropy: err = t != 0 ? -log(p) : 0; delta = t - p.
  * blas.zig:247-252 */
 int dkz_softmax_cross_entropy(int n, const float *pred, const float *truth, float *delta, float *err);

@@ -47,7 +47,7 @@ def exported_symbols() -> set[str]:
 
 def test_header_exports_and_binding_agree():
     declared = header_symbols()
-    assert len(declared) == len(set(declared)) == 53
+    assert len(declared) == len(set(declared)) == 54
     assert set(declared) == exported_symbols()
     assert list(_lib.SIGNATURES) == declared  # same set, same order as the header
 
@@ -151,6 +151,9 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, P, 3, P, 5, 0.0, P, 4), INVALID),  # ldc < n
         (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, None, 3, P, 5, 0.0, P, 5), INVALID),
         (lambda L: L.dkz_gemm(0, 0, 65536, 65536, 3, 1.0, P, 3, P, 65536, 0.0, P, 65536), INVALID),  # > 2^31
+        (lambda L: L.dkz_softmax_layer_forward(2, 10, 3, 1.0, P, P, P, P, P), INVALID),  # 10 % 3 != 0
+        (lambda L: L.dkz_softmax_layer_forward(0, 10, 2, 1.0, None, None, None, None, None), 0),
+        (lambda L: L.dkz_softmax_layer_forward(2, 100, 1, 1.0, P, P, P, None, P), INVALID),  # truth without delta
         (lambda L: L.dkz_malloc(None, 4), INVALID),
         (lambda L: L.dkz_free(None), 0),
         (lambda L: L.dkz_copy_to_host(None, None, 0), 0),
