@@ -133,9 +133,17 @@ struct Slab {
     }
 };
 
-template <int BM, int BN, bool TA, bool TB>
+// D: slabs in flight. The loads of slab s + D are issued while slab s is
+// multiplied, from a ring of D register sets; the 128x128 kernel does four
+// times the MFMAs per slab of the 64x64 one and runs with D = 1, the 64x64
+// one -- used when few workgroups share a CU -- with DKZ_GEMM_SMALL_PREFETCH.
+template <int BM, int BN, bool TA, bool TB, int D>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    // A wave with fewer than four 32x32 blocks spreads each block's MFMAs over
+    // NC accumulators (MFMA q of a slab into accumulator q % NC), so that four
+    // independent MFMAs are always in flight; they are added at the end.
+    constexpr int NC = TM * TN >= 4 ? 1 : 4 / (TM * TN);
     __shared__ float As[2][BM * kPitch];
     __shared__ float Bs[2][BN * kPitch];
 
@@ -149,63 +157,89 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
     const int half = lane >> 5, l32 = lane & 31;
 
-    Slab<BM, !TA> sa;
-    Slab<BN, TB> sb;
+    Slab<BM, !TA> sa[D];
+    Slab<BN, TB> sb[D];
 
-    f32x16 acc[TM][TN];
+    f32x16 acc[NC][TM][TN];
 #pragma unroll
-    for (int ti = 0; ti < TM; ++ti)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int tj = 0; tj < TN; ++tj)
+        for (int ti = 0; ti < TM; ++ti)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[ti][tj][r] = 0.0f;
+            for (int tj = 0; tj < TN; ++tj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[c][ti][tj][r] = 0.0f;
 
     const uint32_t steps = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if ((uint32_t)d < steps) {
+            sa[d].load(g.a, g.lda, m0, rows_a, kbeg + d * kBK, kend, g.vec_a, tid);
+            sb[d].load(g.b, g.ldb, n0, rows_b, kbeg + d * kBK, kend, g.vec_b, tid);
+        }
+    }
     if (steps > 0) {
-        sa.load(g.a, g.lda, m0, rows_a, kbeg, kend, g.vec_a, tid);
-        sb.load(g.b, g.ldb, n0, rows_b, kbeg, kend, g.vec_b, tid);
-        sa.store(As[0], tid);
-        sb.store(Bs[0], tid);
+        sa[0].store(As[0], tid);
+        sb[0].store(Bs[0], tid);
+        // Slot 0 is free again: it takes slab D (slot X % D always holds slab X).
+        if ((uint32_t)D < steps) {
+            sa[0].load(g.a, g.lda, m0, rows_a, kbeg + D * kBK, kend, g.vec_a, tid);
+            sb[0].load(g.b, g.ldb, n0, rows_b, kbeg + D * kBK, kend, g.vec_b, tid);
+        }
         __syncthreads();
     }
-    for (uint32_t s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        const bool more = s + 1 < steps;
-        if (more) {
-            const uint32_t k0 = kbeg + (s + 1) * kBK;
-            sa.load(g.a, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
-            sb.load(g.b, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+    for (uint32_t s0 = 0; s0 < steps; s0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const uint32_t s = s0 + j;
+            if (s >= steps) break;
+            const int cur = s & 1;
+            float4 af[TM][2], bf[TN][2];
+#pragma unroll
+            for (int ti = 0; ti < TM; ++ti) {
+                const float *p = As[cur] + (wm0 + ti * 32 + l32) * kPitch + 8 * half;
+                af[ti][0] = *reinterpret_cast<const float4 *>(p);
+                af[ti][1] = *reinterpret_cast<const float4 *>(p + 4);
+            }
+#pragma unroll
+            for (int tj = 0; tj < TN; ++tj) {
+                const float *p = Bs[cur] + (wn0 + tj * 32 + l32) * kPitch + 8 * half;
+                bf[tj][0] = *reinterpret_cast<const float4 *>(p);
+                bf[tj][1] = *reinterpret_cast<const float4 *>(p + 4);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < TN; ++tj)
+                        acc[q % NC][ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            ::dkz::lane(af[ti][q >> 2], q & 3), ::dkz::lane(bf[tj][q >> 2], q & 3), acc[q % NC][ti][tj],
+                            0, 0, 0);
+            // Slab s + 1 (ring slot (j + 1) % D) goes to the other LDS buffer,
+            // and its registers take the loads of slab s + 1 + D.
+            const int nx = (j + 1) % D;
+            if (s + 1 < steps) {
+                sa[nx].store(As[cur ^ 1], tid);
+                sb[nx].store(Bs[cur ^ 1], tid);
+                if (s + 1 + D < steps) {
+                    const uint32_t k0 = kbeg + (s + 1 + D) * kBK;
+                    sa[nx].load(g.a, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+                    sb[nx].load(g.b, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+                }
+            }
+            __syncthreads();
         }
-        float4 af[TM][2], bf[TN][2];
-#pragma unroll
-        for (int ti = 0; ti < TM; ++ti) {
-            const float *p = As[cur] + (wm0 + ti * 32 + l32) * kPitch + 8 * half;
-            af[ti][0] = *reinterpret_cast<const float4 *>(p);
-            af[ti][1] = *reinterpret_cast<const float4 *>(p + 4);
-        }
-#pragma unroll
-        for (int tj = 0; tj < TN; ++tj) {
-            const float *p = Bs[cur] + (wn0 + tj * 32 + l32) * kPitch + 8 * half;
-            bf[tj][0] = *reinterpret_cast<const float4 *>(p);
-            bf[tj][1] = *reinterpret_cast<const float4 *>(p + 4);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-#pragma unroll
-            for (int ti = 0; ti < TM; ++ti)
-#pragma unroll
-                for (int tj = 0; tj < TN; ++tj)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(::dkz::lane(af[ti][q >> 2], q & 3),
-                                                                        ::dkz::lane(bf[tj][q >> 2], q & 3), acc[ti][tj],
-                                                                        0, 0, 0);
-        if (more) {
-            sa.store(As[cur ^ 1], tid);
-            sb.store(Bs[cur ^ 1], tid);
-        }
-        __syncthreads();
     }
 
-    // acc[ti][tj][r] is C(row, col) of the wave's block (ti, tj) with
+#pragma unroll
+    for (int c = 1; c < NC; ++c)
+#pragma unroll
+        for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < TN; ++tj) acc[0][ti][tj] += acc[c][ti][tj];
+
+    // acc[0][ti][tj][r] is C(row, col) of the wave's block (ti, tj) with
     // row = 8*(r/4) + 4*(lane/32) + r%4 and col = lane%32.
 #pragma unroll
     for (int ti = 0; ti < TM; ++ti)
@@ -218,41 +252,65 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 const uint32_t i = m0 + wm0 + ti * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
                 if (i >= g.m) continue;
                 if (g.splits > 1) {
-                    g.partial[((size_t)split * g.m + i) * g.n + j] = acc[ti][tj][r];
+                    g.partial[((size_t)split * g.m + i) * g.n + j] = acc[0][ti][tj][r];
                 } else {
                     float *cp = g.c + i * g.ldc + j;
                     float cv = 0.0f;
                     if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
-                    *cp = cv + g.alpha * acc[ti][tj][r];
+                    *cp = cv + g.alpha * acc[0][ti][tj][r];
                 }
             }
         }
 }
 
 // The split-K epilogue: C(i, j) = beta-applied C + alpha * (sum of the splits'
-// partials in split order).
-__global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) {
-    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
-    const uint32_t mn = g.m * g.n;
-    if (e >= mn) return;
-    const uint32_t i = e / g.n, j = e - i * g.n;
-    float s = 0.0f;
-    for (uint32_t t = 0; t < g.splits; ++t) s += g.partial[(size_t)t * mn + e];
-    float *cp = g.c + i * g.ldc + j;
+// partials in split order). V4: n % 4 == 0 and C's rows are float4-aligned,
+// so a lane takes four consecutive columns of one row.
+__device__ __forceinline__ float gemm_out(const float *cp, float s, const GemmArgs &g) {
     float cv = 0.0f;
     if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
-    *cp = cv + g.alpha * s;
+    return cv + g.alpha * s;
 }
 
-template <int BM, int BN>
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) {
+    const uint32_t mn = g.m * g.n;
+    if constexpr (V4) {
+        const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
+        if (v >= (mn >> 2)) return;
+        const uint32_t e = v << 2, i = e / g.n, j = e - i * g.n;
+        float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t t = 0; t < g.splits; ++t) {
+            const float4 p = reinterpret_cast<const float4 *>(g.partial + (size_t)t * mn)[v];
+            s.x += p.x;
+            s.y += p.y;
+            s.z += p.z;
+            s.w += p.w;
+        }
+        float *cp = g.c + i * g.ldc + j;
+        const float4 o = make_float4(gemm_out(cp, s.x, g), gemm_out(cp + 1, s.y, g), gemm_out(cp + 2, s.z, g),
+                                     gemm_out(cp + 3, s.w, g));
+        *reinterpret_cast<float4 *>(cp) = o;
+    } else {
+        const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+        if (e >= mn) return;
+        const uint32_t i = e / g.n, j = e - i * g.n;
+        float s = 0.0f;
+        for (uint32_t t = 0; t < g.splits; ++t) s += g.partial[(size_t)t * mn + e];
+        float *cp = g.c + i * g.ldc + j;
+        *cp = gemm_out(cp, s, g);
+    }
+}
+
+template <int BM, int BN, int D>
 int launch_gemm(bool ta, bool tb, GemmArgs g) {
     const uint64_t total = (uint64_t)g.tiles_m * g.tiles_n * g.splits;
     DKZ_REQUIRE(total <= 0x7fffffffull);
     const dim3 grid((uint32_t)total), block(kBlock);
-    if (!ta && !tb) return launch("gemm_nn", gemm_mfma_kernel<BM, BN, false, false>, grid, block, g);
-    if (ta && !tb) return launch("gemm_tn", gemm_mfma_kernel<BM, BN, true, false>, grid, block, g);
-    if (!ta && tb) return launch("gemm_nt", gemm_mfma_kernel<BM, BN, false, true>, grid, block, g);
-    return launch("gemm_tt", gemm_mfma_kernel<BM, BN, true, true>, grid, block, g);
+    if (!ta && !tb) return launch("gemm_nn", gemm_mfma_kernel<BM, BN, false, false, D>, grid, block, g);
+    if (ta && !tb) return launch("gemm_tn", gemm_mfma_kernel<BM, BN, true, false, D>, grid, block, g);
+    if (!ta && tb) return launch("gemm_nt", gemm_mfma_kernel<BM, BN, false, true, D>, grid, block, g);
+    return launch("gemm_tt", gemm_mfma_kernel<BM, BN, true, true, D>, grid, block, g);
 }
 
 // Extent in elements of a rows x cols row-major view with leading dimension ld.
@@ -261,6 +319,16 @@ inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) {
 }
 
 constexpr uint32_t kCus = 256;
+
+// Slabs in flight in the 64x64 kernel (build-time tunable).
+#ifndef DKZ_GEMM_SMALL_PREFETCH
+#define DKZ_GEMM_SMALL_PREFETCH 2
+#endif
+
+// Workgroups per CU that a split-K grid aims for (build-time tunable).
+#ifndef DKZ_GEMM_SPLIT_TARGET
+#define DKZ_GEMM_SPLIT_TARGET 2
+#endif
 
 }  // namespace
 }  // namespace dkz
@@ -300,19 +368,19 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
 
     // 128x128 tiles when they give every CU two workgroups; 64x64 below, and
     // if even those leave CUs idle and K is long, split K (ranges of >= 128)
-    // until about four workgroups per CU, within the scratch.
+    // until about DKZ_GEMM_SPLIT_TARGET workgroups per CU, within the scratch.
     const uint64_t big = (uint64_t)div_up(m, 128) * div_up(n, 128);
     if (big >= 2 * kCus) {
         g.tiles_m = div_up(m, 128);
         g.tiles_n = div_up(n, 128);
-        return launch_gemm<128, 128>(ta != 0, tb != 0, g);
+        return launch_gemm<128, 128, 1>(ta != 0, tb != 0, g);
     }
     g.tiles_m = div_up(m, 64);
     g.tiles_n = div_up(n, 64);
     const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
     uint64_t splits = 1;
     if (tiles < 2 * kCus && k >= 256) {
-        splits = div_up(4 * kCus, tiles);
+        splits = div_up((uint64_t)DKZ_GEMM_SPLIT_TARGET * kCus, tiles);
         const uint64_t by_k = (uint64_t)k / 128;
         if (splits > by_k) splits = by_k;
         Scratch sc;
@@ -329,11 +397,14 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
         Scratch sc;
         DKZ_TRY(device_scratch(&sc));
         g.partial = sc.gemm;
-        DKZ_TRY((launch_gemm<64, 64>(ta != 0, tb != 0, g)));
-        return launch("gemm_splitk_reduce", gemm_splitk_reduce_kernel, dim3(div_up((uint64_t)m * n, kBlock)),
+        DKZ_TRY((launch_gemm<64, 64, DKZ_GEMM_SMALL_PREFETCH>(ta != 0, tb != 0, g)));
+        if (n % 4 == 0 && ldc % 4 == 0 && aligned16(c))
+            return launch("gemm_splitk_reduce", gemm_splitk_reduce_kernel<true>,
+                          dim3(div_up((uint64_t)m * n / 4, kBlock)), dim3(kBlock), g);
+        return launch("gemm_splitk_reduce", gemm_splitk_reduce_kernel<false>, dim3(div_up((uint64_t)m * n, kBlock)),
                       dim3(kBlock), g);
     }
-    return launch_gemm<64, 64>(ta != 0, tb != 0, g);
+    return launch_gemm<64, 64, DKZ_GEMM_SMALL_PREFETCH>(ta != 0, tb != 0, g);
 }
 
 }  // extern "C"

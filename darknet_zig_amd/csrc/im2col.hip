@@ -7,10 +7,10 @@
 // or 0 where the tap falls in the padding.
 //
 // im2col: the column buffer is the large, contiguous stream, so a lane owns
-// float4s of it (kUnroll per lane, all gathers issued before the stores) and
-// decomposes each element's flat index with multiply-high divisions. The
-// input taps are gathers that the caches serve: each input element feeds up
-// to ksize^2 rows.
+// float4s of it (kUnroll per lane, all gathers issued before the stores),
+// decomposes a float4's first flat index with multiply-high divisions and
+// steps the coordinates to the next three. The input taps are gathers that
+// the caches serve: each input element feeds up to ksize^2 rows.
 //
 // col2im: a lane owns image elements and gathers their contributions, so
 // every image element is written once and no atomics are needed. The CPU twin
@@ -51,6 +51,48 @@ __device__ __forceinline__ float im2col_at(const float *__restrict__ im, uint32_
     return im[(c_im * g.H + y) * g.W + x];
 }
 
+// Column coordinates of flat element e, stepped one element at a time so a
+// float4 costs one decomposition.
+struct ColPos {
+    uint32_t w, h, kw, kh, c;
+};
+
+__device__ __forceinline__ ColPos col_pos(uint32_t e, const ColGeom &g) {
+    ColPos q;
+    const uint32_t row = fdiv(e, g.div_plane);
+    const uint32_t pix = e - row * g.div_plane.d;
+    q.h = fdiv(pix, g.div_wo);
+    q.w = pix - q.h * g.Wo;
+    const uint32_t t = fdiv(row, g.div_k);
+    q.kw = row - t * g.k;
+    q.c = fdiv(t, g.div_k);
+    q.kh = t - q.c * g.k;
+    return q;
+}
+
+__device__ __forceinline__ void col_next(ColPos &q, const ColGeom &g) {
+    if (++q.w == g.Wo) {
+        q.w = 0;
+        if (++q.h == g.Ho) {
+            q.h = 0;
+            if (++q.kw == g.k) {
+                q.kw = 0;
+                if (++q.kh == g.k) {
+                    q.kh = 0;
+                    ++q.c;
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float col_tap(const float *__restrict__ im, const ColPos &q, const ColGeom &g) {
+    const uint32_t y = q.h * g.s + q.kh - g.p;  // wraps above H in the top padding
+    const uint32_t x = q.w * g.s + q.kw - g.p;
+    if (y >= g.H || x >= g.W) return 0.0f;
+    return im[(q.c * g.H + y) * g.W + x];
+}
+
 template <bool NT>
 __global__ __launch_bounds__(kBlock) void im2col_vec_kernel(const float *__restrict__ im, float *__restrict__ col,
                                                             ColGeom g, uint32_t n) {
@@ -59,17 +101,22 @@ __global__ __launch_bounds__(kBlock) void im2col_vec_kernel(const float *__restr
     float4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t q = base + u * kBlock;
-        if (q < nv) {
-            const uint32_t e = q << 2;
-            v[u] = make_float4(im2col_at(im, e, g), im2col_at(im, e + 1, g), im2col_at(im, e + 2, g),
-                               im2col_at(im, e + 3, g));
+        const uint32_t q4 = base + u * kBlock;
+        if (q4 < nv) {
+            ColPos q = col_pos(q4 << 2, g);
+            v[u].x = col_tap(im, q, g);
+            col_next(q, g);
+            v[u].y = col_tap(im, q, g);
+            col_next(q, g);
+            v[u].z = col_tap(im, q, g);
+            col_next(q, g);
+            v[u].w = col_tap(im, q, g);
         }
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t q = base + u * kBlock;
-        if (q < nv) st4<NT>(col, q, v[u]);
+        const uint32_t q4 = base + u * kBlock;
+        if (q4 < nv) st4<NT>(col, q4, v[u]);
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3u)) {
         const uint32_t e = (nv << 2) + threadIdx.x;
@@ -83,9 +130,10 @@ __global__ __launch_bounds__(kBlock) void im2col_scalar_kernel(const float *__re
 }
 
 // Image element e = (c, y, x): its value plus every column entry that im2col
-// took from it, in ascending (kh, kw).
-__device__ __forceinline__ float col2im_at(const float *__restrict__ col, float acc, uint32_t e,
-                                           const ColGeom &g) {
+// took from it, in ascending (kh, kw). S1: stride 1, so output position
+// (h, w) = (y + p - kh, x + p - kw) needs no division.
+template <bool S1>
+__device__ __forceinline__ float col2im_at(const float *__restrict__ col, float acc, uint32_t e, const ColGeom &g) {
     const uint32_t t = fdiv(e, g.div_w);
     const uint32_t x = e - t * g.W;
     const uint32_t c = fdiv(t, g.div_h);
@@ -94,24 +142,25 @@ __device__ __forceinline__ float col2im_at(const float *__restrict__ col, float 
     for (uint32_t kh = 0; kh < g.k; ++kh) {
         const uint32_t hy = y + g.p - kh;  // h*stride for the output row h that used this tap
         if ((int)hy < 0) break;            // larger kh only lowers it further
-        const uint32_t h = fdiv(hy, g.div_s);
-        if (h * g.s != hy || h >= g.Ho) continue;
+        const uint32_t h = S1 ? hy : fdiv(hy, g.div_s);
+        if ((!S1 && h * g.s != hy) || h >= g.Ho) continue;
         const float *rowp = col + ((c * g.k + kh) * g.k) * plane + h * g.Wo;
         for (uint32_t kw = 0; kw < g.k; ++kw) {
             const uint32_t wx = x + g.p - kw;
             if ((int)wx < 0) break;
-            const uint32_t w = fdiv(wx, g.div_s);
-            if (w * g.s != wx || w >= g.Wo) continue;
+            const uint32_t w = S1 ? wx : fdiv(wx, g.div_s);
+            if ((!S1 && w * g.s != wx) || w >= g.Wo) continue;
             acc += rowp[kw * plane + w];
         }
     }
     return acc;
 }
 
+template <bool S1>
 __global__ __launch_bounds__(kBlock) void col2im_kernel(const float *__restrict__ col, float *__restrict__ im,
                                                         ColGeom g, uint32_t n) {
     const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
-    if (e < n) im[e] = col2im_at(col, im[e], e, g);
+    if (e < n) im[e] = col2im_at<S1>(col, im[e], e, g);
 }
 
 // gpu.zig:652-653: height_col = (height + 2*pad - ksize)/stride + 1 in usize.
@@ -173,7 +222,8 @@ int dkz_col2im(const float *col, int channels, int height, int width, int ksize,
     if (nim == 0) return 0;
     DKZ_REQUIRE(im != nullptr && col != nullptr);
     const uint32_t n = (uint32_t)nim;
-    return launch("col2im", col2im_kernel, dim3(div_up(n, kBlock)), dim3(kBlock), col, im, g, n);
+    if (stride == 1) return launch("col2im", col2im_kernel<true>, dim3(div_up(n, kBlock)), dim3(kBlock), col, im, g, n);
+    return launch("col2im", col2im_kernel<false>, dim3(div_up(n, kBlock)), dim3(kBlock), col, im, g, n);
 }
 
 }  // extern "C"
