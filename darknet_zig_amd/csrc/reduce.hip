@@ -83,8 +83,9 @@ __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const f
 template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
 __global__ __launch_bounds__(BS) void chan_reduce_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g) {
     __shared__ double lds[BS / kWave];
+    const float pre = threadIdx.x == 0 ? fin.pre(blockIdx.x) : 0.0f;
     const double total = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, blockIdx.x, 0, lds);
-    if (threadIdx.x == 0) fin(blockIdx.x, total);
+    if (threadIdx.x == 0) fin(blockIdx.x, total, pre);
 }
 
 // K > 1, pass 1: workgroup (f, k) stores its partial at partials[f*K + k].
@@ -104,10 +105,11 @@ __global__ __launch_bounds__(kBlock) void chan_finalize_kernel(Fin fin, const do
                                                                uint32_t K) {
     const uint32_t f = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (f >= F) return;  // whole waves leave together
+    const float pre = fin.pre(f);
     double s = 0.0;
     for (uint32_t i = threadIdx.x & (kWave - 1); i < K; i += kWave) s += partials[f * K + i];
     s = wave_sum(s);
-    if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s);
+    if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s, pre);
 }
 
 template <int H, class T, class Fin, bool TWO>
@@ -179,28 +181,34 @@ struct SumProdDev {
 
 // ---- finalisations ----------------------------------------------------------
 
+// Each finaliser reads what it needs of channel f besides the sum (pre) before
+// the sum is formed, so that load overlaps the partial sums' loads.
 struct FinScale {  // out[f] = sum * scale_f (blas.zig:114, 133)
     float *out;
     float scale;
-    __device__ void operator()(uint32_t f, double s) const { out[f] = (float)s * scale; }
+    __device__ float pre(uint32_t) const { return 0.0f; }
+    __device__ void operator()(uint32_t f, double s, float) const { out[f] = (float)s * scale; }
 };
 struct FinMeanDelta {  // blas.zig:155
     float *out;
     const float *variance;
-    __device__ void operator()(uint32_t f, double s) const {
-        out[f] = (float)s * (-1.0f / sqrtf(variance[f] + 1e-5f));
+    __device__ float pre(uint32_t f) const { return variance[f]; }
+    __device__ void operator()(uint32_t f, double s, float v) const {
+        out[f] = (float)s * (-1.0f / sqrtf(v + 1e-5f));
     }
 };
 struct FinVarianceDelta {  // blas.zig:176: (sum * -0.5) * pow(v + 1e-5, -1.5)
     float *out;
     const float *variance;
-    __device__ void operator()(uint32_t f, double s) const {
-        out[f] = ((float)s * -0.5f) * pow_m1p5(variance[f] + 1e-5f);
+    __device__ float pre(uint32_t f) const { return variance[f]; }
+    __device__ void operator()(uint32_t f, double s, float v) const {
+        out[f] = ((float)s * -0.5f) * pow_m1p5(v + 1e-5f);
     }
 };
 struct FinAccumulate {  // updates[f] += sum (blas.zig:79, 98)
     float *updates;
-    __device__ void operator()(uint32_t f, double s) const { updates[f] = updates[f] + (float)s; }
+    __device__ float pre(uint32_t f) const { return updates[f]; }
+    __device__ void operator()(uint32_t f, double s, float u) const { updates[f] = u + (float)s; }
 };
 
 // backward_bias with spatial == 1 (gpu.zig:540-543): one lane per filter walks
