@@ -106,7 +106,10 @@ struct Slab {
                 const uint32_t avail = (r < rows && kk < kend) ? (kend - kk < 4 ? kend - kk : 4) : 0;
                 v[l] = load4(p, (r0 + r) * ld + kk, avail, vec);
             } else {
-                const uint32_t kr = f / (R / 4), q = f % (R / 4);
+                // k fastest across lanes: the transposing LDS stores below then
+                // fall in distinct banks (row pitch 80 B: 16 lanes per k-run
+                // cover 16 banks, the next 16 lanes start 16 banks further).
+                const uint32_t kr = f % kBK, q = f / kBK;
                 const uint32_t rr = 4 * q;
                 const uint32_t avail = (k0 + kr < kend && rr < rows) ? (rows - rr < 4 ? rows - rr : 4) : 0;
                 v[l] = load4(p, (k0 + kr) * ld + r0 + rr, avail, vec);
@@ -122,7 +125,7 @@ struct Slab {
                 const int r = f / (kBK / 4), q = f % (kBK / 4);
                 *reinterpret_cast<float4 *>(s + r * kPitch + 4 * q) = v[l];
             } else {
-                const int kr = f / (R / 4), q = f % (R / 4);
+                const int kr = f % kBK, q = f / kBK;
                 float *d = s + (4 * q) * kPitch + kr;
                 d[0] = v[l].x;
                 d[kPitch] = v[l].y;
