@@ -15,7 +15,19 @@
 namespace dkz {
 namespace {
 
-constexpr int kUnroll = 4;
+// float4s per lane per stream, by tensor size: large tensors stream best
+// with one (config-2 chain, scale_bias and normalize_delta: 1 -> 6590 GB/s,
+// 2 -> 6550, 3 -> 6489, 4 -> 6510), the ~33 MB tensors of config 1 with four
+// (normalize 0.63 of peak against 0.57 with one).
+#ifndef DKZ_BCAST_UNROLL_LARGE
+#define DKZ_BCAST_UNROLL_LARGE 1
+#endif
+#ifndef DKZ_BCAST_UNROLL_SMALL
+#define DKZ_BCAST_UNROLL_SMALL 4
+#endif
+#ifndef DKZ_BCAST_LARGE_FLOAT4S
+#define DKZ_BCAST_LARGE_FLOAT4S (1u << 22)  // 16 Mi elements
+#endif
 
 template <class Op, bool TWO, bool ROWWISE, bool S4>
 __device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io, float4 a,
@@ -37,7 +49,7 @@ __device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io,
 }
 
 // H: bit 0 = nontemporal io loads, bit 1 = io stores, bit 2 = loads of a.
-template <class Op, bool TWO, bool ROWWISE, bool S4, int H>
+template <class Op, bool TWO, bool ROWWISE, bool S4, int H, int kUnroll>
 __global__ __launch_bounds__(kBlock) void bcast_vec_kernel(Op op, float *io, const float *a, ChanGeom g,
                                                            uint32_t n) {
     constexpr bool kNtIo = (H & 1) != 0, kNtOut = (H & 2) != 0, kNtA = (H & 4) != 0;
@@ -88,12 +100,21 @@ int run_bcast(const char *name, const Op &op, float *io, const float *a, int bat
     const ChanGeom g{make_fastdiv((uint32_t)spatial), make_fastdiv((uint32_t)filters)};
     if (aligned16(io) && (!TWO || aligned16(a))) {
         const uint32_t nv = n >> 2;
-        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
-        if (spatial % 4 == 0)
-            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H>, dim3(grid), dim3(kBlock), op, io,
-                          a, g, n);
-        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H>, dim3(grid), dim3(kBlock), op, io, a,
-                      g, n);
+        const bool large = nv >= DKZ_BCAST_LARGE_FLOAT4S;
+        const uint32_t u = large ? DKZ_BCAST_UNROLL_LARGE : DKZ_BCAST_UNROLL_SMALL;
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * u);
+        if (spatial % 4 == 0) {
+            if (large)
+                return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, DKZ_BCAST_UNROLL_LARGE>, dim3(grid),
+                              dim3(kBlock), op, io, a, g, n);
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, DKZ_BCAST_UNROLL_SMALL>, dim3(grid),
+                          dim3(kBlock), op, io, a, g, n);
+        }
+        if (large)
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, DKZ_BCAST_UNROLL_LARGE>, dim3(grid),
+                          dim3(kBlock), op, io, a, g, n);
+        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, DKZ_BCAST_UNROLL_SMALL>, dim3(grid),
+                      dim3(kBlock), op, io, a, g, n);
     }
     const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
     return launch(name, bcast_scalar_kernel<Op, TWO, ROWWISE>, dim3(grid), dim3(kBlock), op, io, a, g, n);

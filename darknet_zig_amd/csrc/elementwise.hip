@@ -4,9 +4,9 @@
 // smooth L1, dropout, and the Adam update as one pass).
 //
 // One kernel shape serves all of them: each thread moves kUnroll float4s per
-// stream, issuing every load before the first store, so a wave keeps
-// kUnroll * 16 bytes per lane and stream in flight. The last n % 4 elements
-// go to the first threads of block 0. Streams that are not 16-byte aligned
+// stream (2 or 4, by tensor size), issuing every load before the first
+// store, so a wave keeps kUnroll * 16 bytes per lane and stream in flight.
+// The last n % 4 elements go to the first threads of block 0. Streams that are not 16-byte aligned
 // (a Buf.offset() view, gpu.zig:128-133) take a one-element-per-thread
 // grid-stride kernel with the same arithmetic.
 #include "dkz_device.hpp"
@@ -16,7 +16,20 @@
 namespace dkz {
 namespace {
 
-constexpr int kUnroll = 4;
+// float4s per lane per stream, by tensor size. Large tensors: 2 (config-2
+// gradient 45.5 us against 46.0 with 4; rand_uniform over 103 M floats 66.6
+// against 71.9 us). The ~16 M-element tensors of config 1 and the per-channel
+// vectors: 4 (the config-1 layer sequence, copies and EMA included, 55.8 us
+// against 70.8 with 2).
+#ifndef DKZ_EW_UNROLL_LARGE
+#define DKZ_EW_UNROLL_LARGE 2
+#endif
+#ifndef DKZ_EW_UNROLL_SMALL
+#define DKZ_EW_UNROLL_SMALL 4
+#endif
+#ifndef DKZ_EW_LARGE_FLOAT4S
+#define DKZ_EW_LARGE_FLOAT4S (1u << 22)  // 16 Mi elements
+#endif
 
 // NI input streams, NO output streams; an output may be one of the inputs.
 template <int NI, int NO>
@@ -61,7 +74,7 @@ __device__ __forceinline__ void apply_vec(const Op &op, const Streams<NI, NO> &s
     for (int k = 0; k < NO; ++k) st4<(H & 16) != 0>(s.out[k], v, out[k]);
 }
 
-template <int NI, int NO, int H, class Op>
+template <int NI, int NO, int H, class Op, int kUnroll>
 __global__ __launch_bounds__(kBlock) void ew_vec_kernel(Op op, Streams<NI, NO> s, uint32_t n) {
     const uint32_t nv = n >> 2;
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
@@ -103,8 +116,11 @@ int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
     const uint32_t un = (uint32_t)n;
     if (vec) {
         const uint32_t nv = un >> 2;
-        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
-        return launch(name, ew_vec_kernel<NI, NO, H, Op>, dim3(grid), dim3(kBlock), op, s, un);
+        if (nv >= DKZ_EW_LARGE_FLOAT4S)
+            return launch(name, ew_vec_kernel<NI, NO, H, Op, DKZ_EW_UNROLL_LARGE>,
+                          dim3(div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_LARGE)), dim3(kBlock), op, s, un);
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_SMALL);
+        return launch(name, ew_vec_kernel<NI, NO, H, Op, DKZ_EW_UNROLL_SMALL>, dim3(grid), dim3(kBlock), op, s, un);
     }
     const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
     return launch(name, ew_scalar_kernel<NI, NO, Op>, dim3(grid), dim3(kBlock), op, s, un);
@@ -236,7 +252,7 @@ __device__ __forceinline__ float uniform_at(uint32_t seed, uint32_t i) {
     return (float)(hash_u32(seed ^ hash_u32(i)) >> 8) * (1.0f / 16777216.0f);
 }
 
-template <bool NT>
+template <bool NT, int kUnroll>
 __global__ __launch_bounds__(kBlock) void rand_vec_kernel(float *x, uint32_t seed, uint32_t n) {
     const uint32_t nv = n >> 2;
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
@@ -354,9 +370,13 @@ int dkz_rand_uniform(int n, float *x, unsigned int seed) {
     const uint32_t un = (uint32_t)n;
     if (aligned16(x)) {
         const uint32_t nv = un >> 2;
-        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);
-        return launch("rand_uniform", rand_vec_kernel<(DKZ_HINT_RAND_UNIFORM & 16) != 0>, dim3(grid), dim3(kBlock),
-                      x, (uint32_t)seed, un);
+        constexpr bool kNt = (DKZ_HINT_RAND_UNIFORM & 16) != 0;
+        if (nv >= DKZ_EW_LARGE_FLOAT4S)
+            return launch("rand_uniform", rand_vec_kernel<kNt, DKZ_EW_UNROLL_LARGE>,
+                          dim3(div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_LARGE)), dim3(kBlock), x, (uint32_t)seed, un);
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_SMALL);
+        return launch("rand_uniform", rand_vec_kernel<kNt, DKZ_EW_UNROLL_SMALL>, dim3(grid), dim3(kBlock), x,
+                      (uint32_t)seed, un);
     }
     const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
     return launch("rand_uniform", rand_scalar_kernel, dim3(grid), dim3(kBlock), x, (uint32_t)seed, un);
