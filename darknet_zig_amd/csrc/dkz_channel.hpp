@@ -57,10 +57,13 @@ constexpr uint32_t kWideBlock = 1024;
 //    workgroup per channel and one launch (1024 threads for long channels);
 //  * otherwise about 2048 workgroups of >= 4096 elements, then the finalize
 //    launch. `sums` f64 partials per workgroup must fit the scratch.
+#ifndef DKZ_ONE_LAUNCH_MAX_BYTES
+#define DKZ_ONE_LAUNCH_MAX_BYTES 160000000ull
+#endif
 inline uint32_t pick_split(uint32_t filters, uint32_t chan_len, uint32_t streams, uint32_t sums = 1,
                            uint32_t target = 2048, uint32_t min_chunk = 4096) {
     const uint64_t bytes = (uint64_t)4 * streams * filters * chan_len;
-    if (filters >= 256 || (filters >= 128 && bytes <= 160000000ull)) return 1;
+    if (filters >= 256 || (filters >= 128 && bytes <= DKZ_ONE_LAUNCH_MAX_BYTES)) return 1;
     uint32_t k = div_up(target, filters);
     const uint32_t kmax = chan_len / min_chunk > 1 ? chan_len / min_chunk : 1;
     if (k > kmax) k = kmax;

@@ -48,6 +48,21 @@ def bits(a: np.ndarray) -> np.ndarray:
     return u
 
 
+def chan_sum64(terms: np.ndarray, shape) -> np.ndarray:
+    """Per-channel f64 sums of per-element terms that are already rounded to
+    f32 exactly as the CPU twin rounds them (the product delta*x_norm,
+    (x-m)^2 of the f32 difference, ...): the f64 evaluation the reduction
+    rule compares against."""
+    B, F, S = shape
+    return terms.astype(np.float32).astype(np.float64).reshape(B, F, S).sum(axis=(0, 2))
+
+
+def chan_f32(vec: np.ndarray, shape) -> np.ndarray:
+    """A per-channel vector broadcast over an NCHW tensor, in f32."""
+    B, F, S = shape
+    return np.broadcast_to(vec.astype(np.float32)[None, :, None], (B, F, S)).ravel()
+
+
 def assert_bitexact(got: np.ndarray, want: np.ndarray, name: str) -> None:
     assert got.shape == want.shape and got.dtype == want.dtype, (name, got.shape, want.shape)
     g, w = bits(got).ravel(), bits(want).ravel()

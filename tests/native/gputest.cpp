@@ -119,16 +119,19 @@ Vec pull(gpu::Buf b, size_t n) {
     return h;
 }
 
-// f64 references of the per-channel sums (blas.zig:73-178 in exact-ish arithmetic)
+// f64 sums of the per-channel terms, each term rounded to f32 as the twin
+// rounds it (blas.zig:73-178): x, x*y (the product in f32), or (x-m)^2 (the
+// difference and the square in f32).
 std::vector<double> chan_sum64(const Vec &x, const Vec *y, size_t B, size_t F, size_t S, const Vec *mean) {
     std::vector<double> out(F, 0.0);
     for (size_t b = 0; b < B; ++b)
         for (size_t f = 0; f < F; ++f)
             for (size_t s = 0; s < S; ++s) {
                 const size_t i = (b * F + f) * S + s;
-                double v = x[i];
-                if (mean) v -= (*mean)[f];
-                out[f] += y ? v * (double)(*y)[i] : (mean ? v * v : v);
+                float v = x[i];
+                if (mean) v = v - (*mean)[f];
+                const float t = y ? v * (*y)[i] : (mean ? v * v : v);
+                out[f] += (double)t;
             }
     return out;
 }
@@ -494,7 +497,7 @@ void restOfSurface(Rng &rng) {
                 for (size_t f = 0; f < F; ++f)
                     for (size_t s = 0; s < S; ++s) {
                         const size_t i = (bb * F + f) * S + s;
-                        r64[f] += (double)delta[i] * ((double)x[i] - mean[f]);
+                        r64[f] += (double)(delta[i] * (x[i] - mean[f]));  // f32 terms, blas.zig:174
                     }
             for (size_t f = 0; f < F; ++f) r64[f] *= -0.5 * std::pow((double)var[f] + 1e-5, -1.5);
             gpu::varianceDelta(dx, dd, dm, dvv, B, F, S, out);

@@ -17,7 +17,7 @@ import pytest
 from darknet_zig_amd import gpu
 from darknet_zig_amd.activations import Activation
 from oracle import ref
-from tests.helpers import assert_bitexact, assert_r5, down, normal, rng, uniform, up
+from tests.helpers import assert_bitexact, assert_r5, chan_f32, chan_sum64, down, normal, rng, uniform, up
 
 pytestmark = pytest.mark.gpu
 
@@ -89,7 +89,8 @@ def test_mean_variance_normalize(dev, shape):
     v_gpu = down(dvar, v_cpu)
     if B * S > 1:
         scale_v = np.float32(1.0) / np.float32(B * S - 1)
-        dev64 = ((x64 - m_cpu.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2))
+        diff = x - chan_f32(m_cpu, shape)  # blas.zig:128-131: f32 difference, f32 square
+        dev64 = chan_sum64(diff * diff, shape)
         assert_r5(v_gpu, v_cpu, dev64 * np.float64(scale_v), f"variance {shape}")
 
     # normalize with the CPU statistics: bit-exact
@@ -118,7 +119,7 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
          upd0.astype(np.float64) + d64.sum(axis=(0, 2))),
         ("backward_scale", lambda u: gpu.backwardScale(dxn, dd, B, F, S, u),
          lambda u: ref.backwardScale(x_norm, delta, B, F, S, u),
-         upd0.astype(np.float64) + (d64 * xn64).sum(axis=(0, 2))),
+         upd0.astype(np.float64) + chan_sum64(delta * x_norm, shape)),  # f32 products, blas.zig:96
     ):
         cpu = upd0.copy()
         cpu_fn(cpu)
@@ -140,7 +141,7 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
     fac = np.float32(-1.0) / np.sqrt(v + np.float32(1e-5))
     assert_r5(down(dmd, md_cpu), md_cpu, d64.sum(axis=(0, 2)) * fac.astype(np.float64), f"mean_delta {shape}")
     v64 = (v + np.float32(1e-5)).astype(np.float64)
-    vd64 = (d64 * (x64 - m.astype(np.float64)[None, :, None])).sum(axis=(0, 2)) * -0.5 * v64**-1.5
+    vd64 = chan_sum64(delta * (x - chan_f32(m, shape)), shape) * -0.5 * v64**-1.5  # blas.zig:174
     assert_r5(down(dvd, vd_cpu), vd_cpu, vd64, f"variance_delta {shape}")
 
     # normalize_delta with the CPU per-channel inputs: bit-exact
@@ -267,7 +268,7 @@ def test_bn_layer_backward_sequence(dev):
     ref.gradientArray(y, Activation.leaky, d_c)
     g64 = _chan64(d_c, CONFIG2)  # the gradient is bit-exact, so both sides reduce this
     bu64 = g64.sum(axis=(0, 2))
-    su64 = (g64 * _chan64(x_norm, CONFIG2)).sum(axis=(0, 2))
+    su64 = chan_sum64(d_c * x_norm, CONFIG2)  # f32 products of the (bit-exact) gradient
     ref.backwardBias(bu, d_c, B, F, S)
     ref.backwardScale(x_norm, d_c, B, F, S, su)
     ref.scaleBias(d_c, scales, B, F, S)

@@ -81,6 +81,8 @@ def _forward_case(shape, act, train, inplace, seed):
         x64 = _chan64(inp, shape)
         assert_r5(g_m, c_m, x64.sum(axis=(0, 2)) * np.float64(np.float32(1) / np.float32(B * S)), f"mean {shape}")
         if B * S > 1:
+            # the fused statistics sum exact (x - c) terms in f64 (not the twin's
+            # f32-rounded (x - m)^2), so their f64 reference is the exact one
             dev64 = ((x64 - c_m.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2))
             assert_r5(g_v, c_v, dev64 * np.float64(np.float32(1) / np.float32(B * S - 1)), f"variance {shape}")
         # the rolling averages from the GPU statistics: scal then axpy, bit-exact
