@@ -110,9 +110,11 @@
 #define DKZ_HINT_SHORTCUT 1
 #endif
 
-// im2col.hip: bit 1 = column buffer store (the GEMM reads it next)
+// im2col.hip: bit 1 = column buffer store. Nontemporal although the GEMM
+// reads the buffer next: im2col of a [128,56,56] image 8.1 -> 6.6 us, and the
+// im2col + GEMM pair of a convolution's forward step no slower (31.9 -> 31.1 us).
 #ifndef DKZ_HINT_IM2COL
-#define DKZ_HINT_IM2COL 0
+#define DKZ_HINT_IM2COL 2
 #endif
 
 // batchnorm.hip, the fused layer passes. The statistics pass keeps its input

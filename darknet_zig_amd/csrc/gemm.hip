@@ -275,6 +275,8 @@ __device__ __forceinline__ float gemm_out(const float *cp, float s, const GemmAr
     return cv + g.alpha * s;
 }
 
+constexpr int kReduceBatch = 8;
+
 template <bool V4>
 __global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) {
     const uint32_t mn = g.m * g.n;
@@ -282,13 +284,22 @@ __global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) 
         const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
         if (v >= (mn >> 2)) return;
         const uint32_t e = v << 2, i = e / g.n, j = e - i * g.n;
+        // Eight partials in flight at a time, added in split order; the
+        // missing ones of the last batch are +0, which leaves the sum as is.
         float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (uint32_t t = 0; t < g.splits; ++t) {
-            const float4 p = reinterpret_cast<const float4 *>(g.partial + (size_t)t * mn)[v];
-            s.x += p.x;
-            s.y += p.y;
-            s.z += p.z;
-            s.w += p.w;
+        for (uint32_t t = 0; t < g.splits; t += kReduceBatch) {
+            float4 p[kReduceBatch];
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u)
+                p[u] = t + u < g.splits ? reinterpret_cast<const float4 *>(g.partial + (size_t)(t + u) * mn)[v]
+                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u) {
+                s.x += p[u].x;
+                s.y += p[u].y;
+                s.z += p[u].z;
+                s.w += p[u].w;
+            }
         }
         float *cp = g.c + i * g.ldc + j;
         const float4 o = make_float4(gemm_out(cp, s.x, g), gemm_out(cp + 1, s.y, g), gemm_out(cp + 2, s.z, g),
@@ -299,7 +310,13 @@ __global__ __launch_bounds__(kBlock) void gemm_splitk_reduce_kernel(GemmArgs g) 
         if (e >= mn) return;
         const uint32_t i = e / g.n, j = e - i * g.n;
         float s = 0.0f;
-        for (uint32_t t = 0; t < g.splits; ++t) s += g.partial[(size_t)t * mn + e];
+        for (uint32_t t = 0; t < g.splits; t += kReduceBatch) {
+            float p[kReduceBatch];
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u) p[u] = t + u < g.splits ? g.partial[(size_t)(t + u) * mn + e] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kReduceBatch; ++u) s += p[u];
+        }
         float *cp = g.c + i * g.ldc + j;
         *cp = gemm_out(cp, s, g);
     }

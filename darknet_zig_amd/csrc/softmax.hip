@@ -60,6 +60,23 @@ __device__ __forceinline__ void xent1(float p, float t, float &d, float &l) {
     d = t - p;
 }
 
+__device__ __forceinline__ void read32(const float4 *lds, uint32_t batch, float4 (&v)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = lds[batch * 8 + u];
+}
+
+// s plus the 32 values, one at a time, left to right.
+__device__ __forceinline__ float add32(float s, const float4 (&v)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        s += v[u].x;
+        s += v[u].y;
+        s += v[u].z;
+        s += v[u].w;
+    }
+    return s;
+}
+
 // V4: the row is 16-byte aligned and n % 4 == 0 (every pointer too), so it
 // moves in float4s.
 template <bool SEQ, bool XENT, bool V4>
@@ -108,22 +125,21 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
         }
         __syncthreads();
         if (threadIdx.x == 0) {
-            // The one sequential part: 8 LDS reads in flight ahead of the adds.
+            // The one sequential part, in batches of 32 exps: the LDS reads of
+            // the next batch are in flight while this one is added.
             float s = 0.0f;
-            uint32_t i = 0;
-            for (; i + 32 <= n; i += 32) {
-                float4 v[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = e_lds4[(i >> 2) + u];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    s += v[u].x;
-                    s += v[u].y;
-                    s += v[u].z;
-                    s += v[u].w;
-                }
+            const uint32_t nb = n >> 5;
+            float4 va[8], vb[8];
+            if (nb > 0) read32(e_lds4, 0, va);
+            for (uint32_t b = 0; b < nb;) {
+                if (b + 1 < nb) read32(e_lds4, b + 1, vb);
+                s = add32(s, va);
+                if (++b >= nb) break;
+                if (b + 1 < nb) read32(e_lds4, b + 1, va);
+                s = add32(s, vb);
+                ++b;
             }
-            for (; i < n; ++i) s += e_lds[i];
+            for (uint32_t i = nb << 5; i < n; ++i) s += e_lds[i];
             sum_sh = s;
         }
         __syncthreads();
