@@ -22,7 +22,9 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                a fraction of 8 TB/s: sustained (back-to-back launches, the
                per-launch time of a stream of such calls) and single-launch
                (an event pair around each launch); plus rand_uniform/dropout,
-               the one-pass Adam update and im2col/col2im
+               the one-pass Adam update, im2col/col2im, and shapes off the
+               configs' fast paths (a 3x3/s2 max pool, a spatial softmax, a
+               connected layer's bias gradient)
   gemm         dkz_gemm at config 2's convolution shapes and a large square,
                TFLOP/s against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
@@ -452,6 +454,45 @@ def per_op_table(gpu, hip, stream, launches: int):
         [lambda i=i, s_=s_: gpu.randUniform(nin, i, s_) for i, s_ in zip(ins, seeds)])
     add("dropout[256,512,28,28]", "dropout", 3 * 4 * nin,
         [lambda i=i, o=o: gpu.dropout(i, nin, o, 0.5, 2.0) for i, o in zip(ins, ins[::-1])])
+    dev.free()
+
+    # -- shapes off the configs' fast paths: a 3x3/s2 max pool (the generic
+    # kernels), a detection head's spatial softmax (groups of 85 classes, 169
+    # positions apart) and a connected layer's bias gradient (spatial 1)
+    dev = Device(gpu)
+    r = gen(6)
+    gb, gc, gh, gsz, gst, gpad = 64, 128, 56, 3, 2, 2
+    gin = gb * gc * gh * gh
+    goh = (gh + gpad - gsz) // gst + 1
+    gout = gb * gc * goh * goh
+    R = rotations(4 * (gin + 2 * gout))
+    gins = [dev.up(r.uniform(-1, 1, gin).astype(np.float32)) for _ in range(R)]
+    gouts = [dev.zeros(gout) for _ in range(R)]
+    gidx = [dev.zeros(gout) for _ in range(R)]
+    cfg = "pool[64,128,56,56]"
+    add(cfg, "maxpool_fwd 3x3/s2 (generic)", 4 * (gin + 2 * gout),
+        [lambda i=i, o=o, x=x: gpu.forwardMaxpool(gout, gh, gh, gc, gst, gsz, gpad, i, o, x)
+         for i, o, x in zip(gins, gouts, gidx)])
+    add(cfg, "maxpool_bwd 3x3/s2 (generic)", 4 * (2 * gout + 2 * gin),
+        [lambda d=d, p=p, x=x: gpu.backwardMaxpool(gin, gh, gh, gc, gst, gsz, gpad, d, p, x)
+         for d, p, x in zip(gouts, gins, gidx)])
+    dev.free()
+    dev = Device(gpu)
+    sb, sc, ss = 64, 85, 169
+    sn = sb * sc * ss
+    R = rotations(8 * sn)
+    sxs = [dev.up(r.normal(0, 2, sn).astype(np.float32)) for _ in range(R)]
+    sys_ = [dev.zeros(sn) for _ in range(R)]
+    add(f"softmax[{sb},{sc},13,13]", "spatial softmax (groups across positions)", 2 * 4 * sn,
+        [lambda x=x, y=y: gpu.softmax(x, sc, sb, sc * ss, ss, 1, ss, 1.0, y) for x, y in zip(sxs, sys_)])
+    dev.free()
+    dev = Device(gpu)
+    cb, cf = 256, 1000
+    R = rotations(4 * cb * cf)
+    cds = [dev.up(r.normal(0, 1, cb * cf).astype(np.float32)) for _ in range(R)]
+    cu = dev.zeros(cf)
+    add(f"connected[{cb},{cf}]", "backward_bias (spatial 1)", 4 * (cb * cf + 2 * cf),
+        [lambda d=d: gpu.backwardBias(cu, d, cb, cf, 1) for d in cds])
     dev.free()
 
     # -- the Adam update (gpu.zig:804-830) over config 4's 25e6 weights, one pass

@@ -29,11 +29,17 @@ namespace {
 
 struct PoolGeom {
     uint32_t h, w, c, oh, ow, size, stride, half_pad;  // window offset is -half_pad
-    FastDiv div_w, div_h, div_ow, div_oh;
+    FastDiv div_w, div_h, div_ow, div_oh, div_size, div_stride;
 };
+
+// The generic kernels visit a window's taps (forward) or an element's
+// candidate outputs (backward) in batches of TB -- 4 when the window (or the
+// candidate set) is at most 2x2, else 9, a whole 3x3 window: a batch's loads
+// are all issued before any of them is used.
 
 // ---- generic ----------------------------------------------------------------
 
+template <int TB>
 __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g,
                                                              uint32_t out_n) {
     const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
@@ -45,17 +51,28 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
     const uint32_t plane = t2;  // k + b*c
     float mx = -FLT_MAX;
     int mi = -1;
-    for (uint32_t n = 0; n < g.size; ++n) {
-        const int ch = (int)(i * g.stride + n) - (int)g.half_pad;
-        if (ch < 0 || ch >= (int)g.h) continue;
-        for (uint32_t m = 0; m < g.size; ++m) {
+    // Taps in the twin's order (window row n, then column m); those outside
+    // the input are skipped.
+    const uint32_t taps = g.size * g.size;
+    for (uint32_t t0 = 0; t0 < taps; t0 += TB) {
+        float v[TB];
+        uint32_t at[TB];
+        bool ok[TB];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            const uint32_t tap = t0 + u;
+            const uint32_t n = fdiv(tap, g.div_size), m = tap - n * g.size;
+            const int ch = (int)(i * g.stride + n) - (int)g.half_pad;
             const int cw = (int)(j * g.stride + m) - (int)g.half_pad;
-            if (cw < 0 || cw >= (int)g.w) continue;
-            const uint32_t index = (uint32_t)cw + g.w * ((uint32_t)ch + g.h * plane);
-            const float val = in[index];
-            if (val > mx) {
-                mx = val;
-                mi = (int)index;
+            ok[u] = tap < taps && ch >= 0 && ch < (int)g.h && cw >= 0 && cw < (int)g.w;
+            at[u] = (uint32_t)cw + g.w * ((uint32_t)ch + g.h * plane);
+            v[u] = ok[u] ? in[at[u]] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            if (ok[u] && v[u] > mx) {
+                mx = v[u];
+                mi = (int)at[u];
             }
         }
     }
@@ -63,6 +80,7 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
     idx[o] = mi;
 }
 
+template <int TB>
 __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta, float *prev, const int *idx,
                                                              PoolGeom g, uint32_t in_n) {
     const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
@@ -75,20 +93,43 @@ __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta,
     // Outputs i with i*stride + n - half_pad == y for some n in [0, size).
     const int yp = (int)(y + g.half_pad), xp = (int)(x + g.half_pad);
     const int s = (int)g.stride, sz = (int)g.size;
-    const int ilo = yp - sz + 1 <= 0 ? 0 : (yp - sz + 1 + s - 1) / s;
-    const int jlo = xp - sz + 1 <= 0 ? 0 : (xp - sz + 1 + s - 1) / s;
-    const int ihi = min(yp / s, (int)g.oh - 1);
-    const int jhi = min(xp / s, (int)g.ow - 1);
+    const int ilo = yp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(yp - sz + s), g.div_stride);  // ceil((yp-sz+1)/s)
+    const int jlo = xp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(xp - sz + s), g.div_stride);
+    const int ihi = min((int)fdiv((uint32_t)yp, g.div_stride), (int)g.oh - 1);
+    const int jhi = min((int)fdiv((uint32_t)xp, g.div_stride), (int)g.ow - 1);
     if (ilo > ihi || jlo > jhi) return;
+    // Candidates in ascending o (row i, then column j): a batch's indexes are
+    // loaded together, then the deltas of those that name e -- and, at the
+    // first hit, e's own value -- then the deltas are added in order.
+    const uint32_t cnt = (uint32_t)(ihi - ilo + 1) * (uint32_t)(jhi - jlo + 1);
+    int ci = ilo, cj = jlo;
     float v = 0.0f;
     bool touched = false;
-    for (int i = ilo; i <= ihi; ++i) {
-        for (int j = jlo; j <= jhi; ++j) {
-            const uint32_t o = (uint32_t)j + g.ow * ((uint32_t)i + g.oh * plane);
-            if (idx[o] == (int)e) {
-                if (!touched) v = prev[e];
+    for (uint32_t c0 = 0; c0 < cnt; c0 += TB) {
+        uint32_t o[TB];
+        bool hit[TB];
+        float d[TB];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            const bool ok = c0 + u < cnt;
+            o[u] = (uint32_t)cj + g.ow * ((uint32_t)ci + g.oh * plane);
+            hit[u] = ok && idx[o[u]] == (int)e;
+            if (++cj > jhi) {
+                cj = jlo;
+                ++ci;
+            }
+        }
+        bool any = false;
+#pragma unroll
+        for (int u = 0; u < TB; ++u) any = any || hit[u];
+        if (any && !touched) v = prev[e];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) d[u] = hit[u] ? delta[o[u]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            if (hit[u]) {
                 touched = true;
-                v += delta[o];
+                v += d[u];
             }
         }
     }
@@ -174,6 +215,7 @@ int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, P
                   bool *fast) {
     DKZ_REQUIRE(in_h >= 0 && in_w >= 0 && in_c >= 0 && pad >= 0);
     DKZ_REQUIRE(stride >= 1 && size >= 1);
+    DKZ_REQUIRE((uint64_t)size * (uint64_t)size <= kMaxElems - 16);  // taps counted below 2^31
     DKZ_REQUIRE((int64_t)in_w + pad >= size && (int64_t)in_h + pad >= size);  // pooling.zig:33-34
     g->h = (uint32_t)in_h;
     g->w = (uint32_t)in_w;
@@ -187,6 +229,8 @@ int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, P
     g->div_h = make_fastdiv(g->h ? g->h : 1);
     g->div_ow = make_fastdiv(g->ow);
     g->div_oh = make_fastdiv(g->oh);
+    g->div_size = make_fastdiv(g->size);
+    g->div_stride = make_fastdiv(g->stride);
     *planes = 0;
     *fast = size == 2 && stride == 2 && pad / 2 == 0 && in_w % 4 == 0 && in_h % 2 == 0 && in_w > 0 && in_h > 0;
     return 0;
@@ -217,8 +261,12 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
         return launch("forward_maxpool_2x2", maxpool2_fwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
                       input, output, indexes, g, pairs);
     }
-    return launch("forward_maxpool", maxpool_fwd_kernel, dim3(div_up((uint32_t)out_n, kBlock)), dim3(kBlock),
-                  input, output, indexes, g, (uint32_t)out_n);
+    const dim3 grid(div_up((uint32_t)out_n, kBlock));
+    if (g.size <= 2)
+        return launch("forward_maxpool", maxpool_fwd_kernel<4>, grid, dim3(kBlock), input, output, indexes, g,
+                      (uint32_t)out_n);
+    return launch("forward_maxpool", maxpool_fwd_kernel<9>, grid, dim3(kBlock), input, output, indexes, g,
+                  (uint32_t)out_n);
 }
 
 int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int size, int pad,
@@ -239,8 +287,14 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
         return launch("backward_maxpool_2x2", maxpool2_bwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
                       delta, prev_delta, indexes, g, pairs);
     }
-    return launch("backward_maxpool", maxpool_bwd_kernel, dim3(div_up((uint32_t)in_n, kBlock)), dim3(kBlock),
-                  delta, prev_delta, indexes, g, (uint32_t)in_n);
+    // Outputs whose window covers one input, per dimension: at most ceil(size / stride).
+    const uint32_t per_dim = (g.size + g.stride - 1) / g.stride;
+    const dim3 grid(div_up((uint32_t)in_n, kBlock));
+    if (per_dim <= 2)
+        return launch("backward_maxpool", maxpool_bwd_kernel<4>, grid, dim3(kBlock), delta, prev_delta, indexes, g,
+                      (uint32_t)in_n);
+    return launch("backward_maxpool", maxpool_bwd_kernel<9>, grid, dim3(kBlock), delta, prev_delta, indexes, g,
+                  (uint32_t)in_n);
 }
 
 }  // extern "C"

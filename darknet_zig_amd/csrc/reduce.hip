@@ -214,12 +214,23 @@ struct FinAccumulate {  // updates[f] += sum (blas.zig:79, 98)
 // backward_bias with spatial == 1 (gpu.zig:540-543): one lane per filter walks
 // the batch in order, adding each row's one-element sum (0 + delta) to the
 // update exactly as blas.zig:73-82 does -- bit-exact, and coalesced across f.
+// A layer has few filters, so each lane keeps 32 rows' loads in flight
+// before their adds.
 __global__ __launch_bounds__(kBlock) void backward_bias_conn_kernel(float *updates, const float *delta,
                                                                     uint32_t batch, uint32_t filters) {
+    constexpr uint32_t kRows = 32;
     const uint32_t f = blockIdx.x * kBlock + threadIdx.x;
     if (f >= filters) return;
     float u = updates[f];
-    for (uint32_t b = 0; b < batch; ++b) u += 0.0f + delta[b * filters + f];
+    uint32_t b = 0;
+    for (; b + kRows <= batch; b += kRows) {
+        float v[kRows];
+#pragma unroll
+        for (uint32_t k = 0; k < kRows; ++k) v[k] = delta[(b + k) * filters + f];
+#pragma unroll
+        for (uint32_t k = 0; k < kRows; ++k) u += 0.0f + v[k];
+    }
+    for (; b < batch; ++b) u += 0.0f + delta[b * filters + f];
     updates[f] = u;
 }
 

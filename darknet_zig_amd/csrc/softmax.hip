@@ -16,9 +16,13 @@
 //  * contiguous groups with n > kSeqMax: the same, but the sum is an f64
 //    tree (within 1e-5 relative of the twin) because the row no longer fits
 //    in LDS.
-//  * strided groups (spatial softmax) or n <= 32: one lane per group runs the
-//    twin's three loops; adjacent lanes are adjacent groups, so with
-//    group_offset 1 the loads coalesce. Bit-exact.
+//  * strided groups that sit side by side (group_offset 1, the spatial
+//    softmax over the classes of each position) with n <= kTileMaxN: a
+//    workgroup stages 64 consecutive groups in LDS; all its lanes share the
+//    loads, exps and divides, and lane g < 64 takes group g's max and its
+//    sequential sum. Bit-exact.
+//  * other strided groups, or n <= 32: one lane per group runs the twin's
+//    three loops, eight loads at a time. Bit-exact.
 //
 // dkz_softmax_layer_forward runs the layer's two calls (softmax, then
 // softmax_x_ent over the whole batch) as one pass where the block kernels
@@ -186,6 +190,57 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
     }
 }
 
+constexpr uint32_t kTileRows = 64;
+constexpr uint32_t kTileMaxN = 128;
+
+// Rows r0 .. r0+63 (group r = b*groups + g); tile[i*64 + l] holds element i of
+// row r0 + l.
+__global__ __launch_bounds__(kBlock) void softmax_tile_kernel(const float *in, float *out, Groups G, uint32_t rows) {
+    __shared__ float tile[kTileMaxN * kTileRows];
+    __shared__ uint32_t base_sh[kTileRows];
+    __shared__ float mt_sh[kTileRows], sum_sh[kTileRows];
+    const uint32_t r0 = blockIdx.x * kTileRows;
+    const uint32_t nr = rows - r0 < kTileRows ? rows - r0 : kTileRows;
+    const uint32_t n = G.n, st = G.stride, total = n * kTileRows;
+    const uint32_t t = threadIdx.x;
+    if (t < kTileRows) base_sh[t] = t < nr ? group_base(r0 + t, G) : 0u;
+    __syncthreads();
+    // Eight loads per lane in flight: element i of row l for q = i*64 + l.
+    for (uint32_t q0 = t; q0 < total; q0 += kBlock * 8) {
+        float v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t q = q0 + u * kBlock, l = q & (kTileRows - 1);
+            v[u] = q < total && l < nr ? in[base_sh[l] + (q / kTileRows) * st] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (q0 + u * kBlock < total) tile[q0 + u * kBlock] = v[u];
+    }
+    __syncthreads();
+    if (t < nr) {
+        float mx = -FLT_MAX;
+        for (uint32_t i = 0; i < n; ++i) mx = fmaxf(mx, tile[i * kTileRows + t]);
+        mt_sh[t] = mx / G.temp;
+    }
+    __syncthreads();
+    for (uint32_t q = t; q < total; q += kBlock) {
+        const uint32_t l = q & (kTileRows - 1);
+        if (l < nr) tile[q] = expf_libm(tile[q] / G.temp - mt_sh[l]);
+    }
+    __syncthreads();
+    if (t < nr) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < n; ++i) s += tile[i * kTileRows + t];
+        sum_sh[t] = s;
+    }
+    __syncthreads();
+    for (uint32_t q = t; q < total; q += kBlock) {
+        const uint32_t l = q & (kTileRows - 1);
+        if (l < nr) out[base_sh[l] + (q / kTileRows) * st] = tile[q] / sum_sh[l];
+    }
+}
+
 // One lane per group: blas.zig:213-223 verbatim.
 __global__ __launch_bounds__(kBlock) void softmax_lane_kernel(const float *in, float *out, Groups G,
                                                               uint32_t rows) {
@@ -195,16 +250,45 @@ __global__ __launch_bounds__(kBlock) void softmax_lane_kernel(const float *in, f
     const float *x = in + off;
     float *y = out + off;
     const uint32_t n = G.n, st = G.stride;
+    // Each loop takes its loads eight at a time, ahead of the arithmetic,
+    // which stays in element order.
+    constexpr uint32_t kB = 8;
     float mx = -FLT_MAX;
-    for (uint32_t i = 0; i < n; ++i) mx = fmaxf(mx, x[i * st]);
+    uint32_t i = 0;
+    for (; i + kB <= n; i += kB) {
+        float v[kB];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) v[k] = x[(i + k) * st];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) mx = fmaxf(mx, v[k]);
+    }
+    for (; i < n; ++i) mx = fmaxf(mx, x[i * st]);
     const float mt = mx / G.temp;
     float s = 0.0f;
-    for (uint32_t i = 0; i < n; ++i) {
+    for (i = 0; i + kB <= n; i += kB) {
+        float v[kB];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) v[k] = x[(i + k) * st];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) {
+            const float e = expf_libm(v[k] / G.temp - mt);
+            s += e;
+            y[(i + k) * st] = e;
+        }
+    }
+    for (; i < n; ++i) {
         const float e = expf_libm(x[i * st] / G.temp - mt);
         s += e;
         y[i * st] = e;
     }
-    for (uint32_t i = 0; i < n; ++i) y[i * st] = y[i * st] / s;
+    for (i = 0; i + kB <= n; i += kB) {
+        float v[kB];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) v[k] = y[(i + k) * st];
+#pragma unroll
+        for (uint32_t k = 0; k < kB; ++k) y[(i + k) * st] = v[k] / s;
+    }
+    for (; i < n; ++i) y[i * st] = y[i * st] / s;
 }
 
 int softmax_run(const float *input, int n, int batch, int batch_offset, int groups, int group_offset, int stride,
@@ -222,6 +306,9 @@ int softmax_run(const float *input, int n, int batch, int batch_offset, int grou
                    (uint32_t)stride, temp,             make_fastdiv((uint32_t)groups)};
     if (!(stride == 1 && n > 32)) {
         DKZ_REQUIRE(xe == nullptr);
+        if (group_offset == 1 && stride > 1 && (uint32_t)n <= kTileMaxN)
+            return launch("softmax_tile", softmax_tile_kernel, dim3(div_up(rows, kTileRows)), dim3(kBlock), input,
+                          output, G, rows);
         return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
                       G, rows);
     }

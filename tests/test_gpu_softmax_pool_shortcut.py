@@ -52,13 +52,15 @@ def test_softmax_long_rows(dev):
     assert_r5(got, cpu, (e / e.sum(axis=1, keepdims=True)).ravel(), "softmax long rows")
 
 
-def test_softmax_spatial_groups(dev):
+@pytest.mark.parametrize("b, c, s", [(2, 11, 49), (3, 85, 169), (2, 128, 65), (2, 130, 13), (1, 1, 7)])
+def test_softmax_spatial_groups(dev, b, c, s):
     # Spatial softmax: groups = positions, elements `spatial` apart
     # (n = channels, batch_offset = c*s, groups = s, group_offset = 1, stride = s).
-    b, c, s = 2, 11, 49
-    x = normal(rng(11), b * c * s, 0, 2.0)
+    # Up to 128 channels the groups go through the LDS tile kernel (64 groups
+    # per workgroup, the last tile partial); above, one lane per group.
+    x = normal(rng(11 + c + s), b * c * s, 0, 2.0)
     got, cpu = _softmax_case(x, c, b, c * s, s, 1, s, 1.0)
-    assert_bitexact(got, cpu, "spatial softmax")
+    assert_bitexact(got, cpu, f"spatial softmax {b}x{c}x{s}")
     np.testing.assert_allclose(got.reshape(b, c, s).sum(axis=1), 1.0, rtol=1e-5)
 
 
