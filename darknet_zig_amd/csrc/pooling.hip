@@ -8,11 +8,14 @@
 // index is the absolute flat index into the batched input.
 //
 // Backward: the twin scatters prev_delta[idx[o]] += delta[o] over ascending o.
-// Here each input element gathers instead: it visits the outputs whose window
-// covers it in ascending o and adds delta[o] whenever idx[o] names it, so an
-// element with several contributors receives them in the twin's order and the
-// result is bit-exact with no atomics. Elements with no contributor are not
-// written (0 + -0 would otherwise flip a sign).
+// With stride 1 each input element gathers instead: it visits the outputs
+// whose window covers it in ascending o and adds delta[o] whenever idx[o]
+// names it. With stride >= 2 (a quarter as many outputs as inputs, or fewer)
+// each output lane takes its argmax t, and the lowest output naming t adds all
+// of t's contributions. Either way an element with several contributors
+// receives them in the twin's order, each element is written by one lane, and
+// the result is bit-exact with no atomics. Elements with no contributor are
+// not written (0 + -0 would otherwise flip a sign).
 //
 // Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
 // a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
@@ -38,6 +41,19 @@ struct PoolGeom {
 // are all issued before any of them is used.
 
 // ---- generic ----------------------------------------------------------------
+
+// Candidate outputs of input (y, x) -- those whose window covers it: rows
+// i with i*stride + n - half_pad == y for some n in [0, size), i.e. rows
+// [ilo, ihi], and likewise columns [jlo, jhi].
+__device__ __forceinline__ void pool_candidates(uint32_t y, uint32_t x, const PoolGeom &g, int &ilo, int &ihi,
+                                                int &jlo, int &jhi) {
+    const int yp = (int)(y + g.half_pad), xp = (int)(x + g.half_pad);
+    const int s = (int)g.stride, sz = (int)g.size;
+    ilo = yp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(yp - sz + s), g.div_stride);  // ceil((yp-sz+1)/s)
+    jlo = xp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(xp - sz + s), g.div_stride);
+    ihi = min((int)fdiv((uint32_t)yp, g.div_stride), (int)g.oh - 1);
+    jhi = min((int)fdiv((uint32_t)xp, g.div_stride), (int)g.ow - 1);
+}
 
 template <int TB>
 __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g,
@@ -90,13 +106,8 @@ __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta,
     const uint32_t t2 = fdiv(t, g.div_h);
     const uint32_t y = t - t2 * g.h;
     const uint32_t plane = t2;
-    // Outputs i with i*stride + n - half_pad == y for some n in [0, size).
-    const int yp = (int)(y + g.half_pad), xp = (int)(x + g.half_pad);
-    const int s = (int)g.stride, sz = (int)g.size;
-    const int ilo = yp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(yp - sz + s), g.div_stride);  // ceil((yp-sz+1)/s)
-    const int jlo = xp - sz + 1 <= 0 ? 0 : (int)fdiv((uint32_t)(xp - sz + s), g.div_stride);
-    const int ihi = min((int)fdiv((uint32_t)yp, g.div_stride), (int)g.oh - 1);
-    const int jhi = min((int)fdiv((uint32_t)xp, g.div_stride), (int)g.ow - 1);
+    int ilo, ihi, jlo, jhi;
+    pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
     if (ilo > ihi || jlo > jhi) return;
     // Candidates in ascending o (row i, then column j): a batch's indexes are
     // loaded together, then the deltas of those that name e -- and, at the
@@ -134,6 +145,64 @@ __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta,
         }
     }
     if (touched) prev[e] = v;
+}
+
+// Backward, one lane per output (stride >= 2, where outputs are a quarter of
+// the inputs or fewer): output o names input t = idx[o]. Of the outputs that
+// name t, the lowest o -- the first to add into t in the twin's ascending
+// scatter -- adds all of them in order, so each touched input is written by
+// exactly one lane and untouched inputs are not visited. A lane finds out
+// whether it is that output from the indexes of t's candidate outputs below o.
+template <int TB>
+__global__ __launch_bounds__(kBlock) void maxpool_bwd_out_kernel(const float *delta, float *prev, const int *idx,
+                                                                 PoolGeom g, uint32_t out_n, uint32_t in_n) {
+    const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
+    if (o >= out_n) return;
+    const int tv = idx[o];
+    if (tv < 0 || (uint32_t)tv >= in_n) return;  // -1: no tap of o's window was taken
+    const uint32_t t = (uint32_t)tv;
+    const uint32_t q = fdiv(t, g.div_w);
+    const uint32_t x = t - q * g.w;
+    const uint32_t plane = fdiv(q, g.div_h);
+    const uint32_t y = q - plane * g.h;
+    int ilo, ihi, jlo, jhi;
+    pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
+    if (ilo > ihi || jlo > jhi) return;
+    const uint32_t cnt = (uint32_t)(ihi - ilo + 1) * (uint32_t)(jhi - jlo + 1);
+    const float p0 = prev[t];
+    float v = 0.0f;
+    bool mine = false;
+    int ci = ilo, cj = jlo;
+    for (uint32_t c0 = 0; c0 < cnt; c0 += TB) {
+        uint32_t oc[TB];
+        int ix[TB];
+        bool ok[TB];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            ok[u] = c0 + u < cnt;
+            oc[u] = (uint32_t)cj + g.ow * ((uint32_t)ci + g.oh * plane);
+            ix[u] = ok[u] && oc[u] != o ? idx[oc[u]] : tv;
+            if (++cj > jhi) {
+                cj = jlo;
+                ++ci;
+            }
+        }
+        float d[TB];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) d[u] = ok[u] && oc[u] >= o && ix[u] == tv ? delta[oc[u]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            if (!ok[u] || ix[u] != tv) continue;
+            if (oc[u] < o) return;  // a lower output adds into t first
+            if (oc[u] == o) {
+                v = p0 + d[u];
+                mine = true;
+            } else if (mine) {
+                v += d[u];
+            }
+        }
+    }
+    if (mine) prev[t] = v;
 }
 
 // ---- 2x2, stride 2, offset 0 ------------------------------------------------
@@ -289,6 +358,15 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
     }
     // Outputs whose window covers one input, per dimension: at most ceil(size / stride).
     const uint32_t per_dim = (g.size + g.stride - 1) / g.stride;
+    if (g.stride >= 2) {
+        const uint32_t out_n = (uint32_t)(planes * g.oh * g.ow);
+        const dim3 ogrid(div_up(out_n, kBlock));
+        if (per_dim <= 2)
+            return launch("backward_maxpool", maxpool_bwd_out_kernel<4>, ogrid, dim3(kBlock), delta, prev_delta,
+                          indexes, g, out_n, (uint32_t)in_n);
+        return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
+                      indexes, g, out_n, (uint32_t)in_n);
+    }
     const dim3 grid(div_up((uint32_t)in_n, kBlock));
     if (per_dim <= 2)
         return launch("backward_maxpool", maxpool_bwd_kernel<4>, grid, dim3(kBlock), delta, prev_delta, indexes, g,

@@ -132,6 +132,59 @@ def test_maxpool(dev, case):
         gpu.free(b)
 
 
+def _shared_peaks(batch, c, h, w, size, stride, pad, seed):
+    """Input whose large values sit on the rows and columns that two or more
+    windows share: a peak above its neighbours is then the argmax of every
+    window that holds it."""
+    r = rng(seed)
+    x = uniform(r, (batch, c, h, w), -1.0, 0.0)
+    hp = pad // 2
+
+    def shared(n, on):
+        cover = np.zeros(n, int)
+        for i in range(on):
+            lo = i * stride - hp
+            cover[max(lo, 0):max(min(lo + size, n), 0)] += 1
+        return cover >= 2
+
+    rows = shared(h, ref.maxpool_out_dim(h, size, stride, pad))
+    cols = shared(w, ref.maxpool_out_dim(w, size, stride, pad))
+    mask = rows[:, None] & cols[None, :]
+    x[:, :, mask] = uniform(r, (batch, c, int(mask.sum())), 1.0, 2.0)
+    return x.ravel()
+
+
+@pytest.mark.parametrize("case", [(2, 3, 11, 13, 3, 2, 2), (2, 2, 12, 12, 5, 3, 4), (1, 2, 9, 9, 3, 1, 2),
+                                  (2, 2, 10, 10, 4, 2, 2)], ids=str)
+def test_maxpool_shared_argmax(dev, case):
+    """Inputs that are the argmax of several outputs: the backward pass must
+    add their deltas in ascending output order (the output-per-lane kernel for
+    stride >= 2, the gather kernel for stride 1)."""
+    batch, c, h, w, size, stride, pad = case
+    oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
+    x = _shared_peaks(*case, seed=sum(case))
+    out_n = batch * c * oh * ow
+    out_c, idx_c = np.empty(out_n, np.float32), np.empty(out_n, np.int32)
+    ref.forwardMaxpool(batch, h, w, c, size, stride, pad, x, out_c, idx_c)
+    counts = np.bincount(idx_c[idx_c >= 0], minlength=x.size)
+    assert counts.max() >= 2, "the case must have inputs with several contributors"
+    dx, dout, didx = up(x), gpu.alloc(out_n), gpu.allocInts(out_n)
+    gpu.forwardMaxpool(out_n, h, w, c, stride, size, pad, dx, dout, didx)
+    assert_bitexact(down(didx, idx_c), idx_c, f"maxpool idx {case}")
+    r = rng(sum(case))
+    # magnitudes over six decades, so that adding a shared input's deltas in
+    # another order changes the rounded result
+    delta = (normal(r, out_n) * np.float32(10.0) ** uniform(r, out_n, -3, 3)).astype(np.float32)
+    prev = normal(r, x.size)
+    prev_c = prev.copy()
+    ref.backwardMaxpool(idx_c, delta, prev_c)
+    dd, dprev = up(delta), up(prev)
+    gpu.backwardMaxpool(x.size, h, w, c, stride, size, pad, dd, dprev, didx)
+    assert_bitexact(down(dprev, prev), prev_c, f"maxpool bwd shared argmax {case}")
+    for b in (dx, dout, didx, dd, dprev):
+        gpu.free(b)
+
+
 @pytest.mark.parametrize("batch, c, h, w", [(3, 6, 14, 14), (2, 5, 7, 7), (4, 3, 1, 1), (256, 512, 28, 28)])
 def test_avgpool(dev, batch, c, h, w):
     r = rng(batch * c + h)
