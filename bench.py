@@ -368,6 +368,18 @@ def per_op_table(gpu, hip, stream, launches: int):
         add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
     add_seq("fused", "cfg2 batchnorm_backward(leaky): sums + apply", 8 * 4 * h["n"],
             [[lambda d=d: fused_backward(gpu, d, h)] for d in sets])
+    # config 1's forward ops on the largest batch-norm tensor of the configs
+    # (config 2's x): each op at its largest shape, as the north star asks
+    B2, F2, S2, n2 = 64, 128, 56 * 56, h["n"]
+    cfg = "cfg1_ops_at_cfg2_shape[64,128,56,56]"
+    bias2 = dev.up(gen(7).normal(0, 0.1, F2).astype(np.float32))
+    add(cfg, "mean", 4 * n2, [lambda d=d: gpu.mean(d["x"], B2, F2, S2, d["md"]) for d in sets])
+    add(cfg, "variance", 4 * n2, [lambda d=d: gpu.variance(d["x"], d["mean"], B2, F2, S2, d["vd"]) for d in sets])
+    add(cfg, "normalize", 8 * n2, [lambda d=d: gpu.normalize(d["x_norm"], d["mean"], d["var"], B2, F2, S2)
+                                   for d in sets])
+    add(cfg, "add_bias", 8 * n2, [lambda d=d: gpu.addBias(d["x_norm"], bias2, B2, F2, S2) for d in sets])
+    add(cfg, "activate(leaky)", 8 * n2, [lambda d=d: gpu.activateArray(d["x_norm"], n2, Activation.leaky)
+                                         for d in sets])
     dev.free()
 
     # -- config 3: softmax + cross-entropy delta, [256,1000], logits ~N(0,4)
