@@ -29,16 +29,21 @@ inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args..
 }
 
 // Scratch of the current device, allocated once by dkz_init (or on first
-// use): the f64 partial sums one split channel reduction hands from its first
-// launch to its second, and the partial tiles of a split-K gemm. Every user
-// writes all the scratch it then reads.
+// use) and zeroed then: the f64 partial sums one split channel reduction
+// hands from its first launch to its second, the partial tiles of a split-K
+// gemm, and one 64-bit meeting slot per channel for the reductions whose two
+// workgroups per channel meet inside one launch. Every user writes all the
+// partials and tiles it then reads; the slots start at zero and every user
+// leaves them at zero.
 struct Scratch {
     double *partials;
     float *gemm;
     uint64_t gemm_floats;
+    uint64_t *slots;
 };
 constexpr uint32_t kScratchPartials = 1u << 18;    // channels * chunks (2 MiB of f64)
 constexpr uint64_t kScratchGemmFloats = 1ull << 23;  // split-K partial tiles (32 MiB)
+constexpr uint32_t kScratchSlots = 1u << 12;         // channels
 int device_scratch(Scratch *out);
 
 // Largest element count any op indexes with 32-bit arithmetic, as the

@@ -29,6 +29,11 @@ namespace dkz {
 namespace {
 
 constexpr int kUnroll = 4;
+constexpr uint32_t kCuCount = 256;
+
+#ifndef DKZ_CHAN_PAIR
+#define DKZ_CHAN_PAIR 1
+#endif
 
 template <class Term>
 __device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
@@ -88,6 +93,34 @@ __global__ __launch_bounds__(BS) void chan_reduce_kernel(T t, Fin fin, const flo
     if (threadIdx.x == 0) fin(blockIdx.x, total, pre);
 }
 
+// K == 1 with fewer channels than CUs: two workgroups per channel in one
+// launch, so that every CU streams. The two meet in channel f's 64-bit slot
+// (zero when empty): each swaps its partial in with one agent-scope atomic
+// exchange, which returns what the slot held. The one that gets the other's
+// partial back adds the two (f64 addition is commutative, so the sum does not
+// depend on which finished first), empties the slot for the next launch and
+// finalises. A partial travels as its bits XOR kSlotKey -- a NaN payload no
+// sum produces, since NaNs reaching it carry an f32 payload whose low 29 bits
+// are zero -- so a stored partial is never zero.
+constexpr uint64_t kSlotKey = 0xFFF8DEADBEEF0001ull;
+
+template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
+__global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
+                                                       uint64_t *slots) {
+    __shared__ double lds[BS / kWave];
+    const uint32_t f = blockIdx.x >> 1, k = blockIdx.x & 1;
+    const float pre = threadIdx.x == 0 ? fin.pre(f) : 0.0f;
+    const double s = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, f, k, lds);
+    if (threadIdx.x == 0) {
+        const uint64_t mine = __builtin_bit_cast(uint64_t, s) ^ kSlotKey;
+        const uint64_t held = __hip_atomic_exchange(&slots[f], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (held != 0) {
+            __hip_atomic_store(&slots[f], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            fin(f, s + __builtin_bit_cast(double, held ^ kSlotKey), pre);
+        }
+    }
+}
+
 // K > 1, pass 1: workgroup (f, k) stores its partial at partials[f*K + k].
 template <class T, bool TWO, bool VEC, int H>
 __global__ __launch_bounds__(kBlock) void chan_partial_kernel(T t, const float *p0, const float *p1, RedGeom g,
@@ -121,6 +154,22 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
     const RedGeom g = make_red_geom(F, S, L, pick_split(F, L, TWO ? 2 : 1), vec);
     const uint32_t K = g.K;
+#if DKZ_CHAN_PAIR
+    if (K == 1 && F < kCuCount && F <= kScratchSlots && L >= 32 * kWideBlock) {
+        // Two halves per channel, whole float4s each.
+        const RedGeom g2 = make_red_geom(F, S, L, 2, vec);
+        Scratch sc{nullptr};
+        DKZ_TRY(device_scratch(&sc));
+        if (g2.K == 2) {
+            const dim3 block(kWideBlock);
+            if (vec)
+                return launch(name, chan_pair_kernel<T, Fin, TWO, true, H, kWideBlock>, dim3(2 * F), block, t, fin,
+                              p0, p1, g2, sc.slots);
+            return launch(name, chan_pair_kernel<T, Fin, TWO, false, H, kWideBlock>, dim3(2 * F), block, t, fin, p0,
+                          p1, g2, sc.slots);
+        }
+    }
+#endif
     if (K == 1) {
         if (L >= 16 * kWideBlock) {
             const dim3 block(kWideBlock);

@@ -30,7 +30,8 @@ bool env_flag(const char *name) {
     return v != nullptr && v[0] != '\0' && v[0] != '0';
 }
 
-constexpr size_t kScratchBytes = kScratchPartials * sizeof(double) + kScratchGemmFloats * sizeof(float);
+constexpr size_t kScratchBytes =
+    kScratchPartials * sizeof(double) + kScratchGemmFloats * sizeof(float) + kScratchSlots * sizeof(uint64_t);
 
 int ensure_scratch(int dev) {
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -90,6 +91,7 @@ int device_scratch(Scratch *out) {
     out->partials = static_cast<double *>(g_devices[dev].scratch);
     out->gemm = reinterpret_cast<float *>(out->partials + kScratchPartials);
     out->gemm_floats = kScratchGemmFloats;
+    out->slots = reinterpret_cast<uint64_t *>(out->gemm + kScratchGemmFloats);
     return 0;
 }
 
