@@ -38,10 +38,12 @@
  *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
- *   - The library owns one scratch buffer per device (34 MiB), allocated by
- *     dkz_init: the f64 partial sums a per-channel reduction passes from its
- *     first launch to its second (2 MiB) and the partial tiles of a split-K
- *     gemm (32 MiB). Ops never allocate. Reductions or gemms issued
+ *   - The library owns one scratch buffer per device (34 MiB), allocated and
+ *     zeroed by dkz_init: the f64 partial sums a per-channel reduction passes
+ *     from its first launch to its second (2 MiB), the partial tiles of a
+ *     split-K gemm (32 MiB) and the 64-bit slots (32 KiB) in which the two
+ *     workgroups of a channel meet in one-launch reductions. Ops never
+ *     allocate. Reductions or gemms issued
  *     concurrently on two streams of one device share that buffer and race;
  *     issue them on one stream.
  */
