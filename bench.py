@@ -37,7 +37,7 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                this host, one thread, median of 3 full config-2 chains
 
 Algorithmic bytes count every logical fp32/int32 element read or written once
-(4 B); per-channel vectors are not counted (BASELINE.md's accounting).
+(4 B); per-channel vectors of C floats are not counted.
 """
 
 from __future__ import annotations

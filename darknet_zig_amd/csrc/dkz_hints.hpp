@@ -3,7 +3,7 @@
 // A nontemporal (NT) access keeps a line out of the caches' normal
 // replacement order. Measured on MI355X, NT loads and stores make every op
 // faster when its operands are cold in HBM (a 2-read/1-write stream: 5.5 ->
-// 6.5 TB/s), and also in two of the three op sequences of BASELINE.json's
+// 6.5 TB/s), and also in two of the three op sequences of the benchmark's
 // configs -- the SGD step (axpy, axpy, scal over 2 x 100 MB: 6.27 -> 6.48 TB/s)
 // and the batch-norm forward + leaky sequence (4.09 -> 4.46 TB/s). The
 // exception is the batch-norm backward sequence: all seven ops read the same

@@ -6,7 +6,7 @@ to bit-exactness. Reductions (mean, variance, mean_delta, variance_delta,
 backward_bias, backward_scale) are held to the 1e-5 rule of tests/helpers.py
 against an f64 evaluation of the same formula. Shapes: gputest's B4*F17*S53
 (gputest.zig:157-160), odd and tiny shapes, spatial == 1 (connected layers),
-and BASELINE configs 1 ([128,32,32,32]) and 2 ([64,128,56,56]) at full size.
+and the benchmark configs 1 ([128,32,32,32]) and 2 ([64,128,56,56]) at full size.
 """
 
 from __future__ import annotations

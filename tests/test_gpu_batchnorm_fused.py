@@ -33,7 +33,7 @@ FAST = [
     (2, 8, 20000),    # few channels, long: split with a ragged last chunk
     (16, 5, 600),     # split; an apply tile spans up to 8 rows, channels repeat within it
     (8, 6, 1536),     # split; apply tiles finalise their own channels
-    (128, 32, 1024),
+    (128, 32, 1024),  # benchmark config 1
 ]
 FALLBACK = [
     (4, 17, 53),      # gputest's shape: spatial % 4 != 0
