@@ -408,6 +408,26 @@ def per_op_table(gpu, hip, stream, launches: int):
         [lambda a=a, p=p, t=t, d=d, e=e: gpu.softmaxLayerForward(b3, c3, 1, 1.0, a, t, p, d, e)
          for a, p, t, d, e in zip(ls, ps, ts, ds_, es)])
     dev.free()
+    # the same two ops at a larger batch (config 3 is a 2 MB tensor, which one
+    # launch cannot stream at full rate): each op at a large shape
+    dev = Device(gpu)
+    b3l = 8192
+    n3l = b3l * c3
+    logits = r.normal(0, 4.0, n3l).astype(np.float32)
+    truth = np.zeros(n3l, np.float32)
+    truth[np.arange(b3l) * c3 + r.integers(0, c3, b3l)] = 1.0
+    R = rotations(4 * 4 * n3l)
+    ls = dev.clone(dev.up(logits), n3l, R)
+    ps = [dev.zeros(n3l) for _ in range(R)]
+    ts = dev.clone(dev.up(truth), n3l, R)
+    ds_ = [dev.zeros(n3l) for _ in range(R)]
+    es = [dev.zeros(n3l) for _ in range(R)]
+    cfg = f"cfg3_ops_at[{b3l},1000]"
+    add(cfg, "softmax", 2 * 4 * n3l,
+        [lambda a=a, p=p: gpu.softmax(a, c3, b3l, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)])
+    add(cfg, "softmax_x_ent", 4 * 4 * n3l,
+        [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3l, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)])
+    dev.free()
 
     # -- config 4: SGD over 25e6 floats ~N(0,0.05), and the stride-2 shortcut
     dev = Device(gpu)
