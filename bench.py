@@ -755,12 +755,13 @@ def main() -> int:
         result["per_op"] = table
         result["gemm"] = gemm_table(gpu, hip, stream)
         named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
-        fwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg1") and k.split("/", 1)[1] in named)
-        fwd_chain = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/chain" in k)
-        fwd_layer = next(v["us"] for k, v in table.items() if k.startswith("cfg1") and "/layer sequence" in k)
+        cfg1, cfg2 = "cfg1_bn_fwd[", "cfg2_bn_bwd["  # the config rows, not the same ops at other shapes
+        fwd = sum(v["us"] for k, v in table.items() if k.startswith(cfg1) and k.split("/", 1)[1] in named)
+        fwd_chain = next(v["us"] for k, v in table.items() if k.startswith(cfg1) and "/chain" in k)
+        fwd_layer = next(v["us"] for k, v in table.items() if k.startswith(cfg1) and "/layer sequence" in k)
         fwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg1"))
         bwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg2"))
-        bwd = sum(v["us"] for k, v in table.items() if k.startswith("cfg2"))
+        bwd = sum(v["us"] for k, v in table.items() if k.startswith(cfg2))
         e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
         result["bn_act_gelem_s"] = {
             "fwd_cfg1_chained": round(e1 / (fwd_chain * 1e-6) / 1e9, 2),
