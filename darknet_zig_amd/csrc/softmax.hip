@@ -13,6 +13,11 @@
 //    group; the row is read once into LDS (in float4s when aligned), max by
 //    wave64 DPP + LDS, the exps in parallel in place, one lane adds them in
 //    order, then all lanes divide. Bit-exact.
+//  * many contiguous groups (at least kRowsMin) with 32 < n <= kRowsMaxN (256):
+//    a workgroup stages kRows groups in LDS (odd row pitch, so lanes walking
+//    columns of different rows use different banks); all its lanes share the
+//    loads, exps and divides, and lane r of the first wave runs group r's max
+//    and its sequential sum, so kRows sums advance per instruction. Bit-exact.
 //  * contiguous groups with n > kSeqMax: the same, but the sum is an f64
 //    tree (within 1e-5 relative of the twin) because the row no longer fits
 //    in LDS.
@@ -190,6 +195,97 @@ __global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, 
     }
 }
 
+constexpr uint32_t kRows = 16;
+// Up to 256 elements a row (16 KiB of LDS a workgroup): measured against the
+// one-workgroup-per-row kernel, [16384,100] 28.7 -> 9.6 us and [8192,256]
+// 18.0 -> 14.8 us, while rows of 1000 were slower (64 KiB a workgroup leaves
+// two per CU, too few loads in flight).
+constexpr uint32_t kRowsMaxN = 256;
+constexpr uint32_t kRowsMin = 4096;
+
+// op(...op(op(acc, row[0]), row[1])..., row[n-1]): one lane's sequential fold
+// of an LDS row, with the reads of the next 16 elements in flight while the
+// current 16 are folded.
+template <class Op>
+__device__ __forceinline__ float row_fold(const float *row, uint32_t n, float acc, Op op) {
+    constexpr uint32_t kB = 16;
+    const uint32_t nb = n / kB;
+    float a[kB], b[kB];
+    if (nb > 0) {
+#pragma unroll
+        for (uint32_t u = 0; u < kB; ++u) a[u] = row[u];
+    }
+    for (uint32_t j = 0; j < nb;) {
+        if (j + 1 < nb) {
+#pragma unroll
+            for (uint32_t u = 0; u < kB; ++u) b[u] = row[(j + 1) * kB + u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kB; ++u) acc = op(acc, a[u]);
+        if (++j >= nb) break;
+        if (j + 1 < nb) {
+#pragma unroll
+            for (uint32_t u = 0; u < kB; ++u) a[u] = row[(j + 1) * kB + u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kB; ++u) acc = op(acc, b[u]);
+        ++j;
+    }
+    for (uint32_t i = nb * kB; i < n; ++i) acc = op(acc, row[i]);
+    return acc;
+}
+
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct AddOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+
+// Groups r0 .. r0+kRows-1, contiguous (stride 1); tile[l*pitch + i] holds
+// element i of group r0 + l.
+__global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const float *in, float *out, Groups G, FastDiv div_n,
+                                                              uint32_t pitch, uint32_t rows) {
+    extern __shared__ float tile[];
+    __shared__ uint32_t base_sh[kRows];
+    __shared__ float mt_sh[kRows], sum_sh[kRows];
+    const uint32_t r0 = blockIdx.x * kRows;
+    const uint32_t nr = rows - r0 < kRows ? rows - r0 : kRows;
+    const uint32_t n = G.n, total = nr * n, t = threadIdx.x;
+    if (t < kRows) base_sh[t] = t < nr ? group_base(r0 + t, G) : 0u;
+    __syncthreads();
+    // Eight loads per lane in flight: element i of row l for q = l*n + i.
+    for (uint32_t q0 = t; q0 < total; q0 += kBlock * 8) {
+        float v[8];
+        uint32_t at[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t q = q0 + u * kBlock;
+            const uint32_t l = fdiv(q, div_n), i = q - l * n;
+            at[u] = l * pitch + i;
+            v[u] = q < total ? in[base_sh[q < total ? l : 0] + i] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (q0 + u * kBlock < total) tile[at[u]] = v[u];
+    }
+    __syncthreads();
+    if (t < nr) mt_sh[t] = row_fold(tile + t * pitch, n, -FLT_MAX, MaxOp{}) / G.temp;
+    __syncthreads();
+    for (uint32_t q = t; q < total; q += kBlock) {
+        const uint32_t l = fdiv(q, div_n), i = q - l * n;
+        float &e = tile[l * pitch + i];
+        e = expf_libm(e / G.temp - mt_sh[l]);
+    }
+    __syncthreads();
+    if (t < nr) sum_sh[t] = row_fold(tile + t * pitch, n, 0.0f, AddOp{});
+    __syncthreads();
+    for (uint32_t q = t; q < total; q += kBlock) {
+        const uint32_t l = fdiv(q, div_n), i = q - l * n;
+        out[base_sh[l] + i] = tile[l * pitch + i] / sum_sh[l];
+    }
+}
+
 constexpr uint32_t kTileRows = 64;
 constexpr uint32_t kTileMaxN = 128;
 
@@ -311,6 +407,14 @@ int softmax_run(const float *input, int n, int batch, int batch_offset, int grou
                           output, G, rows);
         return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
                       G, rows);
+    }
+    if (!xe && rows >= kRowsMin && (uint32_t)n <= kRowsMaxN) {
+        const uint32_t pitch = (uint32_t)n | 1u;  // odd: the rows' columns fall in distinct banks
+        const size_t lds = (size_t)kRows * pitch * sizeof(float);
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(softmax_rows_kernel, dim3(div_up(rows, kRows)), dim3(kBlock), lds, current_stream(),
+                           input, output, G, make_fastdiv((uint32_t)n), pitch, rows);
+        return after_launch("softmax_rows", dim3(div_up(rows, kRows)), dim3(kBlock));
     }
     const bool seq = (uint32_t)n <= kSeqMax;
     bool v4 = n % 4 == 0 && batch_offset % 4 == 0 && group_offset % 4 == 0 && aligned16(input) && aligned16(output);
