@@ -130,6 +130,56 @@ __global__ __launch_bounds__(kBlock) void im2col_vec_kernel(const float *__restr
     }
 }
 
+// Stride 1 with W % 4 == 0 and Wo % 4 == 0: a column float4 (four outputs
+// of one output row) holds input elements x0 .. x0+3 of one input row, x0 =
+// w + kw - pad. They come from the aligned float4 at or below x0 and, unless
+// x0 is itself aligned, the next one -- two 16-byte loads instead of four
+// gathers. A block outside its row is not loaded and reads as zeros, which is
+// exactly the padding (the row holds whole blocks, as W % 4 == 0).
+__device__ __forceinline__ float pick(const float4 &a, const float4 &b, int i) {
+    switch (i) {
+        case 0: return a.x;
+        case 1: return a.y;
+        case 2: return a.z;
+        case 3: return a.w;
+        case 4: return b.x;
+        case 5: return b.y;
+        case 6: return b.z;
+        default: return b.w;
+    }
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void im2col_s1_kernel(const float *__restrict__ im, float *__restrict__ col,
+                                                           ColGeom g, uint32_t nv) {
+    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 out[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q4 = base + u * kBlock;
+        out[u] = zero;
+        if (q4 >= nv) continue;
+        const ColPos q = col_pos(q4 << 2, g);
+        const int y = (int)(q.h + q.kh) - (int)g.p;
+        if (y < 0 || y >= (int)g.H) continue;
+        const int x0 = (int)(q.w + q.kw) - (int)g.p;
+        const int sh = x0 & 3;  // x0 mod 4, also for x0 < 0
+        const int xa = x0 - sh;  // aligned start of the first block
+        const int xb = xa + 4;
+        const uint32_t row4 = ((q.c * g.H + (uint32_t)y) * g.W) >> 2;
+        // A block is loaded only when it lies within the row: 0 <= start < W.
+        const float4 a = xa >= 0 && xa < (int)g.W ? ld4<false>(im, row4 + (uint32_t)(xa >> 2)) : zero;
+        const float4 b = sh != 0 && xb >= 0 && xb < (int)g.W ? ld4<false>(im, row4 + (uint32_t)(xb >> 2)) : zero;
+        out[u] = make_float4(pick(a, b, sh), pick(a, b, sh + 1), pick(a, b, sh + 2), pick(a, b, sh + 3));
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q4 = base + u * kBlock;
+        if (q4 < nv) st4<NT>(col, q4, out[u]);
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void im2col_scalar_kernel(const float *__restrict__ im, float *__restrict__ col,
                                                                ColGeom g, uint32_t n) {
     for (uint32_t e = blockIdx.x * kBlock + threadIdx.x; e < n; e += gridDim.x * kBlock) col[e] = im2col_at(im, e, g);
@@ -222,6 +272,12 @@ int dkz_im2col(const float *im, int channels, int height, int width, int ksize, 
     if (ncol == 0) return 0;
     DKZ_REQUIRE(im != nullptr && col != nullptr);
     const uint32_t n = (uint32_t)ncol;
+    if (stride == 1 && width % 4 == 0 && g.Wo % 4 == 0 && aligned16(im) && aligned16(col)) {
+        const uint32_t nv = n >> 2;  // n % 4 == 0 as Wo % 4 == 0
+        const uint32_t grid = div_up(nv, (uint64_t)kBlock * kUnroll);
+        return launch("im2col_s1", im2col_s1_kernel<(DKZ_HINT_IM2COL & 2) != 0>, dim3(grid), dim3(kBlock), im, col,
+                      g, nv);
+    }
     if (aligned16(col)) {
         const uint32_t nv = n >> 2;
         const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * kUnroll);

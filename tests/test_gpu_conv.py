@@ -32,6 +32,13 @@ SHAPES = [
     (3, 4, 4, 4, 1, 3),  # pad 3 with a 4-wide kernel
     (64, 28, 28, 3, 1, 1),
     (128, 56, 56, 3, 1, 1),  # config 2's layer, one image
+    # stride 1 with W and the output width multiples of 4 (two aligned
+    # 16-byte loads per column float4), pads that push whole blocks out of a row
+    (1, 6, 8, 5, 1, 4),
+    (2, 4, 8, 3, 1, 5),
+    (1, 4, 12, 9, 1, 4),
+    (2, 3, 4, 1, 1, 6),
+    (3, 5, 16, 5, 1, 2),
 ]
 
 
