@@ -33,6 +33,8 @@
 // at once share A and B panels, and neighbouring tile numbers are placed on
 // one XCD (workgroups are dealt to the 8 XCDs round robin) so that they share
 // its L2.
+#include <type_traits>
+
 #include "dkz_device.hpp"
 #include "dkz_internal.hpp"
 
@@ -46,6 +48,15 @@ constexpr int kPitch = kBK + 4;  // LDS row pitch in words
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
+// The B operand of a convolution taken straight from the image (implicit
+// im2col): B[k][p] = im2col(image)[k][p] for k = (c, kh, kw) over a group's
+// channels and p = (h, w) over the output positions (im2col.zig:13-49).
+struct ConvB {
+    uint32_t H, W, Wo, ksz, stride, pad;
+    FastDiv div_kk, div_k, div_wo;  // ksz*ksz, ksz, Wo
+    uint32_t s1;  // stride 1, W % 4 == 0, Wo % 4 == 0, images 16-byte aligned
+};
+
 struct GemmArgs {
     const float *a;
     const float *b;
@@ -55,6 +66,10 @@ struct GemmArgs {
     float alpha, beta;
     uint32_t tiles_m, tiles_n, splits, k_chunk;
     uint32_t vec_a, vec_b;  // operand 16-byte aligned with a leading dimension % 4 == 0
+    // Batched launches (one workgroup row per matrix product, z = blockIdx.y):
+    // A at a + (z % zgroups) * a_z, B at b + z * b_z, C at c + z * c_z.
+    uint32_t zgroups, a_z, b_z, c_z;
+    ConvB cv;  // implicit-im2col kernels only
 };
 
 __device__ __forceinline__ void tile_of(uint32_t w, const GemmArgs &g, uint32_t &tm, uint32_t &tn, uint32_t &split) {
@@ -83,6 +98,20 @@ __device__ __forceinline__ float4 load4(const float *p, uint32_t idx, uint32_t a
     if (avail > 2) v.z = p[idx + 2];
     if (avail > 3) v.w = p[idx + 3];
     return v;
+}
+
+// Element i (0..7) of the eight floats a, b.
+__device__ __forceinline__ float pick8(const float4 &a, const float4 &b, int i) {
+    switch (i) {
+        case 0: return a.x;
+        case 1: return a.y;
+        case 2: return a.z;
+        case 3: return a.w;
+        case 4: return b.x;
+        case 5: return b.y;
+        case 6: return b.z;
+        default: return b.w;
+    }
 }
 
 // One operand's slab loader. ROWK: the operand's rows run along the tile
@@ -136,12 +165,72 @@ struct Slab {
     }
 };
 
+// The implicit-im2col B slab: the same layout and LDS store as a row-major
+// B (rows along k, the output positions contiguous), each float4 gathered
+// from the image. With cv.s1 a float4 (four positions of one output row, as
+// n0 and Wo are multiples of 4) is four consecutive elements of one input row,
+// from the aligned float4 at or below x0 = w + kw - pad and, unless x0 is
+// aligned, the next one; a block outside its row reads as the padding's zeros.
+template <int R, bool S1>
+struct ConvSlab : Slab<R, false> {
+    using Slab<R, false>::kLoads;
+    using Slab<R, false>::v;
+
+    __device__ __forceinline__ void load_conv(const float *img, const ConvB &cv, uint32_t r0, uint32_t rows,
+                                              uint32_t k0, uint32_t kend, int tid) {
+        const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const int f = tid + l * kBlock;
+            const uint32_t kr = f % kBK, rr = 4 * (f / kBK);
+            const uint32_t kidx = k0 + kr;
+            float4 out = zero;
+            if (kidx < kend && rr < rows) {
+                const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
+                const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
+                const uint32_t p0 = r0 + rr;
+                const uint32_t avail = rows - rr < 4 ? rows - rr : 4;
+                if constexpr (S1) {
+                    const uint32_t h = fdiv(p0, cv.div_wo), w = p0 - h * cv.Wo;
+                    const int y = (int)(h + kh) - (int)cv.pad;
+                    if (y >= 0 && y < (int)cv.H) {
+                        const int x0 = (int)(w + kw) - (int)cv.pad;
+                        const int sh = x0 & 3, xa = x0 - sh, xb = xa + 4;
+                        const uint32_t row4 = ((c * cv.H + (uint32_t)y) * cv.W) >> 2;
+                        const float4 a = xa >= 0 && xa < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xa >> 2)) : zero;
+                        const float4 b =
+                            sh != 0 && xb >= 0 && xb < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xb >> 2)) : zero;
+                        out = make_float4(pick8(a, b, sh), pick8(a, b, sh + 1), pick8(a, b, sh + 2), pick8(a, b, sh + 3));
+                    }
+                } else {
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; ++j) {
+                        if (j >= avail) break;
+                        const uint32_t p = p0 + j, h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
+                        const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
+                        const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
+                        if (y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W)
+                            ::dkz::lane(out, j) = img[(c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x];
+                    }
+                }
+            }
+            v[l] = out;
+        }
+    }
+};
+
 // D: slabs in flight. The loads of slab s + D are issued while slab s is
 // multiplied, from a ring of D register sets; the 128x128 kernel does four
 // times the MFMAs per slab of the 64x64 one and runs with D = 1, the 64x64
 // one -- used when few workgroups share a CU -- with DKZ_GEMM_SMALL_PREFETCH.
-template <int BM, int BN, bool TA, bool TB, int D>
+// IM: B is a convolution's implicit im2col (NN only): kImGather gathers each
+// element, kImS1 takes a float4 from two aligned loads (ConvB::s1). Each
+// workgroup row z = blockIdx.y computes its own product (see GemmArgs).
+constexpr int kImNone = 0, kImGather = 1, kImS1 = 2;
+
+template <int BM, int BN, bool TA, bool TB, int D, int IM = kImNone>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
+    static_assert(IM == kImNone || (!TA && !TB), "the implicit im2col operand is B of an NN product");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     // A wave with fewer than four 32x32 blocks spreads each block's MFMAs over
     // NC accumulators (MFMA q of a slab into accumulator q % NC), so that four
@@ -152,6 +241,10 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
 
     uint32_t tm, tn, split;
     tile_of(blockIdx.x, g, tm, tn, split);
+    const uint32_t z = blockIdx.y;
+    const float *ga = g.a + (size_t)(z % g.zgroups) * g.a_z;
+    const float *gb = g.b + (size_t)z * g.b_z;
+    float *gc = g.c + (size_t)z * g.c_z;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t rows_a = g.m - m0, rows_b = g.n - n0;
     const uint32_t kbeg = split * g.k_chunk;
@@ -161,7 +254,11 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     const int half = lane >> 5, l32 = lane & 31;
 
     Slab<BM, !TA> sa[D];
-    Slab<BN, TB> sb[D];
+    std::conditional_t<IM != kImNone, ConvSlab<BN, IM == kImS1>, Slab<BN, TB>> sb[D];
+    auto load_b = [&](auto &slab, uint32_t k0) {
+        if constexpr (IM != kImNone) slab.load_conv(gb, g.cv, n0, rows_b, k0, kend, tid);
+        else slab.load(gb, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+    };
 
     f32x16 acc[NC][TM][TN];
 #pragma unroll
@@ -177,8 +274,8 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         if ((uint32_t)d < steps) {
-            sa[d].load(g.a, g.lda, m0, rows_a, kbeg + d * kBK, kend, g.vec_a, tid);
-            sb[d].load(g.b, g.ldb, n0, rows_b, kbeg + d * kBK, kend, g.vec_b, tid);
+            sa[d].load(ga, g.lda, m0, rows_a, kbeg + d * kBK, kend, g.vec_a, tid);
+            load_b(sb[d], kbeg + d * kBK);
         }
     }
     if (steps > 0) {
@@ -186,8 +283,8 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
         sb[0].store(Bs[0], tid);
         // Slot 0 is free again: it takes slab D (slot X % D always holds slab X).
         if ((uint32_t)D < steps) {
-            sa[0].load(g.a, g.lda, m0, rows_a, kbeg + D * kBK, kend, g.vec_a, tid);
-            sb[0].load(g.b, g.ldb, n0, rows_b, kbeg + D * kBK, kend, g.vec_b, tid);
+            sa[0].load(ga, g.lda, m0, rows_a, kbeg + D * kBK, kend, g.vec_a, tid);
+            load_b(sb[0], kbeg + D * kBK);
         }
         __syncthreads();
     }
@@ -227,8 +324,8 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 sb[nx].store(Bs[cur ^ 1], tid);
                 if (s + 1 + D < steps) {
                     const uint32_t k0 = kbeg + (s + 1 + D) * kBK;
-                    sa[nx].load(g.a, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
-                    sb[nx].load(g.b, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+                    sa[nx].load(ga, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+                    load_b(sb[nx], k0);
                 }
             }
             __syncthreads();
@@ -257,7 +354,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 if (g.splits > 1) {
                     g.partial[((size_t)split * g.m + i) * g.n + j] = acc[0][ti][tj][r];
                 } else {
-                    float *cp = g.c + i * g.ldc + j;
+                    float *cp = gc + i * g.ldc + j;
                     float cv = 0.0f;
                     if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
                     *cp = cv + g.alpha * acc[0][ti][tj][r];
@@ -333,6 +430,14 @@ int launch_gemm(bool ta, bool tb, GemmArgs g) {
     return launch("gemm_tt", gemm_mfma_kernel<BM, BN, true, true, D>, grid, block, g);
 }
 
+// A batched NN product over z = 0 .. zcount-1 (one grid row each); IM != kImNone:
+// B is the implicit im2col of image z.
+template <int BM, int BN, int D, int IM>
+int launch_batched(const GemmArgs &g, uint32_t zcount) {
+    const dim3 grid(g.tiles_m * g.tiles_n, zcount);
+    return launch("convolution_forward", gemm_mfma_kernel<BM, BN, false, false, D, IM>, grid, dim3(kBlock), g);
+}
+
 // Extent in elements of a rows x cols row-major view with leading dimension ld.
 inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) {
     return rows == 0 || cols == 0 ? 0 : (rows - 1) * ld + cols;
@@ -385,6 +490,7 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
     g.vec_b = aligned16(b) && ldb % 4 == 0;
     g.splits = 1;
     g.k_chunk = (uint32_t)k;
+    g.zgroups = 1;
 
     // 128x128 tiles when they give every CU two workgroups; 64x64 below, and
     // if even those leave CUs idle and K is long, split K (ranges of >= 128)
@@ -425,6 +531,92 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
                       dim3(kBlock), g);
     }
     return launch_gemm<64, 64, DKZ_GEMM_SMALL_PREFETCH>(ta != 0, tb != 0, g);
+}
+
+// convolutional.zig:240-260 in one launch: for image i and group j,
+// output(i, j) (m x n, m = filters/groups, n = out_h*out_w) += weights(j)
+// (m x k, k = ksize^2 * channels/groups) x im2col(input(i, j)) (k x n), with
+// out_h = (height + 2*pad - ksize)/stride + 1 as outHeight computes it. The
+// layer zero-fills the output first; this adds to it (beta = 1), as its gemm
+// calls do. ksize 1 multiplies by the input itself (ldb = n), as the layer
+// does. No workspace: the im2col operand is gathered inside the product.
+int dkz_convolution_forward(int batch, int groups, int channels, int height, int width, int filters, int ksize,
+                            int stride, int pad, const float *weights, const float *input, float *output) {
+    DKZ_REQUIRE(batch >= 0 && groups >= 1 && groups <= 65535 && channels >= 0 && height >= 0 && width >= 0 &&
+                filters >= 0);
+    DKZ_REQUIRE(ksize >= 1 && stride >= 1 && pad >= 0);
+    DKZ_REQUIRE(channels % groups == 0 && filters % groups == 0);
+    DKZ_REQUIRE((int64_t)height + 2 * (int64_t)pad >= ksize && (int64_t)width + 2 * (int64_t)pad >= ksize);
+    const uint64_t m = (uint64_t)filters / groups, cg = (uint64_t)channels / groups;
+    const uint64_t ho = ((uint64_t)height + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t wo = ((uint64_t)width + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t n = ho * wo, k = (uint64_t)ksize * ksize * cg;
+    const uint64_t zcount = (uint64_t)batch * groups, in_group = cg * height * width;
+    if (zcount == 0 || m == 0 || n == 0 || k == 0) return 0;
+    DKZ_REQUIRE(weights && input && output);
+    DKZ_REQUIRE(zcount * m * n <= kMaxElems && zcount * in_group <= kMaxElems && (uint64_t)groups * m * k <= kMaxElems);
+    DKZ_REQUIRE(ksize != 1 || n <= (uint64_t)height * width);  // the input is read as a k x n matrix
+    GemmArgs g{};
+    g.a = weights;
+    g.b = input;
+    g.c = output;
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)n;
+    g.k = (uint32_t)k;
+    g.lda = (uint32_t)k;
+    g.ldb = (uint32_t)n;
+    g.ldc = (uint32_t)n;
+    g.alpha = 1.0f;
+    g.beta = 1.0f;
+    g.splits = 1;
+    g.k_chunk = (uint32_t)k;
+    g.vec_a = aligned16(weights) && k % 4 == 0 && (m * k) % 4 == 0;
+    g.vec_b = aligned16(input) && n % 4 == 0 && in_group % 4 == 0;
+    g.zgroups = (uint32_t)groups;
+    g.a_z = (uint32_t)(m * k);
+    g.b_z = (uint32_t)in_group;
+    g.c_z = (uint32_t)(m * n);
+    const bool im = ksize != 1;
+    if (im) {
+        ConvB &cv = g.cv;
+        cv.H = (uint32_t)height;
+        cv.W = (uint32_t)width;
+        cv.Wo = (uint32_t)wo;
+        cv.ksz = (uint32_t)ksize;
+        cv.stride = (uint32_t)stride;
+        cv.pad = (uint32_t)pad;
+        cv.div_kk = make_fastdiv((uint32_t)(ksize * ksize));
+        cv.div_k = make_fastdiv((uint32_t)ksize);
+        cv.div_wo = make_fastdiv((uint32_t)wo);
+        cv.s1 = stride == 1 && width % 4 == 0 && wo % 4 == 0 && aligned16(input);
+    }
+    // 128x128 tiles when m fills them and the whole batch gives every CU two
+    // workgroups, else 64x64.
+    const bool big = m >= 128 && (uint64_t)div_up(m, 128) * div_up(n, 128) * zcount >= 2 * kCus;
+    g.tiles_m = (uint32_t)div_up(m, big ? 128 : 64);
+    g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
+    // At most 65535 grid rows per launch, whole images each (a multiple of
+    // groups), so that every launch starts at group 0.
+    const uint64_t chunk = 65535 - 65535 % (uint64_t)groups;
+    for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
+        const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
+        GemmArgs gz = g;
+        gz.b = input + z0 * in_group;
+        gz.c = output + z0 * m * n;
+        const int kind = !im ? kImNone : g.cv.s1 ? kImS1 : kImGather;
+        int e;
+        if (big) {
+            if (kind == kImS1) e = launch_batched<128, 128, 1, kImS1>(gz, zc);
+            else if (kind == kImGather) e = launch_batched<128, 128, 1, kImGather>(gz, zc);
+            else e = launch_batched<128, 128, 1, kImNone>(gz, zc);
+        } else {
+            if (kind == kImS1) e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImS1>(gz, zc);
+            else if (kind == kImGather) e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImGather>(gz, zc);
+            else e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImNone>(gz, zc);
+        }
+        if (e != 0) return e;
+    }
+    return 0;
 }
 
 }  // extern "C"

@@ -384,6 +384,14 @@ def gemm(
                                ldc), "gemm")
 
 
+def convolutionForward(
+    batch: int, groups: int, channels: int, height: int, width: int, filters: int, ksize: int, stride: int,
+    pad: int, weights: Buf, input: Buf, output: Buf,
+) -> None:  # the per-image loop of layers/convolutional.zig:240-260 in one call
+    _must(_lib.load().dkz_convolution_forward(batch, groups, channels, height, width, filters, ksize, stride, pad,
+                                              _p(weights), _p(input), _p(output)), "convolution_forward")
+
+
 def dropout(input: Buf, size: int, rand_buf: Buf, prob: float, scale: float) -> None:  # gpu.zig:769
     _must(_lib.load().dkz_dropout(_p(input), size, _p(rand_buf), prob, scale), "dropout")
 

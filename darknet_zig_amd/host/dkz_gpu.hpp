@@ -255,6 +255,15 @@ inline void gemm(bool ta, bool tb, size_t m, size_t n, size_t k, float alpha, Bu
          "gemm");
 }
 
+// The per-image im2col + gemm loop of layers/convolutional.zig:240-260 in one call.
+inline void convolutionForward(size_t batch, size_t groups, size_t channels, size_t height, size_t width,
+                               size_t filters, size_t ksize, size_t stride, size_t pad, Buf weights, Buf input,
+                               Buf output) {
+    must(dkz_convolution_forward(ci(batch), ci(groups), ci(channels), ci(height), ci(width), ci(filters), ci(ksize),
+                                 ci(stride), ci(pad), weights.f(), input.f(), output.f()),
+         "convolution_forward");
+}
+
 // ---- pooling, dropout, shortcut, adam (gpu.zig:725-830) --------------------------
 
 inline void forwardMaxpool(size_t out_n, size_t in_h, size_t in_w, size_t in_c, size_t stride, size_t size,

@@ -319,6 +319,22 @@ int dkz_col2im(const float *col, int channels, int height, int width, int ksize,
 int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, int lda, const float *b,
              int ldb, float beta, float *c, int ldc);
 
+/* The forward loop of a convolutional layer (layers/convolutional.zig:240-260)
+ * in one call, beside the per-image im2col + gemm it replaces: for image i <
+ * batch and group j < groups,
+ *     output(i, j) += weights(j) x im2col(input(i, j))
+ * with m = filters/groups, k = ksize^2 * channels/groups, n = out_h*out_w,
+ * out_h = (height + 2*pad - ksize)/stride + 1 (convolutional.zig:21-27),
+ * output(i, j) = output + (i*groups + j)*m*n, weights(j) = weights + j*m*k,
+ * input(i, j) = input + (i*groups + j)*(channels/groups)*height*width. Like
+ * the layer's gemm calls it adds to output (the layer zero-fills it first),
+ * and for ksize == 1 it multiplies by the input itself read as a k x n
+ * matrix, as the layer does. The im2col operand is gathered inside the
+ * product: no workspace. channels and filters must be multiples of groups.
+ * Results agree with the per-image calls within fp32 summation error. */
+int dkz_convolution_forward(int batch, int groups, int channels, int height, int width, int filters, int ksize,
+                            int stride, int pad, const float *weights, const float *input, float *output);
+
 /* gpu.zig:769 dropout(input, size, rand, prob, scale): input[i] = rand[i] < prob ?
  * 0 : input[i] * scale, the rule of layers/misc.zig:105-127 (forward after
  * randUniform, and backward on the delta with the same draws). */

@@ -1,0 +1,117 @@
+"""dkz_convolution_forward: the per-image im2col + gemm loop of a
+convolutional layer's forward (layers/convolutional.zig:240-260) in one
+launch, the im2col operand gathered inside the product.
+
+Reference per image i and group j: the oracle's im2col of the image (a copy,
+bit-exact) times the group's weights in f64, added to the output's previous
+contents. Tolerance per element as for dkz_gemm: Higham's bound
+gamma_(k+3) * (sum_p |w_p col_p| + |out0|). For ksize 1 the layer multiplies
+by the input itself, read as a k x n matrix; so does the entry point, also
+where that reading is the layer's own (stride 2 with ksize 1)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from darknet_zig_amd import gpu
+from oracle import ref
+from tests.helpers import down, rng, up
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+CASES = [
+    # batch, groups, channels, height, width, filters, ksize, stride, pad
+    (2, 1, 16, 16, 16, 32, 3, 1, 1),   # stride 1, widths % 4 == 0: two-block gathers
+    (3, 2, 8, 10, 12, 6, 3, 2, 1),     # groups, stride 2: per-element gathers
+    (2, 1, 4, 9, 9, 5, 1, 1, 0),       # ksize 1: the input is the operand
+    (1, 1, 3, 8, 8, 4, 1, 2, 0),       # ksize 1, stride 2: the layer's own reading of the input
+    (4, 1, 32, 28, 28, 64, 3, 1, 1),   # 64x64 tiles
+    (24, 1, 16, 56, 56, 128, 3, 1, 1),  # 128x128 tiles (600 of them), config 2's image size
+    (2, 1, 3, 8, 8, 4, 5, 1, 4),       # pad 4: whole blocks outside a row
+    (2, 3, 9, 7, 5, 6, 3, 1, 2),       # three groups, odd widths
+    (1, 1, 1, 3, 4, 1, 3, 1, 1),       # one channel, one filter
+]
+
+
+def _reference(case, x, w, out0):
+    batch, groups, C, H, W, F, ks, s, p = case
+    cg, m = C // groups, F // groups
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    n, k = ho * wo, ks * ks * cg
+    in_group = cg * H * W
+    want = out0.astype(np.float64).copy()
+    bound = np.abs(out0.astype(np.float64))
+    for i in range(batch):
+        for j in range(groups):
+            z = i * groups + j
+            img = x[z * in_group:(z + 1) * in_group]
+            if ks == 1:
+                col = img[: k * n].reshape(k, n)
+            else:
+                col = np.empty(k * n, np.float32)
+                ref.im2col(img, cg, H, W, ks, s, p, col)
+                col = col.reshape(k, n)
+            wj = w[j * m * k:(j + 1) * m * k].reshape(m, k).astype(np.float64)
+            sl = slice(z * m * n, (z + 1) * m * n)
+            want[sl] += (wj @ col.astype(np.float64)).ravel()
+            bound[sl] += (np.abs(wj) @ np.abs(col.astype(np.float64))).ravel()
+    g = (k + 3) * U / (1 - (k + 3) * U)
+    return want, g * bound, (m, n, k)
+
+
+@pytest.mark.parametrize("case", CASES, ids=str)
+def test_convolution_forward(dev, case):
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(sum(case))
+    x = r.uniform(-1, 1, batch * C * H * W).astype(np.float32)
+    w = r.uniform(-1, 1, F * (C // groups) * ks * ks).astype(np.float32)
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    out0 = r.uniform(-1, 1, batch * F * ho * wo).astype(np.float32)
+    want, bd, (m, n, k) = _reference(case, x, w, out0)
+    dx, dw, do = up(x), up(w), up(out0)
+    gpu.convolutionForward(batch, groups, C, H, W, F, ks, s, p, dw, dx, do)
+    got = down(do, out0).astype(np.float64)
+    err = np.abs(got - want)
+    bad = ~(err <= bd)
+    assert not bad.any(), (f"convolution {case}: {int(bad.sum())} beyond the fp32 bound; "
+                           f"max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}")
+    for b in (dx, dw, do):
+        gpu.free(b)
+
+
+def test_convolution_forward_matches_per_image_calls(dev):
+    """The same layer through the per-image calls the reference makes
+    (im2col into a workspace, then gemm with beta 1): both within the bound of
+    the f64 product, and identical wherever the products are exact (integer
+    inputs)."""
+    case = (3, 1, 8, 12, 12, 16, 3, 1, 1)
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(5)
+    x = r.integers(-3, 4, batch * C * H * W).astype(np.float32)
+    w = r.integers(-3, 4, F * C * ks * ks).astype(np.float32)
+    n, k = H * W, ks * ks * C
+    dx, dw = up(x), up(w)
+    fused, loop = gpu.alloc(batch * F * n), gpu.alloc(batch * F * n)
+    gpu.convolutionForward(batch, groups, C, H, W, F, ks, s, p, dw, dx, fused)
+    ws = gpu.alloc(k * n)
+    for i in range(batch):
+        gpu.im2col(dx.offset(i * C * H * W), C, H, W, ks, s, p, ws)
+        gpu.gemm(False, False, F, n, k, 1.0, dw, k, ws, n, 1.0, loop.offset(i * F * n), n)
+    a, b = down(fused, np.empty(batch * F * n, np.float32)), down(loop, np.empty(batch * F * n, np.float32))
+    assert np.array_equal(a, b)  # integer-valued: every order is exact
+    for buf in (dx, dw, fused, loop, ws):
+        gpu.free(buf)
+
+
+def test_convolution_forward_rejects_bad_groups(dev):
+    from darknet_zig_amd import _lib
+    lib = _lib.load()
+    buf = gpu.alloc(64)
+    # channels not a multiple of groups, and a window larger than the padded image
+    assert lib.dkz_convolution_forward(1, 2, 3, 4, 4, 2, 3, 1, 1, buf.ptr, buf.ptr, buf.ptr) != 0
+    assert lib.dkz_convolution_forward(1, 1, 1, 2, 2, 1, 5, 1, 0, buf.ptr, buf.ptr, buf.ptr) != 0
+    assert lib.dkz_convolution_forward(0, 1, 1, 2, 2, 1, 1, 1, 0, None, None, None) == 0  # empty batch
+    gpu.free(buf)
