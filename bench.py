@@ -26,7 +26,9 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                configs' fast paths (a 3x3/s2 max pool, a spatial softmax, a
                connected layer's bias gradient)
   gemm         dkz_gemm at config 2's convolution shapes and a large square,
-               TFLOP/s against the 157.3 TFLOP/s fp32 matrix-core peak
+               and config 2's convolutional layer forward over the batch (the
+               per-image loop against dkz_convolution_forward), TFLOP/s
+               against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
                pass and one apply pass, 32 B/elem instead of 56)
   bn_act_gelem_s  config 1 elements / config 1 forward time and config 2
@@ -582,6 +584,31 @@ def gemm_table(gpu, hip, stream):
         rows[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / GEMM_PEAK_TFLOPS, 4),
                       "flops": flops}
         dev.free()
+    # config 2's convolutional layer forward, the whole batch: the per-image
+    # im2col + gemm loop of convolutional.zig:249-260 against one
+    # dkz_convolution_forward call (implicit im2col, no workspace)
+    B, C, H, F, K = 64, 128, 56, 128, 3
+    hw, kk = H * H, C * K * K
+    dev = Device(gpu)
+    x = dev.up(r.uniform(-1, 1, B * C * hw).astype(np.float32))
+    w = dev.up(r.uniform(-1, 1, F * kk).astype(np.float32))
+    y = dev.zeros(B * F * hw)
+    ws = dev.zeros(kk * hw)
+    flops = 2 * B * F * hw * kk
+
+    def per_image():
+        for i in range(B):
+            gpu.im2col(x.offset(i * C * hw), C, H, H, K, 1, 1, ws)
+            gpu.gemm(False, False, F, hw, kk, 1.0, w, kk, ws, hw, 1.0, y.offset(i * F * hw), hw)
+
+    for name, fn, reps in (("conv layer fwd [64,128,56,56]->128 3x3: per-image im2col+gemm", per_image, 3),
+                           ("conv layer fwd [64,128,56,56]->128 3x3: convolution_forward",
+                            lambda: gpu.convolutionForward(B, 1, C, H, H, F, K, 1, 1, w, x, y), 10)):
+        ms = time_seq(hip, stream, [[fn]], reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        rows[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / GEMM_PEAK_TFLOPS, 4),
+                      "flops": flops}
+    dev.free()
     return rows
 
 
