@@ -26,8 +26,9 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                configs' fast paths (a 3x3/s2 max pool, a spatial softmax, a
                connected layer's bias gradient)
   gemm         dkz_gemm at config 2's convolution shapes and a large square,
-               and config 2's convolutional layer forward over the batch (the
-               per-image loop against dkz_convolution_forward), TFLOP/s
+               and config 2's convolutional layer forward and weight gradient
+               over the batch (the per-image loops against
+               dkz_convolution_forward / _weight_gradient), TFLOP/s
                against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
                pass and one apply pass, 32 B/elem instead of 56)
@@ -601,9 +602,23 @@ def gemm_table(gpu, hip, stream):
             gpu.im2col(x.offset(i * C * hw), C, H, H, K, 1, 1, ws)
             gpu.gemm(False, False, F, hw, kk, 1.0, w, kk, ws, hw, 1.0, y.offset(i * F * hw), hw)
 
+    # ... and its weight gradient (convolutional.zig:288-297): the per-image
+    # im2col + gemm(false, true, beta 1) loop against one
+    # dkz_convolution_weight_gradient call (split-K, partial tiles in the
+    # library's scratch); y stands in for delta
+    wu = dev.zeros(F * kk)
+
+    def per_image_wgrad():
+        for i in range(B):
+            gpu.im2col(x.offset(i * C * hw), C, H, H, K, 1, 1, ws)
+            gpu.gemm(False, True, F, kk, hw, 1.0, y.offset(i * F * hw), hw, ws, hw, 1.0, wu, kk)
+
     for name, fn, reps in (("conv layer fwd [64,128,56,56]->128 3x3: per-image im2col+gemm", per_image, 3),
                            ("conv layer fwd [64,128,56,56]->128 3x3: convolution_forward",
-                            lambda: gpu.convolutionForward(B, 1, C, H, H, F, K, 1, 1, w, x, y), 10)):
+                            lambda: gpu.convolutionForward(B, 1, C, H, H, F, K, 1, 1, w, x, y), 10),
+                           ("conv layer wgrad [64,128,56,56]->128 3x3: per-image im2col+gemm", per_image_wgrad, 3),
+                           ("conv layer wgrad [64,128,56,56]->128 3x3: convolution_weight_gradient",
+                            lambda: gpu.convolutionWeightGradient(B, 1, C, H, H, F, K, 1, 1, y, x, wu), 10)):
         ms = time_seq(hip, stream, [[fn]], reps)
         tf = flops / (ms * 1e-3) / 1e12
         rows[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / GEMM_PEAK_TFLOPS, 4),

@@ -42,7 +42,10 @@ struct Scratch {
     uint64_t *slots;
 };
 constexpr uint32_t kScratchPartials = 1u << 18;    // channels * chunks (2 MiB of f64)
-constexpr uint64_t kScratchGemmFloats = 1ull << 23;  // split-K partial tiles (32 MiB)
+#ifndef DKZ_SCRATCH_GEMM_LOG2
+#define DKZ_SCRATCH_GEMM_LOG2 25
+#endif
+constexpr uint64_t kScratchGemmFloats = 1ull << DKZ_SCRATCH_GEMM_LOG2;  // split-K partial tiles (128 MiB)
 constexpr uint32_t kScratchSlots = 1u << 12;         // channels
 int device_scratch(Scratch *out);
 

@@ -48,6 +48,33 @@ constexpr int kPitch = kBK + 4;  // LDS row pitch in words
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
+// Slabs in flight in the 64x64 kernel (build-time tunable).
+#ifndef DKZ_GEMM_SMALL_PREFETCH
+#define DKZ_GEMM_SMALL_PREFETCH 2
+#endif
+
+// Workgroups per CU that a split-K grid aims for (build-time tunable).
+#ifndef DKZ_GEMM_SPLIT_TARGET
+#define DKZ_GEMM_SPLIT_TARGET 2
+#endif
+
+// The weight gradient: 128x128 tiles when filters per group fill them
+// (DKZ_WGRAD_BIG), and the workgroups per CU its K split aims for.
+#ifndef DKZ_WGRAD_BIG
+#define DKZ_WGRAD_BIG 1
+#endif
+#ifndef DKZ_WGRAD_TARGET
+#define DKZ_WGRAD_TARGET 4
+#endif
+#ifndef DKZ_WGRAD_TARGET_RAW
+#define DKZ_WGRAD_TARGET_RAW 2
+#endif
+// The shortest K range of a weight-gradient split: below it the partial tiles
+// the reduce reads cost more than the parallelism gains.
+#ifndef DKZ_WGRAD_MIN_CHUNK
+#define DKZ_WGRAD_MIN_CHUNK 512
+#endif
+
 // The B operand of a convolution taken straight from the image (implicit
 // im2col): B[k][p] = im2col(image)[k][p] for k = (c, kh, kw) over a group's
 // channels and p = (h, w) over the output positions (im2col.zig:13-49).
@@ -55,6 +82,12 @@ struct ConvB {
     uint32_t H, W, Wo, ksz, stride, pad;
     FastDiv div_kk, div_k, div_wo;  // ksz*ksz, ksz, Wo
     uint32_t s1;  // stride 1, W % 4 == 0, Wo % 4 == 0, images 16-byte aligned
+    // Weight gradient (k runs over image and position): positions per image,
+    // and the element strides from one image to the next of delta (A) and of
+    // the input (B); npos4: npos % 4 == 0, so no float4 spans two images.
+    uint32_t npos;
+    FastDiv div_npos;
+    uint32_t a_img, b_img, npos4, a_vec, b_vec;  // a_vec / b_vec: delta / input 16-byte aligned
 };
 
 struct GemmArgs {
@@ -165,52 +198,129 @@ struct Slab {
     }
 };
 
-// The implicit-im2col B slab: the same layout and LDS store as a row-major
-// B (rows along k, the output positions contiguous), each float4 gathered
-// from the image. With cv.s1 a float4 (four positions of one output row, as
-// n0 and Wo are multiples of 4) is four consecutive elements of one input row,
-// from the aligned float4 at or below x0 = w + kw - pad and, unless x0 is
-// aligned, the next one; a block outside its row reads as the padding's zeros.
-template <int R, bool S1>
-struct ConvSlab : Slab<R, false> {
-    using Slab<R, false>::kLoads;
-    using Slab<R, false>::v;
+// Gather modes of the implicit im2col operand: kRaw reads the input itself as
+// a k x npos matrix (what the layer multiplies by when ksize == 1), kGather
+// takes each element's tap, kTwoBlock takes four positions of one output row
+// (stride 1, W and Wo multiples of 4) from the aligned float4 at or below
+// x0 = w + kw - pad and, unless x0 is aligned, the next one; a block outside
+// its row reads as the padding's zeros.
+constexpr int kRaw = 0, kGather = 1, kTwoBlock = 2;
 
-    __device__ __forceinline__ void load_conv(const float *img, const ConvB &cv, uint32_t r0, uint32_t rows,
+// im2col(img)[kidx][p] (0 in the padding).
+template <int MODE>
+__device__ __forceinline__ float conv_col1(const float *img, const ConvB &cv, uint32_t kidx, uint32_t p) {
+    if constexpr (MODE == kRaw) {
+        return img[kidx * cv.npos + p];
+    } else {
+        const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
+        const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
+        const uint32_t h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
+        const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
+        const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
+        return y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W ? img[(c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x]
+                                                                   : 0.0f;
+    }
+}
+
+// im2col(img)[kidx][p0 .. p0+avail-1], zeros past avail. kTwoBlock needs
+// avail == 4 and p0 % 4 == 0; kRaw loads a float4 when npos4 and avail == 4.
+template <int MODE>
+__device__ __forceinline__ float4 conv_col4(const float *img, const ConvB &cv, uint32_t kidx, uint32_t p0,
+                                            uint32_t avail) {
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (MODE == kTwoBlock) {
+        const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
+        const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
+        const uint32_t h = fdiv(p0, cv.div_wo), w = p0 - h * cv.Wo;
+        const int y = (int)(h + kh) - (int)cv.pad;
+        if (y < 0 || y >= (int)cv.H) return zero;
+        const int x0 = (int)(w + kw) - (int)cv.pad;
+        const int sh = x0 & 3, xa = x0 - sh, xb = xa + 4;
+        const uint32_t row4 = ((c * cv.H + (uint32_t)y) * cv.W) >> 2;
+        const float4 a = xa >= 0 && xa < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xa >> 2)) : zero;
+        const float4 b = sh != 0 && xb >= 0 && xb < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xb >> 2)) : zero;
+        return make_float4(pick8(a, b, sh), pick8(a, b, sh + 1), pick8(a, b, sh + 2), pick8(a, b, sh + 3));
+    } else {
+        if (MODE == kRaw && avail == 4 && cv.npos4 && cv.b_vec)
+            return ld4<false>(img + kidx * cv.npos, p0 >> 2);
+        float4 out = zero;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+            if (j < avail) ::dkz::lane(out, j) = conv_col1<MODE>(img, cv, kidx, p0 + j);
+        return out;
+    }
+}
+
+// The implicit im2col operand's slab. ROWK false: B of the forward product
+// (rows along k = kidx, the positions contiguous). ROWK true: B of the weight
+// gradient, transposed (rows along the tile dimension = kidx, k = image *
+// npos + position). Same layouts and LDS stores as the ordinary slabs.
+template <int R, bool ROWK, int MODE>
+struct ConvSlab : Slab<R, ROWK> {
+    using Slab<R, ROWK>::kLoads;
+    using Slab<R, ROWK>::v;
+
+    __device__ __forceinline__ void load_conv(const float *img0, const ConvB &cv, uint32_t r0, uint32_t rows,
                                               uint32_t k0, uint32_t kend, int tid) {
         const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int l = 0; l < kLoads; ++l) {
             const int f = tid + l * kBlock;
-            const uint32_t kr = f % kBK, rr = 4 * (f / kBK);
-            const uint32_t kidx = k0 + kr;
             float4 out = zero;
-            if (kidx < kend && rr < rows) {
-                const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
-                const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
-                const uint32_t p0 = r0 + rr;
-                const uint32_t avail = rows - rr < 4 ? rows - rr : 4;
-                if constexpr (S1) {
-                    const uint32_t h = fdiv(p0, cv.div_wo), w = p0 - h * cv.Wo;
-                    const int y = (int)(h + kh) - (int)cv.pad;
-                    if (y >= 0 && y < (int)cv.H) {
-                        const int x0 = (int)(w + kw) - (int)cv.pad;
-                        const int sh = x0 & 3, xa = x0 - sh, xb = xa + 4;
-                        const uint32_t row4 = ((c * cv.H + (uint32_t)y) * cv.W) >> 2;
-                        const float4 a = xa >= 0 && xa < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xa >> 2)) : zero;
-                        const float4 b =
-                            sh != 0 && xb >= 0 && xb < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xb >> 2)) : zero;
-                        out = make_float4(pick8(a, b, sh), pick8(a, b, sh + 1), pick8(a, b, sh + 2), pick8(a, b, sh + 3));
+            if constexpr (!ROWK) {
+                const uint32_t kr = f % kBK, rr = 4 * (f / kBK);
+                const uint32_t kidx = k0 + kr;
+                if (kidx < kend && rr < rows)
+                    out = conv_col4<MODE>(img0, cv, kidx, r0 + rr, rows - rr < 4 ? rows - rr : 4);
+            } else {
+                const uint32_t r = f / (kBK / 4), kk = k0 + 4 * (f % (kBK / 4));
+                if (r < rows && kk < kend) {
+                    const uint32_t kidx = r0 + r, avail = kend - kk < 4 ? kend - kk : 4;
+                    if (cv.npos4) {  // the four k are one image's positions
+                        const uint32_t i = fdiv(kk, cv.div_npos);
+                        out = conv_col4<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, kk - i * cv.npos, avail);
+                    } else if constexpr (MODE != kTwoBlock) {
+#pragma unroll
+                        for (uint32_t j = 0; j < 4; ++j) {
+                            if (j >= avail) break;
+                            const uint32_t i = fdiv(kk + j, cv.div_npos);
+                            ::dkz::lane(out, j) =
+                                conv_col1<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, kk + j - i * cv.npos);
+                        }
                     }
+                }
+            }
+            v[l] = out;
+        }
+    }
+};
+
+// A of the weight gradient: delta, row f of the product holding filter f's
+// deltas of every image in turn -- k = image * npos + position.
+template <int R>
+struct SegSlab : Slab<R, true> {
+    using Slab<R, true>::kLoads;
+    using Slab<R, true>::v;
+
+    __device__ __forceinline__ void load_seg(const float *a0, const ConvB &cv, uint32_t r0, uint32_t rows,
+                                             uint32_t k0, uint32_t kend, int tid) {
+        const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const int f = tid + l * kBlock;
+            const uint32_t r = f / (kBK / 4), kk = k0 + 4 * (f % (kBK / 4));
+            float4 out = zero;
+            if (r < rows && kk < kend) {
+                const uint32_t row = r0 + r, avail = kend - kk < 4 ? kend - kk : 4;
+                if (cv.npos4 && avail == 4 && cv.a_vec) {
+                    const uint32_t i = fdiv(kk, cv.div_npos);
+                    out = ld4<false>(a0 + (size_t)i * cv.a_img + row * cv.npos, (kk - i * cv.npos) >> 2);
                 } else {
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) {
                         if (j >= avail) break;
-                        const uint32_t p = p0 + j, h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
-                        const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
-                        const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
-                        if (y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W)
-                            ::dkz::lane(out, j) = img[(c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x];
+                        const uint32_t i = fdiv(kk + j, cv.div_npos);
+                        ::dkz::lane(out, j) = a0[(size_t)i * cv.a_img + row * cv.npos + (kk + j - i * cv.npos)];
                     }
                 }
             }
@@ -223,14 +333,18 @@ struct ConvSlab : Slab<R, false> {
 // multiplied, from a ring of D register sets; the 128x128 kernel does four
 // times the MFMAs per slab of the 64x64 one and runs with D = 1, the 64x64
 // one -- used when few workgroups share a CU -- with DKZ_GEMM_SMALL_PREFETCH.
-// IM: B is a convolution's implicit im2col (NN only): kImGather gathers each
-// element, kImS1 takes a float4 from two aligned loads (ConvB::s1). Each
-// workgroup row z = blockIdx.y computes its own product (see GemmArgs).
-constexpr int kImNone = 0, kImGather = 1, kImS1 = 2;
+// IM: a convolution's operands. kFwd + mode: B of an NN product is the
+// implicit im2col of the image; kWgrad + mode: the weight gradient, an NT
+// product whose A is delta and whose B is the im2col, k running over image
+// and position (modes: kRaw, kGather, kTwoBlock). Each workgroup row z =
+// blockIdx.y computes its own product (see GemmArgs).
+constexpr int kImNone = -1, kFwd = 0, kWgrad = 8;
 
 template <int BM, int BN, bool TA, bool TB, int D, int IM = kImNone>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
-    static_assert(IM == kImNone || (!TA && !TB), "the implicit im2col operand is B of an NN product");
+    constexpr bool kWg = IM >= kWgrad;
+    constexpr int kMode = IM == kImNone ? 0 : kWg ? IM - kWgrad : IM - kFwd;
+    static_assert(IM == kImNone || (!TA && TB == kWg), "forward: NN; weight gradient: NT");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     // A wave with fewer than four 32x32 blocks spreads each block's MFMAs over
     // NC accumulators (MFMA q of a slab into accumulator q % NC), so that four
@@ -253,8 +367,12 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
     const int half = lane >> 5, l32 = lane & 31;
 
-    Slab<BM, !TA> sa[D];
-    std::conditional_t<IM != kImNone, ConvSlab<BN, IM == kImS1>, Slab<BN, TB>> sb[D];
+    std::conditional_t<kWg, SegSlab<BM>, Slab<BM, !TA>> sa[D];
+    std::conditional_t<IM != kImNone, ConvSlab<BN, kWg, kMode>, Slab<BN, TB>> sb[D];
+    auto load_a = [&](auto &slab, uint32_t k0) {
+        if constexpr (kWg) slab.load_seg(ga, g.cv, m0, rows_a, k0, kend, tid);
+        else slab.load(ga, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+    };
     auto load_b = [&](auto &slab, uint32_t k0) {
         if constexpr (IM != kImNone) slab.load_conv(gb, g.cv, n0, rows_b, k0, kend, tid);
         else slab.load(gb, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
@@ -274,7 +392,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         if ((uint32_t)d < steps) {
-            sa[d].load(ga, g.lda, m0, rows_a, kbeg + d * kBK, kend, g.vec_a, tid);
+            load_a(sa[d], kbeg + d * kBK);
             load_b(sb[d], kbeg + d * kBK);
         }
     }
@@ -283,7 +401,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
         sb[0].store(Bs[0], tid);
         // Slot 0 is free again: it takes slab D (slot X % D always holds slab X).
         if ((uint32_t)D < steps) {
-            sa[0].load(ga, g.lda, m0, rows_a, kbeg + D * kBK, kend, g.vec_a, tid);
+            load_a(sa[0], kbeg + D * kBK);
             load_b(sb[0], kbeg + D * kBK);
         }
         __syncthreads();
@@ -324,7 +442,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 sb[nx].store(Bs[cur ^ 1], tid);
                 if (s + 1 + D < steps) {
                     const uint32_t k0 = kbeg + (s + 1 + D) * kBK;
-                    sa[nx].load(ga, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+                    load_a(sa[nx], k0);
                     load_b(sb[nx], k0);
                 }
             }
@@ -438,6 +556,32 @@ int launch_batched(const GemmArgs &g, uint32_t zcount) {
     return launch("convolution_forward", gemm_mfma_kernel<BM, BN, false, false, D, IM>, grid, dim3(kBlock), g);
 }
 
+template <int IM>
+int launch_fwd(const GemmArgs &g, uint32_t zcount, bool big) {
+    if (big) return launch_batched<128, 128, 1, IM>(g, zcount);
+    return launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, IM>(g, zcount);
+}
+
+// The weight gradient's NT product (BM x BM tiles, K split into ranges),
+// then the split-K reduce.
+template <int BM, int IM>
+int launch_wgrad(const GemmArgs &g) {
+    const dim3 grid(g.tiles_m * g.tiles_n * g.splits);
+    constexpr int D = BM == 128 ? 1 : DKZ_GEMM_SMALL_PREFETCH;
+    DKZ_TRY(launch("convolution_weight_gradient", gemm_mfma_kernel<BM, BM, false, true, D, IM>, grid, dim3(kBlock), g));
+    if (g.splits == 1) return 0;
+    if (g.n % 4 == 0 && g.ldc % 4 == 0 && aligned16(g.c))
+        return launch("convolution_weight_gradient", gemm_splitk_reduce_kernel<true>,
+                      dim3(div_up((uint64_t)g.m * g.n / 4, kBlock)), dim3(kBlock), g);
+    return launch("convolution_weight_gradient", gemm_splitk_reduce_kernel<false>,
+                  dim3(div_up((uint64_t)g.m * g.n, kBlock)), dim3(kBlock), g);
+}
+
+template <int IM>
+int launch_wgrad_tiles(const GemmArgs &g, bool big) {
+    return big ? launch_wgrad<128, IM>(g) : launch_wgrad<64, IM>(g);
+}
+
 // Extent in elements of a rows x cols row-major view with leading dimension ld.
 inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) {
     return rows == 0 || cols == 0 ? 0 : (rows - 1) * ld + cols;
@@ -445,15 +589,6 @@ inline uint64_t extent(uint64_t rows, uint64_t cols, uint64_t ld) {
 
 constexpr uint32_t kCus = 256;
 
-// Slabs in flight in the 64x64 kernel (build-time tunable).
-#ifndef DKZ_GEMM_SMALL_PREFETCH
-#define DKZ_GEMM_SMALL_PREFETCH 2
-#endif
-
-// Workgroups per CU that a split-K grid aims for (build-time tunable).
-#ifndef DKZ_GEMM_SPLIT_TARGET
-#define DKZ_GEMM_SPLIT_TARGET 2
-#endif
 
 }  // namespace
 }  // namespace dkz
@@ -603,18 +738,110 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         GemmArgs gz = g;
         gz.b = input + z0 * in_group;
         gz.c = output + z0 * m * n;
-        const int kind = !im ? kImNone : g.cv.s1 ? kImS1 : kImGather;
+        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
         int e;
-        if (big) {
-            if (kind == kImS1) e = launch_batched<128, 128, 1, kImS1>(gz, zc);
-            else if (kind == kImGather) e = launch_batched<128, 128, 1, kImGather>(gz, zc);
-            else e = launch_batched<128, 128, 1, kImNone>(gz, zc);
-        } else {
-            if (kind == kImS1) e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImS1>(gz, zc);
-            else if (kind == kImGather) e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImGather>(gz, zc);
-            else e = launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, kImNone>(gz, zc);
-        }
+        if (!im) e = launch_fwd<kImNone>(gz, zc, big);
+        else if (g.cv.s1) e = launch_fwd<kS1>(gz, zc, big);
+        else e = launch_fwd<kGa>(gz, zc, big);
         if (e != 0) return e;
+    }
+    return 0;
+}
+
+// convolutional.zig:288-297 (the weight-gradient half of the per-image
+// backward loop) in one product: for group j,
+//     weight_updates(j) (m x k) += sum over images i of delta(i, j) (m x n) x im2col(input(i, j))^T (n x k)
+// with the same m, n, k, offsets and ksize-1 reading of the input as
+// dkz_convolution_forward, delta(i, j) = delta + (i*groups + j)*m*n and
+// weight_updates(j) = weight_updates + j*m*k. One NT product per group whose
+// k runs over (image, position), split into ranges of k that are added in
+// order.
+int dkz_convolution_weight_gradient(int batch, int groups, int channels, int height, int width, int filters,
+                                    int ksize, int stride, int pad, const float *delta, const float *input,
+                                    float *weight_updates) {
+    DKZ_REQUIRE(batch >= 0 && groups >= 1 && channels >= 0 && height >= 0 && width >= 0 && filters >= 0);
+    DKZ_REQUIRE(ksize >= 1 && stride >= 1 && pad >= 0);
+    DKZ_REQUIRE(channels % groups == 0 && filters % groups == 0);
+    DKZ_REQUIRE((int64_t)height + 2 * (int64_t)pad >= ksize && (int64_t)width + 2 * (int64_t)pad >= ksize);
+    const uint64_t m = (uint64_t)filters / groups, cg = (uint64_t)channels / groups;
+    const uint64_t ho = ((uint64_t)height + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t wo = ((uint64_t)width + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t npos = ho * wo, kw = (uint64_t)ksize * ksize * cg, in_group = cg * height * width;
+    if (batch == 0 || m == 0 || kw == 0 || npos == 0) return 0;
+    DKZ_REQUIRE(delta && input && weight_updates);
+    const uint64_t images = (uint64_t)batch * groups;
+    DKZ_REQUIRE(images * m * npos <= kMaxElems && images * in_group <= kMaxElems && (uint64_t)groups * m * kw <= kMaxElems);
+    DKZ_REQUIRE((uint64_t)batch * npos <= kMaxElems);
+    DKZ_REQUIRE(ksize != 1 || npos <= (uint64_t)height * width);  // the input is read as a k x n matrix
+    GemmArgs g{};
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)kw;
+    g.k = (uint32_t)((uint64_t)batch * npos);
+    g.ldc = (uint32_t)kw;
+    g.alpha = 1.0f;
+    g.beta = 1.0f;
+    g.zgroups = 1;
+    ConvB &cv = g.cv;
+    cv.H = (uint32_t)height;
+    cv.W = (uint32_t)width;
+    cv.Wo = (uint32_t)wo;
+    cv.ksz = (uint32_t)ksize;
+    cv.stride = (uint32_t)stride;
+    cv.pad = (uint32_t)pad;
+    cv.div_kk = make_fastdiv((uint32_t)(ksize * ksize));
+    cv.div_k = make_fastdiv((uint32_t)ksize);
+    cv.div_wo = make_fastdiv((uint32_t)wo);
+    cv.npos = (uint32_t)npos;
+    cv.div_npos = make_fastdiv((uint32_t)npos);
+    cv.a_img = (uint32_t)((uint64_t)groups * m * npos);
+    cv.b_img = (uint32_t)((uint64_t)groups * in_group);
+    cv.npos4 = npos % 4 == 0;
+    cv.a_vec = aligned16(delta) && (m * npos) % 4 == 0;
+    cv.b_vec = aligned16(input) && in_group % 4 == 0;
+    const bool s1 = ksize != 1 && stride == 1 && width % 4 == 0 && wo % 4 == 0 && aligned16(input) &&
+                    in_group % 4 == 0;
+    cv.s1 = s1;
+    const bool big = DKZ_WGRAD_BIG && m >= 128;
+    g.tiles_m = (uint32_t)div_up(m, big ? 128 : 64);
+    g.tiles_n = (uint32_t)div_up(kw, big ? 128 : 64);
+    // Split K (image-major positions) into ranges of whole slabs, toward
+    // DKZ_WGRAD_TARGET workgroups per CU (the kernels fit four per CU; with
+    // ksize 1, whose operands stream as plain float4s, DKZ_WGRAD_TARGET_RAW)
+    // with ranges of at least DKZ_WGRAD_MIN_CHUNK, within the scratch,
+    // preferring a workgroup count that is a multiple of the XCD count (the
+    // tile mapping then keeps each range's tiles on one XCD, sharing its
+    // delta rows in L2).
+    const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
+    const uint64_t kt = (uint64_t)batch * npos;
+    const uint64_t target = ksize == 1 ? DKZ_WGRAD_TARGET_RAW : DKZ_WGRAD_TARGET;
+    uint64_t want = div_up(target * kCus, tiles);
+    const uint64_t by_k = div_up(kt, (uint64_t)DKZ_WGRAD_MIN_CHUNK);
+    if (want > by_k) want = by_k;
+    Scratch sc;
+    DKZ_TRY(device_scratch(&sc));
+    const uint64_t cap = sc.gemm_floats / (m * kw);
+    if (want > cap) want = cap;
+    if (want < 1) want = 1;
+    uint64_t chunk = div_up(div_up(kt, want), (uint64_t)kBK) * kBK;
+    for (uint64_t s = want; s > want / 2 && s > 1; --s) {
+        const uint64_t c = div_up(div_up(kt, s), (uint64_t)kBK) * kBK;
+        if (div_up(kt, c) * tiles % kXcds == 0) {
+            chunk = c;
+            break;
+        }
+    }
+    g.splits = (uint32_t)div_up(kt, chunk);
+    g.k_chunk = (uint32_t)chunk;
+    g.partial = sc.gemm;
+    constexpr int kWgRaw = kWgrad + kRaw, kWgGa = kWgrad + kGather, kWgS1 = kWgrad + kTwoBlock;
+    for (int j = 0; j < groups; ++j) {
+        GemmArgs gj = g;
+        gj.a = delta + (uint64_t)j * m * npos;
+        gj.b = input + (uint64_t)j * in_group;
+        gj.c = weight_updates + (uint64_t)j * m * kw;
+        if (ksize == 1) DKZ_TRY(launch_wgrad_tiles<kWgRaw>(gj, big));
+        else if (s1) DKZ_TRY(launch_wgrad_tiles<kWgS1>(gj, big));
+        else DKZ_TRY(launch_wgrad_tiles<kWgGa>(gj, big));
     }
     return 0;
 }

@@ -392,6 +392,15 @@ def convolutionForward(
                                               _p(weights), _p(input), _p(output)), "convolution_forward")
 
 
+def convolutionWeightGradient(
+    batch: int, groups: int, channels: int, height: int, width: int, filters: int, ksize: int, stride: int,
+    pad: int, delta: Buf, input: Buf, weight_updates: Buf,
+) -> None:  # the weight-gradient gemms of layers/convolutional.zig:288-297 in one call
+    _must(_lib.load().dkz_convolution_weight_gradient(batch, groups, channels, height, width, filters, ksize, stride,
+                                                      pad, _p(delta), _p(input), _p(weight_updates)),
+          "convolution_weight_gradient")
+
+
 def dropout(input: Buf, size: int, rand_buf: Buf, prob: float, scale: float) -> None:  # gpu.zig:769
     _must(_lib.load().dkz_dropout(_p(input), size, _p(rand_buf), prob, scale), "dropout")
 

@@ -264,6 +264,15 @@ inline void convolutionForward(size_t batch, size_t groups, size_t channels, siz
          "convolution_forward");
 }
 
+// The weight-gradient gemms of layers/convolutional.zig:288-297 in one call.
+inline void convolutionWeightGradient(size_t batch, size_t groups, size_t channels, size_t height, size_t width,
+                                      size_t filters, size_t ksize, size_t stride, size_t pad, Buf delta, Buf input,
+                                      Buf weight_updates) {
+    must(dkz_convolution_weight_gradient(ci(batch), ci(groups), ci(channels), ci(height), ci(width), ci(filters),
+                                         ci(ksize), ci(stride), ci(pad), delta.f(), input.f(), weight_updates.f()),
+         "convolution_weight_gradient");
+}
+
 // ---- pooling, dropout, shortcut, adam (gpu.zig:725-830) --------------------------
 
 inline void forwardMaxpool(size_t out_n, size_t in_h, size_t in_w, size_t in_c, size_t stride, size_t size,

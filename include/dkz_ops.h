@@ -38,12 +38,12 @@
  *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
- *   - The library owns one scratch buffer per device (34 MiB), allocated and
+ *   - The library owns one scratch buffer per device (130 MiB), allocated and
  *     zeroed by dkz_init: the f64 partial sums a per-channel reduction passes
  *     from its first launch to its second (2 MiB), the partial tiles of a
- *     split-K gemm (32 MiB) and the 64-bit slots (32 KiB) in which the two
- *     workgroups of a channel meet in one-launch reductions. Ops never
- *     allocate. Reductions or gemms issued
+ *     split-K gemm or convolution weight gradient (128 MiB) and the 64-bit
+ *     slots (32 KiB) in which the two workgroups of a channel meet in
+ *     one-launch reductions. Ops never allocate. Reductions or gemms issued
  *     concurrently on two streams of one device share that buffer and race;
  *     issue them on one stream.
  */
@@ -334,6 +334,19 @@ int dkz_gemm(int ta, int tb, int m, int n, int k, float alpha, const float *a, i
  * Results agree with the per-image calls within fp32 summation error. */
 int dkz_convolution_forward(int batch, int groups, int channels, int height, int width, int filters, int ksize,
                             int stride, int pad, const float *weights, const float *input, float *output);
+
+/* The weight-gradient half of a convolutional layer's backward loop
+ * (layers/convolutional.zig:288-297, one gemm(false, true, ...) per image
+ * into the shared weight_updates) in one call: for each group j,
+ *     weight_updates(j) += sum over images i of delta(i, j) x im2col(input(i, j))^T
+ * with m, n, k, the offsets and the ksize-1 reading of the input as in
+ * dkz_convolution_forward, delta(i, j) = delta + (i*groups + j)*m*n and
+ * weight_updates(j) = weight_updates + j*m*k. The images' contributions are
+ * summed in a fixed order; results agree with the per-image calls within fp32
+ * summation error. No workspace. */
+int dkz_convolution_weight_gradient(int batch, int groups, int channels, int height, int width, int filters,
+                                    int ksize, int stride, int pad, const float *delta, const float *input,
+                                    float *weight_updates);
 
 /* gpu.zig:769 dropout(input, size, rand, prob, scale): input[i] = rand[i] < prob ?
  * 0 : input[i] * scale, the rule of layers/misc.zig:105-127 (forward after

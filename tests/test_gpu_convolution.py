@@ -1,6 +1,7 @@
-"""dkz_convolution_forward: the per-image im2col + gemm loop of a
-convolutional layer's forward (layers/convolutional.zig:240-260) in one
-launch, the im2col operand gathered inside the product.
+"""dkz_convolution_forward and dkz_convolution_weight_gradient: the
+per-image im2col + gemm loops of a convolutional layer's forward
+(layers/convolutional.zig:240-260) and weight gradient (:288-297) as single
+products, the im2col operand gathered inside them.
 
 Reference per image i and group j: the oracle's im2col of the image (a copy,
 bit-exact) times the group's weights in f64, added to the output's previous
@@ -30,6 +31,7 @@ CASES = [
     (1, 1, 3, 8, 8, 4, 1, 2, 0),       # ksize 1, stride 2: the layer's own reading of the input
     (4, 1, 32, 28, 28, 64, 3, 1, 1),   # 64x64 tiles
     (24, 1, 16, 56, 56, 128, 3, 1, 1),  # 128x128 tiles (600 of them), config 2's image size
+    (64, 1, 4, 64, 64, 16, 3, 2, 1),   # 64x64 tiles (1024), per-element gathers
     (2, 1, 3, 8, 8, 4, 5, 1, 4),       # pad 4: whole blocks outside a row
     (2, 3, 9, 7, 5, 6, 3, 1, 2),       # three groups, odd widths
     (1, 1, 1, 3, 4, 1, 3, 1, 1),       # one channel, one filter
@@ -115,3 +117,89 @@ def test_convolution_forward_rejects_bad_groups(dev):
     assert lib.dkz_convolution_forward(1, 1, 1, 2, 2, 1, 5, 1, 0, buf.ptr, buf.ptr, buf.ptr) != 0
     assert lib.dkz_convolution_forward(0, 1, 1, 2, 2, 1, 1, 1, 0, None, None, None) == 0  # empty batch
     gpu.free(buf)
+
+
+WG_CASES = [
+    # batch, groups, channels, height, width, filters, ksize, stride, pad
+    (2, 1, 16, 16, 16, 32, 3, 1, 1),   # stride 1, widths % 4 == 0: two-block gathers
+    (3, 2, 8, 10, 12, 6, 3, 2, 1),     # groups, stride 2: per-element gathers
+    (2, 1, 4, 9, 9, 5, 1, 1, 0),       # ksize 1: the input itself (81 positions: float4s span images)
+    (1, 1, 3, 8, 8, 4, 1, 2, 0),       # ksize 1, stride 2: the layer's own reading of the input
+    (5, 1, 8, 7, 7, 16, 3, 1, 1),      # 49 positions: per-element loads across image boundaries
+    (64, 1, 16, 28, 28, 32, 3, 1, 1),  # many images: the product split over image ranges
+    (2, 3, 9, 7, 5, 6, 3, 1, 2),       # three groups, odd widths
+    (4, 1, 8, 20, 20, 96, 3, 1, 1),    # 96 filters: 64x64 tiles, a partial row tile
+    (4, 1, 16, 24, 24, 128, 3, 1, 1),  # 128x128 tiles
+    (3, 1, 8, 17, 17, 160, 3, 2, 1),   # 128x128 tiles, stride 2, a partial row tile
+    (4, 1, 32, 16, 16, 128, 1, 1, 0),  # 128x128 tiles, ksize 1
+]
+
+
+def _wgrad_reference(case, x, d, wu0):
+    batch, groups, C, H, W, F, ks, s, p = case
+    cg, m = C // groups, F // groups
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    n, k = ho * wo, ks * ks * cg
+    in_group = cg * H * W
+    want = wu0.astype(np.float64).copy()
+    bound = np.abs(wu0.astype(np.float64))
+    for i in range(batch):
+        for j in range(groups):
+            z = i * groups + j
+            img = x[z * in_group:(z + 1) * in_group]
+            if ks == 1:
+                col = img[: k * n].reshape(k, n)
+            else:
+                col = np.empty(k * n, np.float32)
+                ref.im2col(img, cg, H, W, ks, s, p, col)
+                col = col.reshape(k, n)
+            dz = d[z * m * n:(z + 1) * m * n].reshape(m, n).astype(np.float64)
+            sl = slice(j * m * k, (j + 1) * m * k)
+            want[sl] += (dz @ col.astype(np.float64).T).ravel()
+            bound[sl] += (np.abs(dz) @ np.abs(col.astype(np.float64)).T).ravel()
+    kt = batch * n  # every image's positions are one sum
+    g = (kt + 3) * U / (1 - (kt + 3) * U)
+    return want, g * bound
+
+
+@pytest.mark.parametrize("case", WG_CASES, ids=str)
+def test_convolution_weight_gradient(dev, case):
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(sum(case) + 1)
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    x = r.uniform(-1, 1, batch * C * H * W).astype(np.float32)
+    d = r.uniform(-1, 1, batch * F * ho * wo).astype(np.float32)
+    wu0 = r.uniform(-1, 1, F * (C // groups) * ks * ks).astype(np.float32)
+    want, bd = _wgrad_reference(case, x, d, wu0)
+    dx, dd, dw = up(x), up(d), up(wu0)
+    gpu.convolutionWeightGradient(batch, groups, C, H, W, F, ks, s, p, dd, dx, dw)
+    got = down(dw, wu0).astype(np.float64)
+    err = np.abs(got - want)
+    bad = ~(err <= bd)
+    assert not bad.any(), (f"weight gradient {case}: {int(bad.sum())} beyond the fp32 bound; "
+                           f"max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}")
+    for b in (dx, dd, dw):
+        gpu.free(b)
+
+
+def test_convolution_weight_gradient_matches_per_image_calls(dev):
+    """The layer's per-image calls (im2col, then gemm(false, true, ..., beta 1)
+    into the shared weight_updates) and the one product agree exactly on
+    integer-valued inputs, where every summation order is exact."""
+    case = (6, 1, 8, 12, 12, 16, 3, 1, 1)
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(9)
+    x = r.integers(-3, 4, batch * C * H * W).astype(np.float32)
+    d = r.integers(-3, 4, batch * F * H * W).astype(np.float32)
+    n, k = H * W, ks * ks * C
+    dx, dd = up(x), up(d)
+    fused, loop = gpu.alloc(F * k), gpu.alloc(F * k)
+    gpu.convolutionWeightGradient(batch, groups, C, H, W, F, ks, s, p, dd, dx, fused)
+    ws = gpu.alloc(k * n)
+    for i in range(batch):
+        gpu.im2col(dx.offset(i * C * H * W), C, H, W, ks, s, p, ws)
+        gpu.gemm(False, True, F, k, n, 1.0, dd.offset(i * F * n), n, ws, n, 1.0, loop, k)
+    a, b = down(fused, np.empty(F * k, np.float32)), down(loop, np.empty(F * k, np.float32))
+    assert np.array_equal(a, b)
+    for buf in (dx, dd, fused, loop, ws):
+        gpu.free(buf)
