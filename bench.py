@@ -41,6 +41,11 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
 
 Algorithmic bytes count every logical fp32/int32 element read or written once
 (4 B); per-channel vectors of C floats are not counted.
+
+--per-op-traffic runs each per-op row's first three launches once between two
+marker dispatches and prints the rows, for a rocprofv3 FETCH_SIZE/WRITE_SIZE
+run to attribute HBM traffic per row (profiles/traffic_per_op.md);
+--copy-calibration runs the known-size copy that scales those counters.
 """
 
 from __future__ import annotations
@@ -284,10 +289,40 @@ def gbs(nbytes: int, ms: float) -> float:
 # ---------------------------------------------------------------------------
 
 
-def per_op_table(gpu, hip, stream, launches: int):
+# Traffic mode: a row's launches sit between two marker dispatches -- a fill
+# of a misaligned buffer, which runs the one-lane-per-element fill kernel on
+# exactly MARK_BASE + 2*row (+1 for the end) workgroups of 256 -- so that a
+# counter profile (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) can attribute every
+# dispatch to its row from the dispatch order and grid sizes alone.
+MARK_BASE = 50000
+TRAFFIC_PASSES = 3
+
+
+def per_op_table(gpu, hip, stream, launches: int, traffic=None):
+    """The per-op table; with `traffic` (a list), no timing: each row's first
+    TRAFFIC_PASSES launches (or call sequences) run once between markers and
+    the row is appended to `traffic`."""
     from darknet_zig_amd.activations import Activation
 
     rows = {}
+    if traffic is not None:
+        mark_buf = gpu.alloc((MARK_BASE + 256) * 256 + 1)
+
+    def marker(grid):
+        gpu.fill(mark_buf.offset(1), grid * 256, 0.0)
+
+    def traced(cfg, name, nbytes, seqs):
+        i = len(traffic)
+        passes = min(TRAFFIC_PASSES, len(seqs))
+        hip.sync()
+        marker(MARK_BASE + 2 * i)
+        for seq in seqs[:passes]:
+            for fn in seq:
+                fn()
+        marker(MARK_BASE + 2 * i + 1)
+        hip.sync()
+        traffic.append({"row": f"{cfg}/{name}", "bytes": nbytes, "passes": passes, "begin_grid": MARK_BASE + 2 * i})
+        print(f"traffic row {i}: {cfg}/{name}", file=sys.stderr, flush=True)
 
     def row(cfg, name, nbytes, ms, single_ms=None):
         g = gbs(nbytes, ms)
@@ -302,12 +337,16 @@ def per_op_table(gpu, hip, stream, launches: int):
         around the run: the per-launch figure of a stream of such calls) and
         single-launch (an event pair around each launch, which also times
         ~2 us of dispatch and completion)."""
+        if traffic is not None:
+            return traced(cfg, name, nbytes, [[f] for f in fns])
         k = max(launches, len(fns))
         row(cfg, name, nbytes, time_seq(hip, stream, [[f] for f in fns], k), time_op(hip, stream, fns, k))
 
     def add_seq(cfg, name, nbytes, seqs):
         """A call sequence (or a multi-launch entry point), events only around
         the whole timed region, as a layer would issue it back to back."""
+        if traffic is not None:
+            return traced(cfg, name, nbytes, seqs)
         row(cfg, name, nbytes, time_seq(hip, stream, seqs, max(launches, len(seqs))))
 
     # -- config 1: BN forward + leaky, [128,32,32,32], x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1)
@@ -554,6 +593,8 @@ def per_op_table(gpu, hip, stream, launches: int):
     add(cfg, "col2im (one image)", 4 * (ncol + 2 * nim),
         [lambda i=i, c=c: gpu.col2im(c, C2, H2, H2, K2, 1, 1, i) for i, c in zip(ims, cols)])
     dev.free()
+    if traffic is not None:
+        gpu.free(mark_buf)
     return rows
 
 
@@ -685,6 +726,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--per-op-only", action="store_true",
                     help="only run the per-op table (for a kernel trace without the chain's launches)")
+    ap.add_argument("--per-op-traffic", action="store_true",
+                    help="only run each per-op row's first launches once, between marker dispatches "
+                         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per row)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run dkz_copy over MIB MiB (x4 launches, rotated): the known-size kernel "
                          "that scales rocprofv3's FETCH_SIZE/WRITE_SIZE")
@@ -710,6 +754,12 @@ def main() -> int:
         dev.free()
         print(json.dumps({"copy_calibration": {"bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 4,
                                                "us": round(ms * 1e3, 2)}}), flush=True)
+        return 0
+
+    if args.per_op_traffic:
+        traffic = []
+        per_op_table(gpu, hip, stream, 1, traffic)
+        print(json.dumps({"per_op_traffic": traffic, "mark_base": MARK_BASE}), flush=True)
         return 0
 
     if args.per_op_only:
