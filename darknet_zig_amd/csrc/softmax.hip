@@ -18,9 +18,13 @@
 //    columns of different rows use different banks); all its lanes share the
 //    loads, exps and divides, and lane r of the first wave runs group r's max
 //    and its sequential sum, so kRows sums advance per instruction. Bit-exact.
-//  * contiguous groups with n > kSeqMax: the same, but the sum is an f64
-//    tree (within 1e-5 relative of the twin) because the row no longer fits
-//    in LDS.
+//  * many contiguous groups (at least DKZ_SOFTMAX_WIDE_MIN) with
+//    kRowsMaxN < n <= kWideMaxN (1024): 2, 4 or 8 groups a workgroup held
+//    in registers; maxes and exps on all lanes, then lane l of the first
+//    wave adds group l's exps in order from LDS. Bit-exact.
+//  * contiguous groups with n > kSeqMax: one workgroup per group, the row
+//    not staged, and the sum an f64 tree (within 1e-5 relative of the twin)
+//    because the row no longer fits in LDS.
 //  * strided groups that sit side by side (group_offset 1, the spatial
 //    softmax over the classes of each position) with n <= kTileMaxN: a
 //    workgroup stages 64 consecutive groups in LDS; all its lanes share the
@@ -286,6 +290,151 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const float *in, f
     }
 }
 
+// Many contiguous groups of kRowsMaxN < n <= kWideMaxN: R groups a
+// workgroup (R * 1028 floats of LDS at most), held in registers -- lane t holds elements 4t..4t+3 (V4) or
+// t, t+256, t+512, t+768 of each -- so the maxes (wave64 DPP + LDS) and the
+// exps run on all lanes; the exps then go to LDS (row pitch a multiple of 4
+// but not of 32) where lane l < R of the first wave adds group l's in order,
+// so R sequential sums advance per instruction, and all lanes divide their
+// registers by the sums. Bit-exact.
+// Groups a workgroup: about 1024 workgroups (fewer leave the loads, the
+// VALU-heavy exps and divides and the stores of the workgroups in lock step;
+// more repeat the per-workgroup barriers and sums): measured at n = 1000,
+// 2048 groups 16.8 -> 12.4 us (R = 2), 4096 24.5 -> 17.5 (R = 4), 8192
+// 41.5 -> 28.9 and 16384 80 -> 50.5 (R = 8); below 2048 groups the
+// one-workgroup-per-group kernel is as fast.
+#ifndef DKZ_SOFTMAX_WIDE_MIN
+#define DKZ_SOFTMAX_WIDE_MIN 2048
+#endif
+constexpr uint32_t kWideMaxN = 4 * kBlock;
+
+template <int R, bool V4, bool XENT>
+__global__ __launch_bounds__(kBlock) void softmax_wide_kernel(const float *in, float *out, Groups G, uint32_t rows,
+                                                              uint32_t pitch, Xent xe) {
+    extern __shared__ float4 wide_lds4[];  // R rows of `pitch` floats
+    float *tile = reinterpret_cast<float *>(wide_lds4);
+    __shared__ float red[R][kBlock / kWave];
+    __shared__ float sum_sh[R];
+    const uint32_t t = threadIdx.x, n = G.n, r0 = blockIdx.x * R;
+    const uint32_t nr = rows - r0 < (uint32_t)R ? rows - r0 : (uint32_t)R;
+    const int wave = (int)(t / kWave);
+    // Element j of this lane's four in a group (V4: 4t + j; else t + 256j).
+    auto at = [&](int j) -> uint32_t { return V4 ? 4 * t + (uint32_t)j : t + (uint32_t)j * kBlock; };
+
+    float v[R][4];
+    uint32_t base[R];
+#pragma unroll
+    for (int l = 0; l < R; ++l) base[l] = group_base(r0 + ((uint32_t)l < nr ? (uint32_t)l : 0u), G);
+#pragma unroll
+    for (int l = 0; l < R; ++l) {
+        const bool live = (uint32_t)l < nr;
+        if constexpr (V4) {
+            float4 a = make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
+            if (live && 4 * t < n) a = ld4<false>(in + base[l], t);
+            v[l][0] = a.x;
+            v[l][1] = a.y;
+            v[l][2] = a.z;
+            v[l][3] = a.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[l][j] = live && at(j) < n ? in[base[l] + at(j)] : -FLT_MAX;
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < R; ++l) {
+        const float m = wave_max(fmaxf(fmaxf(v[l][0], v[l][1]), fmaxf(v[l][2], v[l][3])));
+        if ((t & (kWave - 1)) == 0) red[l][wave] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int l = 0; l < R; ++l) {
+        const float mt = fmaxf(fmaxf(red[l][0], red[l][1]), fmaxf(red[l][2], red[l][3])) / G.temp;
+        float *row = tile + l * pitch;
+        if constexpr (V4) {
+            if (4 * t < n) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[l][j] = expf_libm(v[l][j] / G.temp - mt);
+                reinterpret_cast<float4 *>(row)[t] = make_float4(v[l][0], v[l][1], v[l][2], v[l][3]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (at(j) < n) {
+                    v[l][j] = expf_libm(v[l][j] / G.temp - mt);
+                    row[at(j)] = v[l][j];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (t < nr) {
+        // Group t's exps left to right, 32 at a time, the next 32's LDS reads
+        // in flight while these are added.
+        const float4 *row4 = reinterpret_cast<const float4 *>(tile + t * pitch);
+        float s = 0.0f;
+        const uint32_t nb = n >> 5;
+        float4 va[8], vb[8];
+        if (nb > 0) read32(row4, 0, va);
+        for (uint32_t b = 0; b < nb;) {
+            if (b + 1 < nb) read32(row4, b + 1, vb);
+            s = add32(s, va);
+            if (++b >= nb) break;
+            if (b + 1 < nb) read32(row4, b + 1, va);
+            s = add32(s, vb);
+            ++b;
+        }
+        for (uint32_t i = nb << 5; i < n; ++i) s += tile[t * pitch + i];
+        sum_sh[t] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int l = 0; l < R; ++l) {
+        if ((uint32_t)l >= nr) break;
+        const float sum = sum_sh[l];
+        const uint32_t off = base[l];
+        if constexpr (V4) {
+            if (4 * t < n) {
+                const float4 p = make_float4(v[l][0] / sum, v[l][1] / sum, v[l][2] / sum, v[l][3] / sum);
+                st4<false>(out + off, t, p);
+                if constexpr (XENT) {
+                    const float4 tr = ld4<false>(xe.truth + off, t);
+                    float4 d, ls;
+                    xent1(p.x, tr.x, d.x, ls.x);
+                    xent1(p.y, tr.y, d.y, ls.y);
+                    xent1(p.z, tr.z, d.z, ls.z);
+                    xent1(p.w, tr.w, d.w, ls.w);
+                    st4<false>(xe.delta + off, t, d);
+                    st4<false>(xe.loss + off, t, ls);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (at(j) < n) {
+                    const float p = v[l][j] / sum;
+                    out[off + at(j)] = p;
+                    if constexpr (XENT) xent1(p, xe.truth[off + at(j)], xe.delta[off + at(j)], xe.loss[off + at(j)]);
+                }
+            }
+        }
+    }
+}
+
+template <int R>
+int launch_wide(const float *input, float *output, const Groups &G, uint32_t rows, bool v4, const Xent *xe) {
+    const uint32_t n4 = (G.n + 3) & ~3u;
+    const uint32_t pitch = n4 % 32 == 0 ? n4 + 4 : n4;  // a multiple of 4, not of 32
+    const size_t lds = (size_t)R * pitch * sizeof(float);
+    const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
+    void (*k)(const float *, float *, Groups, uint32_t, uint32_t, Xent);
+    if (xe) k = v4 ? softmax_wide_kernel<R, true, true> : softmax_wide_kernel<R, false, true>;
+    else k = v4 ? softmax_wide_kernel<R, true, false> : softmax_wide_kernel<R, false, false>;
+    const dim3 grid(div_up(rows, (uint32_t)R));
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, current_stream(), input, output, G, rows, pitch, x);
+    return after_launch(xe ? "softmax_xent_wide" : "softmax_wide", grid, dim3(kBlock));
+}
+
 constexpr uint32_t kTileRows = 64;
 constexpr uint32_t kTileMaxN = 128;
 
@@ -419,6 +568,11 @@ int softmax_run(const float *input, int n, int batch, int batch_offset, int grou
     const bool seq = (uint32_t)n <= kSeqMax;
     bool v4 = n % 4 == 0 && batch_offset % 4 == 0 && group_offset % 4 == 0 && aligned16(input) && aligned16(output);
     if (xe) v4 = v4 && aligned16(xe->truth) && aligned16(xe->delta) && aligned16(xe->loss);
+    if (rows >= DKZ_SOFTMAX_WIDE_MIN && (uint32_t)n > kRowsMaxN && (uint32_t)n <= kWideMaxN) {
+        if (rows >= 8192) return launch_wide<8>(input, output, G, rows, v4, xe);
+        if (rows >= 4096) return launch_wide<4>(input, output, G, rows, v4, xe);
+        return launch_wide<2>(input, output, G, rows, v4, xe);
+    }
     const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
     const size_t lds = seq ? (size_t)n * sizeof(float) : 0;
     void (*k)(const float *, float *, Groups, Xent);

@@ -17,6 +17,8 @@ from darknet_zig_amd.activations import Activation
 from oracle import ref
 from tests.helpers import assert_bitexact, assert_r5, chan_f32, chan_sum64, down, normal, rng, uniform, up
 from tests.test_gpu_batchnorm_fused import _backward_case, _forward_case
+from tests.test_gpu_convolution import _reference as conv_reference
+from tests.test_gpu_convolution import _wgrad_reference as wgrad_reference
 from tests.test_gpu_gemm import check as gemm_check
 
 pytestmark = pytest.mark.gpu
@@ -29,6 +31,20 @@ CONV = sorted({(int(_R.integers(1, 9)), int(_R.integers(3, 24)), int(_R.integers
                 int(_R.integers(1, 3)), int(_R.integers(0, 3))) for _ in range(12)})
 GEMM = sorted({(bool(_R.integers(0, 2)), bool(_R.integers(0, 2)), int(_R.integers(1, 300)), int(_R.integers(1, 300)),
                 int(_R.integers(0, 700))) for _ in range(16)})
+
+
+def _layer():
+    """batch, groups, channels, height, width, filters, ksize, stride, pad with
+    the window inside the padded image."""
+    while True:
+        batch, groups, k = int(_R.integers(1, 7)), int(_R.integers(1, 4)), int(_R.choice([1, 1, 2, 3, 3, 5]))
+        h, w, stride, pad = int(_R.integers(3, 21)), int(_R.integers(3, 21)), int(_R.integers(1, 4)), int(_R.integers(0, 4))
+        if h + 2 * pad >= k and w + 2 * pad >= k:
+            return (batch, groups, groups * int(_R.integers(1, 10)), h, w, groups * int(_R.integers(1, 41)), k, stride,
+                    pad)
+
+
+LAYERS = sorted({_layer() for _ in range(14)})
 
 
 @pytest.mark.parametrize("shape", CHANNEL_SHAPES, ids=str)
@@ -162,3 +178,27 @@ def test_conv_lowering(dev, C, H, W, k, s, p):
 def test_gemm(dev, ta, tb, m, n, k):
     gemm_check(ta, tb, m, n, k, 1.25 if k % 2 else -0.5, (0.0, 1.0, 0.5)[k % 3], seed=m + n + k,
                pad=(m % 3, n % 2, k % 4))
+
+
+@pytest.mark.parametrize("case", LAYERS, ids=str)
+def test_convolution_layer(dev, case):
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(sum(case) * 7 + 3)
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    if ks == 1 and ho * wo > H * W:
+        pytest.skip("ksize 1 with padding: the layer reads past the image as a k x n matrix")
+    x = uniform(r, batch * C * H * W)
+    w = uniform(r, F * (C // groups) * ks * ks)
+    d = uniform(r, batch * F * ho * wo)
+    out0, wu0 = uniform(r, batch * F * ho * wo), uniform(r, F * (C // groups) * ks * ks)
+    dx, dw, dd, do, du = up(x), up(w), up(d), up(out0), up(wu0)
+    want, bd, _ = conv_reference(case, x, w, out0)
+    gpu.convolutionForward(batch, groups, C, H, W, F, ks, s, p, dw, dx, do)
+    err = np.abs(down(do, out0).astype(np.float64) - want)
+    assert (err <= bd).all(), f"forward {case}: max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}"
+    want, bd = wgrad_reference(case, x, d, wu0)
+    gpu.convolutionWeightGradient(batch, groups, C, H, W, F, ks, s, p, dd, dx, du)
+    err = np.abs(down(du, wu0).astype(np.float64) - want)
+    assert (err <= bd).all(), f"weight gradient {case}: max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}"
+    for b in (dx, dw, dd, do, du):
+        gpu.free(b)

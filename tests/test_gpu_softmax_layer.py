@@ -92,6 +92,13 @@ def test_config3_one_pass(dev):
     (5, 40, 2, 2.0),
     (2, 8192, 1, 1.0),  # the longest row staged in LDS
     (2, 12000, 1, 1.0),  # longer: the f64-sum path
+    # at least 2048 rows of 257..1024 held in registers, 2, 4 or 8 a
+    # workgroup, the last tile partial; float4 and per-element layouts
+    (2051, 1000, 1, 1.0),
+    (4096, 1000, 1, 1.0),
+    (4101, 600, 2, 0.7),
+    (4097, 777, 1, 1.0),
+    (4100, 1024, 1, 1.0),
 ])
 def test_shapes(dev, batch, inputs, groups, temp):
     r = rng(batch * inputs + groups)
@@ -112,12 +119,12 @@ def test_shapes(dev, batch, inputs, groups, temp):
     _check(x, t, batch, inputs, groups, temp, name=f"{batch}x{inputs}/{groups}")
 
 
-@pytest.mark.parametrize("offset", [1, 2])
-def test_misaligned_views(dev, offset):
-    batch, classes = 6, 500
+@pytest.mark.parametrize("offset,batch", [(1, 6), (2, 6), (1, 4100)])
+def test_misaligned_views(dev, offset, batch):
+    classes = 500
     r = rng(offset)
     x = normal(r, batch * classes, 0, 2.0)
-    _check(x, _one_hot(r, batch, classes), batch, classes, 1, 1.0, offset, name=f"offset {offset}")
+    _check(x, _one_hot(r, batch, classes), batch, classes, 1, 1.0, offset, name=f"offset {offset}, {batch} rows")
 
 
 def test_no_truth_is_softmax_only(dev):

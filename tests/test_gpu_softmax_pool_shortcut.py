@@ -36,8 +36,14 @@ def _softmax_case(x, n, batch, batch_offset, groups, group_offset, stride, temp)
     [(8, 137, 1.0, 1.0), (256, 1000, 4.0, 1.0), (3, 33, 10.0, 0.5), (5, 8192, 2.0, 1.0), (17, 1, 1.0, 1.0),
      (4, 5, 1.0, 2.0),
      # many short rows: 16 rows per workgroup staged in LDS, the last tile
-     # partial; and just past the longest such row
-     (4096, 256, 4.0, 1.0), (5000, 37, 2.0, 0.7), (4104, 100, 3.0, 1.0), (4096, 257, 3.0, 1.0)],
+     # partial
+     (4096, 256, 4.0, 1.0), (5000, 37, 2.0, 0.7), (4104, 100, 3.0, 1.0),
+     # at least 2048 rows of 257..1024: 2, 4 or 8 rows per workgroup (by the
+     # row count) in registers, float4 or per-element layout, the last tile
+     # partial
+     (2049, 500, 3.0, 1.0), (3000, 333, 2.0, 1.0), (4096, 257, 3.0, 1.0), (4096, 1000, 4.0, 1.0),
+     (4100, 300, 3.0, 1.0), (4097, 777, 2.0, 0.7), (4100, 1024, 3.0, 1.0), (8195, 1021, 2.0, 1.0),
+     (8200, 1000, 4.0, 1.0)],
 )
 def test_softmax_rows_bitexact(dev, batch, classes, sigma, temp):
     x = normal(rng(classes + batch), batch * classes, 0, sigma)
