@@ -26,9 +26,10 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                configs' fast paths (a 3x3/s2 max pool, a spatial softmax, a
                connected layer's bias gradient)
   gemm         dkz_gemm at config 2's convolution shapes and a large square,
-               and config 2's convolutional layer forward and weight gradient
-               over the batch (the per-image loops against
-               dkz_convolution_forward / _weight_gradient), TFLOP/s
+               and config 2's convolutional layer forward, weight gradient
+               and data gradient over the batch (the per-image loops against
+               dkz_convolution_forward / _weight_gradient / _data_gradient),
+               TFLOP/s
                against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
                pass and one apply pass, 32 B/elem instead of 56)
@@ -654,12 +655,24 @@ def gemm_table(gpu, hip, stream):
             gpu.im2col(x.offset(i * C * hw), C, H, H, K, 1, 1, ws)
             gpu.gemm(False, True, F, kk, hw, 1.0, y.offset(i * F * hw), hw, ws, hw, 1.0, wu, kk)
 
+    # ... and its data gradient (convolutional.zig:299-305): per image
+    # gemm(true, false, beta 0) into the workspace and col2im into the
+    # previous layer's delta, against one dkz_convolution_data_gradient call
+    # (y stands in for delta, x for the previous delta)
+    def per_image_dgrad():
+        for i in range(B):
+            gpu.gemm(True, False, kk, hw, F, 1.0, w, kk, y.offset(i * F * hw), hw, 0.0, ws, hw)
+            gpu.col2im(ws, C, H, H, K, 1, 1, x.offset(i * C * hw))
+
     for name, fn, reps in (("conv layer fwd [64,128,56,56]->128 3x3: per-image im2col+gemm", per_image, 3),
                            ("conv layer fwd [64,128,56,56]->128 3x3: convolution_forward",
                             lambda: gpu.convolutionForward(B, 1, C, H, H, F, K, 1, 1, w, x, y), 10),
                            ("conv layer wgrad [64,128,56,56]->128 3x3: per-image im2col+gemm", per_image_wgrad, 3),
                            ("conv layer wgrad [64,128,56,56]->128 3x3: convolution_weight_gradient",
-                            lambda: gpu.convolutionWeightGradient(B, 1, C, H, H, F, K, 1, 1, y, x, wu), 10)):
+                            lambda: gpu.convolutionWeightGradient(B, 1, C, H, H, F, K, 1, 1, y, x, wu), 10),
+                           ("conv layer dgrad [64,128,56,56]->128 3x3: per-image gemm+col2im", per_image_dgrad, 3),
+                           ("conv layer dgrad [64,128,56,56]->128 3x3: convolution_data_gradient",
+                            lambda: gpu.convolutionDataGradient(B, 1, C, H, H, F, K, 1, 1, w, y, x), 10)):
         ms = time_seq(hip, stream, [[fn]], reps)
         tf = flops / (ms * 1e-3) / 1e12
         rows[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / GEMM_PEAK_TFLOPS, 4),

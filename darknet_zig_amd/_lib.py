@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_gemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "dkz_convolution_forward": (_i, [_i] * 9 + [_p] * 3),
     "dkz_convolution_weight_gradient": (_i, [_i] * 9 + [_p] * 3),
+    "dkz_convolution_data_gradient": (_i, [_i] * 9 + [_p] * 3),
     "dkz_dropout": (_i, [_p, _i, _p, _f, _f]),
     "dkz_adam_update": (_i, [_p, _p, _p, _p, _f, _f, _f, _f, _f, _i, _i, _i]),
     "dkz_batchnorm_forward": (_i, [_i, _i, _i, _i, _i] + [_p] * 10),

@@ -551,15 +551,38 @@ int launch_gemm(bool ta, bool tb, GemmArgs g) {
 // A batched NN product over z = 0 .. zcount-1 (one grid row each); IM != kImNone:
 // B is the implicit im2col of image z.
 template <int BM, int BN, int D, int IM>
-int launch_batched(const GemmArgs &g, uint32_t zcount) {
+int launch_batched(const char *name, const GemmArgs &g, uint32_t zcount) {
     const dim3 grid(g.tiles_m * g.tiles_n, zcount);
-    return launch("convolution_forward", gemm_mfma_kernel<BM, BN, false, false, D, IM>, grid, dim3(kBlock), g);
+    return launch(name, gemm_mfma_kernel<BM, BN, false, false, D, IM>, grid, dim3(kBlock), g);
+}
+
+// A batched TN product (A = weights, m x k stored k-major), no implicit
+// operand: the data gradient of a 1x1 convolution.
+template <int BM, int BN, int D>
+int launch_batched_tn(const GemmArgs &g, uint32_t zcount) {
+    const dim3 grid(g.tiles_m * g.tiles_n, zcount);
+    return launch("convolution_data_gradient", gemm_mfma_kernel<BM, BN, true, false, D>, grid, dim3(kBlock), g);
+}
+
+// The data gradient's A: at[j][c][(f*ks + kh)*ks + kw] = w[j][f][c][ks-1-kh][ks-1-kw]
+// for group j, channel c < cg and filter f < m -- the group's weights with
+// channels as rows and the window flipped, so that the product with the
+// implicit gather of delta is col2im(w^T x delta) (im2col.zig:51-79).
+__global__ __launch_bounds__(kBlock) void flip_weights_kernel(const float *w, float *at, uint32_t kk, FastDiv div_kk,
+                                                             FastDiv div_mkk, FastDiv div_cgmkk, uint32_t cg,
+                                                             uint32_t total) {
+    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+    if (e >= total) return;
+    const uint32_t j = fdiv(e, div_cgmkk), r = e - j * div_cgmkk.d;
+    const uint32_t c = fdiv(r, div_mkk), q = r - c * div_mkk.d;
+    const uint32_t f = fdiv(q, div_kk), t = q - f * kk;
+    at[e] = w[(size_t)j * div_cgmkk.d + (size_t)f * cg * kk + c * kk + (kk - 1 - t)];
 }
 
 template <int IM>
-int launch_fwd(const GemmArgs &g, uint32_t zcount, bool big) {
-    if (big) return launch_batched<128, 128, 1, IM>(g, zcount);
-    return launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, IM>(g, zcount);
+int launch_fwd(const char *name, const GemmArgs &g, uint32_t zcount, bool big) {
+    if (big) return launch_batched<128, 128, 1, IM>(name, g, zcount);
+    return launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, IM>(name, g, zcount);
 }
 
 // The weight gradient's NT product (BM x BM tiles, K split into ranges),
@@ -740,10 +763,176 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         gz.c = output + z0 * m * n;
         constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
         int e;
-        if (!im) e = launch_fwd<kImNone>(gz, zc, big);
-        else if (g.cv.s1) e = launch_fwd<kS1>(gz, zc, big);
-        else e = launch_fwd<kGa>(gz, zc, big);
+        if (!im) e = launch_fwd<kImNone>("convolution_forward", gz, zc, big);
+        else if (g.cv.s1) e = launch_fwd<kS1>("convolution_forward", gz, zc, big);
+        else e = launch_fwd<kGa>("convolution_forward", gz, zc, big);
         if (e != 0) return e;
+    }
+    return 0;
+}
+
+// convolutional.zig:299-305 (the data-gradient half of the per-image
+// backward loop) in one call. For image i and group j, with m, n, k, the
+// offsets and out_h, out_w as in dkz_convolution_forward and
+// input_delta(i, j) = input_delta + (i*groups + j)*in_group:
+//   ksize 1: input_delta(i, j), read as a k x n matrix as the layer reads it,
+//            = weights(j)^T (k x m) x delta(i, j) (m x n) -- overwritten
+//            (the layer's gemm with beta 0);
+//   else:    input_delta(i, j) += col2im(weights(j)^T x delta(i, j)) -- the
+//            layer's gemm into the workspace, then col2im, which adds.
+// With stride 1 and pad < ksize the second is one product per image and
+// group: input channels by input positions, k = (filter, tap) over the
+// group's flipped weights (transposed once into the library's scratch) and
+// delta gathered at each tap's output position, so col2im's adds join the
+// product's sum. Otherwise the layer's two steps run batched over as many
+// images as the scratch holds. No workspace.
+int dkz_convolution_data_gradient(int batch, int groups, int channels, int height, int width, int filters, int ksize,
+                                  int stride, int pad, const float *weights, const float *delta,
+                                  float *input_delta) {
+    DKZ_REQUIRE(batch >= 0 && groups >= 1 && groups <= 65535 && channels >= 0 && height >= 0 && width >= 0 &&
+                filters >= 0);
+    DKZ_REQUIRE(ksize >= 1 && stride >= 1 && pad >= 0);
+    DKZ_REQUIRE(channels % groups == 0 && filters % groups == 0);
+    DKZ_REQUIRE((int64_t)height + 2 * (int64_t)pad >= ksize && (int64_t)width + 2 * (int64_t)pad >= ksize);
+    const uint64_t m = (uint64_t)filters / groups, cg = (uint64_t)channels / groups;
+    const uint64_t ho = ((uint64_t)height + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t wo = ((uint64_t)width + 2 * (uint64_t)pad - ksize) / stride + 1;
+    const uint64_t npos = ho * wo, kk = (uint64_t)ksize * ksize, kw = kk * cg;
+    const uint64_t zcount = (uint64_t)batch * groups, in_group = cg * height * width;
+    if (zcount == 0 || cg == 0 || npos == 0 || in_group == 0) return 0;
+    DKZ_REQUIRE(weights && delta && input_delta);
+    DKZ_REQUIRE(zcount * m * npos <= kMaxElems && zcount * in_group <= kMaxElems &&
+                (uint64_t)groups * m * kw <= kMaxElems);
+    DKZ_REQUIRE(ksize != 1 || npos <= (uint64_t)height * width);  // the k x n view stays inside the image
+    const uint64_t chunk = 65535 - 65535 % (uint64_t)groups;
+    GemmArgs g{};
+    g.alpha = 1.0f;
+    g.splits = 1;
+    g.zgroups = (uint32_t)groups;
+    g.b_z = (uint32_t)(m * npos);
+    g.c_z = (uint32_t)in_group;
+    if (ksize == 1) {
+        // C(i, j) = A^T x B with A = weights(j) (m x cg, k-major), B = delta(i, j);
+        // with m == 0 the sum is empty and beta 0 leaves zeros (gemm.zig:121-131).
+        g.a = weights;
+        g.m = (uint32_t)cg;
+        g.n = (uint32_t)npos;
+        g.k = (uint32_t)m;
+        g.k_chunk = (uint32_t)m;
+        g.lda = (uint32_t)cg;
+        g.ldb = (uint32_t)npos;
+        g.ldc = (uint32_t)npos;
+        g.beta = 0.0f;
+        g.a_z = (uint32_t)(m * cg);
+        g.vec_a = aligned16(weights) && cg % 4 == 0;
+        g.vec_b = aligned16(delta) && npos % 4 == 0 && (m * npos) % 4 == 0;
+        const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(npos, 128) * zcount >= 2 * kCus;
+        g.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
+        g.tiles_n = (uint32_t)div_up(npos, big ? 128 : 64);
+        for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
+            const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
+            GemmArgs gz = g;
+            gz.b = delta + z0 * m * npos;
+            gz.c = input_delta + z0 * in_group;
+            DKZ_TRY(big ? (launch_batched_tn<128, 128, 1>(gz, zc))
+                        : (launch_batched_tn<64, 64, DKZ_GEMM_SMALL_PREFETCH>(gz, zc)));
+        }
+        return 0;
+    }
+    if (m == 0) return 0;  // col2im adds an empty sum
+    Scratch sc;
+    DKZ_TRY(device_scratch(&sc));
+    if (stride == 1 && pad <= ksize - 1) {
+        // input_delta(i, j) += A x im2col(delta(i, j)) with A the group's
+        // weights flipped and transposed (flip_weights_kernel, into the
+        // scratch) and the im2col of delta (out_h x out_w, pad ksize-1-pad)
+        // gathered inside the product: out_h + 2*(ksize-1-pad) - ksize + 1 =
+        // height, and tap (kh, kw) of input position (y, x) reads delta at
+        // (y + kh - (ksize-1-pad), ...), i.e. the layer's col2im term of tap
+        // (ksize-1-kh, ksize-1-kw).
+        const uint64_t at_floats = (uint64_t)groups * cg * m * kk;
+        DKZ_REQUIRE(at_floats <= sc.gemm_floats);
+        DKZ_TRY(launch("convolution_data_gradient", flip_weights_kernel, dim3(div_up(at_floats, kBlock)),
+                       dim3(kBlock), weights, sc.gemm, (uint32_t)kk, make_fastdiv((uint32_t)kk),
+                       make_fastdiv((uint32_t)(m * kk)), make_fastdiv((uint32_t)(cg * m * kk)), (uint32_t)cg,
+                       (uint32_t)at_floats));
+        const uint64_t n = (uint64_t)height * width, k = m * kk;
+        g.a = sc.gemm;
+        g.m = (uint32_t)cg;
+        g.n = (uint32_t)n;
+        g.k = (uint32_t)k;
+        g.k_chunk = (uint32_t)k;
+        g.lda = (uint32_t)k;
+        g.ldb = (uint32_t)n;
+        g.ldc = (uint32_t)n;
+        g.beta = 1.0f;
+        g.a_z = (uint32_t)(cg * k);
+        g.vec_a = k % 4 == 0;  // the scratch is 256-byte aligned
+        ConvB &cv = g.cv;
+        cv.H = (uint32_t)ho;
+        cv.W = (uint32_t)wo;
+        cv.Wo = (uint32_t)width;
+        cv.ksz = (uint32_t)ksize;
+        cv.stride = 1;
+        cv.pad = (uint32_t)(ksize - 1 - pad);
+        cv.div_kk = make_fastdiv((uint32_t)kk);
+        cv.div_k = make_fastdiv((uint32_t)ksize);
+        cv.div_wo = make_fastdiv((uint32_t)width);
+        cv.s1 = width % 4 == 0 && wo % 4 == 0 && aligned16(delta);
+        const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
+        g.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
+        g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
+        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
+        constexpr const char *kName = "convolution_data_gradient";
+        for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
+            const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
+            GemmArgs gz = g;
+            gz.b = delta + z0 * m * npos;
+            gz.c = input_delta + z0 * in_group;
+            DKZ_TRY(cv.s1 ? launch_fwd<kS1>(kName, gz, zc, big) : launch_fwd<kGa>(kName, gz, zc, big));
+        }
+        return 0;
+    }
+    // Strided (or pad >= ksize): the im2col of delta would have holes between
+    // the strided outputs, so the layer's two steps stay, batched over as many
+    // images as the scratch holds: col(i) = weights(j)^T x delta(i, j) for a
+    // run of images into the scratch (beta 0), then col2im of each into its
+    // image -- the same multiply-adds as the per-image loop, in fewer launches.
+    const uint64_t col_floats = kw * npos;
+    DKZ_REQUIRE(col_floats <= sc.gemm_floats);
+    uint64_t per = sc.gemm_floats / col_floats;
+    if (per > (uint64_t)batch) per = batch;
+    if (per > 65535) per = 65535;
+    g.m = (uint32_t)kw;
+    g.n = (uint32_t)npos;
+    g.k = (uint32_t)m;
+    g.k_chunk = (uint32_t)m;
+    g.lda = (uint32_t)kw;
+    g.ldb = (uint32_t)npos;
+    g.ldc = (uint32_t)npos;
+    g.beta = 0.0f;
+    g.zgroups = 1;
+    g.a_z = 0;
+    g.b_z = (uint32_t)((uint64_t)groups * m * npos);  // image i + 1 of the same group
+    g.c_z = (uint32_t)col_floats;
+    g.vec_a = aligned16(weights) && kw % 4 == 0;
+    g.vec_b = aligned16(delta) && npos % 4 == 0 && (m * npos) % 4 == 0;
+    g.c = sc.gemm;
+    for (int j = 0; j < groups; ++j) {
+        for (uint64_t i0 = 0; i0 < (uint64_t)batch; i0 += per) {
+            const uint32_t ic = (uint32_t)((uint64_t)batch - i0 < per ? (uint64_t)batch - i0 : per);
+            const bool big = kw >= 128 && (uint64_t)div_up(kw, 128) * div_up(npos, 128) * ic >= 2 * kCus;
+            GemmArgs gz = g;
+            gz.tiles_m = (uint32_t)div_up(kw, big ? 128 : 64);
+            gz.tiles_n = (uint32_t)div_up(npos, big ? 128 : 64);
+            gz.a = weights + (uint64_t)j * m * kw;
+            gz.b = delta + (i0 * groups + j) * m * npos;
+            DKZ_TRY(big ? (launch_batched_tn<128, 128, 1>(gz, ic))
+                        : (launch_batched_tn<64, 64, DKZ_GEMM_SMALL_PREFETCH>(gz, ic)));
+            DKZ_TRY(col2im_images(sc.gemm, (int)cg, height, width, ksize, stride, pad,
+                                  input_delta + (i0 * groups + j) * in_group, ic, col_floats,
+                                  (uint64_t)groups * in_group));
+        }
     }
     return 0;
 }

@@ -401,6 +401,15 @@ def convolutionWeightGradient(
           "convolution_weight_gradient")
 
 
+def convolutionDataGradient(
+    batch: int, groups: int, channels: int, height: int, width: int, filters: int, ksize: int, stride: int,
+    pad: int, weights: Buf, delta: Buf, input_delta: Buf,
+) -> None:  # the data-gradient gemms and col2im of layers/convolutional.zig:299-305 in one call
+    _must(_lib.load().dkz_convolution_data_gradient(batch, groups, channels, height, width, filters, ksize, stride,
+                                                    pad, _p(weights), _p(delta), _p(input_delta)),
+          "convolution_data_gradient")
+
+
 def dropout(input: Buf, size: int, rand_buf: Buf, prob: float, scale: float) -> None:  # gpu.zig:769
     _must(_lib.load().dkz_dropout(_p(input), size, _p(rand_buf), prob, scale), "dropout")
 

@@ -273,6 +273,15 @@ inline void convolutionWeightGradient(size_t batch, size_t groups, size_t channe
          "convolution_weight_gradient");
 }
 
+// The data-gradient gemms and col2im of layers/convolutional.zig:299-305 in one call.
+inline void convolutionDataGradient(size_t batch, size_t groups, size_t channels, size_t height, size_t width,
+                                    size_t filters, size_t ksize, size_t stride, size_t pad, Buf weights, Buf delta,
+                                    Buf input_delta) {
+    must(dkz_convolution_data_gradient(ci(batch), ci(groups), ci(channels), ci(height), ci(width), ci(filters),
+                                       ci(ksize), ci(stride), ci(pad), weights.f(), delta.f(), input_delta.f()),
+         "convolution_data_gradient");
+}
+
 // ---- pooling, dropout, shortcut, adam (gpu.zig:725-830) --------------------------
 
 inline void forwardMaxpool(size_t out_n, size_t in_h, size_t in_w, size_t in_c, size_t stride, size_t size,

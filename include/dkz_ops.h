@@ -348,6 +348,22 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
                                     int ksize, int stride, int pad, const float *delta, const float *input,
                                     float *weight_updates);
 
+/* The data-gradient half of a convolutional layer's backward loop
+ * (layers/convolutional.zig:299-305, per image gemm(true, false, ...) into the
+ * workspace with beta 0 and col2im into the previous layer's delta) in one
+ * call: with m, n, k and the offsets as in dkz_convolution_forward and
+ * input_delta(i, j) = input_delta + (i*groups + j)*(channels/groups)*height*width,
+ *     ksize == 1: input_delta(i, j) = weights(j)^T x delta(i, j), written as
+ *                 a k x n matrix (the layer's beta-0 gemm straight into it);
+ *     otherwise:  input_delta(i, j) += col2im(weights(j)^T x delta(i, j)).
+ * Results agree with the per-image calls within fp32 summation error. Uses
+ * the library's scratch (32 Mi floats) for the flipped weights or, with
+ * stride > 1 or pad >= ksize, the column buffers of as many images as fit
+ * (one must: ksize^2*channels/groups*out_h*out_w floats); no workspace. */
+int dkz_convolution_data_gradient(int batch, int groups, int channels, int height, int width, int filters,
+                                  int ksize, int stride, int pad, const float *weights, const float *delta,
+                                  float *input_delta);
+
 /* gpu.zig:769 dropout(input, size, rand, prob, scale): input[i] = rand[i] < prob ?
  * 0 : input[i] * scale, the rule of layers/misc.zig:105-127 (forward after
  * randUniform, and backward on the delta with the same draws). */

@@ -94,3 +94,23 @@ def assert_r5(got: np.ndarray, cpu: np.ndarray, ref64: np.ndarray, name: str) ->
         "max_rel_gpu_vs_f64": float(np.max(np.abs(got64 - ref) / scale)),
         "max_rel_cpu_vs_f64": float(np.max(np.abs(cpu64 - ref) / scale)),
     }
+
+
+def col2im64(col: np.ndarray, channels: int, height: int, width: int, ksize: int, stride: int,
+             pad: int) -> np.ndarray:
+    """col2im (im2col.zig:51-79) in f64 into a zero image: every column entry
+    (c, kh, kw, h, w) added to image element (c, h*stride + kh - pad,
+    w*stride + kw - pad) when that lies inside the image. For fixed (kh, kw)
+    the targets are distinct, so each tap is one vectorised add."""
+    ho = (height + 2 * pad - ksize) // stride + 1
+    wo = (width + 2 * pad - ksize) // stride + 1
+    colr = np.asarray(col, np.float64).reshape(channels, ksize, ksize, ho, wo)
+    im = np.zeros((channels, height, width))
+    for kh in range(ksize):
+        ys = kh - pad + stride * np.arange(ho)
+        vy = (ys >= 0) & (ys < height)
+        for kw in range(ksize):
+            xs = kw - pad + stride * np.arange(wo)
+            vx = (xs >= 0) & (xs < width)
+            im[:, ys[vy][:, None], xs[vx][None, :]] += colr[:, kh, kw][:, vy][:, :, vx]
+    return im.ravel()

@@ -1,7 +1,8 @@
-"""dkz_convolution_forward and dkz_convolution_weight_gradient: the
-per-image im2col + gemm loops of a convolutional layer's forward
-(layers/convolutional.zig:240-260) and weight gradient (:288-297) as single
-products, the im2col operand gathered inside them.
+"""dkz_convolution_forward, dkz_convolution_weight_gradient and
+dkz_convolution_data_gradient: the per-image im2col + gemm (+ col2im) loops
+of a convolutional layer's forward (layers/convolutional.zig:240-260),
+weight gradient (:288-297) and data gradient (:299-305) as single products,
+the im2col operand (of the input, or of delta) gathered inside them.
 
 Reference per image i and group j: the oracle's im2col of the image (a copy,
 bit-exact) times the group's weights in f64, added to the output's previous
@@ -17,7 +18,7 @@ import pytest
 
 from darknet_zig_amd import gpu
 from oracle import ref
-from tests.helpers import down, rng, up
+from tests.helpers import col2im64, down, rng, up
 
 pytestmark = pytest.mark.gpu
 
@@ -202,4 +203,99 @@ def test_convolution_weight_gradient_matches_per_image_calls(dev):
     a, b = down(fused, np.empty(F * k, np.float32)), down(loop, np.empty(F * k, np.float32))
     assert np.array_equal(a, b)
     for buf in (dx, dd, fused, loop, ws):
+        gpu.free(buf)
+
+
+DG_CASES = [
+    # batch, groups, channels, height, width, filters, ksize, stride, pad
+    (2, 1, 16, 16, 16, 32, 3, 1, 1),    # stride 1, pad < ksize, widths % 4 == 0: two-block gathers of delta
+    (3, 1, 5, 9, 11, 7, 3, 1, 1),       # stride 1, odd widths: per-element gathers
+    (3, 2, 8, 10, 12, 6, 3, 2, 1),      # groups, stride 2: gemm into the scratch, then col2im
+    (2, 1, 3, 8, 8, 4, 5, 1, 4),        # pad >= ksize: the same with stride 1
+    (2, 1, 4, 13, 13, 6, 2, 2, 0),      # even window, stride 2
+    (10, 1, 64, 160, 160, 8, 3, 2, 1),  # stride 2, two runs of images through the scratch (9 fit)
+    (2, 3, 9, 7, 5, 6, 3, 1, 2),        # three groups, odd widths
+    (4, 1, 16, 24, 24, 128, 3, 1, 1),   # 128 filters: k = 1152
+    (24, 1, 128, 56, 56, 8, 3, 1, 1),   # 128 input channels: 128x128 tiles (600 of them)
+    (2, 1, 4, 9, 9, 5, 1, 1, 0),        # ksize 1: overwritten (beta 0)
+    (1, 1, 3, 8, 8, 4, 1, 2, 0),        # ksize 1, stride 2: the k x n view, a prefix of the image
+    (3, 2, 6, 5, 7, 10, 1, 1, 0),       # ksize 1, groups
+]
+
+
+def _dgrad_reference(case, w, d, im0):
+    batch, groups, C, H, W, F, ks, s, p = case
+    cg, m = C // groups, F // groups
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    n, k = ho * wo, ks * ks * cg
+    in_group = cg * H * W
+    want = im0.astype(np.float64).copy()
+    bound = np.abs(want)
+    for i in range(batch):
+        for j in range(groups):
+            z = i * groups + j
+            wj = w[j * m * k:(j + 1) * m * k].reshape(m, k).astype(np.float64)
+            dz = d[z * m * n:(z + 1) * m * n].reshape(m, n).astype(np.float64)
+            col, acol = wj.T @ dz, np.abs(wj).T @ np.abs(dz)
+            sl = slice(z * in_group, (z + 1) * in_group)
+            if ks == 1:  # the layer's beta-0 gemm straight into the image, as a k x n matrix
+                want[z * in_group:z * in_group + k * n] = col.ravel()
+                bound[z * in_group:z * in_group + k * n] = acol.ravel()
+            else:
+                want[sl] += col2im64(col, cg, H, W, ks, s, p)
+                bound[sl] += col2im64(acol, cg, H, W, ks, s, p)
+    terms = m * ks * ks + 1  # every product of every tap, plus the image's value
+    g = (terms + 3) * U / (1 - (terms + 3) * U)
+    return want, g * bound
+
+
+@pytest.mark.parametrize("case", DG_CASES, ids=str)
+def test_convolution_data_gradient(dev, case):
+    batch, groups, C, H, W, F, ks, s, p = case
+    r = rng(sum(case) + 2)
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    w = r.uniform(-1, 1, F * (C // groups) * ks * ks).astype(np.float32)
+    d = r.uniform(-1, 1, batch * F * ho * wo).astype(np.float32)
+    im0 = r.uniform(-1, 1, batch * C * H * W).astype(np.float32)
+    want, bd = _dgrad_reference(case, w, d, im0)
+    dw, dd, di = up(w), up(d), up(im0)
+    gpu.convolutionDataGradient(batch, groups, C, H, W, F, ks, s, p, dw, dd, di)
+    got = down(di, im0).astype(np.float64)
+    err = np.abs(got - want)
+    bad = ~(err <= bd)
+    assert not bad.any(), (f"data gradient {case}: {int(bad.sum())} beyond the fp32 bound; "
+                           f"max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}")
+    for b in (dw, dd, di):
+        gpu.free(b)
+
+
+@pytest.mark.parametrize("case", [(5, 1, 8, 12, 12, 16, 3, 1, 1), (4, 2, 6, 11, 9, 8, 3, 2, 1),
+                                  (3, 1, 8, 10, 10, 12, 1, 1, 0)], ids=str)
+def test_convolution_data_gradient_matches_per_image_calls(dev, case):
+    """The layer's per-image calls (gemm(true, false, ..., beta 0) into the
+    workspace, then col2im into the image; for ksize 1 the gemm straight into
+    the image) and the one call agree exactly on integer-valued inputs, where
+    every summation order is exact."""
+    batch, groups, C, H, W, F, ks, s, p = case
+    cg, m = C // groups, F // groups
+    ho, wo = ref.conv_out_dim(H, ks, s, p), ref.conv_out_dim(W, ks, s, p)
+    n, k, in_group = ho * wo, ks * ks * cg, cg * H * W
+    r = rng(sum(case))
+    w = r.integers(-3, 4, F * k).astype(np.float32)
+    d = r.integers(-3, 4, batch * F * n).astype(np.float32)
+    im0 = r.integers(-3, 4, batch * C * H * W).astype(np.float32)
+    dw, dd = up(w), up(d)
+    fused, loop = up(im0), up(im0)
+    gpu.convolutionDataGradient(batch, groups, C, H, W, F, ks, s, p, dw, dd, fused)
+    ws = gpu.alloc(k * n)
+    for i in range(batch):
+        for j in range(groups):
+            z = i * groups + j
+            dst = loop.offset(z * in_group) if ks == 1 else ws
+            gpu.gemm(True, False, k, n, m, 1.0, dw.offset(j * m * k), k, dd.offset(z * m * n), n, 0.0, dst, n)
+            if ks != 1:
+                gpu.col2im(ws, cg, H, W, ks, s, p, loop.offset(z * in_group))
+    a, b = down(fused, im0), down(loop, im0)
+    assert np.array_equal(a, b)
+    for buf in (dw, dd, fused, loop, ws):
         gpu.free(buf)
