@@ -88,6 +88,10 @@ struct ConvB {
     uint32_t npos;
     FastDiv div_npos;
     uint32_t a_img, b_img, npos4, a_vec, b_vec;  // a_vec / b_vec: delta / input 16-byte aligned
+    // Products whose columns run over (image, position) (kSpan): C's element
+    // stride from one image to the next; B's is b_img, the positions per
+    // image npos.
+    uint32_t c_img;
 };
 
 struct GemmArgs {
@@ -251,11 +255,44 @@ __device__ __forceinline__ float4 conv_col4(const float *img, const ConvB &cv, u
     }
 }
 
+// Columns q .. q+avail-1 of the im2col over (image, position) pairs, npos
+// positions per image, images b_img apart: one image's conv_col4 when npos
+// % 4 == 0 (!ODD; kTwoBlock needs it), else element by element, the tap
+// decomposed once and (image, position) stepped along.
+template <int MODE, bool ODD>
+__device__ __forceinline__ float4 conv_span4(const float *img0, const ConvB &cv, uint32_t kidx, uint32_t q,
+                                             uint32_t avail) {
+    uint32_t i = fdiv(q, cv.div_npos), p = q - i * cv.npos;
+    if constexpr (!ODD) return conv_col4<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, p, avail);
+    static_assert(!ODD || MODE != kTwoBlock, "two-block gathers need npos % 4 == 0");
+    float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (MODE == kRaw) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (j < avail) ::dkz::lane(out, j) = img0[(size_t)i * cv.b_img + kidx * cv.npos + p];
+            if (++p == cv.npos) p = 0, ++i;
+        }
+    } else {
+        const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
+        const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
+            const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
+            const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
+            if (j < avail && y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W)
+                ::dkz::lane(out, j) = img0[(size_t)i * cv.b_img + (c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x];
+            if (++p == cv.npos) p = 0, ++i;
+        }
+    }
+    return out;
+}
+
 // The implicit im2col operand's slab. ROWK false: B of the forward product
 // (rows along k = kidx, the positions contiguous). ROWK true: B of the weight
 // gradient, transposed (rows along the tile dimension = kidx, k = image *
 // npos + position). Same layouts and LDS stores as the ordinary slabs.
-template <int R, bool ROWK, int MODE>
+template <int R, bool ROWK, int MODE, int SPAN = 0>  // SPAN: 0 no, 1 npos % 4 == 0, 2 any npos
 struct ConvSlab : Slab<R, ROWK> {
     using Slab<R, ROWK>::kLoads;
     using Slab<R, ROWK>::v;
@@ -267,11 +304,16 @@ struct ConvSlab : Slab<R, ROWK> {
         for (int l = 0; l < kLoads; ++l) {
             const int f = tid + l * kBlock;
             float4 out = zero;
-            if constexpr (!ROWK) {
+            if constexpr (!ROWK && SPAN == 0) {
                 const uint32_t kr = f % kBK, rr = 4 * (f / kBK);
                 const uint32_t kidx = k0 + kr;
                 if (kidx < kend && rr < rows)
                     out = conv_col4<MODE>(img0, cv, kidx, r0 + rr, rows - rr < 4 ? rows - rr : 4);
+            } else if constexpr (!ROWK) {
+                const uint32_t kr = f % kBK, rr = 4 * (f / kBK);
+                const uint32_t kidx = k0 + kr;
+                if (kidx < kend && rr < rows)
+                    out = conv_span4<MODE, SPAN == 2>(img0, cv, kidx, r0 + rr, rows - rr < 4 ? rows - rr : 4);
             } else {
                 const uint32_t r = f / (kBK / 4), kk = k0 + 4 * (f % (kBK / 4));
                 if (r < rows && kk < kend) {
@@ -336,14 +378,19 @@ struct SegSlab : Slab<R, true> {
 // IM: a convolution's operands. kFwd + mode: B of an NN product is the
 // implicit im2col of the image; kWgrad + mode: the weight gradient, an NT
 // product whose A is delta and whose B is the im2col, k running over image
-// and position (modes: kRaw, kGather, kTwoBlock). Each workgroup row z =
-// blockIdx.y computes its own product (see GemmArgs).
-constexpr int kImNone = -1, kFwd = 0, kWgrad = 8;
+// and position; kSpan + mode: as kFwd, but the columns run over (image,
+// position) of every image, so small images fill whole tiles (kSpanOdd: the
+// positions per image are not a multiple of 4) (modes: kRaw, kGather,
+// kTwoBlock). Each workgroup row z = blockIdx.y computes its own product
+// (see GemmArgs).
+constexpr int kImNone = -1, kFwd = 0, kWgrad = 8, kSpan = 16, kSpanOdd = 24;
 
 template <int BM, int BN, bool TA, bool TB, int D, int IM = kImNone>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
-    constexpr bool kWg = IM >= kWgrad;
-    constexpr int kMode = IM == kImNone ? 0 : kWg ? IM - kWgrad : IM - kFwd;
+    constexpr bool kWg = IM >= kWgrad && IM < kSpan;
+    constexpr bool kSp = IM >= kSpan;
+    constexpr int kSpanKind = IM >= kSpanOdd ? 2 : kSp ? 1 : 0;
+    constexpr int kMode = IM == kImNone ? 0 : IM % 8;
     static_assert(IM == kImNone || (!TA && TB == kWg), "forward: NN; weight gradient: NT");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     // A wave with fewer than four 32x32 blocks spreads each block's MFMAs over
@@ -368,7 +415,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     const int half = lane >> 5, l32 = lane & 31;
 
     std::conditional_t<kWg, SegSlab<BM>, Slab<BM, !TA>> sa[D];
-    std::conditional_t<IM != kImNone, ConvSlab<BN, kWg, kMode>, Slab<BN, TB>> sb[D];
+    std::conditional_t<IM != kImNone, ConvSlab<BN, kWg, kMode, kSpanKind>, Slab<BN, TB>> sb[D];
     auto load_a = [&](auto &slab, uint32_t k0) {
         if constexpr (kWg) slab.load_seg(ga, g.cv, m0, rows_a, k0, kend, tid);
         else slab.load(ga, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
@@ -465,6 +512,11 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
         for (int tj = 0; tj < TN; ++tj) {
             const uint32_t j = n0 + wn0 + tj * 32 + l32;
             if (j >= g.n) continue;
+            float *ccol = gc + j;  // column j of C
+            if constexpr (kSp) {
+                const uint32_t img = fdiv(j, g.cv.div_npos);
+                ccol = gc + (size_t)img * g.cv.c_img + (j - img * g.cv.npos);
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t i = m0 + wm0 + ti * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
@@ -472,7 +524,7 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 if (g.splits > 1) {
                     g.partial[((size_t)split * g.m + i) * g.n + j] = acc[0][ti][tj][r];
                 } else {
-                    float *cp = gc + i * g.ldc + j;
+                    float *cp = ccol + i * g.ldc;
                     float cv = 0.0f;
                     if (g.beta != 0.0f) cv = (g.beta == 1.0f) ? *cp : *cp * g.beta;
                     *cp = cv + g.alpha * acc[0][ti][tj][r];
@@ -583,6 +635,46 @@ template <int IM>
 int launch_fwd(const char *name, const GemmArgs &g, uint32_t zcount, bool big) {
     if (big) return launch_batched<128, 128, 1, IM>(name, g, zcount);
     return launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, IM>(name, g, zcount);
+}
+
+// Columns over (image, position) of all `batch` images (kSpan), in 64x64
+// tiles: g holds one image's product per group (z = group); B and C advance
+// b_img and c_img elements per image. Measured against per-image tiles:
+// [64,512,14,14]->512 3x3 forward 1132 -> 975 us, [64,1024,13,13]->1024
+// 3324 -> 2642 us (data gradients alike), while with a fifth or less of
+// the last tile empty ([64,256,28,28]->256, 26x26) the per-image 128x128
+// tiles stay 3-5% ahead; 128x128 tiles over (image, position) were slower
+// than either (too few workgroups, and the per-tap gather spills).
+#ifndef DKZ_CONV_SPAN
+#define DKZ_CONV_SPAN 1
+#endif
+
+// Whether per-image column tiles of bn leave more than a fifth of their
+// columns past the image's n positions.
+inline bool span_pays(uint64_t n, uint64_t bn) {
+    const uint64_t t = (uint64_t)div_up(n, bn) * bn;
+    return (t - n) * 5 > t;
+}
+
+template <int MODE>
+int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, uint64_t b_img, uint64_t c_img) {
+    const uint32_t npos = g.n;
+    g.n = batch * npos;
+    g.tiles_m = div_up(g.m, 64);
+    g.tiles_n = div_up(g.n, 64);
+    g.cv.npos = npos;
+    g.cv.div_npos = make_fastdiv(npos);
+    g.cv.npos4 = npos % 4 == 0;
+    g.cv.b_img = (uint32_t)b_img;
+    g.cv.c_img = (uint32_t)c_img;
+    constexpr int D = DKZ_GEMM_SMALL_PREFETCH;
+    if (npos % 4 == 0) return launch_batched<64, 64, D, kSpan + MODE>(name, g, groups);
+    if constexpr (MODE == kTwoBlock) {
+        DKZ_REQUIRE(npos % 4 == 0);  // two-block gathers are chosen only then
+        return 0;
+    } else {
+        return launch_batched<64, 64, D, kSpanOdd + MODE>(name, g, groups);
+    }
 }
 
 // The weight gradient's NT product (BM x BM tiles, K split into ranges),
@@ -753,6 +845,16 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
     const bool big = m >= 128 && (uint64_t)div_up(m, 128) * div_up(n, 128) * zcount >= 2 * kCus;
     g.tiles_m = (uint32_t)div_up(m, big ? 128 : 64);
     g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
+    // Small images (the last column tile of each mostly empty): one product
+    // per group with columns over every image's positions.
+    if (DKZ_CONV_SPAN && batch > 1 && span_pays(n, big ? 128 : 64)) {
+        constexpr const char *kName = "convolution_forward";
+        const uint64_t b_img = (uint64_t)groups * in_group, c_img = (uint64_t)groups * m * n;
+        g.cv.b_vec = g.vec_b;  // ksize 1: float4 rows of the input matrix
+        if (!im) return launch_span<kRaw>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+        if (g.cv.s1) return launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+        return launch_span<kGather>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+    }
     // At most 65535 grid rows per launch, whole images each (a multiple of
     // groups), so that every launch starts at group 0.
     const uint64_t chunk = 65535 - 65535 % (uint64_t)groups;
@@ -858,6 +960,8 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
                        (uint32_t)at_floats));
         const uint64_t n = (uint64_t)height * width, k = m * kk;
         g.a = sc.gemm;
+        g.b = delta;
+        g.c = input_delta;
         g.m = (uint32_t)cg;
         g.n = (uint32_t)n;
         g.k = (uint32_t)k;
@@ -884,6 +988,11 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
         constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
         constexpr const char *kName = "convolution_data_gradient";
+        if (DKZ_CONV_SPAN && batch > 1 && span_pays(n, big ? 128 : 64)) {
+            const uint64_t b_img = (uint64_t)groups * m * npos, c_img = (uint64_t)groups * in_group;
+            return cv.s1 ? launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img)
+                         : launch_span<kGather>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+        }
         for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
             const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
             GemmArgs gz = g;

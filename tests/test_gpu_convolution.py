@@ -36,6 +36,17 @@ CASES = [
     (2, 1, 3, 8, 8, 4, 5, 1, 4),       # pad 4: whole blocks outside a row
     (2, 3, 9, 7, 5, 6, 3, 1, 2),       # three groups, odd widths
     (1, 1, 1, 3, 4, 1, 3, 1, 1),       # one channel, one filter
+    # small images (over a fifth of the last column tile empty): 64x64 tiles
+    # whose columns run over every image's positions -- two-block, per-tap,
+    # odd positions per image, ksize 1
+    (6, 1, 8, 12, 12, 16, 3, 1, 1),
+    (8, 1, 16, 14, 14, 32, 3, 1, 1),
+    (5, 1, 8, 9, 9, 24, 3, 1, 1),
+    (4, 1, 8, 12, 12, 16, 1, 1, 0),
+    (3, 2, 6, 7, 7, 10, 1, 1, 0),
+    (64, 1, 8, 14, 14, 512, 3, 1, 1),  # 512 filters (128x128 tiles per image would leave 23% empty)
+    (64, 1, 8, 13, 13, 512, 3, 1, 1),  # the same, 169 positions per image
+    (4, 1, 8, 13, 13, 24, 3, 1, 1),    # 169 positions, 64x64 tiles per image (12% empty): per image
 ]
 
 
@@ -217,6 +228,9 @@ DG_CASES = [
     (2, 3, 9, 7, 5, 6, 3, 1, 2),        # three groups, odd widths
     (4, 1, 16, 24, 24, 128, 3, 1, 1),   # 128 filters: k = 1152
     (24, 1, 128, 56, 56, 8, 3, 1, 1),   # 128 input channels: 128x128 tiles (600 of them)
+    (6, 1, 8, 12, 12, 16, 3, 1, 1),     # small images: columns over every image's positions, two-block
+    (64, 1, 512, 14, 14, 8, 3, 1, 1),   # the same for 512 channels, per-tap gathers
+    (7, 2, 6, 9, 9, 8, 3, 1, 1),        # 81 positions per image, groups
     (2, 1, 4, 9, 9, 5, 1, 1, 0),        # ksize 1: overwritten (beta 0)
     (1, 1, 3, 8, 8, 4, 1, 2, 0),        # ksize 1, stride 2: the k x n view, a prefix of the image
     (3, 2, 6, 5, 7, 10, 1, 1, 0),       # ksize 1, groups

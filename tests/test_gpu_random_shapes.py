@@ -3,9 +3,11 @@ at each op family's parity bar: the per-channel ops and the fused batch-norm
 passes over random (batch, filters, spatial) -- every residue of spatial mod
 4, filters on both sides of the one-launch/split thresholds, ragged last
 chunks --, elementwise ops over random lengths and misaligned views, the
-convolution lowering over random geometries, and the GEMM over random
-shapes, transposes and leading dimensions. The shapes are drawn once from a
-fixed seed, so a failure names a reproducible case."""
+convolution lowering over random geometries, the GEMM over random shapes,
+transposes and leading dimensions, and the whole-batch convolution forward,
+weight gradient and data gradient over random layers (groups, ksize, stride,
+pad). The shapes are drawn once from a fixed seed, so a failure names a
+reproducible case."""
 
 from __future__ import annotations
 
@@ -17,6 +19,7 @@ from darknet_zig_amd.activations import Activation
 from oracle import ref
 from tests.helpers import assert_bitexact, assert_r5, chan_f32, chan_sum64, down, normal, rng, uniform, up
 from tests.test_gpu_batchnorm_fused import _backward_case, _forward_case
+from tests.test_gpu_convolution import _dgrad_reference as dgrad_reference
 from tests.test_gpu_convolution import _reference as conv_reference
 from tests.test_gpu_convolution import _wgrad_reference as wgrad_reference
 from tests.test_gpu_gemm import check as gemm_check
@@ -200,5 +203,11 @@ def test_convolution_layer(dev, case):
     gpu.convolutionWeightGradient(batch, groups, C, H, W, F, ks, s, p, dd, dx, du)
     err = np.abs(down(du, wu0).astype(np.float64) - want)
     assert (err <= bd).all(), f"weight gradient {case}: max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}"
-    for b in (dx, dw, dd, do, du):
+    im0 = uniform(r, batch * C * H * W)
+    di = up(im0)
+    want, bd = dgrad_reference(case, w, d, im0)
+    gpu.convolutionDataGradient(batch, groups, C, H, W, F, ks, s, p, dw, dd, di)
+    err = np.abs(down(di, im0).astype(np.float64) - want)
+    assert (err <= bd).all(), f"data gradient {case}: max err/bound {float(np.max(err / np.maximum(bd, 1e-300))):.3g}"
+    for b in (dx, dw, dd, do, du, di):
         gpu.free(b)
