@@ -151,6 +151,23 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, P, 3, P, 5, 0.0, P, 4), INVALID),  # ldc < n
         (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, None, 3, P, 5, 0.0, P, 5), INVALID),
         (lambda L: L.dkz_gemm(0, 0, 65536, 65536, 3, 1.0, P, 3, P, 65536, 0.0, P, 65536), INVALID),  # > 2^31
+        # the three convolution entry points share their shape checks
+        *[(lambda L, f=f, a=a, ptrs=ptrs: getattr(L, f)(*a, *ptrs), want)
+          for f in ("dkz_convolution_forward", "dkz_convolution_weight_gradient", "dkz_convolution_data_gradient")
+          for a, ptrs, want in (
+              ((2, 0, 4, 8, 8, 4, 3, 1, 1), (P, P, P), INVALID),  # groups 0
+              ((2, 3, 4, 8, 8, 6, 3, 1, 1), (P, P, P), INVALID),  # channels % groups != 0
+              ((2, 2, 4, 8, 8, 5, 3, 1, 1), (P, P, P), INVALID),  # filters % groups != 0
+              ((2, 1, 4, 8, 8, 6, 0, 1, 1), (P, P, P), INVALID),  # ksize 0
+              ((2, 1, 4, 8, 8, 6, 3, 0, 1), (P, P, P), INVALID),  # stride 0
+              ((2, 1, 4, 8, 8, 6, 3, 1, -1), (P, P, P), INVALID),  # pad < 0
+              ((2, 1, 4, 2, 2, 6, 7, 1, 1), (P, P, P), INVALID),  # window larger than the padded image
+              ((2, 1, 4, 8, 8, 6, 1, 1, 1), (P, P, P), INVALID),  # ksize 1 reading past the image (n > h*w)
+              ((2, 1, 4, 8, 8, 6, 3, 1, 1), (None, P, P), INVALID),
+              ((2, 1, 4, 8, 8, 6, 3, 1, 1), (P, P, None), INVALID),
+              ((65536, 1, 1, 256, 256, 1, 1, 1, 0), (P, P, P), INVALID),  # beyond 32-bit indexing
+              ((0, 1, 4, 8, 8, 6, 3, 1, 1), (None, None, None), 0),  # no images: nothing to do
+          )],
         (lambda L: L.dkz_softmax_layer_forward(2, 10, 3, 1.0, P, P, P, P, P), INVALID),  # 10 % 3 != 0
         (lambda L: L.dkz_softmax_layer_forward(0, 10, 2, 1.0, None, None, None, None, None), 0),
         (lambda L: L.dkz_softmax_layer_forward(2, 100, 1, 1.0, P, P, P, None, P), INVALID),  # truth without delta
