@@ -47,6 +47,11 @@ CASES = [
     (64, 1, 8, 14, 14, 512, 3, 1, 1),  # 512 filters (128x128 tiles per image would leave 23% empty)
     (64, 1, 8, 13, 13, 512, 3, 1, 1),  # the same, 169 positions per image
     (4, 1, 8, 13, 13, 24, 3, 1, 1),    # 169 positions, 64x64 tiles per image (12% empty): per image
+    # stride 2, even and odd windows, per image and over (image, position)
+    (2, 1, 8, 16, 16, 16, 3, 2, 1),
+    (2, 1, 4, 16, 16, 8, 2, 2, 0),
+    (2, 1, 4, 16, 16, 8, 5, 2, 2),
+    (6, 1, 8, 24, 24, 16, 3, 2, 1),    # ... over (image, position) columns
 ]
 
 
@@ -140,6 +145,8 @@ WG_CASES = [
     (5, 1, 8, 7, 7, 16, 3, 1, 1),      # 49 positions: per-element loads across image boundaries
     (64, 1, 16, 28, 28, 32, 3, 1, 1),  # many images: the product split over image ranges
     (2, 3, 9, 7, 5, 6, 3, 1, 2),       # three groups, odd widths
+    (3, 1, 8, 16, 16, 16, 3, 2, 1),    # stride 2
+    (2, 2, 8, 16, 16, 8, 5, 2, 2),     # the same, 5x5, groups
     (4, 1, 8, 20, 20, 96, 3, 1, 1),    # 96 filters: 64x64 tiles, a partial row tile
     (4, 1, 16, 24, 24, 128, 3, 1, 1),  # 128x128 tiles
     (3, 1, 8, 17, 17, 160, 3, 2, 1),   # 128x128 tiles, stride 2, a partial row tile
