@@ -44,8 +44,10 @@ Algorithmic bytes count every logical fp32/int32 element read or written once
 (4 B); per-channel vectors of C floats are not counted.
 
 --per-op-traffic runs each per-op row's first three launches once between two
-marker dispatches and prints the rows, for a rocprofv3 FETCH_SIZE/WRITE_SIZE
-run to attribute HBM traffic per row (profiles/traffic_per_op.md);
+marker dispatches (after one untimed pass over all its rotations) and prints
+the rows, for
+rocprofv3 FETCH_SIZE/WRITE_SIZE runs and a kernel trace to attribute HBM
+traffic and kernel time per row (profiles/traffic_per_op.md);
 --copy-calibration runs the known-size copy that scales those counters.
 """
 
@@ -291,11 +293,15 @@ def gbs(nbytes: int, ms: float) -> float:
 
 
 # Traffic mode: a row's launches sit between two marker dispatches -- a fill
-# of a misaligned buffer, which runs the one-lane-per-element fill kernel on
-# exactly MARK_BASE + 2*row (+1 for the end) workgroups of 256 -- so that a
-# counter profile (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) can attribute every
-# dispatch to its row from the dispatch order and grid sizes alone.
-MARK_BASE = 50000
+# of a misaligned buffer (no row fills one), which runs the one-lane-per-
+# element fill kernel on exactly MARK_BASE + 2*row (+1 for the end)
+# workgroups of 256, about 1 MB -- so that a profile (rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE, or a kernel trace) can attribute every dispatch to
+# its row from the dispatch order and grid sizes alone. Every rotation runs
+# once, untimed, before the begin marker: the traced passes then find their
+# pages mapped (as in a stream of such calls) but their data, at least
+# 512 MB back, out of the 256 MB Infinity Cache.
+MARK_BASE = 1000
 TRAFFIC_PASSES = 3
 
 
@@ -315,6 +321,9 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     def traced(cfg, name, nbytes, seqs):
         i = len(traffic)
         passes = min(TRAFFIC_PASSES, len(seqs))
+        for seq in seqs:
+            for fn in seq:
+                fn()
         hip.sync()
         marker(MARK_BASE + 2 * i)
         for seq in seqs[:passes]:
