@@ -53,6 +53,12 @@ constexpr int kXcds = 8;
 #define DKZ_GEMM_SMALL_PREFETCH 2
 #endif
 
+// Unchecked float4 loads for slabs wholly inside the matrix (build-time
+// switch, for measurement).
+#ifndef DKZ_GEMM_FULL_SLABS
+#define DKZ_GEMM_FULL_SLABS 1
+#endif
+
 // Workgroups per CU that a split-K grid aims for (build-time tunable).
 #ifndef DKZ_GEMM_SPLIT_TARGET
 #define DKZ_GEMM_SPLIT_TARGET 2
@@ -163,6 +169,22 @@ struct Slab {
     // k and the end of this split's range.
     __device__ __forceinline__ void load(const float *p, uint32_t ld, uint32_t r0, uint32_t rows, uint32_t k0,
                                          uint32_t kend, bool vec, int tid) {
+        // A whole slab inside the matrix (the usual case): every float4 is
+        // there, so no per-element checks (a branch the whole workgroup takes).
+        if (DKZ_GEMM_FULL_SLABS && vec && rows >= (uint32_t)R && kend - k0 >= (uint32_t)kBK) {
+#pragma unroll
+            for (int l = 0; l < kLoads; ++l) {
+                const int f = tid + l * kBlock;
+                if constexpr (ROWK) {
+                    const uint32_t r = f / (kBK / 4), q = f % (kBK / 4);
+                    v[l] = *reinterpret_cast<const float4 *>(p + (r0 + r) * ld + k0 + 4 * q);
+                } else {
+                    const uint32_t kr = f % kBK, q = f / kBK;
+                    v[l] = *reinterpret_cast<const float4 *>(p + (k0 + kr) * ld + r0 + 4 * q);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int l = 0; l < kLoads; ++l) {
             const int f = tid + l * kBlock;  // float4 number within the slab
