@@ -65,12 +65,10 @@ constexpr int kXcds = 8;
 #endif
 
 // The weight gradient: 128x128 tiles when filters per group fill them
-// (DKZ_WGRAD_BIG), and the workgroups per CU its K split aims for.
+// (DKZ_WGRAD_BIG), and with ksize 1 the workgroups per CU its K split aims
+// for.
 #ifndef DKZ_WGRAD_BIG
 #define DKZ_WGRAD_BIG 1
-#endif
-#ifndef DKZ_WGRAD_TARGET
-#define DKZ_WGRAD_TARGET 4
 #endif
 #ifndef DKZ_WGRAD_TARGET_RAW
 #define DKZ_WGRAD_TARGET_RAW 2
@@ -339,19 +337,11 @@ struct ConvSlab : Slab<R, ROWK> {
             } else {
                 const uint32_t r = f / (kBK / 4), kk = k0 + 4 * (f % (kBK / 4));
                 if (r < rows && kk < kend) {
+                    // The four k are (image, position) pairs, like the
+                    // columns of a spanning forward product.
                     const uint32_t kidx = r0 + r, avail = kend - kk < 4 ? kend - kk : 4;
-                    if (cv.npos4) {  // the four k are one image's positions
-                        const uint32_t i = fdiv(kk, cv.div_npos);
-                        out = conv_col4<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, kk - i * cv.npos, avail);
-                    } else if constexpr (MODE != kTwoBlock) {
-#pragma unroll
-                        for (uint32_t j = 0; j < 4; ++j) {
-                            if (j >= avail) break;
-                            const uint32_t i = fdiv(kk + j, cv.div_npos);
-                            ::dkz::lane(out, j) =
-                                conv_col1<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, kk + j - i * cv.npos);
-                        }
-                    }
+                    if (cv.npos4) out = conv_span4<MODE, false>(img0, cv, kidx, kk, avail);
+                    else if constexpr (MODE != kTwoBlock) out = conv_span4<MODE, true>(img0, cv, kidx, kk, avail);
                 }
             }
             v[l] = out;
@@ -1124,31 +1114,56 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
     const bool big = DKZ_WGRAD_BIG && m >= 128;
     g.tiles_m = (uint32_t)div_up(m, big ? 128 : 64);
     g.tiles_n = (uint32_t)div_up(kw, big ? 128 : 64);
-    // Split K (image-major positions) into ranges of whole slabs, toward
-    // DKZ_WGRAD_TARGET workgroups per CU (the kernels fit four per CU; with
-    // ksize 1, whose operands stream as plain float4s, DKZ_WGRAD_TARGET_RAW)
-    // with ranges of at least DKZ_WGRAD_MIN_CHUNK, within the scratch,
-    // preferring a workgroup count that is a multiple of the XCD count (the
-    // tile mapping then keeps each range's tiles on one XCD, sharing its
-    // delta rows in L2).
+    // Split K (image-major positions) into ranges of whole slabs, of at
+    // least DKZ_WGRAD_MIN_CHUNK and within the scratch. The gathering kernels
+    // run four workgroups per CU, so workgroups come in rounds of 4 * 256: the
+    // split count is the smallest whose rounds are, within 2%, as full as the
+    // best one's (a last round a tenth full leaves CUs idle for most of a
+    // workgroup's time; measured at config 2's layer, 504 / 774 / 1008 /
+    // 1512 workgroups 827 / 769 / 696 / 739 us; [64,512,14,14]->512 1152 ->
+    // 1008 workgroups 758 -> 647 us, [64,1024,13,13]->1024 1152 -> 1728
+    // 2949 -> 2558 us), and among those the smallest whose workgroup count is
+    // a multiple of the XCD count, if any (the tile mapping then keeps each
+    // range's tiles on one XCD, sharing its delta rows in L2: 999 instead of
+    // 1008 workgroups cost 3% at config 2's layer).
+    // With ksize 1, whose operands stream as plain float4s and whose partial
+    // tiles weigh more, toward DKZ_WGRAD_TARGET_RAW workgroups per CU.
     const uint64_t tiles = (uint64_t)g.tiles_m * g.tiles_n;
     const uint64_t kt = (uint64_t)batch * npos;
-    const uint64_t target = ksize == 1 ? DKZ_WGRAD_TARGET_RAW : DKZ_WGRAD_TARGET;
-    uint64_t want = div_up(target * kCus, tiles);
     const uint64_t by_k = div_up(kt, (uint64_t)DKZ_WGRAD_MIN_CHUNK);
-    if (want > by_k) want = by_k;
     Scratch sc;
     DKZ_TRY(device_scratch(&sc));
     const uint64_t cap = sc.gemm_floats / (m * kw);
-    if (want > cap) want = cap;
-    if (want < 1) want = 1;
-    uint64_t chunk = div_up(div_up(kt, want), (uint64_t)kBK) * kBK;
-    for (uint64_t s = want; s > want / 2 && s > 1; --s) {
-        const uint64_t c = div_up(div_up(kt, s), (uint64_t)kBK) * kBK;
-        if (div_up(kt, c) * tiles % kXcds == 0) {
-            chunk = c;
-            break;
+    const uint64_t slots = (uint64_t)kCus * 4;
+    uint64_t smax = by_k < cap ? by_k : cap;
+    if (smax > 8 * slots / tiles + 1) smax = 8 * slots / tiles + 1;  // beyond eight rounds nothing changes
+    if (smax < 1) smax = 1;
+    auto chunk_of = [&](uint64_t s) { return div_up(div_up(kt, s), (uint64_t)kBK) * kBK; };
+    uint64_t chunk = chunk_of(1);
+    if (ksize == 1) {
+        uint64_t want = div_up((uint64_t)DKZ_WGRAD_TARGET_RAW * kCus, tiles);
+        if (want > smax) want = smax;
+        chunk = chunk_of(want);
+        for (uint64_t s = want; s > want / 2 && s > 1; --s) {
+            if (div_up(kt, chunk_of(s)) * tiles % kXcds == 0) {
+                chunk = chunk_of(s);
+                break;
+            }
         }
+    } else {
+        auto count = [&](uint64_t s) { return tiles * div_up(kt, chunk_of(s)); };
+        auto fill = [&](uint64_t s) {
+            const uint64_t w = count(s);
+            return (double)w / (double)(div_up(w, slots) * slots);
+        };
+        double best = 0.0;
+        for (uint64_t s = 1; s <= smax; ++s) best = fill(s) > best ? fill(s) : best;
+        uint64_t pick = 0;
+        for (uint64_t s = 1; s <= smax && pick == 0; ++s)
+            if (fill(s) >= best - 0.02 && count(s) % kXcds == 0) pick = s;
+        for (uint64_t s = 1; s <= smax && pick == 0; ++s)
+            if (fill(s) >= best - 0.02) pick = s;
+        chunk = chunk_of(pick);
     }
     g.splits = (uint32_t)div_up(kt, chunk);
     g.k_chunk = (uint32_t)chunk;
