@@ -49,12 +49,6 @@ constexpr uint64_t kScratchGemmFloats = 1ull << DKZ_SCRATCH_GEMM_LOG2;  // split
 constexpr uint32_t kScratchSlots = 1u << 12;         // channels
 int device_scratch(Scratch *out);
 
-// col2im (dkz_col2im) of `images` column buffers into as many images:
-// column buffer z at col + z*col_z adds into the image at im + z*im_z.
-// images <= 65535. Defined in im2col.hip.
-int col2im_images(const float *col, int channels, int height, int width, int ksize, int stride, int pad, float *im,
-                  uint32_t images, uint64_t col_z, uint64_t im_z);
-
 // Largest element count any op indexes with 32-bit arithmetic, as the
 // reference's kernels do (int global_index(), darknet_kernels.hip:40-42).
 constexpr uint64_t kMaxElems = 0x7fffffffull;

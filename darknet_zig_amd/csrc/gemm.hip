@@ -83,7 +83,8 @@ constexpr int kXcds = 8;
 // im2col): B[k][p] = im2col(image)[k][p] for k = (c, kh, kw) over a group's
 // channels and p = (h, w) over the output positions (im2col.zig:13-49).
 struct ConvB {
-    uint32_t H, W, Wo, ksz, stride, pad;
+    uint32_t H, W, Wo, ksz, stride;
+    int32_t pad, pad_x;  // rows and columns (negative: the window starts inside the image)
     FastDiv div_kk, div_k, div_wo;  // ksz*ksz, ksz, Wo
     uint32_t s1;  // stride 1, W % 4 == 0, Wo % 4 == 0, images 16-byte aligned
     // Weight gradient (k runs over image and position): positions per image,
@@ -96,6 +97,11 @@ struct ConvB {
     // stride from one image to the next; B's is b_img, the positions per
     // image npos.
     uint32_t c_img;
+    // Products over one phase of a strided data gradient (kPhase): column j is
+    // position (yq, xq) = (j / wp, j % wp) of the phase, i.e. input pixel
+    // (ph_s*yq + ph_py, ph_s*xq + ph_px) of an image ph_w wide.
+    FastDiv div_wp;
+    uint32_t ph_s, ph_py, ph_px, ph_w;
 };
 
 struct GemmArgs {
@@ -239,8 +245,8 @@ __device__ __forceinline__ float conv_col1(const float *img, const ConvB &cv, ui
         const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
         const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
         const uint32_t h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
-        const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
-        const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
+        const int y = (int)(h * cv.stride + kh) - cv.pad;
+        const int x = (int)(w * cv.stride + kw) - cv.pad_x;
         return y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W ? img[(c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x]
                                                                    : 0.0f;
     }
@@ -256,9 +262,9 @@ __device__ __forceinline__ float4 conv_col4(const float *img, const ConvB &cv, u
         const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
         const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
         const uint32_t h = fdiv(p0, cv.div_wo), w = p0 - h * cv.Wo;
-        const int y = (int)(h + kh) - (int)cv.pad;
+        const int y = (int)(h + kh) - cv.pad;
         if (y < 0 || y >= (int)cv.H) return zero;
-        const int x0 = (int)(w + kw) - (int)cv.pad;
+        const int x0 = (int)(w + kw) - cv.pad_x;
         const int sh = x0 & 3, xa = x0 - sh, xb = xa + 4;
         const uint32_t row4 = ((c * cv.H + (uint32_t)y) * cv.W) >> 2;
         const float4 a = xa >= 0 && xa < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xa >> 2)) : zero;
@@ -298,8 +304,8 @@ __device__ __forceinline__ float4 conv_span4(const float *img0, const ConvB &cv,
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
             const uint32_t h = fdiv(p, cv.div_wo), w = p - h * cv.Wo;
-            const int y = (int)(h * cv.stride + kh) - (int)cv.pad;
-            const int x = (int)(w * cv.stride + kw) - (int)cv.pad;
+            const int y = (int)(h * cv.stride + kh) - cv.pad;
+            const int x = (int)(w * cv.stride + kw) - cv.pad_x;
             if (j < avail && y >= 0 && y < (int)cv.H && x >= 0 && x < (int)cv.W)
                 ::dkz::lane(out, j) = img0[(size_t)i * cv.b_img + (c * cv.H + (uint32_t)y) * cv.W + (uint32_t)x];
             if (++p == cv.npos) p = 0, ++i;
@@ -392,16 +398,18 @@ struct SegSlab : Slab<R, true> {
 // product whose A is delta and whose B is the im2col, k running over image
 // and position; kSpan + mode: as kFwd, but the columns run over (image,
 // position) of every image, so small images fill whole tiles (kSpanOdd: the
-// positions per image are not a multiple of 4) (modes: kRaw, kGather,
-// kTwoBlock). Each workgroup row z = blockIdx.y computes its own product
-// (see GemmArgs).
-constexpr int kImNone = -1, kFwd = 0, kWgrad = 8, kSpan = 16, kSpanOdd = 24;
+// positions per image are not a multiple of 4); kPhase + mode: as kFwd, but
+// column j goes to the pixel of one phase of a strided data gradient (see
+// ConvB) (modes: kRaw, kGather, kTwoBlock). Each workgroup row z =
+// blockIdx.y computes its own product (see GemmArgs).
+constexpr int kImNone = -1, kFwd = 0, kWgrad = 8, kSpan = 16, kSpanOdd = 24, kPhase = 32;
 
 template <int BM, int BN, bool TA, bool TB, int D, int IM = kImNone>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     constexpr bool kWg = IM >= kWgrad && IM < kSpan;
-    constexpr bool kSp = IM >= kSpan;
-    constexpr int kSpanKind = IM >= kSpanOdd ? 2 : kSp ? 1 : 0;
+    constexpr bool kSp = IM >= kSpan && IM < kPhase;
+    constexpr bool kPh = IM >= kPhase;
+    constexpr int kSpanKind = !kSp ? 0 : IM >= kSpanOdd ? 2 : 1;
     constexpr int kMode = IM == kImNone ? 0 : IM % 8;
     static_assert(IM == kImNone || (!TA && TB == kWg), "forward: NN; weight gradient: NT");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
@@ -528,6 +536,9 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
             if constexpr (kSp) {
                 const uint32_t img = fdiv(j, g.cv.div_npos);
                 ccol = gc + (size_t)img * g.cv.c_img + (j - img * g.cv.npos);
+            } else if constexpr (kPh) {
+                const uint32_t yq = fdiv(j, g.cv.div_wp), xq = j - yq * g.cv.div_wp.d;
+                ccol = gc + (g.cv.ph_s * yq + g.cv.ph_py) * g.cv.ph_w + g.cv.ph_s * xq + g.cv.ph_px;
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -641,6 +652,25 @@ __global__ __launch_bounds__(kBlock) void flip_weights_kernel(const float *w, fl
     const uint32_t c = fdiv(r, div_mkk), q = r - c * div_mkk.d;
     const uint32_t f = fdiv(q, div_kk), t = q - f * kk;
     at[e] = w[(size_t)j * div_cgmkk.d + (size_t)f * cg * kk + c * kk + (kk - 1 - t)];
+}
+
+// One phase's A of a strided data gradient: at[j][c][(f*na + a)*nb + b] =
+// w[j][f][c][kh0 + s*(na-1-a)][kw0 + s*(nb-1-b)], the taps of the phase
+// (kh = kh0 mod s, kw = kw0 mod s) with channels as rows, flipped.
+struct PhaseTaps {
+    uint32_t ks, s, kh0, kw0, na, nb, m, cg;
+    FastDiv div_nb, div_nab, div_mnab, div_cgmnab;
+};
+__global__ __launch_bounds__(kBlock) void flip_phase_kernel(const float *w, float *at, PhaseTaps t, uint32_t total) {
+    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+    if (e >= total) return;
+    const uint32_t j = fdiv(e, t.div_cgmnab), r = e - j * t.div_cgmnab.d;
+    const uint32_t c = fdiv(r, t.div_mnab), q = r - c * t.div_mnab.d;
+    const uint32_t f = fdiv(q, t.div_nab), u = q - f * t.div_nab.d;
+    const uint32_t a = fdiv(u, t.div_nb), b = u - a * t.nb;
+    const uint32_t kh = t.kh0 + t.s * (t.na - 1 - a), kw = t.kw0 + t.s * (t.nb - 1 - b);
+    const size_t kk = (size_t)t.ks * t.ks;
+    at[e] = w[((size_t)j * t.m + f) * t.cg * kk + c * kk + kh * t.ks + kw];
 }
 
 template <int IM>
@@ -846,7 +876,8 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         cv.Wo = (uint32_t)wo;
         cv.ksz = (uint32_t)ksize;
         cv.stride = (uint32_t)stride;
-        cv.pad = (uint32_t)pad;
+        cv.pad = pad;
+        cv.pad_x = pad;
         cv.div_kk = make_fastdiv((uint32_t)(ksize * ksize));
         cv.div_k = make_fastdiv((uint32_t)ksize);
         cv.div_wo = make_fastdiv((uint32_t)wo);
@@ -898,8 +929,8 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
 // group: input channels by input positions, k = (filter, tap) over the
 // group's flipped weights (transposed once into the library's scratch) and
 // delta gathered at each tap's output position, so col2im's adds join the
-// product's sum. Otherwise the layer's two steps run batched over as many
-// images as the scratch holds. No workspace.
+// product's sum. Otherwise the same per phase of the input pixels (y mod
+// stride, x mod stride), each over its own taps. No workspace.
 int dkz_convolution_data_gradient(int batch, int groups, int channels, int height, int width, int filters, int ksize,
                                   int stride, int pad, const float *weights, const float *delta,
                                   float *input_delta) {
@@ -990,7 +1021,8 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         cv.Wo = (uint32_t)width;
         cv.ksz = (uint32_t)ksize;
         cv.stride = 1;
-        cv.pad = (uint32_t)(ksize - 1 - pad);
+        cv.pad = ksize - 1 - pad;
+        cv.pad_x = ksize - 1 - pad;
         cv.div_kk = make_fastdiv((uint32_t)kk);
         cv.div_k = make_fastdiv((uint32_t)ksize);
         cv.div_wo = make_fastdiv((uint32_t)width);
@@ -1015,44 +1047,79 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         return 0;
     }
     // Strided (or pad >= ksize): the im2col of delta would have holes between
-    // the strided outputs, so the layer's two steps stay, batched over as many
-    // images as the scratch holds: col(i) = weights(j)^T x delta(i, j) for a
-    // run of images into the scratch (beta 0), then col2im of each into its
-    // image -- the same multiply-adds as the per-image loop, in fewer launches.
-    const uint64_t col_floats = kw * npos;
-    DKZ_REQUIRE(col_floats <= sc.gemm_floats);
-    uint64_t per = sc.gemm_floats / col_floats;
-    if (per > (uint64_t)batch) per = batch;
-    if (per > 65535) per = 65535;
-    g.m = (uint32_t)kw;
-    g.n = (uint32_t)npos;
-    g.k = (uint32_t)m;
-    g.k_chunk = (uint32_t)m;
-    g.lda = (uint32_t)kw;
-    g.ldb = (uint32_t)npos;
-    g.ldc = (uint32_t)npos;
-    g.beta = 0.0f;
-    g.zgroups = 1;
-    g.a_z = 0;
-    g.b_z = (uint32_t)((uint64_t)groups * m * npos);  // image i + 1 of the same group
-    g.c_z = (uint32_t)col_floats;
-    g.vec_a = aligned16(weights) && kw % 4 == 0;
-    g.vec_b = aligned16(delta) && npos % 4 == 0 && (m * npos) % 4 == 0;
-    g.c = sc.gemm;
-    for (int j = 0; j < groups; ++j) {
-        for (uint64_t i0 = 0; i0 < (uint64_t)batch; i0 += per) {
-            const uint32_t ic = (uint32_t)((uint64_t)batch - i0 < per ? (uint64_t)batch - i0 : per);
-            const bool big = kw >= 128 && (uint64_t)div_up(kw, 128) * div_up(npos, 128) * ic >= 2 * kCus;
-            GemmArgs gz = g;
-            gz.tiles_m = (uint32_t)div_up(kw, big ? 128 : 64);
-            gz.tiles_n = (uint32_t)div_up(npos, big ? 128 : 64);
-            gz.a = weights + (uint64_t)j * m * kw;
-            gz.b = delta + (i0 * groups + j) * m * npos;
-            DKZ_TRY(big ? (launch_batched_tn<128, 128, 1>(gz, ic))
-                        : (launch_batched_tn<64, 64, DKZ_GEMM_SMALL_PREFETCH>(gz, ic)));
-            DKZ_TRY(col2im_images(sc.gemm, (int)cg, height, width, ksize, stride, pad,
-                                  input_delta + (i0 * groups + j) * in_group, ic, col_floats,
-                                  (uint64_t)groups * in_group));
+    // the strided outputs. Input pixel (y, x) takes tap (kh, kw) only when
+    // y + pad - kh is a multiple of stride, so the pixels split into stride^2
+    // phases (y mod stride, x mod stride), each taking the taps kh = kh0 + s*a,
+    // kw = kw0 + s*b with kh0 = (py + pad) mod s: per phase one product over
+    // the phase's pixels whose A is those taps flipped (flip_phase_kernel) and
+    // whose B is a stride-1 im2col of delta with window na x nb and pads
+    // na-1-qy, nb-1-qx (qy = (py + pad - kh0) / s), written to the phase's
+    // pixels. The same multiply-adds as the layer's gemm, no column buffer.
+    const int s = stride;
+    const uint64_t at_all = (uint64_t)groups * cg * m * kk;
+    DKZ_REQUIRE(at_all <= sc.gemm_floats);
+    uint64_t at_off = 0;
+    for (int py = 0; py < s; ++py) {
+        for (int px = 0; px < s; ++px) {
+            const int kh0 = (py + pad) % s, kw0 = (px + pad) % s;
+            const int na = kh0 < ksize ? (ksize - kh0 + s - 1) / s : 0;
+            const int nb = kw0 < ksize ? (ksize - kw0 + s - 1) / s : 0;
+            const int hp = py < height ? (height - py + s - 1) / s : 0;
+            const int wp = px < width ? (width - px + s - 1) / s : 0;
+            if (na == 0 || nb == 0 || hp == 0 || wp == 0) continue;  // no tap reaches these pixels
+            const int qy = (py + pad - kh0) / s, qx = (px + pad - kw0) / s;
+            const uint64_t nab = (uint64_t)na * nb, k = m * nab, n = (uint64_t)hp * wp;
+            const uint64_t at_n = (uint64_t)groups * cg * k;
+            PhaseTaps t{(uint32_t)ksize, (uint32_t)s, (uint32_t)kh0, (uint32_t)kw0, (uint32_t)na, (uint32_t)nb,
+                        (uint32_t)m, (uint32_t)cg, make_fastdiv((uint32_t)nb), make_fastdiv((uint32_t)nab),
+                        make_fastdiv((uint32_t)(m * nab)), make_fastdiv((uint32_t)(cg * k))};
+            float *at = sc.gemm + at_off;
+            at_off += at_n;
+            DKZ_TRY(launch("convolution_data_gradient", flip_phase_kernel, dim3(div_up(at_n, kBlock)), dim3(kBlock),
+                           weights, at, t, (uint32_t)at_n));
+            GemmArgs gp = g;
+            gp.a = at;
+            gp.b = delta;
+            gp.c = input_delta;
+            gp.m = (uint32_t)cg;
+            gp.n = (uint32_t)n;
+            gp.k = (uint32_t)k;
+            gp.k_chunk = (uint32_t)k;
+            gp.lda = (uint32_t)k;
+            gp.ldb = (uint32_t)n;
+            gp.ldc = (uint32_t)((uint64_t)height * width);
+            gp.beta = 1.0f;
+            gp.a_z = (uint32_t)(cg * k);
+            gp.vec_a = k % 4 == 0 && (at_off - at_n) % 4 == 0;
+            ConvB &cv = gp.cv;
+            cv.H = (uint32_t)ho;
+            cv.W = (uint32_t)wo;
+            cv.Wo = (uint32_t)wp;
+            cv.ksz = (uint32_t)nb;
+            cv.stride = 1;
+            cv.pad = na - 1 - qy;
+            cv.pad_x = nb - 1 - qx;
+            cv.div_kk = make_fastdiv((uint32_t)nab);
+            cv.div_k = make_fastdiv((uint32_t)nb);
+            cv.div_wo = make_fastdiv((uint32_t)wp);
+            cv.s1 = wo % 4 == 0 && wp % 4 == 0 && aligned16(delta) && (m * npos) % 4 == 0;
+            cv.div_wp = make_fastdiv((uint32_t)wp);
+            cv.ph_s = (uint32_t)s;
+            cv.ph_py = (uint32_t)py;
+            cv.ph_px = (uint32_t)px;
+            cv.ph_w = (uint32_t)width;
+            const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
+            gp.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
+            gp.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
+            constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather;
+            constexpr const char *kName = "convolution_data_gradient";
+            for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
+                const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
+                GemmArgs gz = gp;
+                gz.b = delta + z0 * m * npos;
+                gz.c = input_delta + z0 * in_group;
+                DKZ_TRY(cv.s1 ? launch_fwd<kPS1>(kName, gz, zc, big) : launch_fwd<kPGa>(kName, gz, zc, big));
+            }
         }
     }
     return 0;
@@ -1097,7 +1164,8 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
     cv.Wo = (uint32_t)wo;
     cv.ksz = (uint32_t)ksize;
     cv.stride = (uint32_t)stride;
-    cv.pad = (uint32_t)pad;
+    cv.pad = pad;
+    cv.pad_x = pad;
     cv.div_kk = make_fastdiv((uint32_t)(ksize * ksize));
     cv.div_k = make_fastdiv((uint32_t)ksize);
     cv.div_wo = make_fastdiv((uint32_t)wo);

@@ -230,15 +230,6 @@ __global__ __launch_bounds__(kBlock) void col2im_kernel(const float *__restrict_
     if (e < n) im[e] = col2im_at<S1>(col, im[e], e, g);
 }
 
-// One image per grid row: column buffer z at col + z*col_z, image at im + z*im_z.
-template <bool S1>
-__global__ __launch_bounds__(kBlock) void col2im_images_kernel(const float *__restrict__ col, float *__restrict__ im,
-                                                               ColGeom g, uint32_t n, uint64_t col_z, uint64_t im_z) {
-    const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
-    float *img = im + blockIdx.y * im_z;
-    if (e < n) img[e] = col2im_at<S1>(col + blockIdx.y * col_z, img[e], e, g);
-}
-
 // gpu.zig:652-653: height_col = (height + 2*pad - ksize)/stride + 1 in usize.
 int make_geom(int channels, int height, int width, int ksize, int stride, int pad, ColGeom *g, uint64_t *ncol,
               uint64_t *nim) {
@@ -268,19 +259,6 @@ int make_geom(int channels, int height, int width, int ksize, int stride, int pa
 }
 
 }  // namespace
-
-int col2im_images(const float *col, int channels, int height, int width, int ksize, int stride, int pad, float *im,
-                  uint32_t images, uint64_t col_z, uint64_t im_z) {
-    ColGeom g;
-    uint64_t ncol, nim;
-    DKZ_TRY(make_geom(channels, height, width, ksize, stride, pad, &g, &ncol, &nim));
-    if (nim == 0 || images == 0) return 0;
-    DKZ_REQUIRE(im != nullptr && col != nullptr && images <= 65535);
-    const uint32_t n = (uint32_t)nim;
-    const dim3 grid(div_up(n, kBlock), images);
-    if (stride == 1) return launch("col2im", col2im_images_kernel<true>, grid, dim3(kBlock), col, im, g, n, col_z, im_z);
-    return launch("col2im", col2im_images_kernel<false>, grid, dim3(kBlock), col, im, g, n, col_z, im_z);
-}
 
 }  // namespace dkz
 

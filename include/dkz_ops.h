@@ -357,9 +357,8 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
  *                 a k x n matrix (the layer's beta-0 gemm straight into it);
  *     otherwise:  input_delta(i, j) += col2im(weights(j)^T x delta(i, j)).
  * Results agree with the per-image calls within fp32 summation error. Uses
- * the library's scratch (32 Mi floats) for the flipped weights or, with
- * stride > 1 or pad >= ksize, the column buffers of as many images as fit
- * (one must: ksize^2*channels/groups*out_h*out_w floats); no workspace. */
+ * the library's scratch (32 Mi floats) for the flipped weights; no
+ * workspace. */
 int dkz_convolution_data_gradient(int batch, int groups, int channels, int height, int width, int filters,
                                   int ksize, int stride, int pad, const float *weights, const float *delta,
                                   float *input_delta);
