@@ -190,6 +190,9 @@ int dkz_scale_bias(float *output, const float *scales, int batch, int filters, i
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (DKZ_EMPTY(batch, filters, spatial)) return 0;
     DKZ_REQUIRE(output && scales);
+    if ((uint64_t)batch * filters * spatial * sizeof(float) < DKZ_SCALE_BIAS_SMALL_BYTES)
+        return run_bcast<DKZ_HINT_SCALE_BIAS_SMALL, ScaleBiasOp, false>("scale_bias", ScaleBiasOp{scales}, output,
+                                                                        nullptr, batch, filters, spatial);
     return run_bcast<DKZ_HINT_SCALE_BIAS, ScaleBiasOp, false>("scale_bias", ScaleBiasOp{scales}, output, nullptr, batch,
                                          filters, spatial);
 }

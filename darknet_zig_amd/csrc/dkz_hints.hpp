@@ -64,6 +64,15 @@
 #ifndef DKZ_HINT_SCALE_BIAS
 #define DKZ_HINT_SCALE_BIAS 0    // also runs on delta inside the backward sequence
 #endif
+// ... below this many bytes the tensor is a forward activation small enough
+// that the ops after it find it again whatever the hint (the backward
+// sequence's delta, which must stay cached, is larger at the configs' shapes)
+#ifndef DKZ_HINT_SCALE_BIAS_SMALL
+#define DKZ_HINT_SCALE_BIAS_SMALL 3
+#endif
+#ifndef DKZ_SCALE_BIAS_SMALL_BYTES
+#define DKZ_SCALE_BIAS_SMALL_BYTES (64ull << 20)
+#endif
 #ifndef DKZ_HINT_NORMALIZE
 #define DKZ_HINT_NORMALIZE 3
 #endif
