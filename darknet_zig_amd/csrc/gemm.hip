@@ -33,6 +33,14 @@
 // at once share A and B panels, and neighbouring tile numbers are placed on
 // one XCD (workgroups are dealt to the 8 XCDs round robin) so that they share
 // its L2.
+//
+// The same kernel runs a convolutional layer's three per-image loops as one
+// call each (dkz_convolution_forward, _weight_gradient, _data_gradient): its
+// B operand is then an im2col gathered inside the slab loads (of the input,
+// or of delta), the grid's second dimension runs over images and groups,
+// and small images, strided data gradients and the weight gradient's long K
+// get their own column orders, pixel mappings and splits (see ConvB and the
+// entry points).
 #include <type_traits>
 
 #include "dkz_device.hpp"
