@@ -94,7 +94,8 @@ struct ConvB {
     uint32_t H, W, Wo, ksz, stride;
     int32_t pad, pad_x;  // rows and columns (negative: the window starts inside the image)
     FastDiv div_kk, div_k, div_wo;  // ksz*ksz, ksz, Wo
-    uint32_t s1;  // stride 1, W % 4 == 0, Wo % 4 == 0, images 16-byte aligned
+    uint32_t s1;    // stride 1, W % 4 == 0, Wo % 4 == 0, images 16-byte aligned
+    uint32_t row4;  // Wo % 4 == 0: a float4's four positions share an output row
     // Weight gradient (k runs over image and position): positions per image,
     // and the element strides from one image to the next of delta (A) and of
     // the input (B); npos4: npos % 4 == 0, so no float4 spans two images.
@@ -241,8 +242,10 @@ struct Slab {
 // takes each element's tap, kTwoBlock takes four positions of one output row
 // (stride 1, W and Wo multiples of 4) from the aligned float4 at or below
 // x0 = w + kw - pad and, unless x0 is aligned, the next one; a block outside
-// its row reads as the padding's zeros.
-constexpr int kRaw = 0, kGather = 1, kTwoBlock = 2;
+// its row reads as the padding's zeros. kRow (Wo a multiple of 4, any
+// stride) takes four positions of one output row: the tap, the row and its
+// bounds once, then four loads stride apart.
+constexpr int kRaw = 0, kGather = 1, kTwoBlock = 2, kRow = 3;
 
 // im2col(img)[kidx][p] (0 in the padding).
 template <int MODE>
@@ -278,6 +281,21 @@ __device__ __forceinline__ float4 conv_col4(const float *img, const ConvB &cv, u
         const float4 a = xa >= 0 && xa < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xa >> 2)) : zero;
         const float4 b = sh != 0 && xb >= 0 && xb < (int)cv.W ? ld4<false>(img, row4 + (uint32_t)(xb >> 2)) : zero;
         return make_float4(pick8(a, b, sh), pick8(a, b, sh + 1), pick8(a, b, sh + 2), pick8(a, b, sh + 3));
+    } else if constexpr (MODE == kRow) {
+        const uint32_t c = fdiv(kidx, cv.div_kk), rem = kidx - c * cv.div_kk.d;
+        const uint32_t kh = fdiv(rem, cv.div_k), kw = rem - kh * cv.ksz;
+        const uint32_t h = fdiv(p0, cv.div_wo), w = p0 - h * cv.Wo;
+        const int y = (int)(h * cv.stride + kh) - cv.pad;
+        if (y < 0 || y >= (int)cv.H) return zero;
+        const float *row = img + (c * cv.H + (uint32_t)y) * cv.W;
+        const int x0 = (int)(w * cv.stride + kw) - cv.pad_x;
+        float4 out = zero;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int x = x0 + j * (int)cv.stride;
+            if (x >= 0 && x < (int)cv.W) ::dkz::lane(out, j) = row[x];
+        }
+        return out;
     } else {
         if (MODE == kRaw && avail == 4 && cv.npos4 && cv.b_vec)
             return ld4<false>(img + kidx * cv.npos, p0 >> 2);
@@ -298,7 +316,7 @@ __device__ __forceinline__ float4 conv_span4(const float *img0, const ConvB &cv,
                                              uint32_t avail) {
     uint32_t i = fdiv(q, cv.div_npos), p = q - i * cv.npos;
     if constexpr (!ODD) return conv_col4<MODE>(img0 + (size_t)i * cv.b_img, cv, kidx, p, avail);
-    static_assert(!ODD || MODE != kTwoBlock, "two-block gathers need npos % 4 == 0");
+    static_assert(!ODD || (MODE != kTwoBlock && MODE != kRow), "row gathers need npos % 4 == 0");
     float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if constexpr (MODE == kRaw) {
 #pragma unroll
@@ -355,7 +373,8 @@ struct ConvSlab : Slab<R, ROWK> {
                     // columns of a spanning forward product.
                     const uint32_t kidx = r0 + r, avail = kend - kk < 4 ? kend - kk : 4;
                     if (cv.npos4) out = conv_span4<MODE, false>(img0, cv, kidx, kk, avail);
-                    else if constexpr (MODE != kTwoBlock) out = conv_span4<MODE, true>(img0, cv, kidx, kk, avail);
+                    else if constexpr (MODE != kTwoBlock && MODE != kRow)
+                        out = conv_span4<MODE, true>(img0, cv, kidx, kk, avail);
                 }
             }
             v[l] = out;
@@ -719,8 +738,8 @@ int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, u
     g.cv.c_img = (uint32_t)c_img;
     constexpr int D = DKZ_GEMM_SMALL_PREFETCH;
     if (npos % 4 == 0) return launch_batched<64, 64, D, kSpan + MODE>(name, g, groups);
-    if constexpr (MODE == kTwoBlock) {
-        DKZ_REQUIRE(npos % 4 == 0);  // two-block gathers are chosen only then
+    if constexpr (MODE == kTwoBlock || MODE == kRow) {
+        DKZ_REQUIRE(npos % 4 == 0);  // row gathers are chosen only then
         return 0;
     } else {
         return launch_batched<64, 64, D, kSpanOdd + MODE>(name, g, groups);
@@ -890,6 +909,7 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         cv.div_k = make_fastdiv((uint32_t)ksize);
         cv.div_wo = make_fastdiv((uint32_t)wo);
         cv.s1 = stride == 1 && width % 4 == 0 && wo % 4 == 0 && aligned16(input);
+        cv.row4 = wo % 4 == 0;
     }
     // 128x128 tiles when m fills them and the whole batch gives every CU two
     // workgroups, else 64x64.
@@ -904,6 +924,7 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         g.cv.b_vec = g.vec_b;  // ksize 1: float4 rows of the input matrix
         if (!im) return launch_span<kRaw>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
         if (g.cv.s1) return launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+        if (g.cv.row4) return launch_span<kRow>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
         return launch_span<kGather>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
     }
     // At most 65535 grid rows per launch, whole images each (a multiple of
@@ -914,10 +935,11 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
         GemmArgs gz = g;
         gz.b = input + z0 * in_group;
         gz.c = output + z0 * m * n;
-        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
+        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather, kRw = kFwd + kRow;
         int e;
         if (!im) e = launch_fwd<kImNone>("convolution_forward", gz, zc, big);
         else if (g.cv.s1) e = launch_fwd<kS1>("convolution_forward", gz, zc, big);
+        else if (g.cv.row4) e = launch_fwd<kRw>("convolution_forward", gz, zc, big);
         else e = launch_fwd<kGa>("convolution_forward", gz, zc, big);
         if (e != 0) return e;
     }
@@ -1038,19 +1060,23 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
         g.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
         g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
-        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather;
+        constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather, kRw = kFwd + kRow;
         constexpr const char *kName = "convolution_data_gradient";
+        cv.row4 = width % 4 == 0;
         if (DKZ_CONV_SPAN && batch > 1 && span_pays(n, big ? 128 : 64)) {
             const uint64_t b_img = (uint64_t)groups * m * npos, c_img = (uint64_t)groups * in_group;
-            return cv.s1 ? launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img)
-                         : launch_span<kGather>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+            if (cv.s1) return launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+            if (cv.row4) return launch_span<kRow>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
+            return launch_span<kGather>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
         }
         for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
             const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
             GemmArgs gz = g;
             gz.b = delta + z0 * m * npos;
             gz.c = input_delta + z0 * in_group;
-            DKZ_TRY(cv.s1 ? launch_fwd<kS1>(kName, gz, zc, big) : launch_fwd<kGa>(kName, gz, zc, big));
+            DKZ_TRY(cv.s1     ? launch_fwd<kS1>(kName, gz, zc, big)
+                    : cv.row4 ? launch_fwd<kRw>(kName, gz, zc, big)
+                              : launch_fwd<kGa>(kName, gz, zc, big));
         }
         return 0;
     }
@@ -1119,14 +1145,17 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
             const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
             gp.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
             gp.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
-            constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather;
+            constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather, kPRw = kPhase + kRow;
+            cv.row4 = wp % 4 == 0;
             constexpr const char *kName = "convolution_data_gradient";
             for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
                 const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
                 GemmArgs gz = gp;
                 gz.b = delta + z0 * m * npos;
                 gz.c = input_delta + z0 * in_group;
-                DKZ_TRY(cv.s1 ? launch_fwd<kPS1>(kName, gz, zc, big) : launch_fwd<kPGa>(kName, gz, zc, big));
+                DKZ_TRY(cv.s1     ? launch_fwd<kPS1>(kName, gz, zc, big)
+                        : cv.row4 ? launch_fwd<kPRw>(kName, gz, zc, big)
+                                  : launch_fwd<kPGa>(kName, gz, zc, big));
             }
         }
     }
@@ -1245,6 +1274,8 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
     g.k_chunk = (uint32_t)chunk;
     g.partial = sc.gemm;
     constexpr int kWgRaw = kWgrad + kRaw, kWgGa = kWgrad + kGather, kWgS1 = kWgrad + kTwoBlock;
+    constexpr int kWgRw = kWgrad + kRow;
+    const bool row4 = ksize != 1 && wo % 4 == 0;
     for (int j = 0; j < groups; ++j) {
         GemmArgs gj = g;
         gj.a = delta + (uint64_t)j * m * npos;
@@ -1252,6 +1283,7 @@ int dkz_convolution_weight_gradient(int batch, int groups, int channels, int hei
         gj.c = weight_updates + (uint64_t)j * m * kw;
         if (ksize == 1) DKZ_TRY(launch_wgrad_tiles<kWgRaw>(gj, big));
         else if (s1) DKZ_TRY(launch_wgrad_tiles<kWgS1>(gj, big));
+        else if (row4) DKZ_TRY(launch_wgrad_tiles<kWgRw>(gj, big));
         else DKZ_TRY(launch_wgrad_tiles<kWgGa>(gj, big));
     }
     return 0;
