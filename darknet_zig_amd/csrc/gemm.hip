@@ -706,16 +706,22 @@ int launch_fwd(const char *name, const GemmArgs &g, uint32_t zcount, bool big) {
     return launch_batched<64, 64, DKZ_GEMM_SMALL_PREFETCH, IM>(name, g, zcount);
 }
 
-// Columns over (image, position) of all `batch` images (kSpan), in 64x64
-// tiles: g holds one image's product per group (z = group); B and C advance
-// b_img and c_img elements per image. Measured against per-image tiles:
-// [64,512,14,14]->512 3x3 forward 1132 -> 975 us, [64,1024,13,13]->1024
-// 3324 -> 2642 us (data gradients alike), while with a fifth or less of
-// the last tile empty ([64,256,28,28]->256, 26x26) the per-image 128x128
-// tiles stay 3-5% ahead; 128x128 tiles over (image, position) were slower
-// than either (too few workgroups, and the per-tap gather spills).
+// Columns over (image, position) of all `batch` images (kSpan), in 128x64
+// tiles (64x64 below 128 rows): g holds one image's product per group
+// (z = group); B and C advance b_img and c_img elements per image. Measured
+// against per-image tiles: [64,512,14,14]->512 3x3 forward 1132 -> 975 us
+// with 64x64 span tiles, 836 us with 128x64 ones (half the gathered B
+// slabs per multiply-add), [64,1024,13,13]->1024 3324 -> 2642 -> 2536 us
+// (data gradients alike), while with a fifth or less of the last tile empty
+// ([64,256,28,28]->256, 26x26) the per-image 128x128 tiles stay 3-5% ahead;
+// 128x128 tiles over (image, position) were slower than either (too few
+// workgroups, and the per-tap gather spills). The 128x64 span kernels keep
+// one slab in flight (two spill).
 #ifndef DKZ_CONV_SPAN
 #define DKZ_CONV_SPAN 1
+#endif
+#ifndef DKZ_SPAN_BM
+#define DKZ_SPAN_BM 128
 #endif
 
 // Whether per-image column tiles of bn leave more than a fifth of their
@@ -737,6 +743,11 @@ int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, u
     g.cv.b_img = (uint32_t)b_img;
     g.cv.c_img = (uint32_t)c_img;
     constexpr int D = DKZ_GEMM_SMALL_PREFETCH;
+    if (DKZ_SPAN_BM == 128 && g.m >= 128) {
+        g.tiles_m = div_up(g.m, 128);
+        if (npos % 4 == 0) return launch_batched<128, 64, 1, kSpan + MODE>(name, g, groups);
+        if constexpr (MODE != kTwoBlock && MODE != kRow) return launch_batched<128, 64, 1, kSpanOdd + MODE>(name, g, groups);
+    }
     if (npos % 4 == 0) return launch_batched<64, 64, D, kSpan + MODE>(name, g, groups);
     if constexpr (MODE == kTwoBlock || MODE == kRow) {
         DKZ_REQUIRE(npos % 4 == 0);  // row gathers are chosen only then
