@@ -731,6 +731,18 @@ inline bool span_pays(uint64_t n, uint64_t bn) {
     return (t - n) * 5 > t;
 }
 
+// Whether a batched convolution product of m rows and n positions per image
+// runs as one span product: always with 128x64 span tiles (m >= 128), which
+// measured ahead of per-image 128x128 tiles at every 3x3 size tried (2% at
+// [64,128,56,56]->128, 6% at [64,256,28,28]->256, 13% at ->512, 30% at
+// [64,256,26,26]->512, whose 1536 per-image tiles fill 1.5 rounds of
+// workgroups) and for 1x1 forwards; below that when per-image tiles waste
+// columns.
+inline bool use_span(uint64_t batch, uint64_t m, uint64_t n, bool big) {
+    if (!DKZ_CONV_SPAN || batch < 2) return false;
+    return (DKZ_SPAN_BM == 128 && m >= 128) || span_pays(n, big ? 128 : 64);
+}
+
 template <int MODE>
 int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, uint64_t b_img, uint64_t c_img) {
     const uint32_t npos = g.n;
@@ -927,9 +939,9 @@ int dkz_convolution_forward(int batch, int groups, int channels, int height, int
     const bool big = m >= 128 && (uint64_t)div_up(m, 128) * div_up(n, 128) * zcount >= 2 * kCus;
     g.tiles_m = (uint32_t)div_up(m, big ? 128 : 64);
     g.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
-    // Small images (the last column tile of each mostly empty): one product
-    // per group with columns over every image's positions.
-    if (DKZ_CONV_SPAN && batch > 1 && span_pays(n, big ? 128 : 64)) {
+    // One product per group with columns over every image's positions (see
+    // use_span), else one per (image, group).
+    if (use_span(batch, m, n, big)) {
         constexpr const char *kName = "convolution_forward";
         const uint64_t b_img = (uint64_t)groups * in_group, c_img = (uint64_t)groups * m * n;
         g.cv.b_vec = g.vec_b;  // ksize 1: float4 rows of the input matrix
@@ -1074,7 +1086,7 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         constexpr int kS1 = kFwd + kTwoBlock, kGa = kFwd + kGather, kRw = kFwd + kRow;
         constexpr const char *kName = "convolution_data_gradient";
         cv.row4 = width % 4 == 0;
-        if (DKZ_CONV_SPAN && batch > 1 && span_pays(n, big ? 128 : 64)) {
+        if (use_span(batch, cg, n, big)) {
             const uint64_t b_img = (uint64_t)groups * m * npos, c_img = (uint64_t)groups * in_group;
             if (cv.s1) return launch_span<kTwoBlock>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
             if (cv.row4) return launch_span<kRow>(kName, g, (uint32_t)batch, (uint32_t)groups, b_img, c_img);
