@@ -41,7 +41,9 @@
 // and small images, strided data gradients and the weight gradient's long K
 // get their own column orders, pixel mappings and splits (see ConvB and the
 // entry points).
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "dkz_device.hpp"
 #include "dkz_internal.hpp"
@@ -113,6 +115,19 @@ struct ConvB {
     uint32_t ph_s, ph_py, ph_px, ph_w;
 };
 
+// One phase of a strided data gradient in a launch that runs several (kPhase):
+// its flipped taps (A, `k` = filters x taps per group), their window (ksz
+// columns, kk = rows x columns) and pads over delta, and the phase's pixel
+// offsets (py, px). Grid row y runs phase y / zrows over (image, group)
+// y % zrows.
+struct PhaseDesc {
+    const float *a;
+    uint32_t k, vec_a, ksz, py, px;
+    int32_t pad, pad_x;
+    FastDiv div_kk, div_k;
+};
+constexpr int kMaxPhases = 4;
+
 struct GemmArgs {
     const float *a;
     const float *b;
@@ -126,6 +141,8 @@ struct GemmArgs {
     // A at a + (z % zgroups) * a_z, B at b + z * b_z, C at c + z * c_z.
     uint32_t zgroups, a_z, b_z, c_z;
     ConvB cv;  // implicit-im2col kernels only
+    PhaseDesc ph[kMaxPhases];  // kPhase kernels only
+    uint32_t zrows;
 };
 
 __device__ __forceinline__ void tile_of(uint32_t w, const GemmArgs &g, uint32_t &tm, uint32_t &tn, uint32_t &split) {
@@ -447,16 +464,41 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     __shared__ float As[2][BM * kPitch];
     __shared__ float Bs[2][BN * kPitch];
 
+    uint32_t z = blockIdx.y;
+    // A and the gather geometry; a phase row of a strided data gradient takes
+    // its phase's taps, window and pixel offsets instead (fields picked with
+    // constant indexes, so the kernel arguments stay where they are).
+    const float *a_base = g.a;
+    uint32_t k_all = g.k, k_chunk = g.k_chunk, lda = g.lda, a_z = g.a_z, vec_a = g.vec_a;
+    ConvB cv = g.cv;
+    if constexpr (kPh) {
+        const uint32_t p = z / g.zrows;
+        z -= p * g.zrows;
+#define DKZ_PHASE_FIELD(f) (p == 0 ? g.ph[0].f : p == 1 ? g.ph[1].f : p == 2 ? g.ph[2].f : g.ph[3].f)
+        a_base = DKZ_PHASE_FIELD(a);
+        k_all = DKZ_PHASE_FIELD(k);
+        vec_a = DKZ_PHASE_FIELD(vec_a);
+        cv.ksz = DKZ_PHASE_FIELD(ksz);
+        cv.pad = DKZ_PHASE_FIELD(pad);
+        cv.pad_x = DKZ_PHASE_FIELD(pad_x);
+        cv.div_kk = DKZ_PHASE_FIELD(div_kk);
+        cv.div_k = DKZ_PHASE_FIELD(div_k);
+        cv.ph_py = DKZ_PHASE_FIELD(py);
+        cv.ph_px = DKZ_PHASE_FIELD(px);
+#undef DKZ_PHASE_FIELD
+        k_chunk = k_all;
+        lda = k_all;
+        a_z = g.m * k_all;
+    }
     uint32_t tm, tn, split;
     tile_of(blockIdx.x, g, tm, tn, split);
-    const uint32_t z = blockIdx.y;
-    const float *ga = g.a + (size_t)(z % g.zgroups) * g.a_z;
+    const float *ga = a_base + (size_t)(z % g.zgroups) * a_z;
     const float *gb = g.b + (size_t)z * g.b_z;
     float *gc = g.c + (size_t)z * g.c_z;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t rows_a = g.m - m0, rows_b = g.n - n0;
-    const uint32_t kbeg = split * g.k_chunk;
-    const uint32_t kend = kbeg + g.k_chunk < g.k ? kbeg + g.k_chunk : g.k;
+    const uint32_t kbeg = split * k_chunk;
+    const uint32_t kend = kbeg + k_chunk < k_all ? kbeg + k_chunk : k_all;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
     const int half = lane >> 5, l32 = lane & 31;
@@ -464,11 +506,11 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     std::conditional_t<kWg, SegSlab<BM>, Slab<BM, !TA>> sa[D];
     std::conditional_t<IM != kImNone, ConvSlab<BN, kWg, kMode, kSpanKind>, Slab<BN, TB>> sb[D];
     auto load_a = [&](auto &slab, uint32_t k0) {
-        if constexpr (kWg) slab.load_seg(ga, g.cv, m0, rows_a, k0, kend, tid);
-        else slab.load(ga, g.lda, m0, rows_a, k0, kend, g.vec_a, tid);
+        if constexpr (kWg) slab.load_seg(ga, cv, m0, rows_a, k0, kend, tid);
+        else slab.load(ga, lda, m0, rows_a, k0, kend, vec_a, tid);
     };
     auto load_b = [&](auto &slab, uint32_t k0) {
-        if constexpr (IM != kImNone) slab.load_conv(gb, g.cv, n0, rows_b, k0, kend, tid);
+        if constexpr (IM != kImNone) slab.load_conv(gb, cv, n0, rows_b, k0, kend, tid);
         else slab.load(gb, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
     };
 
@@ -561,11 +603,11 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
             if (j >= g.n) continue;
             float *ccol = gc + j;  // column j of C
             if constexpr (kSp) {
-                const uint32_t img = fdiv(j, g.cv.div_npos);
-                ccol = gc + (size_t)img * g.cv.c_img + (j - img * g.cv.npos);
+                const uint32_t img = fdiv(j, cv.div_npos);
+                ccol = gc + (size_t)img * cv.c_img + (j - img * cv.npos);
             } else if constexpr (kPh) {
-                const uint32_t yq = fdiv(j, g.cv.div_wp), xq = j - yq * g.cv.div_wp.d;
-                ccol = gc + (g.cv.ph_s * yq + g.cv.ph_py) * g.cv.ph_w + g.cv.ph_s * xq + g.cv.ph_px;
+                const uint32_t yq = fdiv(j, cv.div_wp), xq = j - yq * cv.div_wp.d;
+                ccol = gc + (cv.ph_s * yq + cv.ph_py) * cv.ph_w + cv.ph_s * xq + cv.ph_px;
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -1115,72 +1157,108 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
     const int s = stride;
     const uint64_t at_all = (uint64_t)groups * cg * m * kk;
     DKZ_REQUIRE(at_all <= sc.gemm_floats);
-    uint64_t at_off = 0;
+    // The phases that some tap reaches, most taps first (their workgroups
+    // are the longest, so they start first).
+    struct Phase {
+        int py, px, kh0, kw0, na, nb, hp, wp, qy, qx;
+    };
+    std::vector<Phase> phases;
     for (int py = 0; py < s; ++py) {
         for (int px = 0; px < s; ++px) {
-            const int kh0 = (py + pad) % s, kw0 = (px + pad) % s;
-            const int na = kh0 < ksize ? (ksize - kh0 + s - 1) / s : 0;
-            const int nb = kw0 < ksize ? (ksize - kw0 + s - 1) / s : 0;
-            const int hp = py < height ? (height - py + s - 1) / s : 0;
-            const int wp = px < width ? (width - px + s - 1) / s : 0;
-            if (na == 0 || nb == 0 || hp == 0 || wp == 0) continue;  // no tap reaches these pixels
-            const int qy = (py + pad - kh0) / s, qx = (px + pad - kw0) / s;
-            const uint64_t nab = (uint64_t)na * nb, k = m * nab, n = (uint64_t)hp * wp;
+            Phase q{};
+            q.py = py;
+            q.px = px;
+            q.kh0 = (py + pad) % s;
+            q.kw0 = (px + pad) % s;
+            q.na = q.kh0 < ksize ? (ksize - q.kh0 + s - 1) / s : 0;
+            q.nb = q.kw0 < ksize ? (ksize - q.kw0 + s - 1) / s : 0;
+            q.hp = py < height ? (height - py + s - 1) / s : 0;
+            q.wp = px < width ? (width - px + s - 1) / s : 0;
+            if (q.na == 0 || q.nb == 0 || q.hp == 0 || q.wp == 0) continue;  // no tap reaches these pixels
+            q.qy = (py + pad - q.kh0) / s;
+            q.qx = (px + pad - q.kw0) / s;
+            phases.push_back(q);
+        }
+    }
+    std::stable_sort(phases.begin(), phases.end(),
+                     [](const Phase &x, const Phase &y) { return x.na * x.nb > y.na * y.nb; });
+    // Phases share a launch (grid row = phase x (image, group)) when they
+    // cover equal pixel grids, i.e. the stride divides the input, and a
+    // launch's rows can hold every group of an image for each phase.
+    const bool merge = height % s == 0 && width % s == 0 && (uint64_t)groups * kMaxPhases <= 65535;
+    uint64_t at_off = 0;
+    for (size_t i0 = 0; i0 < phases.size();) {
+        const size_t cnt = merge ? std::min<size_t>(kMaxPhases, phases.size() - i0) : 1;
+        const int hp = phases[i0].hp, wp = phases[i0].wp;
+        const uint64_t n = (uint64_t)hp * wp;
+        GemmArgs gp = g;
+        for (size_t u = 0; u < cnt; ++u) {
+            const Phase &q = phases[i0 + u];
+            const uint64_t nab = (uint64_t)q.na * q.nb, k = m * nab;
             const uint64_t at_n = (uint64_t)groups * cg * k;
-            PhaseTaps t{(uint32_t)ksize, (uint32_t)s, (uint32_t)kh0, (uint32_t)kw0, (uint32_t)na, (uint32_t)nb,
-                        (uint32_t)m, (uint32_t)cg, make_fastdiv((uint32_t)nb), make_fastdiv((uint32_t)nab),
-                        make_fastdiv((uint32_t)(m * nab)), make_fastdiv((uint32_t)(cg * k))};
+            PhaseTaps t{(uint32_t)ksize, (uint32_t)s, (uint32_t)q.kh0, (uint32_t)q.kw0, (uint32_t)q.na,
+                        (uint32_t)q.nb, (uint32_t)m, (uint32_t)cg, make_fastdiv((uint32_t)q.nb),
+                        make_fastdiv((uint32_t)nab), make_fastdiv((uint32_t)(m * nab)),
+                        make_fastdiv((uint32_t)(cg * k))};
             float *at = sc.gemm + at_off;
-            at_off += at_n;
             DKZ_TRY(launch("convolution_data_gradient", flip_phase_kernel, dim3(div_up(at_n, kBlock)), dim3(kBlock),
                            weights, at, t, (uint32_t)at_n));
-            GemmArgs gp = g;
-            gp.a = at;
-            gp.b = delta;
-            gp.c = input_delta;
-            gp.m = (uint32_t)cg;
-            gp.n = (uint32_t)n;
-            gp.k = (uint32_t)k;
-            gp.k_chunk = (uint32_t)k;
-            gp.lda = (uint32_t)k;
-            gp.ldb = (uint32_t)n;
-            gp.ldc = (uint32_t)((uint64_t)height * width);
-            gp.beta = 1.0f;
-            gp.a_z = (uint32_t)(cg * k);
-            gp.vec_a = k % 4 == 0 && (at_off - at_n) % 4 == 0;
-            ConvB &cv = gp.cv;
-            cv.H = (uint32_t)ho;
-            cv.W = (uint32_t)wo;
-            cv.Wo = (uint32_t)wp;
-            cv.ksz = (uint32_t)nb;
-            cv.stride = 1;
-            cv.pad = na - 1 - qy;
-            cv.pad_x = nb - 1 - qx;
-            cv.div_kk = make_fastdiv((uint32_t)nab);
-            cv.div_k = make_fastdiv((uint32_t)nb);
-            cv.div_wo = make_fastdiv((uint32_t)wp);
-            cv.s1 = wo % 4 == 0 && wp % 4 == 0 && aligned16(delta) && (m * npos) % 4 == 0;
-            cv.div_wp = make_fastdiv((uint32_t)wp);
-            cv.ph_s = (uint32_t)s;
-            cv.ph_py = (uint32_t)py;
-            cv.ph_px = (uint32_t)px;
-            cv.ph_w = (uint32_t)width;
-            const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
-            gp.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
-            gp.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
-            constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather, kPRw = kPhase + kRow;
-            cv.row4 = wp % 4 == 0;
-            constexpr const char *kName = "convolution_data_gradient";
-            for (uint64_t z0 = 0; z0 < zcount; z0 += chunk) {
-                const uint32_t zc = (uint32_t)(zcount - z0 < chunk ? zcount - z0 : chunk);
-                GemmArgs gz = gp;
-                gz.b = delta + z0 * m * npos;
-                gz.c = input_delta + z0 * in_group;
-                DKZ_TRY(cv.s1     ? launch_fwd<kPS1>(kName, gz, zc, big)
-                        : cv.row4 ? launch_fwd<kPRw>(kName, gz, zc, big)
-                                  : launch_fwd<kPGa>(kName, gz, zc, big));
-            }
+            gp.ph[u] = PhaseDesc{at,
+                                 (uint32_t)k,
+                                 (uint32_t)(k % 4 == 0 && at_off % 4 == 0),
+                                 (uint32_t)q.nb,
+                                 (uint32_t)q.py,
+                                 (uint32_t)q.px,
+                                 q.na - 1 - q.qy,
+                                 q.nb - 1 - q.qx,
+                                 make_fastdiv((uint32_t)nab),
+                                 make_fastdiv((uint32_t)q.nb)};
+            at_off += at_n;
         }
+        gp.a = gp.ph[0].a;
+        gp.b = delta;
+        gp.c = input_delta;
+        gp.m = (uint32_t)cg;
+        gp.n = (uint32_t)n;
+        gp.k = gp.ph[0].k;
+        gp.k_chunk = gp.k;
+        gp.lda = gp.k;
+        gp.ldb = (uint32_t)n;
+        gp.ldc = (uint32_t)((uint64_t)height * width);
+        gp.beta = 1.0f;
+        gp.a_z = (uint32_t)(cg * gp.k);
+        gp.vec_a = gp.ph[0].vec_a;
+        ConvB &cv = gp.cv;
+        cv.H = (uint32_t)ho;
+        cv.W = (uint32_t)wo;
+        cv.Wo = (uint32_t)wp;
+        cv.stride = 1;
+        cv.div_wo = make_fastdiv((uint32_t)wp);
+        cv.s1 = wo % 4 == 0 && wp % 4 == 0 && aligned16(delta) && (m * npos) % 4 == 0;
+        cv.row4 = wp % 4 == 0;
+        cv.div_wp = make_fastdiv((uint32_t)wp);
+        cv.ph_s = (uint32_t)s;
+        cv.ph_w = (uint32_t)width;
+        const bool big = cg >= 128 && (uint64_t)div_up(cg, 128) * div_up(n, 128) * zcount >= 2 * kCus;
+        gp.tiles_m = (uint32_t)div_up(cg, big ? 128 : 64);
+        gp.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
+        constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather, kPRw = kPhase + kRow;
+        constexpr const char *kName = "convolution_data_gradient";
+        // At most 65535 grid rows: cnt phases x zc (image, group) rows, whole
+        // images each.
+        const uint64_t rows = 65535 / cnt, zchunk = rows - rows % (uint64_t)groups;
+        for (uint64_t z0 = 0; z0 < zcount; z0 += zchunk) {
+            const uint32_t zc = (uint32_t)(zcount - z0 < zchunk ? zcount - z0 : zchunk);
+            GemmArgs gz = gp;
+            gz.b = delta + z0 * m * npos;
+            gz.c = input_delta + z0 * in_group;
+            gz.zrows = zc;
+            const uint32_t zr = (uint32_t)(cnt * zc);
+            DKZ_TRY(cv.s1     ? launch_fwd<kPS1>(kName, gz, zr, big)
+                    : cv.row4 ? launch_fwd<kPRw>(kName, gz, zr, big)
+                              : launch_fwd<kPGa>(kName, gz, zr, big));
+        }
+        i0 += cnt;
     }
     return 0;
 }

@@ -241,6 +241,10 @@ DG_CASES = [
     (2, 1, 4, 9, 9, 5, 1, 1, 0),        # ksize 1: overwritten (beta 0)
     (1, 1, 3, 8, 8, 4, 1, 2, 0),        # ksize 1, stride 2: the k x n view, a prefix of the image
     (3, 2, 6, 5, 7, 10, 1, 1, 0),       # ksize 1, groups
+    (2, 1, 6, 12, 12, 5, 3, 3, 1),      # stride 3: nine one-tap phases, launched four, four and one at a time
+    (2, 2, 10, 12, 10, 6, 5, 3, 2),     # stride 3, window 5 (phases of 4, 2 and 1 taps), width 10: one per launch
+    (3, 1, 5, 15, 15, 7, 5, 3, 1),      # stride 3, window 5, merged phases of unequal tap counts
+    (96, 1, 128, 56, 56, 8, 3, 2, 1),   # stride 2, 128 input channels: four phases per launch in 128x128 tiles
 ]
 
 
