@@ -446,14 +446,15 @@ struct SegSlab : Slab<R, true> {
 // column j goes to the pixel of one phase of a strided data gradient (see
 // ConvB) (modes: kRaw, kGather, kTwoBlock). Each workgroup row z =
 // blockIdx.y computes its own product (see GemmArgs).
-constexpr int kImNone = -1, kFwd = 0, kWgrad = 8, kSpan = 16, kSpanOdd = 24, kPhase = 32;
+constexpr int kImNone = -1, kFwd = 0, kWgrad = 8, kSpan = 16, kSpanOdd = 24, kPhase = 32, kPhaseSpan = 40,
+              kPhaseSpanOdd = 48;
 
 template <int BM, int BN, bool TA, bool TB, int D, int IM = kImNone>
 __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
     constexpr bool kWg = IM >= kWgrad && IM < kSpan;
-    constexpr bool kSp = IM >= kSpan && IM < kPhase;
     constexpr bool kPh = IM >= kPhase;
-    constexpr int kSpanKind = !kSp ? 0 : IM >= kSpanOdd ? 2 : 1;
+    constexpr bool kSp = (IM >= kSpan && IM < kPhase) || IM >= kPhaseSpan;
+    constexpr int kSpanKind = !kSp ? 0 : ((IM >= kSpanOdd && IM < kPhase) || IM >= kPhaseSpanOdd) ? 2 : 1;
     constexpr int kMode = IM == kImNone ? 0 : IM % 8;
     static_assert(IM == kImNone || (!TA && TB == kWg), "forward: NN; weight gradient: NT");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
@@ -601,13 +602,19 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
         for (int tj = 0; tj < TN; ++tj) {
             const uint32_t j = n0 + wn0 + tj * 32 + l32;
             if (j >= g.n) continue;
-            float *ccol = gc + j;  // column j of C
+            // Column j of C: position jp of image img (span), and with a
+            // phase that position's pixel.
+            float *cimg = gc;
+            uint32_t jp = j;
             if constexpr (kSp) {
                 const uint32_t img = fdiv(j, cv.div_npos);
-                ccol = gc + (size_t)img * cv.c_img + (j - img * cv.npos);
-            } else if constexpr (kPh) {
-                const uint32_t yq = fdiv(j, cv.div_wp), xq = j - yq * cv.div_wp.d;
-                ccol = gc + (cv.ph_s * yq + cv.ph_py) * cv.ph_w + cv.ph_s * xq + cv.ph_px;
+                cimg = gc + (size_t)img * cv.c_img;
+                jp = j - img * cv.npos;
+            }
+            float *ccol = cimg + jp;
+            if constexpr (kPh) {
+                const uint32_t yq = fdiv(jp, cv.div_wp), xq = jp - yq * cv.div_wp.d;
+                ccol = cimg + (cv.ph_s * yq + cv.ph_py) * cv.ph_w + cv.ph_s * xq + cv.ph_px;
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -785,8 +792,12 @@ inline bool use_span(uint64_t batch, uint64_t m, uint64_t n, bool big) {
     return (DKZ_SPAN_BM == 128 && m >= 128) || span_pays(n, big ? 128 : 64);
 }
 
-template <int MODE>
-int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, uint64_t b_img, uint64_t c_img) {
+// PH: `phases` phases of a strided data gradient per launch (kPhaseSpan, or
+// kPhaseSpanOdd when the positions per image are not a multiple of 4; grid
+// row = phase x group).
+template <int MODE, bool PH = false>
+int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, uint64_t b_img, uint64_t c_img,
+                uint32_t phases = 1) {
     const uint32_t npos = g.n;
     g.n = batch * npos;
     g.tiles_m = div_up(g.m, 64);
@@ -796,18 +807,37 @@ int launch_span(const char *name, GemmArgs g, uint32_t batch, uint32_t groups, u
     g.cv.npos4 = npos % 4 == 0;
     g.cv.b_img = (uint32_t)b_img;
     g.cv.c_img = (uint32_t)c_img;
+    g.zrows = groups;
     constexpr int D = DKZ_GEMM_SMALL_PREFETCH;
-    if (DKZ_SPAN_BM == 128 && g.m >= 128) {
-        g.tiles_m = div_up(g.m, 128);
-        if (npos % 4 == 0) return launch_batched<128, 64, 1, kSpan + MODE>(name, g, groups);
-        if constexpr (MODE != kTwoBlock && MODE != kRow) return launch_batched<128, 64, 1, kSpanOdd + MODE>(name, g, groups);
-    }
-    if (npos % 4 == 0) return launch_batched<64, 64, D, kSpan + MODE>(name, g, groups);
-    if constexpr (MODE == kTwoBlock || MODE == kRow) {
-        DKZ_REQUIRE(npos % 4 == 0);  // row gathers are chosen only then
-        return 0;
+    if constexpr (PH) {
+        DKZ_REQUIRE(phases >= 1 && phases <= (uint32_t)kMaxPhases);
+        const bool big = DKZ_SPAN_BM == 128 && g.m >= 128;
+        if (big) g.tiles_m = div_up(g.m, 128);
+        if (npos % 4 == 0) {
+            if (big) return launch_batched<128, 64, 1, kPhaseSpan + MODE>(name, g, phases * groups);
+            return launch_batched<64, 64, D, kPhaseSpan + MODE>(name, g, phases * groups);
+        }
+        if constexpr (MODE == kTwoBlock || MODE == kRow) {
+            DKZ_REQUIRE(npos % 4 == 0);  // row gathers are chosen only then
+            return 0;
+        } else {
+            if (big) return launch_batched<128, 64, 1, kPhaseSpanOdd + MODE>(name, g, phases * groups);
+            return launch_batched<64, 64, D, kPhaseSpanOdd + MODE>(name, g, phases * groups);
+        }
     } else {
-        return launch_batched<64, 64, D, kSpanOdd + MODE>(name, g, groups);
+        if (DKZ_SPAN_BM == 128 && g.m >= 128) {
+            g.tiles_m = div_up(g.m, 128);
+            if (npos % 4 == 0) return launch_batched<128, 64, 1, kSpan + MODE>(name, g, groups);
+            if constexpr (MODE != kTwoBlock && MODE != kRow)
+                return launch_batched<128, 64, 1, kSpanOdd + MODE>(name, g, groups);
+        }
+        if (npos % 4 == 0) return launch_batched<64, 64, D, kSpan + MODE>(name, g, groups);
+        if constexpr (MODE == kTwoBlock || MODE == kRow) {
+            DKZ_REQUIRE(npos % 4 == 0);  // row gathers are chosen only then
+            return 0;
+        } else {
+            return launch_batched<64, 64, D, kSpanOdd + MODE>(name, g, groups);
+        }
     }
 }
 
@@ -1244,6 +1274,17 @@ int dkz_convolution_data_gradient(int batch, int groups, int channels, int heigh
         gp.tiles_n = (uint32_t)div_up(n, big ? 128 : 64);
         constexpr int kPS1 = kPhase + kTwoBlock, kPGa = kPhase + kGather, kPRw = kPhase + kRow;
         constexpr const char *kName = "convolution_data_gradient";
+        if (use_span(batch, cg, n, big)) {
+            // Columns over (image, phase position) of every image.
+            const uint64_t b_img = (uint64_t)groups * m * npos, c_img = (uint64_t)groups * in_group;
+            const uint32_t b = (uint32_t)batch, gr = (uint32_t)groups, pc = (uint32_t)cnt;
+            constexpr bool kPh = true;
+            DKZ_TRY(cv.s1     ? (launch_span<kTwoBlock, kPh>(kName, gp, b, gr, b_img, c_img, pc))
+                    : cv.row4 ? (launch_span<kRow, kPh>(kName, gp, b, gr, b_img, c_img, pc))
+                              : (launch_span<kGather, kPh>(kName, gp, b, gr, b_img, c_img, pc)));
+            i0 += cnt;
+            continue;
+        }
         // At most 65535 grid rows: cnt phases x zc (image, group) rows, whole
         // images each.
         const uint64_t rows = 65535 / cnt, zchunk = rows - rows % (uint64_t)groups;

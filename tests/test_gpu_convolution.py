@@ -244,7 +244,13 @@ DG_CASES = [
     (2, 1, 6, 12, 12, 5, 3, 3, 1),      # stride 3: nine one-tap phases, launched four, four and one at a time
     (2, 2, 10, 12, 10, 6, 5, 3, 2),     # stride 3, window 5 (phases of 4, 2 and 1 taps), width 10: one per launch
     (3, 1, 5, 15, 15, 7, 5, 3, 1),      # stride 3, window 5, merged phases of unequal tap counts
-    (96, 1, 128, 56, 56, 8, 3, 2, 1),   # stride 2, 128 input channels: four phases per launch in 128x128 tiles
+    (96, 1, 128, 56, 56, 8, 3, 2, 1),   # stride 2, 128 input channels: four phases per launch over every image
+    (8, 1, 16, 12, 12, 8, 3, 2, 1),     # stride 2, 6x6 phases: columns over (image, phase position), 64x64 tiles
+    (4, 1, 128, 16, 16, 8, 3, 2, 0),    # the same in 128x64 tiles, phase rows of 8 (row gathers), delta rows of 7
+    (4, 1, 128, 12, 12, 8, 3, 2, 1),    # 128x64 tiles, phase rows of 6 (per-element gathers)
+    (4, 2, 256, 12, 12, 8, 3, 2, 1),    # the same with two groups
+    (4, 1, 128, 14, 14, 8, 3, 2, 1),    # 7x7 phases (49 positions per image) over every image, 128x64 tiles
+    (8, 1, 16, 14, 14, 8, 3, 2, 1),     # the same in 64x64 tiles
 ]
 
 
