@@ -17,6 +17,11 @@
 // the result is bit-exact with no atomics. Elements with no contributor are
 // not written (0 + -0 would otherwise flip a sign).
 //
+// Planes that fit in 48 KiB of LDS take one workgroup each: the forward reads
+// the input plane into LDS once and scans every window from there, and the
+// stride-1 backward with windows wider than 2 stages the plane's indexes and
+// deltas the same way before its gather.
+//
 // Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
 // a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
 // two adjacent outputs and their 2x4 input patch, read and written as two
@@ -41,6 +46,12 @@ struct PoolGeom {
 // are all issued before any of them is used.
 
 // ---- generic ----------------------------------------------------------------
+
+// The forward through one workgroup per plane when the plane fits in LDS
+// (build-time switch, for measurement).
+#ifndef DKZ_POOL_PLANE
+#define DKZ_POOL_PLANE 1
+#endif
 
 // Candidate outputs of input (y, x) -- those whose window covers it: rows
 // i with i*stride + n - half_pad == y for some n in [0, size), i.e. rows
@@ -96,6 +107,48 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
     idx[o] = mi;
 }
 
+// Forward, one workgroup per input plane (h*w floats, at most
+// kPlaneMaxFloats): the plane is read once into LDS (float4s when VEC: the
+// planes are 16-byte aligned), then each lane scans its outputs' windows
+// from LDS in the twin's order.
+constexpr uint32_t kPlaneMaxFloats = 12288;  // 48 KiB of LDS
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void maxpool_plane_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g) {
+    extern __shared__ float4 plane_lds4[];
+    float *pl = reinterpret_cast<float *>(plane_lds4);
+    const uint32_t plane = blockIdx.x, hw = g.h * g.w, ohw = g.oh * g.ow;
+    const float *src = in + (size_t)plane * hw;
+    if constexpr (VEC) {
+        for (uint32_t q = threadIdx.x; q < hw / 4; q += kBlock) plane_lds4[q] = reinterpret_cast<const float4 *>(src)[q];
+    } else {
+        for (uint32_t q = threadIdx.x; q < hw; q += kBlock) pl[q] = src[q];
+    }
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < ohw; o += kBlock) {
+        const uint32_t i = fdiv(o, g.div_ow), j = o - i * g.ow;
+        const int ch0 = (int)(i * g.stride) - (int)g.half_pad, cw0 = (int)(j * g.stride) - (int)g.half_pad;
+        float mx = -FLT_MAX;
+        int mi = -1;
+        for (uint32_t n = 0; n < g.size; ++n) {
+            const int ch = ch0 + (int)n;
+            if (ch < 0 || ch >= (int)g.h) continue;
+            const float *row = pl + (uint32_t)ch * g.w;
+            for (uint32_t m = 0; m < g.size; ++m) {
+                const int cw = cw0 + (int)m;
+                if (cw < 0 || cw >= (int)g.w) continue;
+                const float v = row[cw];
+                if (v > mx) {
+                    mx = v;
+                    mi = (int)(plane * hw + (uint32_t)ch * g.w + (uint32_t)cw);
+                }
+            }
+        }
+        out[(size_t)plane * ohw + o] = mx;
+        idx[(size_t)plane * ohw + o] = mi;
+    }
+}
+
 template <int TB>
 __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta, float *prev, const int *idx,
                                                              PoolGeom g, uint32_t in_n) {
@@ -145,6 +198,41 @@ __global__ __launch_bounds__(kBlock) void maxpool_bwd_kernel(const float *delta,
         }
     }
     if (touched) prev[e] = v;
+}
+
+// Backward with stride 1 and windows wider than 2, one workgroup per plane
+// (oh*ow outputs, at most kPlaneMaxFloats / 2): the plane's indexes and deltas are read once into
+// LDS, then each lane gathers for its inputs -- consecutive across lanes --
+// exactly as maxpool_bwd_kernel does, from LDS.
+__global__ __launch_bounds__(kBlock) void maxpool_plane_bwd_kernel(const float *delta, float *prev, const int *idx,
+                                                                   PoolGeom g) {
+    extern __shared__ float4 plane_lds4[];
+    const uint32_t plane = blockIdx.x, hw = g.h * g.w, ohw = g.oh * g.ow;
+    int *il = reinterpret_cast<int *>(plane_lds4);
+    float *dl = reinterpret_cast<float *>(plane_lds4) + ohw;
+    for (uint32_t q = threadIdx.x; q < ohw; q += kBlock) {
+        il[q] = idx[(size_t)plane * ohw + q];
+        dl[q] = delta[(size_t)plane * ohw + q];
+    }
+    __syncthreads();
+    for (uint32_t el = threadIdx.x; el < hw; el += kBlock) {
+        const uint32_t y = fdiv(el, g.div_w), x = el - y * g.w;
+        int ilo, ihi, jlo, jhi;
+        pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
+        const uint32_t e = plane * hw + el;
+        float v = 0.0f;
+        bool touched = false;
+        for (int ci = ilo; ci <= ihi; ++ci) {
+            for (int cj = jlo; cj <= jhi; ++cj) {
+                const uint32_t o = (uint32_t)ci * g.ow + (uint32_t)cj;
+                if (il[o] != (int)e) continue;
+                if (!touched) v = prev[e];
+                touched = true;
+                v += dl[o];
+            }
+        }
+        if (touched) prev[e] = v;
+    }
 }
 
 // Backward, one lane per output (stride >= 2, where outputs are a quarter of
@@ -330,6 +418,16 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
         return launch("forward_maxpool_2x2", maxpool2_fwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
                       input, output, indexes, g, pairs);
     }
+    const uint64_t hw = (uint64_t)g.h * g.w;
+    if (DKZ_POOL_PLANE && hw > 0 && hw <= kPlaneMaxFloats) {
+        const dim3 pgrid((uint32_t)planes), block(kBlock);
+        const size_t lds = (size_t)hw * sizeof(float);
+        const bool vec = aligned16(input) && hw % 4 == 0;
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(vec ? maxpool_plane_fwd_kernel<true> : maxpool_plane_fwd_kernel<false>, pgrid, block, lds,
+                           current_stream(), input, output, indexes, g);
+        return after_launch("forward_maxpool_plane", pgrid, block);
+    }
     const dim3 grid(div_up((uint32_t)out_n, kBlock));
     if (g.size <= 2)
         return launch("forward_maxpool", maxpool_fwd_kernel<4>, grid, dim3(kBlock), input, output, indexes, g,
@@ -366,6 +464,16 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
                           indexes, g, out_n, (uint32_t)in_n);
         return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
                       indexes, g, out_n, (uint32_t)in_n);
+    }
+    const uint64_t ohw = (uint64_t)g.oh * g.ow;
+    // Through LDS when more than 2x2 outputs can cover an input (2x2 windows
+    // measured faster with the batched loads of maxpool_bwd_kernel).
+    if (DKZ_POOL_PLANE && per_dim > 2 && ohw <= kPlaneMaxFloats / 2) {
+        const dim3 pgrid((uint32_t)planes), block(kBlock);
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(maxpool_plane_bwd_kernel, pgrid, block, (size_t)ohw * 8, current_stream(), delta,
+                           prev_delta, indexes, g);
+        return after_launch("backward_maxpool_plane", pgrid, block);
     }
     const dim3 grid(div_up((uint32_t)in_n, kBlock));
     if (per_dim <= 2)

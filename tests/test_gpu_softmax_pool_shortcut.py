@@ -105,6 +105,14 @@ MAXPOOL_CASES = [
     (1, 2, 7, 7, 3, 1, 2),        # darknet size=3 stride=1 (default pad size-1)
     (2, 2, 6, 10, 5, 3, 4),
     (256, 512, 28, 28, 2, 2, 1),  # config 5
+    (8, 64, 56, 56, 3, 2, 2),     # generic forward: one workgroup per plane in LDS (float4 loads)
+    (2, 3, 9, 9, 2, 1, 1),        # plane of 81 floats: element loads
+    (2, 3, 9, 9, 3, 1, 2),        # stride-1 backward through LDS, odd plane
+    (2, 4, 13, 13, 13, 1, 12),    # spatial pyramid pooling's 13x13 window
+    (2, 3, 110, 110, 3, 2, 2),    # the largest planes held in LDS (12100 floats)
+    (2, 3, 120, 120, 3, 2, 2),    # larger planes: one lane per output
+    (2, 3, 78, 78, 3, 1, 2),      # stride-1 backward: the largest output planes held in LDS (6084)
+    (1, 2, 80, 80, 3, 1, 2),      # larger: one lane per input
 ]
 
 
