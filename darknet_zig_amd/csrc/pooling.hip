@@ -52,6 +52,9 @@ struct PoolGeom {
 #ifndef DKZ_POOL_PLANE
 #define DKZ_POOL_PLANE 1
 #endif
+#ifndef DKZ_POOL_PLANE_UNROLL
+#define DKZ_POOL_PLANE_UNROLL 1
+#endif
 
 // Candidate outputs of input (y, x) -- those whose window covers it: rows
 // i with i*stride + n - half_pad == y for some n in [0, size), i.e. rows
@@ -113,7 +116,9 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
 // from LDS in the twin's order.
 constexpr uint32_t kPlaneMaxFloats = 12288;  // 48 KiB of LDS
 
-template <bool VEC>
+// S > 0: the window is S x S (its taps unrolled, all reads issued first);
+// S == 0: g.size.
+template <bool VEC, int S>
 __global__ __launch_bounds__(kBlock) void maxpool_plane_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g) {
     extern __shared__ float4 plane_lds4[];
     float *pl = reinterpret_cast<float *>(plane_lds4);
@@ -130,6 +135,28 @@ __global__ __launch_bounds__(kBlock) void maxpool_plane_fwd_kernel(const float *
         const int ch0 = (int)(i * g.stride) - (int)g.half_pad, cw0 = (int)(j * g.stride) - (int)g.half_pad;
         float mx = -FLT_MAX;
         int mi = -1;
+        if constexpr (S > 0) {
+            float v[S * S];
+            bool ok[S * S];
+#pragma unroll
+            for (int n = 0; n < S; ++n)
+#pragma unroll
+                for (int m = 0; m < S; ++m) {
+                    const int ch = ch0 + n, cw = cw0 + m;
+                    ok[n * S + m] = ch >= 0 && ch < (int)g.h && cw >= 0 && cw < (int)g.w;
+                    v[n * S + m] = ok[n * S + m] ? pl[(uint32_t)ch * g.w + (uint32_t)cw] : 0.0f;
+                }
+#pragma unroll
+            for (int t = 0; t < S * S; ++t) {
+                if (ok[t] && v[t] > mx) {
+                    mx = v[t];
+                    mi = (int)(plane * hw + (uint32_t)(ch0 + t / S) * g.w + (uint32_t)(cw0 + t % S));
+                }
+            }
+            out[(size_t)plane * ohw + o] = mx;
+            idx[(size_t)plane * ohw + o] = mi;
+            continue;
+        }
         for (uint32_t n = 0; n < g.size; ++n) {
             const int ch = ch0 + (int)n;
             if (ch < 0 || ch >= (int)g.h) continue;
@@ -424,8 +451,10 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
         const size_t lds = (size_t)hw * sizeof(float);
         const bool vec = aligned16(input) && hw % 4 == 0;
         (void)hipGetLastError();
-        hipLaunchKernelGGL(vec ? maxpool_plane_fwd_kernel<true> : maxpool_plane_fwd_kernel<false>, pgrid, block, lds,
-                           current_stream(), input, output, indexes, g);
+        auto k = vec ? maxpool_plane_fwd_kernel<true, 0> : maxpool_plane_fwd_kernel<false, 0>;
+        if (DKZ_POOL_PLANE_UNROLL && g.size == 3) k = vec ? maxpool_plane_fwd_kernel<true, 3> : maxpool_plane_fwd_kernel<false, 3>;
+        if (DKZ_POOL_PLANE_UNROLL && g.size == 2) k = vec ? maxpool_plane_fwd_kernel<true, 2> : maxpool_plane_fwd_kernel<false, 2>;
+        hipLaunchKernelGGL(k, pgrid, block, lds, current_stream(), input, output, indexes, g);
         return after_launch("forward_maxpool_plane", pgrid, block);
     }
     const dim3 grid(div_up((uint32_t)out_n, kBlock));
