@@ -20,7 +20,8 @@
 // Planes that fit in 48 KiB of LDS take one workgroup each: the forward reads
 // the input plane into LDS once and scans every window from there, and the
 // stride-1 backward with windows wider than 2 stages the plane's indexes and
-// deltas the same way before its gather.
+// deltas the same way before its gather; with stride >= 2 the plane of
+// prev_delta joins them, is updated in LDS and written back whole.
 //
 // Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
 // a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
@@ -320,6 +321,68 @@ __global__ __launch_bounds__(kBlock) void maxpool_bwd_out_kernel(const float *de
     if (mine) prev[t] = v;
 }
 
+// Backward with stride >= 2, one workgroup per plane (h*w inputs plus oh*ow
+// outputs within kPlaneMaxFloats): the plane of prev_delta and the outputs'
+// indexes and deltas are read into LDS, each output lane applies
+// maxpool_bwd_out_kernel's rule there (the lowest output naming an input
+// adds all of that input's deltas in order, so every touched element has
+// one writer), and the plane is written back whole (untouched elements keep
+// their bits). VEC: the prev_delta planes are 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void maxpool_plane_bwd_out_kernel(const float *delta, float *prev, const int *idx,
+                                                                       PoolGeom g) {
+    extern __shared__ float4 plane_lds4[];
+    const uint32_t plane = blockIdx.x, hw = g.h * g.w, ohw = g.oh * g.ow;
+    float *pl = reinterpret_cast<float *>(plane_lds4);
+    int *il = reinterpret_cast<int *>(pl + hw);
+    float *dl = pl + hw + ohw;
+    float *dst = prev + (size_t)plane * hw;
+    if constexpr (VEC) {
+        for (uint32_t q = threadIdx.x; q < hw / 4; q += kBlock) plane_lds4[q] = reinterpret_cast<const float4 *>(dst)[q];
+    } else {
+        for (uint32_t q = threadIdx.x; q < hw; q += kBlock) pl[q] = dst[q];
+    }
+    for (uint32_t q = threadIdx.x; q < ohw; q += kBlock) {
+        il[q] = idx[(size_t)plane * ohw + q];
+        dl[q] = delta[(size_t)plane * ohw + q];
+    }
+    __syncthreads();
+    const int base = (int)(plane * hw);
+    for (uint32_t o = threadIdx.x; o < ohw; o += kBlock) {
+        const int tv = il[o] - base;
+        if (tv < 0 || (uint32_t)tv >= hw) continue;  // -1, or outside this plane
+        const uint32_t t = (uint32_t)tv;
+        const uint32_t y = fdiv(t, g.div_w), x = t - y * g.w;
+        int ilo, ihi, jlo, jhi;
+        pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
+        bool mine = false, lower = false;
+        float v = 0.0f;
+        for (int ci = ilo; ci <= ihi && !lower; ++ci) {
+            for (int cj = jlo; cj <= jhi; ++cj) {
+                const uint32_t oc = (uint32_t)ci * g.ow + (uint32_t)cj;
+                if (il[oc] != il[o]) continue;
+                if (oc < o) {
+                    lower = true;  // a lower output adds into t first
+                    break;
+                }
+                if (oc == o) {
+                    v = pl[t] + dl[oc];
+                    mine = true;
+                } else if (mine) {
+                    v += dl[oc];
+                }
+            }
+        }
+        if (mine && !lower) pl[t] = v;
+    }
+    __syncthreads();
+    if constexpr (VEC) {
+        for (uint32_t q = threadIdx.x; q < hw / 4; q += kBlock) reinterpret_cast<float4 *>(dst)[q] = plane_lds4[q];
+    } else {
+        for (uint32_t q = threadIdx.x; q < hw; q += kBlock) dst[q] = pl[q];
+    }
+}
+
 // ---- 2x2, stride 2, offset 0 ------------------------------------------------
 
 __device__ __forceinline__ void max_tap(float val, int index, float &mx, int &mi) {
@@ -485,6 +548,16 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
     }
     // Outputs whose window covers one input, per dimension: at most ceil(size / stride).
     const uint32_t per_dim = (g.size + g.stride - 1) / g.stride;
+    const uint64_t ohw = (uint64_t)g.oh * g.ow;
+    if (DKZ_POOL_PLANE && g.stride >= 2 && per_plane + 2 * ohw <= kPlaneMaxFloats) {
+        const dim3 pgrid((uint32_t)planes), block(kBlock);
+        const size_t lds = (size_t)(per_plane + 2 * ohw) * sizeof(float);
+        const bool vec = aligned16(prev_delta) && per_plane % 4 == 0;
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(vec ? maxpool_plane_bwd_out_kernel<true> : maxpool_plane_bwd_out_kernel<false>, pgrid,
+                           block, lds, current_stream(), delta, prev_delta, indexes, g);
+        return after_launch("backward_maxpool_plane", pgrid, block);
+    }
     if (g.stride >= 2) {
         const uint32_t out_n = (uint32_t)(planes * g.oh * g.ow);
         const dim3 ogrid(div_up(out_n, kBlock));
@@ -494,7 +567,6 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
         return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
                       indexes, g, out_n, (uint32_t)in_n);
     }
-    const uint64_t ohw = (uint64_t)g.oh * g.ow;
     // Through LDS when more than 2x2 outputs can cover an input (2x2 windows
     // measured faster with the batched loads of maxpool_bwd_kernel).
     if (DKZ_POOL_PLANE && per_dim > 2 && ohw <= kPlaneMaxFloats / 2) {
