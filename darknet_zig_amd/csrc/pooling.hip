@@ -53,6 +53,10 @@ struct PoolGeom {
 #ifndef DKZ_POOL_PLANE
 #define DKZ_POOL_PLANE 1
 #endif
+// Floats of LDS a plane workgroup may take (12288: 48 KiB).
+#ifndef DKZ_POOL_PLANE_MAX
+#define DKZ_POOL_PLANE_MAX 12288
+#endif
 #ifndef DKZ_POOL_PLANE_UNROLL
 #define DKZ_POOL_PLANE_UNROLL 1
 #endif
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
 // kPlaneMaxFloats): the plane is read once into LDS (float4s when VEC: the
 // planes are 16-byte aligned), then each lane scans its outputs' windows
 // from LDS in the twin's order.
-constexpr uint32_t kPlaneMaxFloats = 12288;  // 48 KiB of LDS
+constexpr uint32_t kPlaneMaxFloats = DKZ_POOL_PLANE_MAX;
 
 // S > 0: the window is S x S (its taps unrolled, all reads issued first);
 // S == 0: g.size.
