@@ -15,16 +15,23 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                duration from per-kernel HIP events over the same steps (less
                the event-pair overhead: the per-step excess of the event-timed
                steps over the clean ones, spread over the 7 pairs), against
-               MI355X's 8 TB/s HBM peak; traffic from the committed counter
-               summary profiles/traffic_bn_backward.txt
+               MI355X's 8 TB/s HBM peak; traffic: that kernel's HBM bytes per
+               launch from the committed counter table
+               profiles/traffic_per_op.md (see traffic_table())
+  chain_kernels  each chain kernel's time; only the first starts cold, the
+               later ones re-read operands the previous kernel touched, which
+               the 256 MB Infinity Cache may hold ("MALL-assisted")
   per_op       every op of BASELINE.json's five configs timed on its own,
                cold (rotated buffers, >= 512 MB per rotation), in GB/s and as
-               a fraction of 8 TB/s: sustained (back-to-back launches, the
-               per-launch time of a stream of such calls) and single-launch
-               (an event pair around each launch); plus rand_uniform/dropout,
-               the one-pass Adam update, im2col/col2im, and shapes off the
-               configs' fast paths (a 3x3/s2 max pool, a spatial softmax, a
-               connected layer's bias gradient)
+               a fraction of 8 TB/s: `us` sustained (the launches captured in
+               a HIP graph and replayed back to back), `issued_us` (issued one
+               by one from Python: host-bound below ~4 us), single-launch (an
+               event pair around each launch); rows marked [hot cache] replay
+               one buffer set, whose data the Infinity Cache holds; plus
+               rand_uniform/dropout, the one-pass Adam update, im2col/col2im,
+               shapes off the configs' fast paths (a 3x3/s2 max pool, a
+               spatial softmax, a connected layer's bias gradient), and the
+               batch-norm layer's other direction at each config's shape
   gemm         dkz_gemm at config 2's convolution shapes and a large square,
                and config 2's convolutional layer forward, weight gradient
                and data gradient over the batch (the per-image loops against
@@ -33,22 +40,22 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (one reduction
                pass and one apply pass, 32 B/elem instead of 56)
-  bn_act_gelem_s  config 1 elements / config 1 forward time and config 2
-               elements / config 2 backward time: per-op (chained, and the sum
-               of single-op times), the whole per-op layer forward with its
-               copies and EMA, and the fused entry points
-  cpu_baseline the CPU twins' C restatement (oracle/) on the same inputs on
-               this host, one thread, median of 3 full config-2 chains
+  bn_act_gelem_s  batch-norm + activation elements per second: config 1's
+               forward and config 2's backward (per op, the whole per-op layer
+               forward, fused), and each config's layer forward + backward
+  cpu_baseline the CPU twins' C restatement (oracle/) on every config's ops
+               and inputs, one host thread, median of 5 runs; `value` is
+               config 2's (the headline workload), `per_config` all five
 
 Algorithmic bytes count every logical fp32/int32 element read or written once
 (4 B); per-channel vectors of C floats are not counted.
 
 --per-op-traffic runs each per-op row's first three launches once between two
 marker dispatches (after one untimed pass over all its rotations) and prints
-the rows, for
-rocprofv3 FETCH_SIZE/WRITE_SIZE runs and a kernel trace to attribute HBM
-traffic and kernel time per row (profiles/traffic_per_op.md);
---copy-calibration runs the known-size copy that scales those counters.
+the rows, for rocprofv3 counter runs (READ_COUNTERS, WRITE_COUNTERS) and a
+kernel trace that attribute HBM traffic and kernel time to each row;
+--copy-calibration runs a known-size copy that checks the counter formula;
+--traffic-table DIR prints the table (profiles/traffic_per_op.md) from them.
 """
 
 from __future__ import annotations
@@ -86,10 +93,20 @@ class Hip:
             "hipEventElapsedTime": [C.POINTER(C.c_float), C.c_void_p, C.c_void_p],
             "hipEventDestroy": [C.c_void_p],
             "hipDeviceSynchronize": [],
+            "hipStreamCreate": [C.POINTER(C.c_void_p)],
+            "hipStreamDestroy": [C.c_void_p],
+            "hipStreamSynchronize": [C.c_void_p],
+            "hipStreamBeginCapture": [C.c_void_p, C.c_int],
+            "hipStreamEndCapture": [C.c_void_p, C.POINTER(C.c_void_p)],
+            "hipGraphInstantiate": [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t],
+            "hipGraphLaunch": [C.c_void_p, C.c_void_p],
+            "hipGraphExecDestroy": [C.c_void_p],
+            "hipGraphDestroy": [C.c_void_p],
         }.items():
             fn = getattr(self.lib, name)
             fn.argtypes = args
             fn.restype = C.c_int
+        self._stream = None
 
     def event(self) -> C.c_void_p:
         e = C.c_void_p()
@@ -107,6 +124,14 @@ class Hip:
 
     def sync(self) -> None:
         assert self.lib.hipDeviceSynchronize() == 0
+
+    def capture_stream(self) -> C.c_void_p:
+        """A stream (default priority) to capture graphs on, made once."""
+        if self._stream is None:
+            s = C.c_void_p()
+            assert self.lib.hipStreamCreate(C.byref(s)) == 0
+            self._stream = s
+        return self._stream
 
 
 # ---------------------------------------------------------------------------
@@ -283,6 +308,48 @@ def time_op(hip, stream, fns, launches, warmup=3):
     return statistics.mean(hip.ms(a, b) for a, b in evs)
 
 
+def time_graph(hip, seqs, launches, warmup=1):
+    """Mean time (ms) of one pass of an op sequence, cycling over rotated
+    sets, with `launches` passes captured into one HIP graph and replayed:
+    the kernels run back to back on the GPU as in a stream of such calls, and
+    the host's per-call issue time (ctypes, ~3 us a call) is not in the
+    figure. The library is pointed at the capture stream for the capture
+    and back at the null stream afterwards."""
+    from darknet_zig_amd import _lib
+
+    lib = _lib.load()
+    s = hip.capture_stream()
+    hip.sync()
+    assert lib.dkz_set_stream(s) == 0
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        assert hip.lib.hipStreamBeginCapture(s, 0) == 0  # hipStreamCaptureModeGlobal
+        try:
+            for k in range(launches):
+                for fn in seqs[k % len(seqs)]:
+                    fn()
+        finally:
+            rc = hip.lib.hipStreamEndCapture(s, C.byref(graph))
+        assert rc == 0, rc
+    finally:
+        lib.dkz_set_stream(None)
+    assert hip.lib.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+    try:
+        for _ in range(warmup):
+            assert hip.lib.hipGraphLaunch(exe, s) == 0
+        assert hip.lib.hipStreamSynchronize(s) == 0
+        a, b = hip.event(), hip.event()
+        hip.record(a, s)
+        assert hip.lib.hipGraphLaunch(exe, s) == 0
+        hip.record(b, s)
+        ms = hip.ms(a, b)
+        assert hip.lib.hipStreamSynchronize(s) == 0
+    finally:
+        hip.lib.hipGraphExecDestroy(exe)
+        hip.lib.hipGraphDestroy(graph)
+    return ms / launches
+
+
 def gbs(nbytes: int, ms: float) -> float:
     return nbytes / (ms * 1e-3) / 1e9
 
@@ -305,13 +372,17 @@ MARK_BASE = 1000
 TRAFFIC_PASSES = 3
 
 
-def per_op_table(gpu, hip, stream, launches: int, traffic=None):
+def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     """The per-op table; with `traffic` (a list), no timing: each row's first
     TRAFFIC_PASSES launches (or call sequences) run once between markers and
-    the row is appended to `traffic`."""
+    the row is appended to `traffic`. `only`: time only rows whose config
+    name contains this string."""
     from darknet_zig_amd.activations import Activation
 
     rows = {}
+
+    def wanted(cfg):
+        return only is None or only in cfg
     if traffic is not None:
         mark_buf = gpu.alloc((MARK_BASE + 256) * 256 + 1)
 
@@ -334,30 +405,48 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
         traffic.append({"row": f"{cfg}/{name}", "bytes": nbytes, "passes": passes, "begin_grid": MARK_BASE + 2 * i})
         print(f"traffic row {i}: {cfg}/{name}", file=sys.stderr, flush=True)
 
-    def row(cfg, name, nbytes, ms, single_ms=None):
+    def row(cfg, name, nbytes, ms, single_ms=None, issued_ms=None):
         g = gbs(nbytes, ms)
         rows[f"{cfg}/{name}"] = r = {"us": round(ms * 1e3, 3), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4),
                                      "bytes": nbytes}
+        if issued_ms is not None:
+            r["issued_us"] = round(issued_ms * 1e3, 3)
         if single_ms is not None:
             r["single_launch_us"] = round(single_ms * 1e3, 3)
             r["single_launch_frac"] = round(gbs(nbytes, single_ms) / PEAK_GBS, 4)
 
-    def add(cfg, name, nbytes, fns):
-        """One op over rotated inputs: sustained (back-to-back launches, events
-        around the run: the per-launch figure of a stream of such calls) and
+    def add(cfg, name, nbytes, fns, hot=False):
+        """One op over rotated inputs (cold: >= 512 MB between two uses of a
+        buffer): sustained (`us`: the launches captured in a HIP graph and
+        replayed back to back, the per-launch figure of a stream of such
+        calls), `issued_us` (the same calls issued one by one from Python,
+        which for launches under ~4 us measures the host's issue rate),
         single-launch (an event pair around each launch, which also times
-        ~2 us of dispatch and completion)."""
+        ~2 us of dispatch and completion). `hot`: also a row labelled
+        [hot cache], the op replayed on one buffer set, whose data the 256 MB
+        Infinity Cache then holds."""
+        if not wanted(cfg):
+            return
         if traffic is not None:
             return traced(cfg, name, nbytes, [[f] for f in fns])
         k = max(launches, len(fns))
-        row(cfg, name, nbytes, time_seq(hip, stream, [[f] for f in fns], k), time_op(hip, stream, fns, k))
+        seqs = [[f] for f in fns]
+        row(cfg, name, nbytes, time_graph(hip, seqs, k), time_op(hip, stream, fns, k), time_seq(hip, stream, seqs, k))
+        if hot:
+            row(cfg, name + " [hot cache]", nbytes, time_graph(hip, seqs[:1], max(launches, 64)))
 
-    def add_seq(cfg, name, nbytes, seqs):
-        """A call sequence (or a multi-launch entry point), events only around
-        the whole timed region, as a layer would issue it back to back."""
+    def add_seq(cfg, name, nbytes, seqs, hot=False):
+        """A call sequence (or a multi-launch entry point) over rotated sets,
+        graph-replayed back to back as a layer would issue it (`issued_us`:
+        issued from Python); `hot` as in add()."""
+        if not wanted(cfg):
+            return
         if traffic is not None:
             return traced(cfg, name, nbytes, seqs)
-        row(cfg, name, nbytes, time_seq(hip, stream, seqs, max(launches, len(seqs))))
+        k = max(launches, len(seqs))
+        row(cfg, name, nbytes, time_graph(hip, seqs, k), issued_ms=time_seq(hip, stream, seqs, k))
+        if hot:
+            row(cfg, name + " [hot cache]", nbytes, time_graph(hip, seqs[:1], max(launches, 64)))
 
     # -- config 1: BN forward + leaky, [128,32,32,32], x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1)
     dev = Device(gpu)
@@ -373,12 +462,12 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     gpu.mean(xs[0], B, F, S, m)
     gpu.variance(xs[0], m, B, F, S, v)
     cfg = "cfg1_bn_fwd[128,32,32,32]"
-    add(cfg, "mean", E, [lambda b=b: gpu.mean(b, B, F, S, m) for b in xs])
-    add(cfg, "variance", E, [lambda b=b: gpu.variance(b, m, B, F, S, v) for b in xs])
-    add(cfg, "normalize", 2 * E, [lambda b=b: gpu.normalize(b, m, v, B, F, S) for b in xs])
-    add(cfg, "scale_bias", 2 * E, [lambda b=b: gpu.scaleBias(b, gam, B, F, S) for b in xs])
-    add(cfg, "add_bias", 2 * E, [lambda b=b: gpu.addBias(b, bet, B, F, S) for b in xs])
-    add(cfg, "activate(leaky)", 2 * E, [lambda b=b: gpu.activateArray(b, n, Activation.leaky) for b in xs])
+    add(cfg, "mean", E, [lambda b=b: gpu.mean(b, B, F, S, m) for b in xs], hot=True)
+    add(cfg, "variance", E, [lambda b=b: gpu.variance(b, m, B, F, S, v) for b in xs], hot=True)
+    add(cfg, "normalize", 2 * E, [lambda b=b: gpu.normalize(b, m, v, B, F, S) for b in xs], hot=True)
+    add(cfg, "scale_bias", 2 * E, [lambda b=b: gpu.scaleBias(b, gam, B, F, S) for b in xs], hot=True)
+    add(cfg, "add_bias", 2 * E, [lambda b=b: gpu.addBias(b, bet, B, F, S) for b in xs], hot=True)
+    add(cfg, "activate(leaky)", 2 * E, [lambda b=b: gpu.activateArray(b, n, Activation.leaky) for b in xs], hot=True)
     ys = [dev.zeros(n) for _ in range(R)]
     add(cfg, "copy (x, x_norm)", 2 * E, [lambda a=a, b=b: gpu.copy(n, a, b) for a, b in zip(xs, ys)])
     # the named ops in the layer's order on one tensor (batchnorm.zig:137-152 + activate)
@@ -386,7 +475,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
              lambda b=b: gpu.normalize(b, m, v, B, F, S), lambda b=b: gpu.scaleBias(b, gam, B, F, S),
              lambda b=b: gpu.addBias(b, bet, B, F, S), lambda b=b: gpu.activateArray(b, n, Activation.leaky)]
             for b in xs]
-    add_seq(cfg, "chain: mean,variance,normalize,scale_bias,add_bias,leaky", 10 * E, seqs)
+    add_seq(cfg, "chain: mean,variance,normalize,scale_bias,add_bias,leaky", 10 * E, seqs, hot=True)
     rm, rv = dev.zeros(F), dev.zeros(F)
     mom, alpha = 0.99, float(np.float32(1) - np.float32(0.99))  # batchnorm.zig:16, :141
 
@@ -408,7 +497,24 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     add_seq(cfg, "layer sequence: copy,mean,variance,ema,normalize,copy,scale_bias,add_bias,leaky", 14 * E, seqs)
     add_seq("fused", "cfg1 batchnorm_forward(train, leaky): stats + apply", 5 * E,
             [[lambda b=b, c=c, xn=xn: gpu.batchnormForward(B, F, S, Activation.leaky, True, b, b, c, xn, m, v, rm, rv,
-                                                           gam, bet)] for b, c, xn in zip(xs, xcs, xns)])
+                                                           gam, bet)] for b, c, xn in zip(xs, xcs, xns)], hot=True)
+    # the backward step at config 1's shape, for the per-layer forward +
+    # backward figure (buffers of the forward rows stand in for y, delta, x,
+    # x_norm: the timing does not depend on the values)
+    bu, su, md1, vd1 = dev.zeros(F), dev.zeros(F), dev.zeros(F), dev.zeros(F)
+    add_seq("fused", "cfg1 shape batchnorm_backward(leaky): sums + apply", 8 * E,
+            [[lambda b=b, c=c, xn=xn: gpu.batchnormBackward(B, F, S, Activation.leaky, b, c, xn, xn, m, v, gam, bu, su,
+                                                            md1, vd1)] for b, c, xn in zip(xs, xcs, xns)])
+    add_seq(cfg, "backward chain: gradient,backward_bias,backward_scale,scale_bias,mean_delta,variance_delta,"
+                 "normalize_delta", 14 * E,
+            [[lambda b=b, c=c: gpu.gradientArray(b, n, Activation.leaky, c),
+              lambda c=c: gpu.backwardBias(bu, c, B, F, S),
+              lambda c=c, xn=xn: gpu.backwardScale(xn, c, B, F, S, su),
+              lambda c=c: gpu.scaleBias(c, gam, B, F, S),
+              lambda c=c: gpu.meanDelta(c, v, B, F, S, md1),
+              lambda c=c, xn=xn: gpu.varianceDelta(xn, c, m, v, B, F, S, vd1),
+              lambda c=c, xn=xn: gpu.normalizeDelta(xn, m, v, md1, vd1, B, F, S, c)]
+             for b, c, xn in zip(xs, xcs, xns)])
     dev.free()
 
     # -- config 2: BN backward ops on their own
@@ -425,6 +531,13 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     B2, F2, S2, n2 = 64, 128, 56 * 56, h["n"]
     cfg = "cfg1_ops_at_cfg2_shape[64,128,56,56]"
     bias2 = dev.up(gen(7).normal(0, 0.1, F2).astype(np.float32))
+    add_seq(cfg, "chain: mean,variance,normalize,scale_bias,add_bias,leaky", 40 * n2,
+            [[lambda d=d: gpu.mean(d["x"], B2, F2, S2, d["md"]),
+              lambda d=d: gpu.variance(d["x"], d["md"], B2, F2, S2, d["vd"]),
+              lambda d=d: gpu.normalize(d["x"], d["mean"], d["var"], B2, F2, S2),
+              lambda d=d: gpu.scaleBias(d["x"], d["scales"], B2, F2, S2),
+              lambda d=d: gpu.addBias(d["x"], bias2, B2, F2, S2),
+              lambda d=d: gpu.activateArray(d["x"], n2, Activation.leaky)] for d in sets])
     add(cfg, "mean", 4 * n2, [lambda d=d: gpu.mean(d["x"], B2, F2, S2, d["md"]) for d in sets])
     add(cfg, "variance", 4 * n2, [lambda d=d: gpu.variance(d["x"], d["mean"], B2, F2, S2, d["vd"]) for d in sets])
     add(cfg, "normalize", 8 * n2, [lambda d=d: gpu.normalize(d["x_norm"], d["mean"], d["var"], B2, F2, S2)
@@ -432,6 +545,12 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     add(cfg, "add_bias", 8 * n2, [lambda d=d: gpu.addBias(d["x_norm"], bias2, B2, F2, S2) for d in sets])
     add(cfg, "activate(leaky)", 8 * n2, [lambda d=d: gpu.activateArray(d["x_norm"], n2, Activation.leaky)
                                          for d in sets])
+    # the fused forward at config 2's shape, for the per-layer forward +
+    # backward figure (it overwrites y, delta and x_norm: these rows come last)
+    m2, v2, rm2, rv2 = dev.zeros(F2), dev.zeros(F2), dev.zeros(F2), dev.zeros(F2)
+    add_seq("fused", "cfg2 shape batchnorm_forward(train, leaky): stats + apply", 20 * n2,
+            [[lambda d=d: gpu.batchnormForward(B2, F2, S2, Activation.leaky, True, d["x"], d["y"], d["delta"],
+                                               d["x_norm"], m2, v2, rm2, rv2, d["scales"], bias2)] for d in sets])
     dev.free()
 
     # -- config 3: softmax + cross-entropy delta, [256,1000], logits ~N(0,4)
@@ -449,16 +568,18 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     ds_ = [dev.zeros(n3) for _ in range(R)]
     es = [dev.zeros(n3) for _ in range(R)]
     cfg = "cfg3_softmax[256,1000]"
-    add(cfg, "softmax", 2 * 4 * n3, [lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)])
+    add(cfg, "softmax", 2 * 4 * n3, [lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)],
+        hot=True)
     add(cfg, "softmax_x_ent", 4 * 4 * n3,
-        [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)])
+        [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)],
+        hot=True)
     add_seq(cfg, "chain: softmax, softmax_x_ent (the layer's two calls)", 6 * 4 * n3,
             [[lambda a=a, p=p: gpu.softmax(a, c3, b3, c3, 1, c3, 1, 1.0, p),
               lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3, p, t, d, e)]
              for a, p, t, d, e in zip(ls, ps, ts, ds_, es)])
     add("fused", "cfg3 softmax_layer_forward (softmax + loss in one pass)", 5 * 4 * n3,
         [lambda a=a, p=p, t=t, d=d, e=e: gpu.softmaxLayerForward(b3, c3, 1, 1.0, a, t, p, d, e)
-         for a, p, t, d, e in zip(ls, ps, ts, ds_, es)])
+         for a, p, t, d, e in zip(ls, ps, ts, ds_, es)], hot=True)
     dev.free()
     # the same two ops at a larger batch (config 3 is a 2 MB tensor, which one
     # launch cannot stream at full rate): each op at a large shape
@@ -491,9 +612,10 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     batch, lr, decay, momentum = 64, 0.1, 0.0005, 0.9
     cfg = "cfg4_sgd[25e6]"
     add(cfg, "axpy(-decay*batch, w, dw)", 3 * 4 * n4,
-        [lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d) for w, d in zip(ws, dws)])
-    add(cfg, "axpy(lr/batch, dw, w)", 3 * 4 * n4, [lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w) for w, d in zip(ws, dws)])
-    add(cfg, "scal(momentum, dw)", 2 * 4 * n4, [lambda d=d: gpu.scal(n4, momentum, d) for d in dws])
+        [lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d) for w, d in zip(ws, dws)], hot=True)
+    add(cfg, "axpy(lr/batch, dw, w)", 3 * 4 * n4, [lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w) for w, d in zip(ws, dws)],
+        hot=True)
+    add(cfg, "scal(momentum, dw)", 2 * 4 * n4, [lambda d=d: gpu.scal(n4, momentum, d) for d in dws], hot=True)
     seqs = [[lambda w=w, d=d: gpu.axpy(n4, -decay * batch, w, d), lambda w=w, d=d: gpu.axpy(n4, lr / batch, d, w),
              lambda d=d: gpu.scal(n4, momentum, d)] for w, d in zip(ws, dws)]
     add_seq(cfg, "chain: axpy,axpy,scal (one SGD step)", 8 * 4 * n4, seqs)
@@ -506,7 +628,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None):
     adds = dev.clone(dev.up(r.normal(0, 0.05, na).astype(np.float32)), na, R)
     outs = dev.clone(dev.up(r.normal(0, 0.05, no).astype(np.float32)), no, R)
     add("cfg4_shortcut[64,256,28,28]->[64,512,14,14]", "shortcut", 3 * 4 * s4,
-        [lambda a=a, o=o: gpu.shortcut(sb, w1, w1, c1, a, w2, w2, c2, 1.0, 1.0, o) for a, o in zip(adds, outs)])
+        [lambda a=a, o=o: gpu.shortcut(sb, w1, w1, c1, a, w2, w2, c2, 1.0, 1.0, o) for a, o in zip(adds, outs)], hot=True)
     dev.free()
 
     # -- config 5: pooling at [256,512,28,28], inputs ~U(-1,1)
@@ -691,22 +813,70 @@ def gemm_table(gpu, hip, stream):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the CPU twins (C restatement) on the same config-2 inputs
+# CPU baseline: the CPU twins (the oracle's C restatement) on every config
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(h, repeats=3):
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _median_time(fn, repeats):
+    """Median wall time (s) of `repeats` calls of fn(), each on fresh state
+    made by fn's own setup (fn returns the timed seconds)."""
+    return statistics.median(fn() for _ in range(repeats))
+
+
+def cpu_baselines(h, repeats=5):
+    """Each config's ops through the oracle's C restatement of the Zig CPU
+    twins (blas.zig, activations.zig, pooling.zig), one host thread, median
+    of `repeats` runs, as algorithmic GB/s (the GPU rows' byte counts). The
+    ops and inputs are the GPU rows'; config 5 runs on a sample of 32 of its
+    256 images (the same per-image work, so the same rate), the rest at full
+    size. About 10 s in all."""
     from darknet_zig_amd.activations import Activation
     from oracle import ref
 
+    out = {}
+    t0 = time.perf_counter
+
+    # config 1: mean, variance, normalize, scale_bias, add_bias, leaky on [128,32,32,32]
+    B, F, S = 128, 32, 1024
+    n = B * F * S
+    r = gen(1)
+    x0 = r.normal(0, 1, n).astype(np.float32)
+    gam, bet = r.uniform(0.5, 1.5, F).astype(np.float32), r.normal(0, 0.1, F).astype(np.float32)
+
+    def cfg1():
+        x = x0.copy()
+        m, v = np.empty(F, np.float32), np.empty(F, np.float32)
+        a = t0()
+        ref.mean(x, B, F, S, m)
+        ref.variance(x, m, B, F, S, v)
+        ref.normalize(x, m, v, B, F, S)
+        ref.scaleBias(x, gam, B, F, S)
+        ref.addBias(x, bet, B, F, S)
+        ref.activateArray(x, Activation.leaky)
+        return t0() - a
+
+    out["cfg1"] = (10 * 4 * n, _median_time(cfg1, repeats),
+                   "config 1's six named ops (mean, variance, normalize, scale_bias, add_bias, leaky) on "
+                   "[128,32,32,32]")
+
+    # config 2: the backward chain on [64,128,56,56] (the headline workload)
     B, F, S = h["B"], h["F"], h["S"]
-    chain_bytes = 14 * 4 * h["n"]
-    times = []
-    for _ in range(repeats):
+
+    def cfg2():
         d = h["delta"].copy()
         bu, su = np.zeros(F, np.float32), np.zeros(F, np.float32)
         md, vd = np.empty(F, np.float32), np.empty(F, np.float32)
-        t0 = time.perf_counter()
+        a = t0()
         ref.gradientArray(h["y"], Activation.leaky, d)
         ref.backwardBias(bu, d, B, F, S)
         ref.backwardScale(h["x_norm"], d, B, F, S, su)
@@ -714,28 +884,268 @@ def cpu_baseline(h, repeats=3):
         ref.meanDelta(d, h["var"], B, F, S, md)
         ref.varianceDelta(h["x"], d, h["mean"], h["var"], B, F, S, vd)
         ref.normalizeDelta(h["x"], h["mean"], h["var"], md, vd, B, F, S, d)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+        return t0() - a
+
+    out["cfg2"] = (14 * 4 * h["n"], _median_time(cfg2, repeats),
+                   "config 2's backward chain (7 ops) on [64,128,56,56], the headline workload's inputs")
+
+    # config 3: softmax then softmax_x_ent on [256,1000], logits ~N(0,4)
+    b3, c3 = 256, 1000
+    n3 = b3 * c3
+    r = gen(3)
+    logits = r.normal(0, 4.0, n3).astype(np.float32)
+    truth = np.zeros(n3, np.float32)
+    truth[np.arange(b3) * c3 + r.integers(0, c3, b3)] = 1.0
+
+    def cfg3():
+        p, d, e = np.empty(n3, np.float32), np.empty(n3, np.float32), np.empty(n3, np.float32)
+        a = t0()
+        ref.softmax(logits, c3, b3, c3, 1, c3, 1, 1.0, p)
+        ref.softmaxCrossEntropy(p, truth, d, e)
+        return t0() - a
+
+    out["cfg3"] = (6 * 4 * n3, _median_time(cfg3, repeats),
+                   "config 3's softmax + softmax_x_ent on [256,1000]")
+
+    # config 4: one SGD step over 25e6 floats, then the stride-2 shortcut
+    n4 = 25_000_000
+    r = gen(4)
+    w0, dw0 = r.normal(0, 0.05, n4).astype(np.float32), r.normal(0, 0.05, n4).astype(np.float32)
+    sb, w1, c1, w2, c2 = 64, 28, 256, 14, 512
+    add0 = r.normal(0, 0.05, sb * c1 * w1 * w1).astype(np.float32)
+    out0 = r.normal(0, 0.05, sb * c2 * w2 * w2).astype(np.float32)
+
+    def cfg4():
+        w, dw, o = w0.copy(), dw0.copy(), out0.copy()
+        a = t0()
+        ref.axpy(-0.0005 * 64, w, dw)
+        ref.axpy(0.1 / 64, dw, w)
+        ref.scal(0.9, dw)
+        ref.shortcut(sb, w1, w1, c1, add0, w2, w2, c2, 1.0, 1.0, o)
+        return t0() - a
+
+    out["cfg4"] = (8 * 4 * n4 + 3 * 4 * sb * c1 * w2 * w2, _median_time(cfg4, repeats),
+                   "config 4's SGD step (axpy, axpy, scal over 25e6 floats) and shortcut "
+                   "[64,256,28,28] -> [64,512,14,14]")
+
+    # config 5: max pool 2x2/s2 fwd + bwd, global avg pool fwd + bwd, on 32 of the 256 images
+    pb, pc, ph = 32, 512, 28
+    nin = pb * pc * ph * ph
+    oh = (ph + 1 - 2) // 2 + 1
+    nout = pb * pc * oh * oh
+    r = gen(5)
+    xin = r.uniform(-1, 1, nin).astype(np.float32)
+    dout = r.uniform(-1, 1, nout).astype(np.float32)
+
+    def cfg5():
+        o, idx = np.empty(nout, np.float32), np.empty(nout, np.int32)
+        prev = np.zeros(nin, np.float32)
+        avg = np.empty(pb * pc, np.float32)
+        a = t0()
+        ref.forwardMaxpool(pb, ph, ph, pc, 2, 2, 1, xin, o, idx)
+        ref.backwardMaxpool(idx, dout, prev)
+        ref.forwardAvgpool(pb, ph, ph, pc, xin, avg)
+        ref.backwardAvgpool(pb, ph, ph, pc, avg, prev)
+        return t0() - a
+
+    out["cfg5"] = (4 * (nin + 2 * nout) + 4 * (2 * nout + 2 * nin) + 4 * (nin + pb * pc) + 4 * (2 * nin + pb * pc),
+                   _median_time(cfg5, repeats),
+                   "config 5's max pool 2x2/s2 forward + backward and global avg pool forward + backward, "
+                   "[32,512,28,28] (32 of the 256 images)")
+
+    cores = os.cpu_count()
+    model = _cpu_model()
+    per = {}
+    for k, (nbytes, t, what) in out.items():
+        per[k] = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "ms": round(t * 1e3, 3),
+                  "sample": f"{what}; median of {repeats} runs"}
+    head = per["cfg2"]
     return {
-        "value": round(chain_bytes / t / 1e9, 3),
+        "value": head["value"],
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"full config-2 chain (7 ops over [64,128,56,56]) on the same inputs, median of {repeats} runs, "
-                   f"{t * 1e3:.1f} ms per chain, 1 thread of {os.cpu_count()} ({model}); C restatement of the Zig "
-                   "CPU twins built -O3 -march=x86-64-v3 -ffp-contract=off"),
+        "sample": (f"{head['sample']}, {head['ms']} ms per chain; 1 thread of {cores} ({model}); the oracle's C "
+                   "restatement of the Zig CPU twins built -O2 -march=x86-64-v3 -ffp-contract=off"),
+        "per_config": per,
     }
 
 
 # ---------------------------------------------------------------------------
+
+
+def bn_gelem(table, bwd_chain_ms):
+    """Batch-norm + activation throughput in GElem/s (elements of the layer's
+    tensor per second): config 1's forward and config 2's backward, per op
+    (chained, and the sum of the ops timed alone), the whole per-op layer
+    forward (copies and EMA included) and the fused entry points; and the
+    layer's forward + backward at each config's shape (E / (t_fwd + t_bwd)),
+    per-op chains and fused."""
+    def us(key):
+        rows = [v["us"] for k, v in table.items() if k == key]
+        return rows[0] if rows else None
+
+    named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
+    c1, c2, c12 = "cfg1_bn_fwd[128,32,32,32]", "cfg2_bn_bwd[64,128,56,56]", "cfg1_ops_at_cfg2_shape[64,128,56,56]"
+    e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
+    fwd_sum = sum(table[f"{c1}/{k}"]["us"] for k in named)
+    bwd_sum = sum(v["us"] for k, v in table.items() if k.startswith(c2 + "/"))
+    fwd1 = us(f"{c1}/chain: mean,variance,normalize,scale_bias,add_bias,leaky")
+    bwd1 = us(f"{c1}/backward chain: gradient,backward_bias,backward_scale,scale_bias,mean_delta,variance_delta,"
+              "normalize_delta")
+    fwd2 = us(f"{c12}/chain: mean,variance,normalize,scale_bias,add_bias,leaky")
+    bwd2 = bwd_chain_ms * 1e3
+    ffwd1 = us("fused/cfg1 batchnorm_forward(train, leaky): stats + apply")
+    fbwd1 = us("fused/cfg1 shape batchnorm_backward(leaky): sums + apply")
+    ffwd2 = us("fused/cfg2 shape batchnorm_forward(train, leaky): stats + apply")
+    fbwd2 = us("fused/cfg2 batchnorm_backward(leaky): sums + apply")
+    layer1 = us(f"{c1}/layer sequence: copy,mean,variance,ema,normalize,copy,scale_bias,add_bias,leaky")
+
+    def g(e, *t):
+        return None if any(v is None for v in t) else round(e / (sum(t) * 1e-6) / 1e9, 2)
+
+    return {
+        "fwd_cfg1_chained": g(e1, fwd1),
+        "bwd_cfg2_chained": g(e2, bwd2),
+        "fwd_cfg1_per_op_sum": g(e1, fwd_sum),
+        "bwd_cfg2_per_op_sum": g(e2, bwd_sum),
+        "fwd_cfg1_layer_sequence": g(e1, layer1),
+        "fwd_cfg1_fused": g(e1, ffwd1),
+        "bwd_cfg2_fused": g(e2, fbwd2),
+        "fwd_bwd_cfg1_shape_per_op": g(e1, fwd1, bwd1),
+        "fwd_bwd_cfg1_shape_fused": g(e1, ffwd1, fbwd1),
+        "fwd_bwd_cfg2_shape_per_op": g(e2, fwd2, bwd2),
+        "fwd_bwd_cfg2_shape_fused": g(e2, ffwd2, fbwd2),
+    }
+
+
+# ---------------------------------------------------------------------------
+# per-op traffic table from rocprofv3 runs of --per-op-traffic
+# ---------------------------------------------------------------------------
+
+# gfx950's L2 (TCC) counts its reads from HBM by request size -- 32, 64 and
+# 128 bytes -- and its writes as 32- or 64-byte requests. FETCH_SIZE's
+# gfx950 formula in rocprofiler-sdk's counter_defs.yaml weighs 128-byte
+# requests through TCC_BUBBLE, which gfx950 does not define, so it undercounts
+# them; these counters give the bytes directly.
+READ_COUNTERS = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_sum")
+WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def _csv(directory: Path, suffix: str):
+    import csv
+    import glob
+
+    files = sorted(glob.glob(str(directory / f"*{suffix}")))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _dispatch_counters(directory: Path):
+    """[(kernel name, workgroups, {counter: value})] in dispatch order."""
+    d = {}
+    for r in _csv(directory, "counter_collection.csv"):
+        k = int(r["Dispatch_Id"])
+        e = d.setdefault(k, [r["Kernel_Name"], int(r["Grid_Size"]) // 256, {}])
+        e[2][r["Counter_Name"]] = e[2].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [d[k] for k in sorted(d)]
+
+
+def _is_marker(name: str, blocks: int, base: int) -> bool:
+    return "FillOp" in name and "ew_scalar_kernel" in name and blocks >= base
+
+
+def _segments(dispatches, base):
+    """Row index -> the dispatches between its begin and end markers."""
+    out, cur = {}, None
+    for name, blocks, val in dispatches:
+        if _is_marker(name, blocks, base):
+            idx = blocks - base
+            cur = idx // 2 if idx % 2 == 0 else None
+            if cur is not None:
+                out[cur] = []
+            continue
+        if cur is not None:
+            out[cur].append((name, val))
+    return out
+
+
+def _read_bytes(c):
+    return 32 * c["TCC_EA0_RDREQ_32B_sum"] + 64 * c["TCC_EA0_RDREQ_64B_sum"] + 128 * c["TCC_EA0_RDREQ_128B_sum"]
+
+
+def _write_bytes(c):
+    return 32 * (c["TCC_EA0_WRREQ_sum"] - c["TCC_EA0_WRREQ_64B_sum"]) + 64 * c["TCC_EA0_WRREQ_64B_sum"]
+
+
+def traffic_table(d: Path) -> str:
+    """The per-op traffic table (markdown) from the outputs under `d`:
+    traffic_rows.json (stdout of `bench.py --per-op-traffic`), read/ and
+    write/ (rocprofv3 --pmc READ_COUNTERS / WRITE_COUNTERS of that command),
+    trace/ (rocprofv3 --kernel-trace of it), and copy.json, copy_read/,
+    copy_write/ (the same for `bench.py --copy-calibration 1024`, whose known
+    bytes check the counter formula)."""
+    def last_json(path):
+        return json.loads([ln for ln in open(path) if ln.startswith("{")][-1])
+
+    meta = last_json(d / "traffic_rows.json")
+    rows, base = meta["per_op_traffic"], meta["mark_base"]
+    rd = _segments([(n, b, c) for n, b, c in _dispatch_counters(d / "read")], base)
+    wr = _segments([(n, b, c) for n, b, c in _dispatch_counters(d / "write")], base)
+    trace = []
+    for r in sorted(_csv(d / "trace", "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"])):
+        trace.append((r["Kernel_Name"], int(r["Grid_Size_X"]) // 256,
+                      (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    tr = _segments(trace, base)
+    check = ""
+    if (d / "copy.json").exists():
+        cal = last_json(d / "copy.json")["copy_calibration"]
+        cr = [c for n, b, c in _dispatch_counters(d / "copy_read") if "CopyOp" in n][-4:]
+        cw = [c for n, b, c in _dispatch_counters(d / "copy_write") if "CopyOp" in n][-4:]
+        fr = statistics.mean(_read_bytes(c) for c in cr) / cal["bytes_read"]
+        fw = statistics.mean(_write_bytes(c) for c in cw) / cal["bytes_written"]
+        check = (f"Check of the formula: a copy of {cal['bytes_read'] / 2**30:.0f} GiB reads {fr:.4f}x and writes "
+                 f"{fw:.4f}x its known bytes by these counters (no scale factor is applied).")
+    lines = [
+        "| row | algorithmic MB | counter MB (read + write) | ratio | 128-B share of reads | kernels | rocprof us "
+        "| algorithmic GB/s | of 8 TB/s | counter GB/s | of 8 TB/s |",
+        "|---|---|---|---|---|---|---|---|---|---|---|",
+    ]
+    for i, r in enumerate(rows):
+        p = r["passes"]
+        reads = sum(_read_bytes(c) for _, c in rd.get(i, [])) / p
+        writes = sum(_write_bytes(c) for _, c in wr.get(i, [])) / p
+        n128 = sum(c["TCC_EA0_RDREQ_128B_sum"] for _, c in rd.get(i, []))
+        nall = sum(c["TCC_EA0_RDREQ_32B_sum"] + c["TCC_EA0_RDREQ_64B_sum"] + c["TCC_EA0_RDREQ_128B_sum"]
+                   for _, c in rd.get(i, []))
+        durs = [t for _, t in tr.get(i, [])]
+        per = max(1, len(durs) // p)
+        us = sorted(sum(durs[k * per:(k + 1) * per]) for k in range(p))[p // 2] if durs else float("nan")
+        t = reads + writes
+        b = r["bytes"]
+        ratio = f"{t / b:.3f}" if b > 1e5 else "(C floats)"
+        share = f"{128 * n128 / max(reads * p, 1):.2f}" if nall else "-"
+        lines.append(f"| {r['row']} | {b / 1e6:.2f} | {t / 1e6:.2f} | {ratio} | {share} | {per} | {us:.2f} | "
+                     f"{b / us / 1e3:.0f} | {b / us / 8e6:.3f} | {t / us / 1e3:.0f} | {t / us / 8e6:.3f} |")
+    return "\n".join(([check, ""] if check else []) + lines)
+
+
+def counter_traffic(row: str):
+    """HBM bytes per launch of a per-op row, from the committed counter table
+    (profiles/traffic_per_op.md, 'counter MB' column), or None."""
+    path = ROOT / "profiles" / "traffic_per_op.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) > 3 and cells[0] == row:
+            try:
+                return int(round(float(cells[2]) * 1e6))
+            except ValueError:
+                return None
+    return None
 
 
 def main() -> int:
@@ -752,13 +1162,22 @@ def main() -> int:
                     help="only run each per-op row's first launches once, between marker dispatches "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per row)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run dkz_copy over MIB MiB (x4 launches, rotated): the known-size kernel "
-                         "that scales rocprofv3's FETCH_SIZE/WRITE_SIZE")
+                    help="only run dkz_copy over MIB MiB (x4 launches, rotated): a known-size kernel that "
+                         "checks the counter formula of the traffic table")
+    ap.add_argument("--rows", default=None, metavar="SUBSTR",
+                    help="with --per-op-only: time only the per-op rows whose config contains SUBSTR")
+    ap.add_argument("--traffic-table", default=None, metavar="DIR",
+                    help="only print the per-op traffic table (markdown) from the rocprofv3 outputs in DIR "
+                         "(see traffic_table())")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(every op runs on one device's share); run with --gpus 1.", file=sys.stderr)
         return 2
+
+    if args.traffic_table:
+        print(traffic_table(Path(args.traffic_table)))
+        return 0
 
     from darknet_zig_amd import gpu
 
@@ -785,8 +1204,10 @@ def main() -> int:
         return 0
 
     if args.per_op_only:
-        print(json.dumps({"per_op": per_op_table(gpu, hip, stream, args.op_launches),
-                          "gemm": gemm_table(gpu, hip, stream)}), flush=True)
+        res = {"per_op": per_op_table(gpu, hip, stream, args.op_launches, only=args.rows)}
+        if args.rows is None:
+            res["gemm"] = gemm_table(gpu, hip, stream)
+        print(json.dumps(res), flush=True)
         return 0
 
     h = config2_host()
@@ -811,18 +1232,17 @@ def main() -> int:
     kernel_ms = [t - overhead_ms for t in per_kernel_ms]
     dom = max(range(len(names)), key=lambda j: kernel_ms[j])
     achieved = gbs(byts[dom], kernel_ms[dom])
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic_bn_backward.txt"
-    if tfile.exists():
-        for line in tfile.read_text().splitlines():
-            if line.startswith(f"{names[dom]}:"):
-                try:
-                    traffic = int(line.split(":", 1)[1].split()[0])
-                except ValueError:
-                    traffic = None
+    traffic = counter_traffic(f"cfg2_bn_bwd[64,128,56,56]/{names[dom]}")
 
+    # Only the step's first kernel starts from data the previous step left
+    # >= 512 MB behind; every later kernel re-reads delta (and x) that the
+    # kernel before it read or wrote, which the 256 MB Infinity Cache may
+    # still hold, so their rates are not pure HBM rates.
     chain_kernels = {names[j]: {"us": round(kernel_ms[j] * 1e3, 2), "GB/s": round(gbs(byts[j], kernel_ms[j]), 1),
-                                "event_pair_us": round(per_kernel_ms[j] * 1e3, 2)} for j in range(len(names))}
+                                "event_pair_us": round(per_kernel_ms[j] * 1e3, 2),
+                                "cache": "cold (HBM)" if j == 0 else "MALL-assisted (re-reads the previous "
+                                                                      "kernel's operands)"}
+                     for j in range(len(names))}
     result = {
         "metric": METRIC,
         "value": round(gbs(chain_bytes * args.steps, ms), 1),
@@ -868,26 +1288,9 @@ def main() -> int:
         table = per_op_table(gpu, hip, stream, args.op_launches)
         result["per_op"] = table
         result["gemm"] = gemm_table(gpu, hip, stream)
-        named = ("mean", "variance", "normalize", "scale_bias", "add_bias", "activate(leaky)")
-        cfg1, cfg2 = "cfg1_bn_fwd[", "cfg2_bn_bwd["  # the config rows, not the same ops at other shapes
-        fwd = sum(v["us"] for k, v in table.items() if k.startswith(cfg1) and k.split("/", 1)[1] in named)
-        fwd_chain = next(v["us"] for k, v in table.items() if k.startswith(cfg1) and "/chain" in k)
-        fwd_layer = next(v["us"] for k, v in table.items() if k.startswith(cfg1) and "/layer sequence" in k)
-        fwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg1"))
-        bwd_fused = next(v["us"] for k, v in table.items() if k.startswith("fused/cfg2"))
-        bwd = sum(v["us"] for k, v in table.items() if k.startswith(cfg2))
-        e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
-        result["bn_act_gelem_s"] = {
-            "fwd_cfg1_chained": round(e1 / (fwd_chain * 1e-6) / 1e9, 2),
-            "bwd_cfg2_chained": round(e2 / (ms / args.steps * 1e-3) / 1e9, 2),
-            "fwd_cfg1_per_op_sum": round(e1 / (fwd * 1e-6) / 1e9, 2),
-            "bwd_cfg2_per_op_sum": round(e2 / (bwd * 1e-6) / 1e9, 2),
-            "fwd_cfg1_layer_sequence": round(e1 / (fwd_layer * 1e-6) / 1e9, 2),
-            "fwd_cfg1_fused": round(e1 / (fwd_fused * 1e-6) / 1e9, 2),
-            "bwd_cfg2_fused": round(e2 / (bwd_fused * 1e-6) / 1e9, 2),
-        }
+        result["bn_act_gelem_s"] = bn_gelem(table, ms / args.steps)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(h)
+        result["cpu_baseline"] = cpu_baselines(h)
     print(json.dumps(result), flush=True)
     return 0
 

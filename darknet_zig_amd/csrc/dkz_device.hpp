@@ -263,6 +263,55 @@ __host__ __device__ __forceinline__ float expf_libm(float x) {
     return (float)(y * s);
 }
 
+// ---------------------------------------------------------------------------
+// exp for softmax, whose contract is 1e-5 relative per element (not bit
+// equality with the host libm): under one ulp at a third of expf_libm's cost
+// and without its per-lane table reads.
+//
+// Cody & Waite's reduction: k = rint(x/ln2), r = x - k*ln2 with ln2 split into
+// a head of 16 significant bits (k*head is exact for |k| <= 2^8) and a tail,
+// so |r| <= ln2/2 up to an error far below ulp(r). exp(r) = 1 + r + r^2 q(r)
+// with q of degree 4, evaluated in Horner form: the coefficients are a
+// minimax fit (Lawson-reweighted least squares over 4000 Chebyshev nodes of
+// [-ln2/2, ln2/2], relative error of exp weighted) rounded to f32, 3.8e-9
+// relative before rounding. 2^k is applied by ldexp, which rounds a subnormal
+// result once. x is clamped to [-104, 89] first (exp(-104) rounds to 0 and
+// exp(89) overflows to +inf, so the clamp changes no result). Only
+// IEEE-exact operations (min, max, multiply, fma, rint, ldexp), so the host
+// build of this function gives the device's bits, and its accuracy is
+// checked on the host over every float input.
+//
+// expf_cw_num requires x not NaN (softmax detects a NaN argument once per
+// group instead of per element); expf_cw passes NaN through.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float expf_cw_num(float x) {
+    constexpr float kLog2e = (float)1.4426950408889634;  // 1/ln2
+    constexpr float kLn2Hi = 0x1.62e4p-1f;               // ln2 to 16 bits
+    constexpr float kLn2Lo = (float)(0.6931471805599453 - (double)kLn2Hi);
+    constexpr float q0 = 0x1.fffffcp-2f, q1 = 0x1.555492p-3f, q2 = 0x1.5558f2p-5f;
+    constexpr float q3 = 0x1.1239d4p-7f, q4 = 0x1.6a244cp-10f;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const float xc = __builtin_amdgcn_fmed3f(x, -104.0f, 89.0f);  // the same clamp for x not NaN
+#else
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);
+#endif
+    const float k = __builtin_rintf(xc * kLog2e);
+    float r = __builtin_fmaf(k, -kLn2Hi, xc);
+    r = __builtin_fmaf(k, -kLn2Lo, r);
+    float p = __builtin_fmaf(q4, r, q3);
+    p = __builtin_fmaf(p, r, q2);
+    p = __builtin_fmaf(p, r, q1);
+    p = __builtin_fmaf(p, r, q0);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)k);
+}
+
+__host__ __device__ __forceinline__ float expf_cw(float x) {
+    const float y = expf_cw_num(x);
+    return x != x ? x : y;
+}
+
 // v^-1.5 as 1/(v*sqrt(v)) in f64, rounded once: the factor of variance_delta.
 // std.math.pow(f32, v, -1.5) (blas.zig:176) goes through f32 exp and log and
 // lands within a few ulps of it.

@@ -4,39 +4,39 @@
 //
 // Group (b, g) holds n elements `stride` apart starting at
 // b*batch_offset + g*group_offset. Per group the CPU twin takes the max
-// (starting from -FLT_MAX), writes e_i = exp(x_i/T - max/T), sums the e_i
-// left to right in f32 and divides. Every step except that sum is exact or
-// elementwise, and exp is the host-identical expf_libm, so the kernels below
-// reproduce the twin bit for bit wherever they keep the sequential sum:
+// (starting from -FLT_MAX), forms e_i = exp(x_i/T - max/T), sums the e_i left
+// to right in f32 and divides. The contract for softmax is 1e-5 relative per
+// element, so the contiguous-group kernels below (stride 1, n > 32) keep the
+// twin's max and its exp argument x_i/T - max/T bit for bit but evaluate exp
+// with expf_cw (under one ulp), add the exps as a tree (pairwise in f32
+// within a lane, then in f64 across lanes by DPP/LDS butterflies:
+// deterministic, and far closer to the exact sum than a sequential f32 one)
+// and scale by one rounded reciprocal; every p is within 1e-6 relative of
+// the exact softmax of the twin's arguments:
 //
-//  * contiguous groups (stride 1) with 32 < n <= kSeqMax: one workgroup per
-//    group; the row is read once into LDS (in float4s when aligned), max by
-//    wave64 DPP + LDS, the exps in parallel in place, one lane adds them in
-//    order, then all lanes divide. Bit-exact.
-//  * many contiguous groups (at least kRowsMin) with 32 < n <= kRowsMaxN (256):
-//    a workgroup stages kRows groups in LDS (odd row pitch, so lanes walking
-//    columns of different rows use different banks); all its lanes share the
-//    loads, exps and divides, and lane r of the first wave runs group r's max
-//    and its sequential sum, so kRows sums advance per instruction. Bit-exact.
-//  * many contiguous groups (at least DKZ_SOFTMAX_WIDE_MIN) with
-//    kRowsMaxN < n <= kWideMaxN (1024): 2, 4 or 8 groups a workgroup held
-//    in registers; maxes and exps on all lanes, then lane l of the first
-//    wave adds group l's exps in order from LDS. Bit-exact.
-//  * contiguous groups with n > kSeqMax: one workgroup per group, the row
-//    not staged, and the sum an f64 tree (within 1e-5 relative of the twin)
-//    because the row no longer fits in LDS.
-//  * strided groups that sit side by side (group_offset 1, the spatial
-//    softmax over the classes of each position) with n <= kTileMaxN: a
+//  * n <= kSegMaxN (2048) with many groups: a segment of L = 4..64 lanes per
+//    group, the group held in registers (16 or 32 floats a lane, read once in
+//    float4s when aligned), max and sum over the segment by DPP.
+//  * n <= kWgMaxN (32768), or few groups: one workgroup (64..1024 lanes) per
+//    group, held in registers, max and sum by DPP within waves and LDS
+//    across them.
+//  * longer groups: one workgroup per group, three passes over x (max; sum;
+//    exps scaled and stored).
+//
+// Strided groups (the spatial softmax, elements `stride` apart) and groups
+// of at most 32 elements keep the twin's sequential sum and the
+// host-libm-identical expf_libm, and are bit-exact:
+//
+//  * side-by-side strided groups (group_offset 1) with n <= kTileMaxN: a
 //    workgroup stages 64 consecutive groups in LDS; all its lanes share the
-//    loads, exps and divides, and lane g < 64 takes group g's max and its
-//    sequential sum. Bit-exact.
+//    loads, exps and divides, and lane g < 64 takes group g's max and sum.
 //  * other strided groups, or n <= 32: one lane per group runs the twin's
-//    three loops, eight loads at a time. Bit-exact.
+//    three loops, eight loads at a time.
 //
 // dkz_softmax_layer_forward runs the layer's two calls (softmax, then
-// softmax_x_ent over the whole batch) as one pass where the block kernels
-// apply: the loss and delta are formed from each probability as it is
-// stored, with softmax_x_ent's expressions.
+// softmax_x_ent over the whole batch) as one pass for contiguous groups
+// longer than 32: the loss and delta are formed from each probability as it
+// is stored, with softmax_x_ent's expressions.
 #include <float.h>
 
 #include "dkz_device.hpp"
@@ -44,8 +44,6 @@
 
 namespace dkz {
 namespace {
-
-constexpr uint32_t kSeqMax = 8192;  // floats staged in LDS (32 KiB)
 
 struct Groups {
     uint32_t n, groups, batch_offset, group_offset, stride;
@@ -73,366 +71,377 @@ __device__ __forceinline__ void xent1(float p, float t, float &d, float &l) {
     d = t - p;
 }
 
-__device__ __forceinline__ void read32(const float4 *lds, uint32_t batch, float4 (&v)[8]) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = lds[batch * 8 + u];
-}
+__device__ __forceinline__ float xent_loss(float p, float t) { return (t != 0.0f) ? -logf(p) : 0.0f; }
 
-// s plus the 32 values, one at a time, left to right.
-__device__ __forceinline__ float add32(float s, const float4 (&v)[8]) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        s += v[u].x;
-        s += v[u].y;
-        s += v[u].z;
-        s += v[u].w;
+// ---------------------------------------------------------------------------
+// Reductions over a segment of L consecutive lanes (L = 4, 8, 16, 32, 64;
+// the whole wave active). Butterfly steps: DPP quad permutes and row mirrors
+// inside 16-lane rows, then lane swaps across rows. Partners combine the same
+// two operands, so every lane of the segment ends with the same bits.
+// ---------------------------------------------------------------------------
+template <int L>
+__device__ __forceinline__ float seg_max(float v) {
+    if constexpr (L == kWave) {
+        return wave_max(v);
+    } else {
+        v = fmaxf(v, dpp_f<kDppXor1>(v));
+        v = fmaxf(v, dpp_f<kDppXor2>(v));
+        if constexpr (L >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+        if constexpr (L >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
+        if constexpr (L >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+        return v;
     }
-    return s;
 }
 
-// V4: the row is 16-byte aligned and n % 4 == 0 (every pointer too), so it
-// moves in float4s.
-template <bool SEQ, bool XENT, bool V4>
-__global__ __launch_bounds__(kBlock) void softmax_block_kernel(const float *in, float *out, Groups G, Xent xe) {
-    extern __shared__ float4 e_lds4[];  // n floats when SEQ; float4 keeps it 16-byte aligned
-    float *e_lds = reinterpret_cast<float *>(e_lds4);
-    __shared__ float red_f[kBlock / kWave];
-    __shared__ double red_d[kBlock / kWave];
-    __shared__ float sum_sh;
+template <int L>
+__device__ __forceinline__ double seg_sum(double v) {
+    if constexpr (L == kWave) {
+        return wave_sum(v);
+    } else {
+        v += dpp_d<kDppXor1>(v);
+        v += dpp_d<kDppXor2>(v);
+        if constexpr (L >= 8) v += dpp_d<kDppHalfMirror>(v);
+        if constexpr (L >= 16) v += dpp_d<kDppMirror>(v);
+        if constexpr (L >= 32) v += __shfl_xor(v, 16);
+        return v;
+    }
+}
+
+// A lane's share of one group, M = 4K floats held in registers. Slot m is
+// element at(m): with float4 access (V4) lane j of P lanes holds float4s
+// j, j+P, ..., otherwise elements j, j+P, j+2P, ...
+template <int K, bool V4>
+struct RowSlice {
+    static constexpr int M = 4 * K;
+    float v[M];
+    uint32_t j, P;
+
+    __device__ __forceinline__ uint32_t at(int m) const {
+        return V4 ? 4 * (j + (uint32_t)(m >> 2) * P) + (uint32_t)(m & 3) : j + (uint32_t)m * P;
+    }
+
+    // Whether slot m lies inside a group of n elements (with float4 access n
+    // is a multiple of 4, so a float4 is inside or outside as a whole).
+    __device__ __forceinline__ bool inside(int m, uint32_t n) const {
+        return V4 ? 4 * (j + (uint32_t)(m >> 2) * P) < n : j + (uint32_t)m * P < n;
+    }
+
+    // Slots past n (or of a dead group) read as `fill`.
+    __device__ __forceinline__ void load(const float *p, uint32_t n, bool live, float fill) {
+        if constexpr (V4) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const uint32_t q = j + (uint32_t)k * P;
+                float4 a = make_float4(fill, fill, fill, fill);
+                if (live && 4 * q < n) a = ld4<false>(p, q);
+                v[4 * k] = a.x;
+                v[4 * k + 1] = a.y;
+                v[4 * k + 2] = a.z;
+                v[4 * k + 3] = a.w;
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) v[m] = (live && inside(m, n)) ? p[at(m)] : fill;
+        }
+    }
+
+    __device__ __forceinline__ float max() const {
+        float mx = v[0];
+#pragma unroll
+        for (int m = 1; m < M; ++m) mx = fmaxf(mx, v[m]);
+        return mx;
+    }
+
+    // v[m] <- exp(v[m]/T - mt) for the slots inside the group (0 elsewhere);
+    // returns their sum, added pairwise in f32 (error below 2^-21 relative
+    // for 32 terms) and widened to f64 for the cross-lane sum -- or NaN when
+    // an argument is NaN (a NaN logit, or +inf's inf - inf), which makes the
+    // whole group NaN as the twin's NaN sum does. The twin's argument
+    // x/T - max/T is formed exactly as the twin forms it (x/1 is x, so T == 1
+    // skips the divides).
+    __device__ __forceinline__ double exps(uint32_t n, bool live, float temp, float mt) {
+        bool nan = false;
+        if (temp == 1.0f) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float a = v[m] - mt;
+                const bool in = live && inside(m, n);
+                nan |= in && a != a;
+                v[m] = expf_cw_num(in ? a : -__builtin_inff());  // exp(-inf) = 0 outside the group
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float a = v[m] / temp - mt;
+                const bool in = live && inside(m, n);
+                nan |= in && a != a;
+                v[m] = expf_cw_num(in ? a : -__builtin_inff());
+            }
+        }
+        float t[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) t[m] = v[m];
+#pragma unroll
+        for (int w = M / 2; w >= 1; w /= 2) {
+#pragma unroll
+            for (int m = 0; m < w; ++m) t[m] = t[m] + t[m + w];
+        }
+        return nan ? (double)__builtin_nanf("") : (double)t[0];
+    }
+
+    // p = e * inv into `out`; with XENT also delta and loss, from the truth
+    // held in `tr` (EARLY) or read from `truth` here. The losses' logs run
+    // only in waves where some lane holds a nonzero truth (with one-hot
+    // truth, most waves store zeros).
+    template <bool XENT, bool EARLY = true>
+    __device__ __forceinline__ void store(float *out, uint32_t n, bool live, float inv, const RowSlice &tr,
+                                          const float *truth, float *delta, float *loss) {
+        float t[XENT ? M : 1];
+        bool any = false;
+        if constexpr (XENT) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if constexpr (EARLY) t[m] = tr.v[m];
+                else t[m] = (live && inside(m, n)) ? truth[at(m)] : 0.0f;
+                any |= t[m] != 0.0f;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) v[m] = v[m] * inv;
+        if constexpr (V4) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const uint32_t q = j + (uint32_t)k * P;
+                if (!(live && 4 * q < n)) continue;
+                st4<false>(out, q, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
+                if constexpr (XENT)
+                    st4<false>(delta, q, make_float4(t[4 * k] - v[4 * k], t[4 * k + 1] - v[4 * k + 1],
+                                                     t[4 * k + 2] - v[4 * k + 2], t[4 * k + 3] - v[4 * k + 3]));
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (!(live && inside(m, n))) continue;
+                out[at(m)] = v[m];
+                if constexpr (XENT) delta[at(m)] = t[m] - v[m];
+            }
+        }
+        if constexpr (XENT) {
+            float l[M];
+            if (__ballot(any) != 0) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) l[m] = xent_loss(v[m], t[m]);
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) l[m] = 0.0f;
+            }
+            if constexpr (V4) {
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    const uint32_t q = j + (uint32_t)k * P;
+                    if (live && 4 * q < n)
+                        st4<false>(loss, q, make_float4(l[4 * k], l[4 * k + 1], l[4 * k + 2], l[4 * k + 3]));
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                    if (live && inside(m, n)) loss[at(m)] = l[m];
+            }
+        }
+    }
+};
+
+// Segments of L lanes, one group each; blockDim.x / L groups a workgroup.
+// The group's truth is read with its logits (XENT), so the loss costs no
+// second memory round trip.
+template <int L, int K, bool V4, bool XENT>
+__global__ __launch_bounds__(kBlock) void softmax_seg_kernel(const float *in, float *out, Groups G, uint32_t rows,
+                                                             Xent xe) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t r = blockIdx.x * (blockDim.x / L) + t / L;
+    const bool live = r < rows;  // the same for the whole segment
+    const uint32_t off = group_base(live ? r : 0u, G), n = G.n;
+    RowSlice<K, V4> x;
+    x.j = t & (L - 1);
+    x.P = L;
+    x.load(in + off, n, live, -FLT_MAX);
+    RowSlice<K, V4> tr;  // the truth (XENT only)
+    if constexpr (XENT) {
+        tr.j = x.j;
+        tr.P = L;
+        tr.load(xe.truth + off, n, live, 0.0f);
+    }
+    const float mx = seg_max<L>(x.max());
+    const double s = seg_sum<L>(x.exps(n, live, G.temp, mx / G.temp));
+    const float inv = (float)(1.0 / s);
+    if constexpr (XENT) {
+        x.template store<true>(out + off, n, live, inv, tr, nullptr, xe.delta + off, xe.loss + off);
+    } else {
+        x.template store<false>(out + off, n, live, inv, x, nullptr, nullptr, nullptr);
+    }
+}
+
+// One workgroup (blockDim.x = 64..1024 lanes) per group.
+template <int K, bool V4, bool XENT>
+__global__ __launch_bounds__(1024) void softmax_wg_kernel(const float *in, float *out, Groups G, Xent xe) {
+    __shared__ float red_f[16];
+    __shared__ double red_d[16];
+    const uint32_t t = threadIdx.x, nw = blockDim.x / kWave, w = t / kWave;
+    const uint32_t off = group_base(blockIdx.x, G), n = G.n;
+    RowSlice<K, V4> x;
+    x.j = t;
+    x.P = blockDim.x;
+    x.load(in + off, n, true, -FLT_MAX);
+    // The truth is read with the logits when it fits in registers beside
+    // them (K <= 4), otherwise as the results are stored.
+    constexpr bool kEarly = K <= 4;
+    RowSlice<K, V4> tr;  // the truth (XENT and kEarly only)
+    if constexpr (XENT && kEarly) {
+        tr.j = t;
+        tr.P = blockDim.x;
+        tr.load(xe.truth + off, n, true, 0.0f);
+    }
+    float mx = wave_max(x.max());
+    if ((t & (kWave - 1)) == 0) red_f[w] = mx;
+    __syncthreads();
+    mx = red_f[0];
+    for (uint32_t i = 1; i < nw; ++i) mx = fmaxf(mx, red_f[i]);
+    double s = wave_sum(x.exps(n, true, G.temp, mx / G.temp));
+    if ((t & (kWave - 1)) == 0) red_d[w] = s;
+    __syncthreads();
+    s = red_d[0];
+    for (uint32_t i = 1; i < nw; ++i) s += red_d[i];
+    const float inv = (float)(1.0 / s);
+    if constexpr (XENT) {
+        x.template store<true, kEarly>(out + off, n, true, inv, tr, xe.truth + off, xe.delta + off,
+                                       xe.loss + off);
+    } else {
+        x.template store<false>(out + off, n, true, inv, x, nullptr, nullptr, nullptr);
+    }
+}
+
+// Groups longer than a workgroup holds in registers: one workgroup of
+// kBigBlock lanes per group, three passes over x (the max; the sum of the
+// exps; the exps scaled and stored, with the loss when XENT), eight elements
+// a lane in flight per step.
+constexpr uint32_t kBigBlock = 1024;
+
+template <bool XENT>
+__global__ __launch_bounds__(kBigBlock) void softmax_big_kernel(const float *in, float *out, Groups G, Xent xe) {
+    __shared__ float red_f[kBigBlock / kWave];
+    __shared__ double red_d[kBigBlock / kWave];
+    constexpr uint32_t kU = 8;
+    const uint32_t t = threadIdx.x, w = t / kWave, n = G.n;
     const uint32_t off = group_base(blockIdx.x, G);
     const float *x = in + off;
-    float *y = out + off;
-    const uint32_t n = G.n, nv = n >> 2;
-
     float mx = -FLT_MAX;
-    float sum;
-    if constexpr (SEQ) {
-        // The row is read once, into LDS; the max is order-free.
-        if constexpr (V4) {
-            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
-                const float4 a = ld4<false>(x, v);
-                e_lds4[v] = a;
-                mx = fmaxf(mx, fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)));
-            }
-        } else {
-            for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
-                const float a = x[i];
-                e_lds[i] = a;
-                mx = fmaxf(mx, a);
-            }
-        }
-        mx = block_max(mx, red_f);
-        const float mt = mx / G.temp;
-        // Each lane turns the entries it loaded into exps, in place.
-        if constexpr (V4) {
-            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
-                float4 a = e_lds4[v];
-                a.x = expf_libm(a.x / G.temp - mt);
-                a.y = expf_libm(a.y / G.temp - mt);
-                a.z = expf_libm(a.z / G.temp - mt);
-                a.w = expf_libm(a.w / G.temp - mt);
-                e_lds4[v] = a;
-            }
-        } else {
-            for (uint32_t i = threadIdx.x; i < n; i += kBlock) e_lds[i] = expf_libm(e_lds[i] / G.temp - mt);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            // The one sequential part, in batches of 32 exps: the LDS reads of
-            // the next batch are in flight while this one is added.
-            float s = 0.0f;
-            const uint32_t nb = n >> 5;
-            float4 va[8], vb[8];
-            if (nb > 0) read32(e_lds4, 0, va);
-            for (uint32_t b = 0; b < nb;) {
-                if (b + 1 < nb) read32(e_lds4, b + 1, vb);
-                s = add32(s, va);
-                if (++b >= nb) break;
-                if (b + 1 < nb) read32(e_lds4, b + 1, va);
-                s = add32(s, vb);
-                ++b;
-            }
-            for (uint32_t i = nb << 5; i < n; ++i) s += e_lds[i];
-            sum_sh = s;
-        }
-        __syncthreads();
-        sum = sum_sh;
-        if constexpr (V4) {
-            for (uint32_t v = threadIdx.x; v < nv; v += kBlock) {
-                const float4 e = e_lds4[v];
-                const float4 p = make_float4(e.x / sum, e.y / sum, e.z / sum, e.w / sum);
-                st4<false>(y, v, p);
-                if constexpr (XENT) {
-                    const float4 t = ld4<false>(xe.truth + off, v);
-                    float4 d, l;
-                    xent1(p.x, t.x, d.x, l.x);
-                    xent1(p.y, t.y, d.y, l.y);
-                    xent1(p.z, t.z, d.z, l.z);
-                    xent1(p.w, t.w, d.w, l.w);
-                    st4<false>(xe.delta + off, v, d);
-                    st4<false>(xe.loss + off, v, l);
-                }
-            }
-        } else {
-            for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
-                const float p = e_lds[i] / sum;
-                y[i] = p;
-                if constexpr (XENT) xent1(p, xe.truth[off + i], xe.delta[off + i], xe.loss[off + i]);
-            }
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) mx = fmaxf(mx, x[i]);
-        mx = block_max(mx, red_f);
-        const float mt = mx / G.temp;
-        double acc = 0.0;
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
-            const float e = expf_libm(x[i] / G.temp - mt);
-            y[i] = e;
-            acc += (double)e;
-        }
-        sum = (float)block_sum(acc, red_d);
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock) {
-            const float p = y[i] / sum;
-            y[i] = p;
+    for (uint32_t i0 = t; i0 < n; i0 += kBigBlock * kU) {
+        float v[kU];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) v[u] = i0 + u * kBigBlock < n ? x[i0 + u * kBigBlock] : -FLT_MAX;
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) mx = fmaxf(mx, v[u]);
+    }
+    mx = wave_max(mx);
+    if ((t & (kWave - 1)) == 0) red_f[w] = mx;
+    __syncthreads();
+    mx = red_f[0];
+    for (uint32_t i = 1; i < kBigBlock / kWave; ++i) mx = fmaxf(mx, red_f[i]);
+    const float mt = mx / G.temp;
+    double s = 0.0;
+    for (uint32_t i0 = t; i0 < n; i0 += kBigBlock * kU) {
+        float v[kU];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) v[u] = i0 + u * kBigBlock < n ? x[i0 + u * kBigBlock] : 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u)
+            if (i0 + u * kBigBlock < n) s += (double)expf_cw(v[u] / G.temp - mt);
+    }
+    s = wave_sum(s);
+    if ((t & (kWave - 1)) == 0) red_d[w] = s;
+    __syncthreads();
+    s = red_d[0];
+    for (uint32_t i = 1; i < kBigBlock / kWave; ++i) s += red_d[i];
+    const float inv = (float)(1.0 / s);
+    for (uint32_t i0 = t; i0 < n; i0 += kBigBlock * kU) {
+        float v[kU];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) v[u] = i0 + u * kBigBlock < n ? x[i0 + u * kBigBlock] : 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < kU; ++u) {
+            const uint32_t i = i0 + u * kBigBlock;
+            if (i >= n) continue;
+            const float p = expf_cw(v[u] / G.temp - mt) * inv;
+            out[off + i] = p;
             if constexpr (XENT) xent1(p, xe.truth[off + i], xe.delta[off + i], xe.loss[off + i]);
         }
     }
 }
 
-constexpr uint32_t kRows = 16;
-// Up to 256 elements a row (16 KiB of LDS a workgroup): measured against the
-// one-workgroup-per-row kernel, [16384,100] 28.7 -> 9.6 us and [8192,256]
-// 18.0 -> 14.8 us, while rows of 1000 were slower (64 KiB a workgroup leaves
-// two per CU, too few loads in flight).
-constexpr uint32_t kRowsMaxN = 256;
-constexpr uint32_t kRowsMin = 4096;
-
-// op(...op(op(acc, row[0]), row[1])..., row[n-1]): one lane's sequential fold
-// of an LDS row, with the reads of the next 16 elements in flight while the
-// current 16 are folded.
-template <class Op>
-__device__ __forceinline__ float row_fold(const float *row, uint32_t n, float acc, Op op) {
-    constexpr uint32_t kB = 16;
-    const uint32_t nb = n / kB;
-    float a[kB], b[kB];
-    if (nb > 0) {
-#pragma unroll
-        for (uint32_t u = 0; u < kB; ++u) a[u] = row[u];
-    }
-    for (uint32_t j = 0; j < nb;) {
-        if (j + 1 < nb) {
-#pragma unroll
-            for (uint32_t u = 0; u < kB; ++u) b[u] = row[(j + 1) * kB + u];
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kB; ++u) acc = op(acc, a[u]);
-        if (++j >= nb) break;
-        if (j + 1 < nb) {
-#pragma unroll
-            for (uint32_t u = 0; u < kB; ++u) a[u] = row[(j + 1) * kB + u];
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kB; ++u) acc = op(acc, b[u]);
-        ++j;
-    }
-    for (uint32_t i = nb * kB; i < n; ++i) acc = op(acc, row[i]);
-    return acc;
-}
-
-struct MaxOp {
-    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-};
-struct AddOp {
-    __device__ float operator()(float a, float b) const { return a + b; }
-};
-
-// Groups r0 .. r0+kRows-1, contiguous (stride 1); tile[l*pitch + i] holds
-// element i of group r0 + l.
-__global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const float *in, float *out, Groups G, FastDiv div_n,
-                                                              uint32_t pitch, uint32_t rows) {
-    extern __shared__ float tile[];
-    __shared__ uint32_t base_sh[kRows];
-    __shared__ float mt_sh[kRows], sum_sh[kRows];
-    const uint32_t r0 = blockIdx.x * kRows;
-    const uint32_t nr = rows - r0 < kRows ? rows - r0 : kRows;
-    const uint32_t n = G.n, total = nr * n, t = threadIdx.x;
-    if (t < kRows) base_sh[t] = t < nr ? group_base(r0 + t, G) : 0u;
-    __syncthreads();
-    // Eight loads per lane in flight: element i of row l for q = l*n + i.
-    for (uint32_t q0 = t; q0 < total; q0 += kBlock * 8) {
-        float v[8];
-        uint32_t at[8];
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) {
-            const uint32_t q = q0 + u * kBlock;
-            const uint32_t l = fdiv(q, div_n), i = q - l * n;
-            at[u] = l * pitch + i;
-            v[u] = q < total ? in[base_sh[q < total ? l : 0] + i] : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u)
-            if (q0 + u * kBlock < total) tile[at[u]] = v[u];
-    }
-    __syncthreads();
-    if (t < nr) mt_sh[t] = row_fold(tile + t * pitch, n, -FLT_MAX, MaxOp{}) / G.temp;
-    __syncthreads();
-    for (uint32_t q = t; q < total; q += kBlock) {
-        const uint32_t l = fdiv(q, div_n), i = q - l * n;
-        float &e = tile[l * pitch + i];
-        e = expf_libm(e / G.temp - mt_sh[l]);
-    }
-    __syncthreads();
-    if (t < nr) sum_sh[t] = row_fold(tile + t * pitch, n, 0.0f, AddOp{});
-    __syncthreads();
-    for (uint32_t q = t; q < total; q += kBlock) {
-        const uint32_t l = fdiv(q, div_n), i = q - l * n;
-        out[base_sh[l] + i] = tile[l * pitch + i] / sum_sh[l];
-    }
-}
-
-// Many contiguous groups of kRowsMaxN < n <= kWideMaxN: R groups a
-// workgroup (R * 1028 floats of LDS at most), held in registers -- lane t holds elements 4t..4t+3 (V4) or
-// t, t+256, t+512, t+768 of each -- so the maxes (wave64 DPP + LDS) and the
-// exps run on all lanes; the exps then go to LDS (row pitch a multiple of 4
-// but not of 32) where lane l < R of the first wave adds group l's in order,
-// so R sequential sums advance per instruction, and all lanes divide their
-// registers by the sums. Bit-exact.
-// Groups a workgroup: about 1024 workgroups (fewer leave the loads, the
-// VALU-heavy exps and divides and the stores of the workgroups in lock step;
-// more repeat the per-workgroup barriers and sums): measured at n = 1000,
-// 2048 groups 16.8 -> 12.4 us (R = 2), 4096 24.5 -> 17.5 (R = 4), 8192
-// 41.5 -> 28.9 and 16384 80 -> 50.5 (R = 8); below 2048 groups the
-// one-workgroup-per-group kernel is as fast.
-#ifndef DKZ_SOFTMAX_WIDE_MIN
-#define DKZ_SOFTMAX_WIDE_MIN 2048
+// Segment path: groups of up to kSegMaxN elements, L lanes each.
+constexpr uint32_t kSegMaxN = 2048;
+// Groups below which one workgroup per group is used even for short groups
+// (more waves per group to spread a small launch over the CUs).
+#ifndef DKZ_SOFTMAX_SEG_MIN_ROWS
+#define DKZ_SOFTMAX_SEG_MIN_ROWS 1024
 #endif
-constexpr uint32_t kWideMaxN = 4 * kBlock;
+// Workgroup path: up to 1024 lanes x 32 floats.
+constexpr uint32_t kWgMaxN = 32768;
 
-template <int R, bool V4, bool XENT>
-__global__ __launch_bounds__(kBlock) void softmax_wide_kernel(const float *in, float *out, Groups G, uint32_t rows,
-                                                              uint32_t pitch, Xent xe) {
-    extern __shared__ float4 wide_lds4[];  // R rows of `pitch` floats
-    float *tile = reinterpret_cast<float *>(wide_lds4);
-    __shared__ float red[R][kBlock / kWave];
-    __shared__ float sum_sh[R];
-    const uint32_t t = threadIdx.x, n = G.n, r0 = blockIdx.x * R;
-    const uint32_t nr = rows - r0 < (uint32_t)R ? rows - r0 : (uint32_t)R;
-    const int wave = (int)(t / kWave);
-    // Element j of this lane's four in a group (V4: 4t + j; else t + 256j).
-    auto at = [&](int j) -> uint32_t { return V4 ? 4 * t + (uint32_t)j : t + (uint32_t)j * kBlock; };
-
-    float v[R][4];
-    uint32_t base[R];
-#pragma unroll
-    for (int l = 0; l < R; ++l) base[l] = group_base(r0 + ((uint32_t)l < nr ? (uint32_t)l : 0u), G);
-#pragma unroll
-    for (int l = 0; l < R; ++l) {
-        const bool live = (uint32_t)l < nr;
-        if constexpr (V4) {
-            float4 a = make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
-            if (live && 4 * t < n) a = ld4<false>(in + base[l], t);
-            v[l][0] = a.x;
-            v[l][1] = a.y;
-            v[l][2] = a.z;
-            v[l][3] = a.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[l][j] = live && at(j) < n ? in[base[l] + at(j)] : -FLT_MAX;
-        }
-    }
-#pragma unroll
-    for (int l = 0; l < R; ++l) {
-        const float m = wave_max(fmaxf(fmaxf(v[l][0], v[l][1]), fmaxf(v[l][2], v[l][3])));
-        if ((t & (kWave - 1)) == 0) red[l][wave] = m;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int l = 0; l < R; ++l) {
-        const float mt = fmaxf(fmaxf(red[l][0], red[l][1]), fmaxf(red[l][2], red[l][3])) / G.temp;
-        float *row = tile + l * pitch;
-        if constexpr (V4) {
-            if (4 * t < n) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[l][j] = expf_libm(v[l][j] / G.temp - mt);
-                reinterpret_cast<float4 *>(row)[t] = make_float4(v[l][0], v[l][1], v[l][2], v[l][3]);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (at(j) < n) {
-                    v[l][j] = expf_libm(v[l][j] / G.temp - mt);
-                    row[at(j)] = v[l][j];
-                }
-            }
-        }
-    }
-    __syncthreads();
-    if (t < nr) {
-        // Group t's exps left to right, 32 at a time, the next 32's LDS reads
-        // in flight while these are added.
-        const float4 *row4 = reinterpret_cast<const float4 *>(tile + t * pitch);
-        float s = 0.0f;
-        const uint32_t nb = n >> 5;
-        float4 va[8], vb[8];
-        if (nb > 0) read32(row4, 0, va);
-        for (uint32_t b = 0; b < nb;) {
-            if (b + 1 < nb) read32(row4, b + 1, vb);
-            s = add32(s, va);
-            if (++b >= nb) break;
-            if (b + 1 < nb) read32(row4, b + 1, va);
-            s = add32(s, vb);
-            ++b;
-        }
-        for (uint32_t i = nb << 5; i < n; ++i) s += tile[t * pitch + i];
-        sum_sh[t] = s;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int l = 0; l < R; ++l) {
-        if ((uint32_t)l >= nr) break;
-        const float sum = sum_sh[l];
-        const uint32_t off = base[l];
-        if constexpr (V4) {
-            if (4 * t < n) {
-                const float4 p = make_float4(v[l][0] / sum, v[l][1] / sum, v[l][2] / sum, v[l][3] / sum);
-                st4<false>(out + off, t, p);
-                if constexpr (XENT) {
-                    const float4 tr = ld4<false>(xe.truth + off, t);
-                    float4 d, ls;
-                    xent1(p.x, tr.x, d.x, ls.x);
-                    xent1(p.y, tr.y, d.y, ls.y);
-                    xent1(p.z, tr.z, d.z, ls.z);
-                    xent1(p.w, tr.w, d.w, ls.w);
-                    st4<false>(xe.delta + off, t, d);
-                    st4<false>(xe.loss + off, t, ls);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (at(j) < n) {
-                    const float p = v[l][j] / sum;
-                    out[off + at(j)] = p;
-                    if constexpr (XENT) xent1(p, xe.truth[off + at(j)], xe.delta[off + at(j)], xe.loss[off + at(j)]);
-                }
-            }
-        }
-    }
+template <int L, int K>
+int launch_seg(const float *input, float *output, const Groups &G, uint32_t rows, bool v4, const Xent *xe) {
+    // Four segments' waves a workgroup when that still gives >= 512
+    // workgroups, else one wave (small launches reach more CUs).
+    const uint32_t per_wave = (uint32_t)(kWave / L);
+    const uint32_t block = (uint64_t)rows >= 512ull * 4 * per_wave ? (uint32_t)kBlock : (uint32_t)kWave;
+    const dim3 grid(div_up(rows, block / L));
+    const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
+    void (*k)(const float *, float *, Groups, uint32_t, Xent);
+    if (xe) k = v4 ? softmax_seg_kernel<L, K, true, true> : softmax_seg_kernel<L, K, false, true>;
+    else k = v4 ? softmax_seg_kernel<L, K, true, false> : softmax_seg_kernel<L, K, false, false>;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k, grid, dim3(block), 0, current_stream(), input, output, G, rows, x);
+    return after_launch(xe ? "softmax_xent_seg" : "softmax_seg", grid, dim3(block));
 }
 
-template <int R>
-int launch_wide(const float *input, float *output, const Groups &G, uint32_t rows, bool v4, const Xent *xe) {
-    const uint32_t n4 = (G.n + 3) & ~3u;
-    const uint32_t pitch = n4 % 32 == 0 ? n4 + 4 : n4;  // a multiple of 4, not of 32
-    const size_t lds = (size_t)R * pitch * sizeof(float);
+template <int K>
+int launch_wg(const float *input, float *output, const Groups &G, uint32_t rows, uint32_t block, bool v4,
+              const Xent *xe) {
     const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
-    void (*k)(const float *, float *, Groups, uint32_t, uint32_t, Xent);
-    if (xe) k = v4 ? softmax_wide_kernel<R, true, true> : softmax_wide_kernel<R, false, true>;
-    else k = v4 ? softmax_wide_kernel<R, true, false> : softmax_wide_kernel<R, false, false>;
-    const dim3 grid(div_up(rows, (uint32_t)R));
+    void (*k)(const float *, float *, Groups, Xent);
+    if (xe) k = v4 ? softmax_wg_kernel<K, true, true> : softmax_wg_kernel<K, false, true>;
+    else k = v4 ? softmax_wg_kernel<K, true, false> : softmax_wg_kernel<K, false, false>;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, current_stream(), input, output, G, rows, pitch, x);
-    return after_launch(xe ? "softmax_xent_wide" : "softmax_wide", grid, dim3(kBlock));
+    hipLaunchKernelGGL(k, dim3(rows), dim3(block), 0, current_stream(), input, output, G, x);
+    return after_launch(xe ? "softmax_xent_wg" : "softmax_wg", dim3(rows), dim3(block));
+}
+
+// Contiguous groups (stride 1) of more than 32 elements.
+int softmax_contiguous(const float *input, float *output, const Groups &G, uint32_t rows, bool v4,
+                       const Xent *xe) {
+    const uint32_t n = G.n;
+    if (n <= kSegMaxN && rows >= DKZ_SOFTMAX_SEG_MIN_ROWS) {
+        if (n <= 64) return launch_seg<4, 4>(input, output, G, rows, v4, xe);
+        if (n <= 128) return launch_seg<8, 4>(input, output, G, rows, v4, xe);
+        if (n <= 256) return launch_seg<16, 4>(input, output, G, rows, v4, xe);
+        if (n <= 512) return launch_seg<32, 4>(input, output, G, rows, v4, xe);
+        if (n <= 1024) return launch_seg<64, 4>(input, output, G, rows, v4, xe);
+        return launch_seg<64, 8>(input, output, G, rows, v4, xe);
+    }
+    if (n <= kWgMaxN) {
+        // Lanes for about four floats each (64..1024), then 4K floats a lane.
+        uint32_t block = kWave;
+        while (block < 1024 && 4 * block < n) block *= 2;
+        const uint32_t per_lane = (n + block - 1) / block;
+        if (per_lane <= 4) return launch_wg<1>(input, output, G, rows, block, v4, xe);
+        if (per_lane <= 8) return launch_wg<2>(input, output, G, rows, block, v4, xe);
+        if (per_lane <= 16) return launch_wg<4>(input, output, G, rows, block, v4, xe);
+        return launch_wg<8>(input, output, G, rows, block, v4, xe);
+    }
+    const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
+    if (xe)
+        return launch("softmax_xent_big", softmax_big_kernel<true>, dim3(rows), dim3(kBigBlock), input, output, G, x);
+    return launch("softmax_big", softmax_big_kernel<false>, dim3(rows), dim3(kBigBlock), input, output, G, x);
 }
 
 constexpr uint32_t kTileRows = 64;
@@ -557,34 +566,9 @@ int softmax_run(const float *input, int n, int batch, int batch_offset, int grou
         return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
                       G, rows);
     }
-    if (!xe && rows >= kRowsMin && (uint32_t)n <= kRowsMaxN) {
-        const uint32_t pitch = (uint32_t)n | 1u;  // odd: the rows' columns fall in distinct banks
-        const size_t lds = (size_t)kRows * pitch * sizeof(float);
-        (void)hipGetLastError();
-        hipLaunchKernelGGL(softmax_rows_kernel, dim3(div_up(rows, kRows)), dim3(kBlock), lds, current_stream(),
-                           input, output, G, make_fastdiv((uint32_t)n), pitch, rows);
-        return after_launch("softmax_rows", dim3(div_up(rows, kRows)), dim3(kBlock));
-    }
-    const bool seq = (uint32_t)n <= kSeqMax;
     bool v4 = n % 4 == 0 && batch_offset % 4 == 0 && group_offset % 4 == 0 && aligned16(input) && aligned16(output);
     if (xe) v4 = v4 && aligned16(xe->truth) && aligned16(xe->delta) && aligned16(xe->loss);
-    if (rows >= DKZ_SOFTMAX_WIDE_MIN && (uint32_t)n > kRowsMaxN && (uint32_t)n <= kWideMaxN) {
-        if (rows >= 8192) return launch_wide<8>(input, output, G, rows, v4, xe);
-        if (rows >= 4096) return launch_wide<4>(input, output, G, rows, v4, xe);
-        return launch_wide<2>(input, output, G, rows, v4, xe);
-    }
-    const Xent x = xe ? *xe : Xent{nullptr, nullptr, nullptr};
-    const size_t lds = seq ? (size_t)n * sizeof(float) : 0;
-    void (*k)(const float *, float *, Groups, Xent);
-    if (seq) {
-        if (xe) k = v4 ? softmax_block_kernel<true, true, true> : softmax_block_kernel<true, true, false>;
-        else k = v4 ? softmax_block_kernel<true, false, true> : softmax_block_kernel<true, false, false>;
-    } else {
-        k = xe ? softmax_block_kernel<false, true, false> : softmax_block_kernel<false, false, false>;
-    }
-    (void)hipGetLastError();
-    hipLaunchKernelGGL(k, dim3(rows), dim3(kBlock), lds, current_stream(), input, output, G, x);
-    return after_launch(xe ? "softmax_xent" : "softmax", dim3(rows), dim3(kBlock));
+    return softmax_contiguous(input, output, G, rows, v4, xe);
 }
 
 }  // namespace

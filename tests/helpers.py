@@ -3,11 +3,14 @@
 Parity rules (north star):
   * elementwise, broadcast and index results: bit-exact (NaNs compare equal
     to each other whatever their payload);
-  * reductions and softmax-derived losses: an element passes when
-    |gpu - cpu| <= 1e-5 * |cpu|, or when the GPU value is at least as close to
-    an f64 evaluation of the same formula as the CPU twin's is. The second
-    clause covers ill-conditioned sums (a channel mean of N(0,1) data is ~0),
-    where the twin's own sequential f32 rounding error exceeds 1e-5 relative.
+  * reductions, softmax and softmax-derived losses: an element passes when
+    |gpu - cpu| <= 1e-5 * max(|cpu|, FLT_MIN), or when the GPU value is at
+    least as close to an f64 evaluation of the same formula as the CPU twin's
+    is. The second clause covers ill-conditioned sums (a channel mean of
+    N(0,1) data is ~0), where the twin's own sequential f32 rounding error
+    exceeds 1e-5 relative. The FLT_MIN floor covers subnormal results, which
+    carry fewer than 24 significant bits, so that 1e-5 relative is finer than
+    their spacing (a softmax probability below 2^-126).
 """
 
 from __future__ import annotations
@@ -17,6 +20,7 @@ import numpy as np
 from darknet_zig_amd import gpu
 
 RTOL = 1e-5
+FLT_MIN = float(np.finfo(np.float32).tiny)
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -79,7 +83,7 @@ def assert_r5(got: np.ndarray, cpu: np.ndarray, ref64: np.ndarray, name: str) ->
     """The reduction rule above; returns error statistics for reporting."""
     got64, cpu64, ref = got.astype(np.float64), cpu.astype(np.float64), ref64.astype(np.float64)
     d = np.abs(got64 - cpu64)
-    ok = (d <= RTOL * np.abs(cpu64)) | (np.abs(got64 - ref) <= np.abs(cpu64 - ref))
+    ok = (d <= RTOL * np.maximum(np.abs(cpu64), FLT_MIN)) | (np.abs(got64 - ref) <= np.abs(cpu64 - ref))
     ok |= (np.isnan(got64) & np.isnan(cpu64)) | (got64 == cpu64)
     if not ok.all():
         i = np.nonzero(~ok)[0][:5]
@@ -114,3 +118,45 @@ def col2im64(col: np.ndarray, channels: int, height: int, width: int, ksize: int
             vx = (xs >= 0) & (xs < width)
             im[:, ys[vy][:, None], xs[vx][None, :]] += colr[:, kh, kw][:, vy][:, :, vx]
     return im.ravel()
+
+
+def softmax_groups(n, batch, batch_offset, groups, group_offset, stride) -> np.ndarray:
+    """[batch*groups, n] flat indices of every group's elements
+    (gpu.zig:614-629: group (b, g) starts at b*batch_offset + g*group_offset,
+    its elements `stride` apart)."""
+    b = np.arange(batch)[:, None] * batch_offset
+    g = np.arange(groups)[None, :] * group_offset
+    start = (b + g).reshape(-1, 1)
+    return start + np.arange(n)[None, :] * stride
+
+
+def softmax_f64(x: np.ndarray, n, batch, batch_offset, groups, group_offset, stride, temp) -> np.ndarray:
+    """The twin's softmax (blas.zig:213-223) in f64 from the twin's own f32
+    exp arguments: max, then a = f32(x/T) - f32(max/T) rounded to f32 exactly
+    as the twin rounds it, then exp, sum and divide in f64. Returns an array
+    shaped like x (NaN outside the groups)."""
+    idx = softmax_groups(n, batch, batch_offset, groups, group_offset, stride)
+    v = x[idx].astype(np.float32)
+    mx = np.maximum(np.max(v, axis=1, keepdims=True), np.float32(-np.finfo(np.float32).max))
+    t = np.float32(temp)
+    a = (v / t - mx / t).astype(np.float32)
+    e = np.exp(a.astype(np.float64))
+    out = np.full(x.shape, np.nan)
+    out[idx] = e / e.sum(axis=1, keepdims=True)
+    return out
+
+
+def assert_softmax(got: np.ndarray, cpu: np.ndarray, p64: np.ndarray, name: str, rel: float = 1e-6) -> dict:
+    """Softmax probabilities: the 1e-5 rule against the twin (assert_r5), and
+    every probability within `rel` relative (FLT_MIN floor) of the f64
+    evaluation -- the device sums in f64 and its exp is within one ulp, so a
+    dropped term, a wrong max or a misplaced element fails this by orders of
+    magnitude."""
+    stats = assert_r5(got, cpu, p64, name)
+    g = got.astype(np.float64)
+    bad = np.abs(g - p64) > rel * np.maximum(np.abs(p64), FLT_MIN)
+    if bad.any():
+        i = np.nonzero(bad)[0][:5]
+        raise AssertionError(f"{name}: {int(bad.sum())} probabilities farther than {rel} from f64; first "
+                             f"{i.tolist()}: gpu={got[i].tolist()} f64={p64[i].tolist()}")
+    return stats

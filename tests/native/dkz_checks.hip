@@ -8,7 +8,11 @@
 //   * chk_expf_hash_host / chk_expf_hash_device: an order-independent hash of
 //     expf over a bit-pattern range, from the C library (host) and from
 //     expf_libm running on the GPU, so the two can be compared without moving
-//     2^32 results.
+//     2^32 results;
+//   * chk_expf_cw / chk_expf_cw_max_err / chk_expf_cw_hash_*: the same for
+//     expf_cw, softmax's exp: its host build against exp in double (the
+//     largest error in ulps over a bit-pattern range), and the hash of its
+//     host build against its device build (they must agree bit for bit).
 //
 // Built by tests/native/build.py into tests/native/libdkz_checks.so.
 #include <math.h>
@@ -60,6 +64,61 @@ uint64_t parallel_sum(uint64_t lo, uint64_t hi, int threads, F f) {
     return s;
 }
 
+template <class F>
+uint64_t parallel_max(uint64_t lo, uint64_t hi, int threads, F f) {
+    if (threads < 1) threads = 1;
+    std::vector<uint64_t> part(threads, 0);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; ++t) {
+        pool.emplace_back([&, t] {
+            const uint64_t a = lo + (hi - lo) * t / threads, b = lo + (hi - lo) * (t + 1) / threads;
+            uint64_t m = 0;
+            for (uint64_t i = a; i < b; ++i) {
+                const uint64_t v = f(i);
+                m = v > m ? v : m;
+            }
+            part[t] = m;
+        });
+    }
+    for (auto &th : pool) th.join();
+    uint64_t m = 0;
+    for (uint64_t v : part) m = v > m ? v : m;
+    return m;
+}
+
+// |expf_cw(x) - exp(x)| in 1/1024 ulps of the float nearest exp(x) (the ulp
+// of a subnormal being 2^-149), exp(x) evaluated in double; 0 for NaN inputs
+// when the result is NaN.
+uint64_t expf_cw_err(uint64_t i) {
+    float x;
+    const uint32_t u = (uint32_t)i;
+    memcpy(&x, &u, 4);
+    const float y = dkz::expf_cw(x);
+    if (x != x) return y != y ? 0u : ~0ull;
+    const double e = exp((double)x);
+    const float ef = (float)e;
+    if (isinf(ef) || isinf(y)) return (isinf(ef) && isinf(y)) ? 0u : ~0ull;
+    int ex = 0;
+    frexp(e, &ex);
+    const double ulp = ldexp(1.0, (ex - 24 < -149) ? -149 : ex - 24);
+    return (uint64_t)(fabs((double)y - e) / ulp * 1024.0);
+}
+
+__global__ void expf_cw_hash_kernel(uint64_t lo, uint64_t hi, unsigned long long *out) {
+    uint64_t s = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = lo + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hi; i += stride) {
+        const uint32_t u = (uint32_t)i;
+        float x;
+        __builtin_memcpy(&x, &u, 4);
+        const float r = dkz::expf_cw(x);
+        uint32_t rb;
+        __builtin_memcpy(&rb, &r, 4);
+        s += mix(i, canon(rb));
+    }
+    atomicAdd(out, (unsigned long long)s);
+}
+
 __global__ void expf_hash_kernel(uint64_t lo, uint64_t hi, unsigned long long *out) {
     uint64_t s = 0;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -101,6 +160,39 @@ uint64_t chk_expf_hash_host(uint64_t lo, uint64_t hi, int threads) {
         memcpy(&x, &u, 4);
         return mix(i, canon(bits_of(expf(x))));
     });
+}
+
+float chk_expf_cw(float x) { return dkz::expf_cw(x); }
+
+uint64_t chk_expf_cw_max_err(uint64_t lo, uint64_t hi, int threads) {
+    return parallel_max(lo, hi, threads, expf_cw_err);
+}
+
+uint64_t chk_expf_cw_hash_host(uint64_t lo, uint64_t hi, int threads) {
+    return parallel_sum(lo, hi, threads, [](uint64_t i) -> uint64_t {
+        float x;
+        const uint32_t u = (uint32_t)i;
+        memcpy(&x, &u, 4);
+        return mix(i, canon(bits_of(dkz::expf_cw(x))));
+    });
+}
+
+// Returns a hipError_t; *hash receives the device-side hash of expf_cw.
+int chk_expf_cw_hash_device(uint64_t lo, uint64_t hi, uint64_t *hash) {
+    unsigned long long *d = nullptr;
+    hipError_t e = hipMalloc(&d, sizeof *d);
+    if (e != hipSuccess) return (int)e;
+    e = hipMemset(d, 0, sizeof *d);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(expf_cw_hash_kernel, dim3(8192), dim3(256), 0, nullptr, lo, hi, d);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    unsigned long long h = 0;
+    if (e == hipSuccess) e = hipMemcpy(&h, d, sizeof h, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    *hash = h;
+    return (int)e;
 }
 
 // Returns a hipError_t; *hash receives the device-side hash.

@@ -6,6 +6,9 @@ compiled for the host from the same source (tests/native/dkz_checks.hip):
   this check is tests/test_gpu_expf.py);
 * its 2^(i/32) table, against 2^(i/32) computed to 60 digits and rounded to
   double;
+* expf_cw, softmax's exp, against exp in double over all 2^32 float inputs:
+  within one ulp everywhere (its device build is checked bit for bit against
+  this host build in tests/test_gpu_expf.py);
 * the launch-constant division against Python's integer division.
 """
 
@@ -32,6 +35,10 @@ def lib():
     L.chk_expf_restated.argtypes = [C.c_float]
     L.chk_expf_host_mismatches.restype = C.c_uint64
     L.chk_expf_host_mismatches.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+    L.chk_expf_cw.restype = C.c_float
+    L.chk_expf_cw.argtypes = [C.c_float]
+    L.chk_expf_cw_max_err.restype = C.c_uint64
+    L.chk_expf_cw_max_err.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
     return L
 
 
@@ -62,6 +69,34 @@ def test_expf_special_values():
 def test_expf_matches_libm_on_every_float():
     threads = min(os.cpu_count() or 4, 16)
     assert lib().chk_expf_host_mismatches(0, 1 << 32, threads) == 0
+
+
+def test_expf_cw_special_values():
+    L = lib()
+    assert L.chk_expf_cw(0.0) == 1.0
+    assert L.chk_expf_cw(-0.0) == 1.0
+    assert L.chk_expf_cw(float("-inf")) == 0.0
+    assert L.chk_expf_cw(float("inf")) == float("inf")
+    assert np.isnan(L.chk_expf_cw(float("nan")))
+    assert L.chk_expf_cw(89.0) == float("inf")
+    assert L.chk_expf_cw(88.72) < float("inf")  # just below FLT_MAX's log
+    assert L.chk_expf_cw(-104.0) == 0.0
+    assert L.chk_expf_cw(-103.9) == np.float32(2.0 ** -149)  # the smallest subnormal
+    assert L.chk_expf_cw(1.0) == np.float32(np.e)
+    for k in range(-149, 128):  # near 2^k: every binade, subnormals included
+        x = float(np.float32(k * np.log(2.0)))
+        want = np.exp(x)
+        ulp = 2.0 ** max(np.frexp(want)[1] - 24, -149)
+        assert abs(L.chk_expf_cw(x) - want) < ulp, k
+
+
+@pytest.mark.parametrize("part", range(4))
+def test_expf_cw_within_one_ulp_everywhere(part):
+    """max |expf_cw(x) - exp(x)| over a quarter of the float bit patterns, in
+    ulps of the result (2^-149 for subnormals): measured 0.94 ulp."""
+    threads = min(os.cpu_count() or 4, 16)
+    lo, hi = part << 30, (part + 1) << 30
+    assert lib().chk_expf_cw_max_err(lo, hi, threads) / 1024.0 < 1.0
 
 
 DIVISORS = sorted({1, 2, 3, 5, 7, 13, 14, 28, 49, 53, 196, 784, 1024, 3136, 4096, 12544, 65535, 65536, 65537,

@@ -201,10 +201,12 @@ def _bn_forward_cpu(x, scales, biases, roll_m, roll_v, shape):
     m, v = np.empty(F, np.float32), np.empty(F, np.float32)
     ref.mean(out, B, F, S, m)
     ref.variance(out, m, B, F, S, v)
-    ref.scal(0.99, roll_m)
-    ref.axpy(0.01, m, roll_m)
-    ref.scal(0.99, roll_v)
-    ref.axpy(0.01, v, roll_v)
+    # batchnorm.zig:140-143 with its f32 constants: scal(rolling_momentum),
+    # axpy(1 - rolling_momentum) -- 0.99f and 0.00999999f, not 0.01
+    ref.scal(ref.ROLLING_MOMENTUM, roll_m)
+    ref.axpy(ref.EMA_ALPHA, m, roll_m)
+    ref.scal(ref.ROLLING_MOMENTUM, roll_v)
+    ref.axpy(ref.EMA_ALPHA, v, roll_v)
     ref.normalize(out, m, v, B, F, S)
     x_norm = out.copy()
     ref.scaleBias(out, scales, B, F, S)
@@ -230,10 +232,10 @@ def test_bn_layer_forward_sequence(dev):
     gpu.copy(n, d_out, d_x)
     gpu.mean(d_out, B, F, S, d_m)
     gpu.variance(d_out, d_m, B, F, S, d_v)
-    gpu.scal(F, 0.99, d_rm)
-    gpu.axpy(F, 0.01, d_m, d_rm)
-    gpu.scal(F, 0.99, d_rv)
-    gpu.axpy(F, 0.01, d_v, d_rv)
+    gpu.scal(F, float(ref.ROLLING_MOMENTUM), d_rm)
+    gpu.axpy(F, float(ref.EMA_ALPHA), d_m, d_rm)
+    gpu.scal(F, float(ref.ROLLING_MOMENTUM), d_rv)
+    gpu.axpy(F, float(ref.EMA_ALPHA), d_v, d_rv)
     gpu.normalize(d_out, d_m, d_v, B, F, S)
     gpu.copy(n, d_out, d_xn)
     gpu.scaleBias(d_out, d_s, B, F, S)
