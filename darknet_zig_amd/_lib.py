@@ -80,6 +80,7 @@ SIGNATURES: dict[str, tuple] = {
     "dkz_adam_update": (_i, [_p, _p, _p, _p, _f, _f, _f, _f, _f, _i, _i, _i]),
     "dkz_batchnorm_forward": (_i, [_i, _i, _i, _i, _i] + [_p] * 10),
     "dkz_batchnorm_backward": (_i, [_i, _i, _i, _i] + [_p] * 11),
+    "dkz_batchnorm_backward_noalloc": (_i, [_i, _i, _i, _i] + [_p] * 11),
 }
 
 _LIB: C.CDLL | None = None

@@ -28,6 +28,9 @@ inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args..
     return after_launch(name, grid, block);
 }
 
+// Devices the library keeps per-device state for (ordinals 0..63).
+constexpr int kMaxDevices = 64;
+
 // Scratch of the current device, allocated once by dkz_init (or on first
 // use) and zeroed then: the f64 partial sums one split channel reduction
 // hands from its first launch to its second, the partial tiles of a split-K
@@ -48,6 +51,24 @@ constexpr uint32_t kScratchPartials = 1u << 18;    // channels * chunks (2 MiB o
 constexpr uint64_t kScratchGemmFloats = 1ull << DKZ_SCRATCH_GEMM_LOG2;  // split-K partial tiles (128 MiB)
 constexpr uint32_t kScratchSlots = 1u << 12;         // channels
 int device_scratch(Scratch *out);
+
+// While one of these lives, device_scratch() on this host thread returns
+// *s instead of the library's allocated scratch (and allocates nothing): the
+// no-allocation entry point runs the regular code with its static scratch.
+class ScratchOverride {
+  public:
+    explicit ScratchOverride(const Scratch *s);
+    ~ScratchOverride();
+    ScratchOverride(const ScratchOverride &) = delete;
+    ScratchOverride &operator=(const ScratchOverride &) = delete;
+
+  private:
+    const Scratch *prev_;
+};
+
+// Per-device set-up of the static scratch of the no-allocation entry point
+// (noalloc.hip): looks its address up once for the current device `dev`.
+int static_scratch_setup(int dev);
 
 // Largest element count any op indexes with 32-bit arithmetic, as the
 // reference's kernels do (int global_index(), darknet_kernels.hip:40-42).

@@ -13,8 +13,6 @@
 namespace dkz {
 namespace {
 
-constexpr int kMaxDevices = 64;
-
 struct DeviceState {
     void *scratch = nullptr;
 };
@@ -24,6 +22,7 @@ std::mutex g_mutex;
 hipStream_t g_stream = nullptr;
 bool g_sync_after_launch = false;
 thread_local char g_context[512] = "";
+thread_local const Scratch *t_scratch_override = nullptr;
 
 bool env_flag(const char *name) {
     const char *v = getenv(name);
@@ -82,7 +81,15 @@ int after_launch(const char *name, dim3 grid, dim3 block) {
     return 0;
 }
 
+ScratchOverride::ScratchOverride(const Scratch *s) : prev_(t_scratch_override) { t_scratch_override = s; }
+
+ScratchOverride::~ScratchOverride() { t_scratch_override = prev_; }
+
 int device_scratch(Scratch *out) {
+    if (t_scratch_override != nullptr) {
+        *out = *t_scratch_override;
+        return 0;
+    }
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;
@@ -123,7 +130,8 @@ int dkz_init(int device) {
         return (int)e;
     }
     if (env_flag("DARKNET_GPU_SYNC") || env_flag("DARKNET_HIP_SYNC")) g_sync_after_launch = true;
-    return ensure_scratch(device);
+    DKZ_TRY(ensure_scratch(device));
+    return static_scratch_setup(device);
 }
 
 int dkz_device_name(int device, char *buf, int len) {

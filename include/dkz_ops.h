@@ -420,6 +420,20 @@ int dkz_batchnorm_backward(int batch, int filters, int spatial, int activation, 
                            const float *variance, const float *scales, float *bias_updates,
                            float *scale_updates, float *mean_delta, float *variance_delta);
 
+/* No counterpart in the reference: dkz_batchnorm_backward for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
+ * results, bit for bit; its scratch is a static device array of 2 MiB of
+ * partial sums + 32 KiB of meeting slots per GPU (held until the process
+ * ends) instead of the library's allocated scratch, and it calls no
+ * hipMalloc/hipFree. Limit: the ABI's 2^31-1 elements, beyond which it
+ * returns hipErrorInvalidValue. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (two streams or host threads) race. */
+int dkz_batchnorm_backward_noalloc(int batch, int filters, int spatial, int activation, const float *output,
+                                   float *delta, const float *x, const float *x_norm, const float *mean,
+                                   const float *variance, const float *scales, float *bias_updates,
+                                   float *scale_updates, float *mean_delta, float *variance_delta);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,7 +47,7 @@ def exported_symbols() -> set[str]:
 
 def test_header_exports_and_binding_agree():
     declared = header_symbols()
-    assert len(declared) == len(set(declared)) == 57
+    assert len(declared) == len(set(declared)) == 58
     assert set(declared) == exported_symbols()
     assert list(_lib.SIGNATURES) == declared  # same set, same order as the header
 
