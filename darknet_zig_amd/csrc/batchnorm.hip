@@ -350,6 +350,143 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
     }
 }
 
+// ---- one-launch forward --------------------------------------------------------
+
+// The K workgroups of one channel wait for each other here (thread 0 of
+// each; the caller's __syncthreads follow). count and gen are the channel's
+// two counter slots: every workgroup reads gen, counts itself in count, and
+// the last to arrive empties count (for the next launch) and advances gen,
+// which releases the others. This workgroup's partial sums were written with
+// coherent atomic stores before it arrives, and the s_waitcnt orders their
+// completion before the arrival, so whoever sees gen move sees them.
+//
+// A channel's workgroups have consecutive indices and the hardware
+// dispatches workgroups in index order, so the lowest channel not yet done
+// always has all its workgroups resident or about to be, and completes: no
+// deadlock for any grid size as long as K workgroups fit the GPU at once.
+// The wait is bounded anyway (kSpinMax sleeps of ~128 cycles, ~0.1 s), so
+// every wave ends even if that assumption failed.
+constexpr uint32_t kSpinMax = 1u << 20;
+
+__device__ __forceinline__ void channel_barrier(uint64_t *count, uint64_t *gen, uint32_t K) {
+    const uint64_t g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint64_t before = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == (uint64_t)(K - 1)) {
+        __hip_atomic_store(count, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __hip_atomic_fetch_add(gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    for (uint32_t it = 0; it < kSpinMax; ++it) {
+        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != g0) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+// Channel f's K partials of each of NS sums (partials[((q*F + f)*K + k) *
+// kPartialStride]), read with coherent loads and added in index order over
+// one wave: every workgroup of the channel gets the same bits.
+template <int NS>
+__device__ __forceinline__ Sums<NS> wave_partials_coherent(const double *partials, uint32_t F, uint32_t K,
+                                                           uint32_t f) {
+    const uint32_t l = threadIdx.x & (kWave - 1);
+    Sums<NS> r;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const double *p = partials + ((uint64_t)q * F + f) * K * kPartialStride;
+        double s = 0.0;
+        for (uint32_t i = l; i < K; i += kWave)
+            s += __hip_atomic_load(&p[(uint64_t)i * kPartialStride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        r.s[q] = wave_sum(s);
+    }
+    return r;
+}
+
+// Chunk of kCoopU float4s a lane: a workgroup owns at most kCoopChunk
+// elements of one channel. Measured at config 1 (cold / Infinity-Cache
+// resident): 4 float4s 17.6 / 13.3 us, 8 16.3 / 12.9, 16 18.0 / 15.6.
+// x, the input's copy, is stored as soon as it is loaded (x after the
+// barrier with the other two outputs: 16.4 / 13.3 us).
+#ifndef DKZ_BN_COOP_U
+#define DKZ_BN_COOP_U 8
+#endif
+constexpr int kCoopU = DKZ_BN_COOP_U;
+#ifndef DKZ_BN_COOP_X_LATE
+#define DKZ_BN_COOP_X_LATE 0
+#endif
+constexpr uint32_t kCoopChunk = kBlock * 4 * kCoopU;
+
+// Forward (train) in one launch: workgroup (f, k) -- channel-major, k
+// fastest -- loads chunk k of channel f into registers once, adds its f64
+// shifted sums (as bn_stats_kernel), posts them, waits at the channel
+// barrier, adds the channel's K partials, forms mean, variance (and, in
+// workgroup k == 0, the rolling averages) exactly as the split statistics
+// path does, and writes x, x_norm and the output from the registers. The
+// input is read once: 16 bytes an element instead of 20.
+template <int A, int H>
+__global__ __launch_bounds__(kBlock) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
+                                                             float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
+                                                             double *partials, uint64_t *slots) {
+    constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
+    constexpr bool kXLate = DKZ_BN_COOP_X_LATE != 0;
+    __shared__ double lds[2 * (kBlock / kWave)];
+    __shared__ FwdChan chan_sh;
+    const uint32_t f = fdiv(blockIdx.x, g.div_k);
+    const uint32_t k = blockIdx.x - f * g.K;
+    const uint32_t F = g.div_filters.d;
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const double c = (double)input[fbase];
+    float4 v[kCoopU];
+    uint32_t at[kCoopU];
+#pragma unroll
+    for (int u = 0; u < kCoopU; ++u) {
+        const uint32_t j = j0 + 4 * threadIdx.x + (uint32_t)u * (4 * kBlock);
+        at[u] = j < j1 ? chan_addr(fbase, j, g) >> 2 : 0xffffffffu;
+        if (j < j1) v[u] = ld4<kNtIn>(input, at[u]);
+    }
+    double a[2] = {0.0, 0.0};
+#pragma unroll
+    for (int u = 0; u < kCoopU; ++u) {
+        if (at[u] == 0xffffffffu) continue;
+        acc_shifted(v[u], c, a[0], a[1]);
+        // x (the input copy) needs no statistics: its stores drain while
+        // the channel meets
+        if constexpr (!kXLate) st4<kNtX>(x, at[u], v[u]);
+    }
+    const Sums<2> r = block_sums<2, kBlock>(a, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const Sums<2> sums = wave_partials_coherent<2>(partials, F, g.K, f);
+        if (threadIdx.x == 0) {
+            float m, var;
+            fin.stats(sums, c, m, var);
+            chan_sh = fwd_chan(m, var, p.scales[f], p.biases[f]);
+            if (k == 0) fin.write(f, m, var);
+        }
+    }
+    __syncthreads();
+    const FwdChan ch = chan_sh;
+#pragma unroll
+    for (int u = 0; u < kCoopU; ++u) {
+        if (at[u] == 0xffffffffu) continue;
+        float4 xn, o;
+        fwd_elem<A>(v[u], ch, xn, o);
+        if constexpr (kXLate) st4<kNtX>(x, at[u], v[u]);
+        st4<kNtXn>(x_norm, at[u], xn);
+        st4<kNtOut>(output, at[u], o);
+    }
+}
+
 // ---- backward -----------------------------------------------------------------
 
 // Per channel: s0 = sum(d1), s1 = sum(d1 * x_norm), s2 = sum(d2),
@@ -531,6 +668,21 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 
 // ---- host ---------------------------------------------------------------------
 
+// The one-launch forward for channels of up to kCoopMaxChan elements (a
+// channel's workgroups must fit the GPU at once: 256 per channel at most,
+// each with a quarter of a CU's wave slots).
+#ifndef DKZ_BN_FWD_COOP
+#define DKZ_BN_FWD_COOP 1
+#endif
+constexpr uint64_t kCoopMaxChan = 256ull * kCoopChunk;
+// ... and at most this many workgroups in all, so that the whole grid is
+// resident at once (otherwise workgroups waiting at their barrier hold CUs
+// that later channels need: config 2's shape, 6272 workgroups, took 105 us
+// against 97 for the two passes).
+#ifndef DKZ_BN_COOP_MAX_WGS
+#define DKZ_BN_COOP_MAX_WGS 2048
+#endif
+
 struct Shape {
     uint32_t B, F, S, n;
 };
@@ -605,6 +757,19 @@ int bn_forward_fused(const FwdArgs &a) {
         const FwdParams p{a.rolling_mean, a.rolling_variance, a.scales, a.biases};
         return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, false, H, false>, grid, block, a.input,
                       a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
+    }
+    if (DKZ_BN_FWD_COOP && L <= kCoopMaxChan && sh.F <= kScratchSlots / kCounterStride &&
+        (uint64_t)sh.F * div_up(L, kCoopChunk) <= DKZ_BN_COOP_MAX_WGS &&
+        2ull * sh.F * div_up(L, kCoopChunk) * kPartialStride <= kScratchPartials) {
+        // one launch: chunks of at most kCoopChunk elements, whole float4s
+        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, div_up(L, kCoopChunk), true);
+        Scratch scc{nullptr};
+        DKZ_TRY(device_scratch(&scc));
+        const FwdFin finc{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
+                          (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
+        const FwdParams p{a.mean, a.variance, a.scales, a.biases};
+        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP>, dim3(sh.F * gc.K),
+                      dim3(kBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc, scc.partials, scc.slots);
     }
     const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;

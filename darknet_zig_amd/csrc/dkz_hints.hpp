@@ -142,6 +142,10 @@
 #ifndef DKZ_HINT_BN_FWD_APPLY
 #define DKZ_HINT_BN_FWD_APPLY 7
 #endif
+// one-launch forward: the same bits as the apply pass
+#ifndef DKZ_HINT_BN_FWD_COOP
+#define DKZ_HINT_BN_FWD_COOP DKZ_HINT_BN_FWD_APPLY
+#endif
 // backward sums: bit 0 = y, bit 1 = delta, bit 2 = x_norm, bit 3 = x loads
 #ifndef DKZ_HINT_BN_BWD_SUMS
 #define DKZ_HINT_BN_BWD_SUMS 15

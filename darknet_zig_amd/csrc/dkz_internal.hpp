@@ -34,8 +34,9 @@ constexpr int kMaxDevices = 64;
 // Scratch of the current device, allocated once by dkz_init (or on first
 // use) and zeroed then: the f64 partial sums one split channel reduction
 // hands from its first launch to its second, the partial tiles of a split-K
-// gemm, and one 64-bit meeting slot per channel for the reductions whose two
-// workgroups per channel meet inside one launch. Every user writes all the
+// gemm, and one 64-bit counter slot per channel for the reductions whose
+// workgroups count themselves in to find the channel's last (reduce.hip).
+// Every user writes all the
 // partials and tiles it then reads; the slots start at zero and every user
 // leaves them at zero.
 struct Scratch {
@@ -49,7 +50,19 @@ constexpr uint32_t kScratchPartials = 1u << 18;    // channels * chunks (2 MiB o
 #define DKZ_SCRATCH_GEMM_LOG2 25
 #endif
 constexpr uint64_t kScratchGemmFloats = 1ull << DKZ_SCRATCH_GEMM_LOG2;  // split-K partial tiles (128 MiB)
-constexpr uint32_t kScratchSlots = 1u << 12;         // channels
+constexpr uint32_t kScratchSlots = 1u << 16;         // 64-bit counter slots (512 KiB)
+// A split reduction's per-channel counters and f64 partials sit
+// kCounterStride / kPartialStride elements apart, so that no two share a
+// 128-byte line: atomics and write-through stores to one line are
+// serialised at the memory side.
+#ifndef DKZ_SPLIT_CSTRIDE
+#define DKZ_SPLIT_CSTRIDE 32
+#endif
+#ifndef DKZ_SPLIT_PSTRIDE
+#define DKZ_SPLIT_PSTRIDE 16
+#endif
+constexpr uint32_t kCounterStride = DKZ_SPLIT_CSTRIDE;
+constexpr uint32_t kPartialStride = DKZ_SPLIT_PSTRIDE;
 int device_scratch(Scratch *out);
 
 // While one of these lives, device_scratch() on this host thread returns

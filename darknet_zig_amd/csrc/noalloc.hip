@@ -8,10 +8,11 @@
 //   * kScratchPartials f64 partial sums (2 MiB): what a split reduction
 //     hands from its partial pass to its finalisation. Every call writes all
 //     the partials it then reads.
-//   * kScratchSlots 64-bit meeting slots (32 KiB): the two workgroups of a
-//     channel reduction meet in their channel's slot, which must be zero when
-//     a call starts. Each call clears the slots of its channels first (a
-//     small kernel, not a memset, so the call can be captured in a graph).
+//   * kScratchSlots 64-bit counter slots (512 KiB): the workgroups of a split
+//     channel reduction count themselves in their channel's slot to find the
+//     last one, so the slot must be zero when a call starts. Each call clears
+//     the slots of its channels first (a small kernel, not a memset, so the
+//     call can be captured in a graph).
 // Nothing here calls hipMalloc, hipFree or an allocating library routine.
 // Each GPU holds its own copy of the array until the process ends; every
 // call on a GPU shares it, so calls that overlap on one GPU (two streams,
@@ -73,8 +74,8 @@ int dkz_batchnorm_backward_noalloc(int batch, int filters, int spatial, int acti
     DKZ_REQUIRE(batch >= 0 && filters >= 0 && spatial >= 0);
     if (filters == 0) return 0;
     // Every split the kernels choose fits the array (pick_split sizes the
-    // partials to kScratchPartials); the slots cover kScratchSlots channels,
-    // the most any channel reduction meets in (reduce.hip).
+    // partials to kScratchPartials); the slots cover every channel a split
+    // channel reduction counts in (reduce.hip).
     if ((uint64_t)batch * (uint64_t)filters * (uint64_t)spatial > kMaxElems) {
         set_error_context("%s: %d x %d x %d elements exceed the 2^31-1 the static scratch path supports", __func__,
                           batch, filters, spatial);
@@ -87,7 +88,8 @@ int dkz_batchnorm_backward_noalloc(int batch, int filters, int spatial, int acti
     unsigned char *base = static_cast<unsigned char *>(g_scratch_ptr[dev]);
     const Scratch sc{reinterpret_cast<double *>(base), nullptr, 0,
                      reinterpret_cast<uint64_t *>(base + kPartialsBytes)};
-    const uint32_t nslots = (uint32_t)filters < kScratchSlots ? (uint32_t)filters : kScratchSlots;
+    const uint64_t want = (uint64_t)filters * kCounterStride;  // channel f's counter is slot f*kCounterStride
+    const uint32_t nslots = want < kScratchSlots ? (uint32_t)want : kScratchSlots;
     DKZ_TRY(launch("batchnorm_backward_noalloc_zero_slots", zero_slots_kernel, dim3(div_up(nslots, kBlock)),
                    dim3(kBlock), sc.slots, nslots));
     const ScratchOverride use(&sc);

@@ -10,16 +10,16 @@
 //     delta*x_norm, delta*(x-m), rounded exactly as blas.zig rounds them -- and
 //     accumulates it in f64. A chunk is then summed by wave64 DPP reductions
 //     and a 4-entry LDS step (dkz_device.hpp).
-//   * K == 1 (enough channels to fill the GPU, see pick_split): the
-//     workgroup, 1024 threads wide for long channels, finalises its channel
-//     itself (one launch).
-//     K > 1: each workgroup stores its f64 partial, and a second, tiny launch
-//     (one wave per channel) adds the K partials in index order and
-//     finalises. The kernel boundary orders the two passes, so no workgroup
-//     needs a device-scope fence (which on gfx950 writes back and invalidates
-//     the whole XCD L2) and nothing uses atomics: the result is deterministic,
-//     and it is the exact sum to within f64 rounding, so its distance to the
-//     CPU twin's sequential f32 sum is that sum's own rounding error.
+//   * K (chan_split) aims at ~2048 workgroups in all, so the grid covers the
+//     256 CUs several times whatever the channel count. K == 1 (channels
+//     alone enough): the workgroup, 1024 threads wide for long channels,
+//     finalises its channel itself. K > 1: one launch in which the last
+//     workgroup of each channel to finish adds the channel's K f64 partials
+//     in index order and finalises (chan_split_kernel: coherent atomic
+//     stores and a per-channel counter, no fence, nothing waits). The result
+//     is deterministic, and it is the exact sum to within f64 rounding, so
+//     its distance to the CPU twin's sequential f32 sum is that sum's own
+//     rounding error.
 //   * The finalisation repeats blas.zig's f32 arithmetic on the f32-rounded
 //     total: sum * (1/(B*S)), sum * (-1/sqrt(v+1e-5)), updates[f] += sum, ...
 #include "dkz_channel.hpp"
@@ -28,11 +28,12 @@
 namespace dkz {
 namespace {
 
-constexpr int kUnroll = 4;
-constexpr uint32_t kCuCount = 256;
-
-#ifndef DKZ_CHAN_PAIR
-#define DKZ_CHAN_PAIR 1
+#ifndef DKZ_CHAN_UNROLL
+#define DKZ_CHAN_UNROLL 4
+#endif
+constexpr int kUnroll = DKZ_CHAN_UNROLL;
+#ifndef DKZ_CHAN_KMAJOR
+#define DKZ_CHAN_KMAJOR 1
 #endif
 
 template <class Term>
@@ -93,56 +94,81 @@ __global__ __launch_bounds__(BS) void chan_reduce_kernel(T t, Fin fin, const flo
     if (threadIdx.x == 0) fin(blockIdx.x, total, pre);
 }
 
-// K == 1 with fewer channels than CUs: two workgroups per channel in one
-// launch, so that every CU streams. The two meet in channel f's 64-bit slot
-// (zero when empty): each swaps its partial in with one agent-scope atomic
-// exchange, which returns what the slot held. The one that gets the other's
-// partial back adds the two (f64 addition is commutative, so the sum does not
-// depend on which finished first), empties the slot for the next launch and
-// finalises. A partial travels as its bits XOR kSlotKey -- a NaN payload no
-// sum produces, since NaNs reaching it carry an f32 payload whose low 29 bits
-// are zero -- so a stored partial is never zero.
-constexpr uint64_t kSlotKey = 0xFFF8DEADBEEF0001ull;
-
-template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
-__global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
-                                                       uint64_t *slots) {
-    __shared__ double lds[BS / kWave];
-    const uint32_t f = blockIdx.x >> 1, k = blockIdx.x & 1;
-    const float pre = threadIdx.x == 0 ? fin.pre(f) : 0.0f;
-    const double s = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, f, k, lds);
+// K > 1, one launch: workgroup (f, k) stores its f64 partial at
+// partials[f*K + k] with an agent-scope atomic store, which is written
+// through to the memory side where every XCD's L2 sees it (gfx950's L2s are
+// not coherent with each other for ordinary stores), waits for that store to
+// complete, and then counts itself in channel f's counter with an
+// agent-scope atomic add. The workgroup that brings the counter to K is the
+// channel's last: it empties the counter for the next launch, reads the K
+// partials with agent-scope atomic loads (which bypass its own L2) and adds
+// them in index order over one wave, exactly as the two-launch finalisation
+// does, then finalises. No fence: a release/acquire fence at agent scope
+// writes back and invalidates the whole L2 of the XCD. Nothing waits on
+// another workgroup, so any grid size is safe, and the sum's order is fixed
+// by the shape alone (deterministic).
+template <class T, class Fin, bool TWO, bool VEC, int H>
+__global__ __launch_bounds__(kBlock) void chan_split_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
+                                                            double *partials, uint64_t *counters) {
+    __shared__ double lds[kBlock / kWave];
+    __shared__ uint32_t last_sh;
+    uint32_t f, k;
+    if constexpr (DKZ_CHAN_KMAJOR != 0) {
+        // consecutive workgroups: the same chunk of consecutive channels, so
+        // the grid sweeps the tensor in address order
+        k = fdiv(blockIdx.x, g.div_filters);
+        f = blockIdx.x - k * g.div_filters.d;
+    } else {
+        f = fdiv(blockIdx.x, g.div_k);
+        k = blockIdx.x - f * g.K;
+    }
+    const uint32_t slot = f * g.K + k;
+    const double total = chunk_sum<T, TWO, VEC, H, kBlock>(t, p0, p1, g, f, k, lds);
     if (threadIdx.x == 0) {
-        const uint64_t mine = __builtin_bit_cast(uint64_t, s) ^ kSlotKey;
-        const uint64_t held = __hip_atomic_exchange(&slots[f], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (held != 0) {
-            __hip_atomic_store(&slots[f], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            fin(f, s + __builtin_bit_cast(double, held ^ kSlotKey), pre);
-        }
+        __hip_atomic_store(&partials[(uint64_t)slot * kPartialStride], total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint64_t before = __hip_atomic_fetch_add(&counters[(uint64_t)f * kCounterStride], 1ull,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_sh = before == (uint64_t)(g.K - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last_sh == 0 || threadIdx.x >= kWave) return;
+    const float pre = fin.pre(f);
+    const double *p = partials + (uint64_t)f * g.K * kPartialStride;
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x; i < g.K; i += kWave)
+        s += __hip_atomic_load(&p[(uint64_t)i * kPartialStride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s = wave_sum(s);
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&counters[(uint64_t)f * kCounterStride], 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        fin(f, s, pre);
     }
 }
 
-// K > 1, pass 1: workgroup (f, k) stores its partial at partials[f*K + k].
-template <class T, bool TWO, bool VEC, int H>
-__global__ __launch_bounds__(kBlock) void chan_partial_kernel(T t, const float *p0, const float *p1, RedGeom g,
-                                                              double *partials) {
-    __shared__ double lds[kBlock / kWave];
-    const uint32_t f = fdiv(blockIdx.x, g.div_k);
-    const uint32_t k = blockIdx.x - f * g.K;
-    const double total = chunk_sum<T, TWO, VEC, H, kBlock>(t, p0, p1, g, f, k, lds);
-    if (threadIdx.x == 0) partials[blockIdx.x] = total;
-}
-
-// K > 1, pass 2: one wave per channel adds its K partials in a fixed order.
-template <class Fin>
-__global__ __launch_bounds__(kBlock) void chan_finalize_kernel(Fin fin, const double *partials, uint32_t F,
-                                                               uint32_t K) {
-    const uint32_t f = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
-    if (f >= F) return;  // whole waves leave together
-    const float pre = fin.pre(f);
-    double s = 0.0;
-    for (uint32_t i = threadIdx.x & (kWave - 1); i < K; i += kWave) s += partials[f * K + i];
-    s = wave_sum(s);
-    if ((threadIdx.x & (kWave - 1)) == 0) fin(f, s, pre);
+// Workgroups per channel of a per-op reduction: about DKZ_CHAN_TARGET_WGS
+// workgroups in all (four per CU), each owning at least DKZ_CHAN_MIN_CHUNK
+// elements; one per channel when the channels alone are that many. From the
+// shape only, so a shape always reduces in the same order. Measured on
+// MI355X with chunk-major order: 2048 / 4096 workgroups gave config 2's
+// backward_bias 19.0 / 25.8 us against 18.8, config 1's mean 6.4 against
+// 5.9 us (every extra workgroup adds an atomic on its channel's counter).
+#ifndef DKZ_CHAN_TARGET_WGS
+#define DKZ_CHAN_TARGET_WGS 1024
+#endif
+#ifndef DKZ_CHAN_MIN_CHUNK
+#define DKZ_CHAN_MIN_CHUNK 2048
+#endif
+// K > 1 only when filters < DKZ_CHAN_TARGET_WGS, so a padded counter per
+// channel always fits the scratch's slots.
+static_assert((uint64_t)DKZ_CHAN_TARGET_WGS * DKZ_SPLIT_CSTRIDE <= kScratchSlots, "one counter per split channel");
+inline uint32_t chan_split(uint32_t filters, uint32_t chan_len) {
+    uint32_t k = div_up(DKZ_CHAN_TARGET_WGS, filters);
+    const uint32_t kmax = chan_len / DKZ_CHAN_MIN_CHUNK > 1 ? chan_len / DKZ_CHAN_MIN_CHUNK : 1;
+    if (k > kmax) k = kmax;
+    while (k > 1 && (uint64_t)filters * k * kPartialStride > kScratchPartials) --k;
+    return k < 1 ? 1 : k;
 }
 
 template <int H, class T, class Fin, bool TWO>
@@ -152,24 +178,8 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     DKZ_REQUIRE(chan_len64 * (uint64_t)filters <= kMaxElems);
     const uint32_t F = (uint32_t)filters, S = (uint32_t)spatial, L = (uint32_t)chan_len64;
     const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
-    const RedGeom g = make_red_geom(F, S, L, pick_split(F, L, TWO ? 2 : 1), vec);
+    const RedGeom g = make_red_geom(F, S, L, chan_split(F, L), vec);
     const uint32_t K = g.K;
-#if DKZ_CHAN_PAIR
-    if (K == 1 && F < kCuCount && F <= kScratchSlots && L >= 32 * kWideBlock) {
-        // Two halves per channel, whole float4s each.
-        const RedGeom g2 = make_red_geom(F, S, L, 2, vec);
-        Scratch sc{nullptr};
-        DKZ_TRY(device_scratch(&sc));
-        if (g2.K == 2) {
-            const dim3 block(kWideBlock);
-            if (vec)
-                return launch(name, chan_pair_kernel<T, Fin, TWO, true, H, kWideBlock>, dim3(2 * F), block, t, fin,
-                              p0, p1, g2, sc.slots);
-            return launch(name, chan_pair_kernel<T, Fin, TWO, false, H, kWideBlock>, dim3(2 * F), block, t, fin, p0,
-                          p1, g2, sc.slots);
-        }
-    }
-#endif
     if (K == 1) {
         if (L >= 16 * kWideBlock) {
             const dim3 block(kWideBlock);
@@ -184,11 +194,10 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     Scratch sc{nullptr};
     DKZ_TRY(device_scratch(&sc));
     if (vec)
-        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, true, H>, dim3(F * K), block, t, p0, p1, g, sc.partials));
-    else
-        DKZ_TRY(launch(name, chan_partial_kernel<T, TWO, false, H>, dim3(F * K), block, t, p0, p1, g, sc.partials));
-    return launch(name, chan_finalize_kernel<Fin>, dim3(div_up(F, kBlock / kWave)), block, fin,
-                  (const double *)sc.partials, F, K);
+        return launch(name, chan_split_kernel<T, Fin, TWO, true, H>, dim3(F * K), block, t, fin, p0, p1, g,
+                      sc.partials, sc.slots);
+    return launch(name, chan_split_kernel<T, Fin, TWO, false, H>, dim3(F * K), block, t, fin, p0, p1, g,
+                  sc.partials, sc.slots);
 }
 
 // ---- per-element terms (f32, rounded as the CPU twin rounds them) ---------

@@ -39,13 +39,13 @@
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
  *   - The library owns one scratch buffer per device (130 MiB), allocated and
- *     zeroed by dkz_init: the f64 partial sums a per-channel reduction passes
- *     from its first launch to its second (2 MiB), the partial tiles of a
- *     split-K gemm or convolution weight gradient (128 MiB) and the 64-bit
- *     slots (32 KiB) in which the two workgroups of a channel meet in
- *     one-launch reductions. Ops never allocate. Reductions or gemms issued
- *     concurrently on two streams of one device share that buffer and race;
- *     issue them on one stream.
+ *     zeroed by dkz_init: the f64 partial sums of the split per-channel
+ *     reductions (2 MiB), the partial tiles of a split-K gemm or convolution
+ *     weight gradient (128 MiB) and one 64-bit counter slot per channel
+ *     (32 KiB) in which a split reduction's workgroups find the channel's
+ *     last. Ops never allocate. Reductions or gemms issued concurrently on
+ *     two streams of one device share that buffer and race; issue them on
+ *     one stream (dkz_set_stream).
  */
 #ifndef DKZ_OPS_H
 #define DKZ_OPS_H
@@ -125,7 +125,11 @@ const char *dkz_last_error_context(void);
 
 /* No counterpart in the reference, which always uses the null stream: choose
  * the hipStream_t (passed as void*) that later ops and copies are issued on.
- * NULL selects the null stream again. */
+ * NULL selects the null stream again. The choice is process-wide. Split
+ * reductions and gemms use the device's one scratch (partials and
+ * per-channel counters), so two streams running them at the same time on
+ * one device race: switch streams only between such ops, not to overlap
+ * them. */
 int dkz_set_stream(void *stream);
 void *dkz_get_stream(void);
 
@@ -424,7 +428,7 @@ int dkz_batchnorm_backward(int batch, int filters, int spatial, int activation, 
  * cannot allocate device memory (code under HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
  * results, bit for bit; its scratch is a static device array of 2 MiB of
- * partial sums + 32 KiB of meeting slots per GPU (held until the process
+ * partial sums + 32 KiB of counter slots per GPU (held until the process
  * ends) instead of the library's allocated scratch, and it calls no
  * hipMalloc/hipFree. Limit: the ABI's 2^31-1 elements, beyond which it
  * returns hipErrorInvalidValue. Every call on one GPU shares that array:

@@ -156,9 +156,9 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
 
 @pytest.mark.parametrize("shape", [CONFIG1, CONFIG2, (16, 64, 3136)], ids=str)
 def test_reductions_deterministic(dev, shape):
-    """Same input, same bits, every time: the split reductions hand their
-    partials to a second launch, which adds them in a fixed order. 200
-    repeats of each op at shapes that split."""
+    """Same input, same bits, every time: a split reduction's last workgroup
+    per channel adds the partials in index order, whichever workgroup that
+    is. 200 repeats of each op at shapes that split."""
     B, F, S = shape
     r = rng(9)
     x, d = normal(r, B * F * S), normal(r, B * F * S)

@@ -291,3 +291,50 @@ def test_empty_batch_follows_the_sequence(dev):
     gpu.batchnormBackward(0, F, 16, Activation.leaky, e, e, e, e, d_m, d_v, d_s, d_bu, d_b, d_md, d_vd)
     assert_bitexact(down(d_bu, np.empty(F, np.float32)), np.full(F, 2.0, np.float32), "no batch, no update")
     _free(d_m, d_v, d_rm, d_rv, d_s, d_b, d_bu, d_md, d_vd)
+
+
+def test_forward_back_to_back(dev):
+    """Channels split over several workgroups meet at a per-channel barrier
+    inside one launch (the one-launch forward). 30 calls on different inputs
+    issued back to back with no synchronisation (sync-after-launch off): a
+    barrier counter not emptied, or partials read before they were visible,
+    would show in a later call's statistics."""
+    from darknet_zig_amd import _lib
+
+    lib = _lib.load()
+    before = lib.dkz_get_sync_after_launch()
+    lib.dkz_set_sync_after_launch(0)
+    try:
+        B, F, S = 16, 24, 1024  # 16384 elements a channel: 4 workgroups per channel
+        n = B * F * S
+        r = rng(123)
+        rounds = 30
+        xs = [normal(r, n, 0.3 * k, 1.0 + 0.1 * k) for k in range(rounds)]
+        scales, biases = uniform(r, F, 0.5, 1.5), normal(r, F, 0, 0.1)
+        d_s, d_b = up(scales), up(biases)
+        bufs = []
+        for k in range(rounds):
+            d = dict(inp=up(xs[k]), out=gpu.alloc(n), x=gpu.alloc(n), xn=gpu.alloc(n), m=gpu.alloc(F),
+                     v=gpu.alloc(F), rm=gpu.alloc(F), rv=gpu.alloc(F))
+            bufs.append(d)
+        for d in bufs:
+            gpu.batchnormForward(B, F, S, Activation.leaky, True, d["inp"], d["out"], d["x"], d["xn"], d["m"], d["v"],
+                                 d["rm"], d["rv"], d_s, d_b)
+        gpu.sync()
+        for k, d in enumerate(bufs):
+            c_m, c_v = np.empty(F, np.float32), np.empty(F, np.float32)
+            ref.mean(xs[k], B, F, S, c_m)
+            ref.variance(xs[k], c_m, B, F, S, c_v)
+            x64 = _chan64(xs[k], (B, F, S))
+            g_m, g_v = down(d["m"], c_m), down(d["v"], c_v)
+            assert_r5(g_m, c_m, x64.sum(axis=(0, 2)) * np.float64(np.float32(1) / np.float32(B * S)), f"mean {k}")
+            dev64 = ((x64 - c_m.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2))
+            assert_r5(g_v, c_v, dev64 * np.float64(np.float32(1) / np.float32(B * S - 1)), f"variance {k}")
+            want = xs[k].copy()
+            ref.normalize(want, g_m, g_v, B, F, S)
+            assert_bitexact(down(d["xn"], xs[k]), want, f"x_norm {k}")
+        for d in bufs:
+            _free(*d.values())
+        _free(d_s, d_b)
+    finally:
+        lib.dkz_set_sync_after_launch(before)

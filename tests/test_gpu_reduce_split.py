@@ -1,9 +1,13 @@
-"""Channel reductions with fewer channels than CUs and one-launch sizes run
-as two workgroups per channel that meet through an agent-scope counter: the
-second to finish reads the other's partial and finalises. Each op is launched
-many times back to back on fresh data, with no synchronisation in between, so
-a partial read before it was visible, or a counter not reset for the next
-launch, would show as a sum off by half a channel."""
+"""Channel reductions split over several workgroups per channel run as one
+launch: each workgroup writes its f64 partial with a coherent (agent-scope)
+store and counts itself in its channel's counter, and the last to arrive adds
+the channel's partials and finalises, then empties the counter. Each op is
+launched many times back to back on fresh data, with no synchronisation in
+between, so a partial read before it was visible, a counter not emptied for
+the next launch, or a channel finalised twice would show as a wrong sum.
+Shapes: 128 channels split 16 ways, config 1's 32 channels split 64 ways,
+1000 channels split 3 ways with a ragged last chunk, and per-element loads
+(spatial not a multiple of 4)."""
 
 from __future__ import annotations
 
@@ -16,8 +20,8 @@ from tests.helpers import assert_r5, chan_f32, chan_sum64, down, normal, rng, up
 
 pytestmark = pytest.mark.gpu
 
-SHAPE = (4, 128, 16384)  # 33.5 MB per stream: one launch, two workgroups per channel
-ROUNDS = 50
+SHAPES = [(4, 128, 16384), (128, 32, 1024), (3, 1000, 2100), (5, 64, 4099)]
+ROUNDS = 30
 
 
 @pytest.fixture
@@ -30,8 +34,9 @@ def quiet(dev):
     gpu.sync()
 
 
-def test_pair_reductions_back_to_back(quiet):
-    B, F, S = SHAPE
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+def test_split_reductions_back_to_back(quiet, shape):
+    B, F, S = shape
     n = B * F * S
     r = rng(77)
     xs = [normal(r, n, 0.1 * k, 1.0) for k in range(ROUNDS)]
@@ -61,8 +66,9 @@ def test_pair_reductions_back_to_back(quiet):
         gpu.free(b)
 
 
-def test_pair_variance_matches_per_round(quiet):
-    B, F, S = SHAPE
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+def test_split_variance_matches_per_round(quiet, shape):
+    B, F, S = shape
     n = B * F * S
     r = rng(78)
     for k in range(10):
@@ -73,8 +79,8 @@ def test_pair_variance_matches_per_round(quiet):
         ref.variance(x, m, B, F, S, v)
         dx, dm, out = up(x), up(m), gpu.alloc(F)
         gpu.variance(dx, dm, B, F, S, out)
-        diff = x - chan_f32(m, SHAPE)
-        want = chan_sum64(diff * diff, SHAPE) * np.float64(np.float32(1) / np.float32(B * S - 1))
+        diff = x - chan_f32(m, shape)
+        want = chan_sum64(diff * diff, shape) * np.float64(np.float32(1) / np.float32(B * S - 1))
         assert_r5(down(out, v), v, want, f"variance round {k}")
         for b in (dx, dm, out):
             gpu.free(b)

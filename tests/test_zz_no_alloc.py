@@ -3,12 +3,12 @@ scratch is a static device array (no allocation), against
 dkz_batchnorm_backward through the C ABI: the same kernels and launch
 geometry, so every output is bit-identical. Two calls in a row, the second
 on a smaller tensor, then the first shape again (the static array keeps the
-previous call's contents: partial sums are rewritten, meeting slots cleared
+previous call's contents: partial sums are rewritten, counter slots cleared
 by each call).
 
   * [8,128,4099]: spatial not a multiple of 4, so the per-op sequence runs,
-    and its channel reductions (128 channels of 32796 elements) meet in the
-    slots;
+    and its channel reductions (128 channels of 32792 elements, each split
+    16 ways) count themselves in the slots;
   * [32,64,28,28]: the fused passes with each channel split over several
     workgroups, whose f64 partials go through the array.
 """
@@ -68,7 +68,7 @@ def _check(shape, seed):
 
 
 def test_two_calls_second_smaller(dev):
-    _check((8, 128, 4099), 1)  # per-op sequence, channel reductions meeting in the slots
+    _check((8, 128, 4099), 1)  # per-op sequence, split channel reductions counting in the slots
     _check((32, 64, 28 * 28), 2)  # smaller: fused passes, split partials
     _check((8, 128, 4099), 3)  # the first shape again, after the array was reused
 
