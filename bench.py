@@ -176,6 +176,9 @@ class Device:
 
 
 def rotations(bytes_per_set: int, min_total: int = 512 << 20, lo: int = 2) -> int:
+    """Buffer sets to cycle through so that an op touching `bytes_per_set`
+    of them cycles >= 512 MB, twice the Infinity Cache: pass the footprint
+    of the block's smallest op, so every row of the block starts cold."""
     return max(lo, -(-min_total // max(bytes_per_set, 1)))
 
 
@@ -520,7 +523,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     # -- config 2: BN backward ops on their own
     h = config2_host()
     dev = Device(gpu)
-    sets = upload_config2(dev, h, 3)
+    sets = upload_config2(dev, h, 5)  # 5 x 102.8 MB of delta: backward_bias alone cycles 514 MB
     chains = [config2_chain_ops(gpu, d, h) for d in sets]
     for j, (name, nbytes, _) in enumerate(chains[0]):
         add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
@@ -561,7 +564,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     logits = r.normal(0, 4.0, n3).astype(np.float32)
     truth = np.zeros(n3, np.float32)
     truth[np.arange(b3) * c3 + r.integers(0, c3, b3)] = 1.0
-    R = rotations(4 * 4 * n3)
+    R = rotations(2 * 4 * n3)  # softmax alone touches x and p: 2 MB a set
     ls = dev.clone(dev.up(logits), n3, R)
     ps = [dev.zeros(n3) for _ in range(R)]
     ts = dev.clone(dev.up(truth), n3, R)
@@ -589,7 +592,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     logits = r.normal(0, 4.0, n3l).astype(np.float32)
     truth = np.zeros(n3l, np.float32)
     truth[np.arange(b3l) * c3 + r.integers(0, c3, b3l)] = 1.0
-    R = rotations(4 * 4 * n3l)
+    R = rotations(2 * 4 * n3l)
     ls = dev.clone(dev.up(logits), n3l, R)
     ps = [dev.zeros(n3l) for _ in range(R)]
     ts = dev.clone(dev.up(truth), n3l, R)
@@ -600,13 +603,16 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         [lambda a=a, p=p: gpu.softmax(a, c3, b3l, c3, 1, c3, 1, 1.0, p) for a, p in zip(ls, ps)])
     add(cfg, "softmax_x_ent", 4 * 4 * n3l,
         [lambda p=p, t=t, d=d, e=e: gpu.softmaxCrossEntropy(n3l, p, t, d, e) for p, t, d, e in zip(ps, ts, ds_, es)])
+    # the floor for softmax's traffic at this size: a copy of the same bytes
+    add(cfg, "copy of the same bytes (reference)", 2 * 4 * n3l,
+        [lambda a=a, p=p: gpu.copy(n3l, a, p) for a, p in zip(ls, ps)])
     dev.free()
 
     # -- config 4: SGD over 25e6 floats ~N(0,0.05), and the stride-2 shortcut
     dev = Device(gpu)
     n4 = 25_000_000
     r = gen(4)
-    R = rotations(2 * 4 * n4)
+    R = rotations(4 * n4)  # scal alone touches dw: 100 MB a set
     ws = dev.clone(dev.up(r.normal(0, 0.05, n4).astype(np.float32)), n4, R)
     dws = dev.clone(dev.up(r.normal(0, 0.05, n4).astype(np.float32)), n4, R)
     batch, lr, decay, momentum = 64, 0.1, 0.0005, 0.9

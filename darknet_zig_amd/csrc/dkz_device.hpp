@@ -118,6 +118,17 @@ __device__ __forceinline__ void st2i(int *p, uint32_t v, int2 x) {
     }
 }
 
+template <bool NT>
+__device__ __forceinline__ float ld1(const float *p, uint32_t i) {
+    if constexpr (NT) return __builtin_nontemporal_load(p + i);
+    else return p[i];
+}
+template <bool NT>
+__device__ __forceinline__ void st1(float *p, uint32_t i, float x) {
+    if constexpr (NT) __builtin_nontemporal_store(x, p + i);
+    else p[i] = x;
+}
+
 __device__ __forceinline__ float &lane(float4 &v, int k) {
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }

@@ -16,7 +16,9 @@
 //
 //  * n <= kSegMaxN (2048) with many groups: a segment of L = 4..64 lanes per
 //    group, the group held in registers (16 or 32 floats a lane, read once in
-//    float4s when aligned), max and sum over the segment by DPP.
+//    float4s when aligned), max and sum over the segment by DPP; from 4096
+//    groups each segment takes two groups in turn, the second's loads issued
+//    before the first is worked on.
 //  * n <= kWgMaxN (32768), or few groups: one workgroup (64..1024 lanes) per
 //    group, held in registers, max and sum by DPP within waves and LDS
 //    across them.
@@ -40,6 +42,7 @@
 #include <float.h>
 
 #include "dkz_device.hpp"
+#include "dkz_hints.hpp"
 #include "dkz_internal.hpp"
 
 namespace dkz {
@@ -126,14 +129,15 @@ struct RowSlice {
         return V4 ? 4 * (j + (uint32_t)(m >> 2) * P) < n : j + (uint32_t)m * P < n;
     }
 
-    // Slots past n (or of a dead group) read as `fill`.
+    // Slots past n (or of a dead group) read as `fill`. NT: nontemporal loads.
+    template <bool NT = false>
     __device__ __forceinline__ void load(const float *p, uint32_t n, bool live, float fill) {
         if constexpr (V4) {
 #pragma unroll
             for (int k = 0; k < K; ++k) {
                 const uint32_t q = j + (uint32_t)k * P;
                 float4 a = make_float4(fill, fill, fill, fill);
-                if (live && 4 * q < n) a = ld4<false>(p, q);
+                if (live && 4 * q < n) a = ld4<NT>(p, q);
                 v[4 * k] = a.x;
                 v[4 * k + 1] = a.y;
                 v[4 * k + 2] = a.z;
@@ -141,7 +145,7 @@ struct RowSlice {
             }
         } else {
 #pragma unroll
-            for (int m = 0; m < M; ++m) v[m] = (live && inside(m, n)) ? p[at(m)] : fill;
+            for (int m = 0; m < M; ++m) v[m] = (live && inside(m, n)) ? ld1<NT>(p, at(m)) : fill;
         }
     }
 
@@ -193,16 +197,17 @@ struct RowSlice {
     // held in `tr` (EARLY) or read from `truth` here. The losses' logs run
     // only in waves where some lane holds a nonzero truth (with one-hot
     // truth, most waves store zeros).
-    template <bool XENT, bool EARLY = true>
+    template <bool XENT, bool EARLY = true, int HS = 0>
     __device__ __forceinline__ void store(float *out, uint32_t n, bool live, float inv, const RowSlice &tr,
                                           const float *truth, float *delta, float *loss) {
+        constexpr bool kNtP = (HS & 2) != 0, kNtT = (HS & 4) != 0, kNtDL = (HS & 8) != 0;
         float t[XENT ? M : 1];
         bool any = false;
         if constexpr (XENT) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if constexpr (EARLY) t[m] = tr.v[m];
-                else t[m] = (live && inside(m, n)) ? truth[at(m)] : 0.0f;
+                else t[m] = (live && inside(m, n)) ? ld1<kNtT>(truth, at(m)) : 0.0f;
                 any |= t[m] != 0.0f;
             }
         }
@@ -213,17 +218,17 @@ struct RowSlice {
             for (int k = 0; k < K; ++k) {
                 const uint32_t q = j + (uint32_t)k * P;
                 if (!(live && 4 * q < n)) continue;
-                st4<false>(out, q, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
+                st4<kNtP>(out, q, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
                 if constexpr (XENT)
-                    st4<false>(delta, q, make_float4(t[4 * k] - v[4 * k], t[4 * k + 1] - v[4 * k + 1],
+                    st4<kNtDL>(delta, q, make_float4(t[4 * k] - v[4 * k], t[4 * k + 1] - v[4 * k + 1],
                                                      t[4 * k + 2] - v[4 * k + 2], t[4 * k + 3] - v[4 * k + 3]));
             }
         } else {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if (!(live && inside(m, n))) continue;
-                out[at(m)] = v[m];
-                if constexpr (XENT) delta[at(m)] = t[m] - v[m];
+                st1<kNtP>(out, at(m), v[m]);
+                if constexpr (XENT) st1<kNtDL>(delta, at(m), t[m] - v[m]);
             }
         }
         if constexpr (XENT) {
@@ -240,12 +245,12 @@ struct RowSlice {
                 for (int k = 0; k < K; ++k) {
                     const uint32_t q = j + (uint32_t)k * P;
                     if (live && 4 * q < n)
-                        st4<false>(loss, q, make_float4(l[4 * k], l[4 * k + 1], l[4 * k + 2], l[4 * k + 3]));
+                        st4<kNtDL>(loss, q, make_float4(l[4 * k], l[4 * k + 1], l[4 * k + 2], l[4 * k + 3]));
                 }
             } else {
 #pragma unroll
                 for (int m = 0; m < M; ++m)
-                    if (live && inside(m, n)) loss[at(m)] = l[m];
+                    if (live && inside(m, n)) st1<kNtDL>(loss, at(m), l[m]);
             }
         }
     }
@@ -257,6 +262,7 @@ struct RowSlice {
 template <int L, int K, bool V4, bool XENT>
 __global__ __launch_bounds__(kBlock) void softmax_seg_kernel(const float *in, float *out, Groups G, uint32_t rows,
                                                              Xent xe) {
+    constexpr int HS = XENT ? DKZ_HINT_SOFTMAX_XENT : DKZ_HINT_SOFTMAX;
     const uint32_t t = threadIdx.x;
     const uint32_t r = blockIdx.x * (blockDim.x / L) + t / L;
     const bool live = r < rows;  // the same for the whole segment
@@ -264,20 +270,59 @@ __global__ __launch_bounds__(kBlock) void softmax_seg_kernel(const float *in, fl
     RowSlice<K, V4> x;
     x.j = t & (L - 1);
     x.P = L;
-    x.load(in + off, n, live, -FLT_MAX);
+    x.template load<(HS & 1) != 0>(in + off, n, live, -FLT_MAX);
     RowSlice<K, V4> tr;  // the truth (XENT only)
     if constexpr (XENT) {
         tr.j = x.j;
         tr.P = L;
-        tr.load(xe.truth + off, n, live, 0.0f);
+        tr.template load<(HS & 4) != 0>(xe.truth + off, n, live, 0.0f);
     }
     const float mx = seg_max<L>(x.max());
     const double s = seg_sum<L>(x.exps(n, live, G.temp, mx / G.temp));
     const float inv = (float)(1.0 / s);
     if constexpr (XENT) {
-        x.template store<true>(out + off, n, live, inv, tr, nullptr, xe.delta + off, xe.loss + off);
+        x.template store<true, true, HS>(out + off, n, live, inv, tr, nullptr, xe.delta + off, xe.loss + off);
     } else {
-        x.template store<false>(out + off, n, live, inv, x, nullptr, nullptr, nullptr);
+        x.template store<false, true, HS>(out + off, n, live, inv, x, nullptr, nullptr, nullptr);
+    }
+}
+
+// The segment kernel as a grid-stride loop: each segment takes groups
+// r, r + R, r + 2R, ... (R = segments in the grid) and loads the next
+// group before working on the current one, so each wave's reads and writes
+// alternate over the kernel instead of all reads landing first.
+template <int L, int K, bool V4>
+__global__ __launch_bounds__(kBlock) void softmax_seg_stream_kernel(const float *in, float *out, Groups G,
+                                                                    uint32_t rows) {
+    constexpr int HS = DKZ_HINT_SOFTMAX;
+    const uint32_t t = threadIdx.x;
+    const uint32_t per_block = blockDim.x / L;
+    const uint32_t stride = gridDim.x * per_block;
+    uint32_t r = blockIdx.x * per_block + t / L;
+    const uint32_t n = G.n;
+    RowSlice<K, V4> cur, nxt;
+    cur.j = nxt.j = t & (L - 1);
+    cur.P = nxt.P = L;
+    bool live = r < rows;
+    uint32_t off = group_base(live ? r : 0u, G);
+    cur.template load<(HS & 1) != 0>(in + off, n, live, -FLT_MAX);
+    // every segment of the grid runs the same number of iterations, so the
+    // whole wave stays active for the DPP reductions
+    const uint32_t iters = (rows + stride - 1) / stride;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t rn = r + stride;
+        const bool live_n = rn < rows;
+        const uint32_t off_n = group_base(live_n ? rn : 0u, G);
+        if (it + 1 < iters) nxt.template load<(HS & 1) != 0>(in + off_n, n, live_n, -FLT_MAX);
+        const float mx = seg_max<L>(cur.max());
+        const double s = seg_sum<L>(cur.exps(n, live, G.temp, mx / G.temp));
+        const float inv = (float)(1.0 / s);
+        cur.template store<false, true, HS>(out + off, n, live, inv, cur, nullptr, nullptr, nullptr);
+#pragma unroll
+        for (int m = 0; m < RowSlice<K, V4>::M; ++m) cur.v[m] = nxt.v[m];
+        r = rn;
+        live = live_n;
+        off = off_n;
     }
 }
 
@@ -288,10 +333,11 @@ __global__ __launch_bounds__(1024) void softmax_wg_kernel(const float *in, float
     __shared__ double red_d[16];
     const uint32_t t = threadIdx.x, nw = blockDim.x / kWave, w = t / kWave;
     const uint32_t off = group_base(blockIdx.x, G), n = G.n;
+    constexpr int HS = XENT ? DKZ_HINT_SOFTMAX_XENT : DKZ_HINT_SOFTMAX;
     RowSlice<K, V4> x;
     x.j = t;
     x.P = blockDim.x;
-    x.load(in + off, n, true, -FLT_MAX);
+    x.template load<(HS & 1) != 0>(in + off, n, true, -FLT_MAX);
     // The truth is read with the logits when it fits in registers beside
     // them (K <= 4), otherwise as the results are stored.
     constexpr bool kEarly = K <= 4;
@@ -299,7 +345,7 @@ __global__ __launch_bounds__(1024) void softmax_wg_kernel(const float *in, float
     if constexpr (XENT && kEarly) {
         tr.j = t;
         tr.P = blockDim.x;
-        tr.load(xe.truth + off, n, true, 0.0f);
+        tr.template load<(HS & 4) != 0>(xe.truth + off, n, true, 0.0f);
     }
     float mx = wave_max(x.max());
     if ((t & (kWave - 1)) == 0) red_f[w] = mx;
@@ -313,10 +359,10 @@ __global__ __launch_bounds__(1024) void softmax_wg_kernel(const float *in, float
     for (uint32_t i = 1; i < nw; ++i) s += red_d[i];
     const float inv = (float)(1.0 / s);
     if constexpr (XENT) {
-        x.template store<true, kEarly>(out + off, n, true, inv, tr, xe.truth + off, xe.delta + off,
-                                       xe.loss + off);
+        x.template store<true, kEarly, HS>(out + off, n, true, inv, tr, xe.truth + off, xe.delta + off,
+                                           xe.loss + off);
     } else {
-        x.template store<false>(out + off, n, true, inv, x, nullptr, nullptr, nullptr);
+        x.template store<false, true, HS>(out + off, n, true, inv, x, nullptr, nullptr, nullptr);
     }
 }
 
@@ -388,8 +434,25 @@ constexpr uint32_t kSegMaxN = 2048;
 // Workgroup path: up to 1024 lanes x 32 floats.
 constexpr uint32_t kWgMaxN = 32768;
 
+// Groups per segment of the grid-stride kernel for many groups (>= 4096):
+// measured cold at [8192,1000], 12.9 us one group per segment, 12.4 two,
+// 13.8 four; 0 turns it off.
+#ifndef DKZ_SOFTMAX_STREAM
+#define DKZ_SOFTMAX_STREAM 2
+#endif
+
 template <int L, int K>
 int launch_seg(const float *input, float *output, const Groups &G, uint32_t rows, bool v4, const Xent *xe) {
+    if (DKZ_SOFTMAX_STREAM > 0 && !xe && rows >= 4096) {
+        // DKZ_SOFTMAX_STREAM groups a segment on average
+        const uint32_t per_block = (uint32_t)(kBlock / L);
+        const dim3 grid(div_up(rows, per_block * DKZ_SOFTMAX_STREAM));
+        void (*k)(const float *, float *, Groups, uint32_t) =
+            v4 ? softmax_seg_stream_kernel<L, K, true> : softmax_seg_stream_kernel<L, K, false>;
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(k, grid, dim3(kBlock), 0, current_stream(), input, output, G, rows);
+        return after_launch("softmax_seg_stream", grid, dim3(kBlock));
+    }
     // Four segments' waves a workgroup when that still gives >= 512
     // workgroups, else one wave (small launches reach more CUs).
     const uint32_t per_wave = (uint32_t)(kWave / L);
