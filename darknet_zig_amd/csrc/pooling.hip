@@ -57,6 +57,16 @@ struct PoolGeom {
 #ifndef DKZ_POOL_PLANE_MAX
 #define DKZ_POOL_PLANE_MAX 12288
 #endif
+static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynamic LDS is at most 64 KiB");
+// The plane kernels run one workgroup per plane: below this many planes the
+// grid would leave most CUs idle, and the per-output kernels (hundreds of
+// workgroups) run instead. Measured 3x3/s2 forward / backward, plane path
+// against per-output kernels: [1,32,56,56] 4.9 / 9.7 against 2.9 / 4.4 us,
+// [1,128,56,56] 5.5 / 9.9 against 3.5 / 5.3, [1,64,104,104] forward 13.9
+// against 4.1.
+#ifndef DKZ_POOL_PLANE_MIN
+#define DKZ_POOL_PLANE_MIN 256
+#endif
 #ifndef DKZ_POOL_PLANE_UNROLL
 #define DKZ_POOL_PLANE_UNROLL 1
 #endif
@@ -513,7 +523,7 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
                       input, output, indexes, g, pairs);
     }
     const uint64_t hw = (uint64_t)g.h * g.w;
-    if (DKZ_POOL_PLANE && hw > 0 && hw <= kPlaneMaxFloats) {
+    if (DKZ_POOL_PLANE && hw > 0 && hw <= kPlaneMaxFloats && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
         const size_t lds = (size_t)hw * sizeof(float);
         const bool vec = aligned16(input) && hw % 4 == 0;
@@ -553,7 +563,7 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
     // Outputs whose window covers one input, per dimension: at most ceil(size / stride).
     const uint32_t per_dim = (g.size + g.stride - 1) / g.stride;
     const uint64_t ohw = (uint64_t)g.oh * g.ow;
-    if (DKZ_POOL_PLANE && g.stride >= 2 && per_plane + 2 * ohw <= kPlaneMaxFloats) {
+    if (DKZ_POOL_PLANE && g.stride >= 2 && per_plane + 2 * ohw <= kPlaneMaxFloats && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
         const size_t lds = (size_t)(per_plane + 2 * ohw) * sizeof(float);
         const bool vec = aligned16(prev_delta) && per_plane % 4 == 0;
@@ -573,7 +583,7 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
     }
     // Through LDS when more than 2x2 outputs can cover an input (2x2 windows
     // measured faster with the batched loads of maxpool_bwd_kernel).
-    if (DKZ_POOL_PLANE && per_dim > 2 && ohw <= kPlaneMaxFloats / 2) {
+    if (DKZ_POOL_PLANE && per_dim > 2 && ohw <= kPlaneMaxFloats / 2 && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
         (void)hipGetLastError();
         hipLaunchKernelGGL(maxpool_plane_bwd_kernel, pgrid, block, (size_t)ohw * 8, current_stream(), delta,

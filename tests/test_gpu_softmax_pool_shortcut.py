@@ -163,13 +163,20 @@ MAXPOOL_CASES = [
     (1, 2, 7, 7, 3, 1, 2),        # darknet size=3 stride=1 (default pad size-1)
     (2, 2, 6, 10, 5, 3, 4),
     (256, 512, 28, 28, 2, 2, 1),  # config 5
-    (8, 64, 56, 56, 3, 2, 2),     # generic forward: one workgroup per plane in LDS (float4 loads)
-    (2, 3, 9, 9, 2, 1, 1),        # plane of 81 floats: element loads
-    (2, 3, 9, 9, 3, 1, 2),        # stride-1 backward through LDS, odd plane
-    (2, 4, 13, 13, 13, 1, 12),    # spatial pyramid pooling's 13x13 window
-    (2, 3, 110, 110, 3, 2, 2),    # the largest planes held in LDS (12100 floats)
+    # one workgroup per plane (at least 256 planes) with the plane in LDS:
+    (8, 64, 56, 56, 3, 2, 2),     # generic forward, float4 loads
+    (86, 3, 9, 9, 2, 1, 1),       # plane of 81 floats: element loads
+    (86, 3, 9, 9, 3, 1, 2),       # stride-1 backward through LDS, odd plane
+    (64, 4, 13, 13, 13, 1, 12),   # spatial pyramid pooling's 13x13 window
+    (86, 3, 110, 110, 3, 2, 2),   # the largest planes held in LDS (12100 floats)
+    (86, 3, 78, 78, 3, 1, 2),     # stride-1 backward: the largest output planes held in LDS (6084)
+    # the same windows on fewer planes, or larger ones: per-output / per-input kernels
+    (2, 3, 9, 9, 2, 1, 1),
+    (2, 3, 9, 9, 3, 1, 2),
+    (2, 4, 13, 13, 13, 1, 12),
+    (2, 3, 110, 110, 3, 2, 2),
     (2, 3, 120, 120, 3, 2, 2),    # larger planes: one lane per output
-    (2, 3, 78, 78, 3, 1, 2),      # stride-1 backward: the largest output planes held in LDS (6084)
+    (2, 3, 78, 78, 3, 1, 2),
     (1, 2, 80, 80, 3, 1, 2),      # larger: one lane per input
 ]
 
@@ -230,11 +237,14 @@ def _shared_peaks(batch, c, h, w, size, stride, pad, seed):
 
 
 @pytest.mark.parametrize("case", [(2, 3, 11, 13, 3, 2, 2), (2, 2, 12, 12, 5, 3, 4), (1, 2, 9, 9, 3, 1, 2),
-                                  (2, 2, 10, 10, 4, 2, 2)], ids=str)
+                                  (2, 2, 10, 10, 4, 2, 2), (1, 2, 120, 120, 3, 2, 2), (86, 3, 11, 13, 3, 2, 2),
+                                  (64, 4, 12, 12, 5, 3, 4), (86, 3, 9, 9, 3, 1, 2)], ids=str)
 def test_maxpool_shared_argmax(dev, case):
     """Inputs that are the argmax of several outputs: the backward pass must
-    add their deltas in ascending output order (the output-per-lane kernel for
-    stride >= 2, the gather kernel for stride 1)."""
+    add their deltas in ascending output order -- the output-per-lane kernel
+    for stride >= 2 (few planes, or planes too large for LDS: 120x120), the
+    plane-in-LDS kernels for at least 256 planes, and the gather kernels for
+    stride 1."""
     batch, c, h, w, size, stride, pad = case
     oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
     x = _shared_peaks(*case, seed=sum(case))
