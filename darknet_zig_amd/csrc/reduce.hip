@@ -10,10 +10,12 @@
 //     delta*x_norm, delta*(x-m), rounded exactly as blas.zig rounds them -- and
 //     accumulates it in f64. A chunk is then summed by wave64 DPP reductions
 //     and a 4-entry LDS step (dkz_device.hpp).
-//   * K (chan_split) aims at ~2048 workgroups in all, so the grid covers the
+//   * K (chan_split) aims at ~1024 workgroups in all, so the grid covers the
 //     256 CUs several times whatever the channel count. K == 1 (channels
 //     alone enough): the workgroup, 1024 threads wide for long channels,
-//     finalises its channel itself. K > 1: one launch in which the last
+//     finalises its channel itself. 128..255 long channels: two 1024-thread
+//     workgroups each, meeting through one atomic exchange
+//     (chan_pair_kernel). Otherwise K > 1: one launch in which the last
 //     workgroup of each channel to finish adds the channel's K f64 partials
 //     in index order and finalises (chan_split_kernel: coherent atomic
 //     stores and a per-channel counter, no fence, nothing waits). The result
@@ -147,6 +149,48 @@ __global__ __launch_bounds__(kBlock) void chan_split_kernel(T t, Fin fin, const 
     }
 }
 
+// Two workgroups per channel, one launch, for 128..255 channels of at least
+// 32 Ki elements and at most DKZ_PAIR_MAX_BYTES (250 MB) to read: 1024-thread
+// workgroups, every CU streaming, and the two halves meet in channel f's
+// counter slot (zero when empty): each swaps its partial in with one
+// agent-scope atomic exchange, which returns what the slot held. The one
+// that gets the other's partial back adds the two (f64 addition is
+// commutative, so the sum does not depend on which finished first), empties
+// the slot and finalises. One memory round trip at the end instead of the
+// split kernel's three (store and wait, count, read the partials). Config
+// 2, cold: backward_bias / mean_delta 19.9 -> 18.5 us, backward_scale /
+// variance_delta 34.4 / 33.8 -> 33.5 / 32.5 us, the backward chain 6584 ->
+// 6680 GB/s (nontemporal delta loads would take backward_bias to 17.4 us
+// alone but cost the chain 3%: delta stays cached). A partial travels as its bits XOR
+// kSlotKey -- a NaN payload no sum produces, since NaNs reaching it carry an
+// f32 payload whose low 29 bits are zero -- so a stored partial is never
+// zero.
+#ifndef DKZ_CHAN_PAIR
+#define DKZ_CHAN_PAIR 1
+#endif
+#ifndef DKZ_PAIR_MAX_BYTES
+#define DKZ_PAIR_MAX_BYTES 250000000ull
+#endif
+constexpr uint64_t kSlotKey = 0xFFF8DEADBEEF0001ull;
+
+template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
+__global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
+                                                       uint64_t *slots) {
+    __shared__ double lds[BS / kWave];
+    const uint32_t f = blockIdx.x >> 1, k = blockIdx.x & 1;
+    const float pre = threadIdx.x == 0 ? fin.pre(f) : 0.0f;
+    const double s = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, f, k, lds);
+    if (threadIdx.x == 0) {
+        uint64_t *slot = &slots[(uint64_t)f * kCounterStride];
+        const uint64_t mine = __builtin_bit_cast(uint64_t, s) ^ kSlotKey;
+        const uint64_t held = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (held != 0) {
+            __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            fin(f, s + __builtin_bit_cast(double, held ^ kSlotKey), pre);
+        }
+    }
+}
+
 // Workgroups per channel of a per-op reduction: about DKZ_CHAN_TARGET_WGS
 // workgroups in all (four per CU), each owning at least DKZ_CHAN_MIN_CHUNK
 // elements; one per channel when the channels alone are that many. From the
@@ -178,6 +222,20 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
     DKZ_REQUIRE(chan_len64 * (uint64_t)filters <= kMaxElems);
     const uint32_t F = (uint32_t)filters, S = (uint32_t)spatial, L = (uint32_t)chan_len64;
     const bool vec = S % 4 == 0 && aligned16(p0) && (!TWO || aligned16(p1));
+    const uint64_t bytes = (uint64_t)4 * (TWO ? 2 : 1) * F * L;
+    if (DKZ_CHAN_PAIR && F >= 128 && F < 256 && L >= 32 * kWideBlock && bytes <= DKZ_PAIR_MAX_BYTES) {
+        const RedGeom g2 = make_red_geom(F, S, L, 2, vec);
+        if (g2.K == 2) {
+            Scratch sc{nullptr};
+            DKZ_TRY(device_scratch(&sc));
+            const dim3 block(kWideBlock);
+            if (vec)
+                return launch(name, chan_pair_kernel<T, Fin, TWO, true, H, kWideBlock>, dim3(2 * F), block, t, fin,
+                              p0, p1, g2, sc.slots);
+            return launch(name, chan_pair_kernel<T, Fin, TWO, false, H, kWideBlock>, dim3(2 * F), block, t, fin, p0,
+                          p1, g2, sc.slots);
+        }
+    }
     const RedGeom g = make_red_geom(F, S, L, chan_split(F, L), vec);
     const uint32_t K = g.K;
     if (K == 1) {
