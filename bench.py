@@ -38,8 +38,10 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                dkz_convolution_forward / _weight_gradient / _data_gradient),
                TFLOP/s
                against the 157.3 TFLOP/s fp32 matrix-core peak
-  fused_bwd    the same step through dkz_batchnorm_backward (one reduction
-               pass and one apply pass, 32 B/elem instead of 56)
+  fused_bwd    the same step through dkz_batchnorm_backward (at this size a
+               reduction pass and an apply pass: 32 B/elem moved instead of
+               the chain's 56; its algorithmic bytes, each tensor once, are
+               20 B/elem)
   bn_act_gelem_s  batch-norm + activation elements per second: config 1's
                forward and config 2's backward (per op, the whole per-op layer
                forward, fused), and each config's layer forward + backward
@@ -218,7 +220,8 @@ def config2_chain_ops(gpu, d, h):
 
 def fused_backward(gpu, d, h):
     """The same layer step through the fused entry point (one reduction pass
-    over y, delta, x_norm, x; one apply pass over y, delta, x): 32 B/elem."""
+    over y, delta, x_norm, x; one apply pass over y, delta, x): 32 B/elem
+    moved, 20 B/elem algorithmic."""
     from darknet_zig_amd.activations import Activation
 
     gpu.batchnormBackward(h["B"], h["F"], h["S"], Activation.leaky, d["y"], d["delta"], d["x"], d["x_norm"],
@@ -498,16 +501,17 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
              lambda b=b: gpu.addBias(b, bet, B, F, S), lambda b=b: gpu.activateArray(b, n, Activation.leaky)]
             for b, c in zip(xs, xcs)]
     add_seq(cfg, "layer sequence: copy,mean,variance,ema,normalize,copy,scale_bias,add_bias,leaky", 14 * E, seqs)
-    add_seq("fused", "cfg1 batchnorm_forward(train, leaky): stats + apply", 5 * E,
+    add_seq("fused", "cfg1 batchnorm_forward(train, leaky)", 4 * E,
             [[lambda b=b, c=c, xn=xn: gpu.batchnormForward(B, F, S, Activation.leaky, True, b, b, c, xn, m, v, rm, rv,
                                                            gam, bet)] for b, c, xn in zip(xs, xcs, xns)], hot=True)
     # the backward step at config 1's shape, for the per-layer forward +
     # backward figure (buffers of the forward rows stand in for y, delta, x,
     # x_norm: the timing does not depend on the values)
     bu, su, md1, vd1 = dev.zeros(F), dev.zeros(F), dev.zeros(F), dev.zeros(F)
-    add_seq("fused", "cfg1 shape batchnorm_backward(leaky): sums + apply", 8 * E,
-            [[lambda b=b, c=c, xn=xn: gpu.batchnormBackward(B, F, S, Activation.leaky, b, c, xn, xn, m, v, gam, bu, su,
-                                                            md1, vd1)] for b, c, xn in zip(xs, xcs, xns)])
+    add_seq("fused", "cfg1 shape batchnorm_backward(leaky)", 5 * E,
+            [[lambda b=b, c=c, xx=xx, xn=xn: gpu.batchnormBackward(B, F, S, Activation.leaky, b, c, xx, xn, m, v, gam,
+                                                                   bu, su, md1, vd1)]
+             for b, c, xx, xn in zip(xs, xcs, ys, xns)])
     add_seq(cfg, "backward chain: gradient,backward_bias,backward_scale,scale_bias,mean_delta,variance_delta,"
                  "normalize_delta", 14 * E,
             [[lambda b=b, c=c: gpu.gradientArray(b, n, Activation.leaky, c),
@@ -515,9 +519,9 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
               lambda c=c, xn=xn: gpu.backwardScale(xn, c, B, F, S, su),
               lambda c=c: gpu.scaleBias(c, gam, B, F, S),
               lambda c=c: gpu.meanDelta(c, v, B, F, S, md1),
-              lambda c=c, xn=xn: gpu.varianceDelta(xn, c, m, v, B, F, S, vd1),
-              lambda c=c, xn=xn: gpu.normalizeDelta(xn, m, v, md1, vd1, B, F, S, c)]
-             for b, c, xn in zip(xs, xcs, xns)])
+              lambda c=c, xx=xx: gpu.varianceDelta(xx, c, m, v, B, F, S, vd1),
+              lambda c=c, xx=xx: gpu.normalizeDelta(xx, m, v, md1, vd1, B, F, S, c)]
+             for b, c, xx, xn in zip(xs, xcs, ys, xns)])
     dev.free()
 
     # -- config 2: BN backward ops on their own
@@ -527,7 +531,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     chains = [config2_chain_ops(gpu, d, h) for d in sets]
     for j, (name, nbytes, _) in enumerate(chains[0]):
         add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
-    add_seq("fused", "cfg2 batchnorm_backward(leaky): sums + apply", 8 * 4 * h["n"],
+    add_seq("fused", "cfg2 batchnorm_backward(leaky)", 5 * 4 * h["n"],
             [[lambda d=d: fused_backward(gpu, d, h)] for d in sets])
     # config 1's forward ops on the largest batch-norm tensor of the configs
     # (config 2's x): each op at its largest shape, as the north star asks
@@ -551,7 +555,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     # the fused forward at config 2's shape, for the per-layer forward +
     # backward figure (it overwrites y, delta and x_norm: these rows come last)
     m2, v2, rm2, rv2 = dev.zeros(F2), dev.zeros(F2), dev.zeros(F2), dev.zeros(F2)
-    add_seq("fused", "cfg2 shape batchnorm_forward(train, leaky): stats + apply", 20 * n2,
+    add_seq("fused", "cfg2 shape batchnorm_forward(train, leaky)", 16 * n2,
             [[lambda d=d: gpu.batchnormForward(B2, F2, S2, Activation.leaky, True, d["x"], d["y"], d["delta"],
                                                d["x_norm"], m2, v2, rm2, rv2, d["scales"], bias2)] for d in sets])
     dev.free()
@@ -1001,10 +1005,10 @@ def bn_gelem(table, bwd_chain_ms):
               "normalize_delta")
     fwd2 = us(f"{c12}/chain: mean,variance,normalize,scale_bias,add_bias,leaky")
     bwd2 = bwd_chain_ms * 1e3
-    ffwd1 = us("fused/cfg1 batchnorm_forward(train, leaky): stats + apply")
-    fbwd1 = us("fused/cfg1 shape batchnorm_backward(leaky): sums + apply")
-    ffwd2 = us("fused/cfg2 shape batchnorm_forward(train, leaky): stats + apply")
-    fbwd2 = us("fused/cfg2 batchnorm_backward(leaky): sums + apply")
+    ffwd1 = us("fused/cfg1 batchnorm_forward(train, leaky)")
+    fbwd1 = us("fused/cfg1 shape batchnorm_backward(leaky)")
+    ffwd2 = us("fused/cfg2 shape batchnorm_forward(train, leaky)")
+    fbwd2 = us("fused/cfg2 batchnorm_backward(leaky)")
     layer1 = us(f"{c1}/layer sequence: copy,mean,variance,ema,normalize,copy,scale_bias,add_bias,leaky")
 
     def g(e, *t):
@@ -1282,10 +1286,11 @@ def main() -> int:
         },
         "chain_kernels": chain_kernels,
         "fused_bwd": {
-            "entry": "dkz_batchnorm_backward (same step, same buffers: one sums pass + one apply pass)",
+            "entry": "dkz_batchnorm_backward (same step, same buffers; here one sums pass + one apply pass, "
+                     "32 B/elem moved; bytes below are algorithmic, 20 B/elem)",
             "us": round(fused_ms * 1e3, 2),
-            "bytes": 8 * 4 * h["n"],
-            "GB/s": round(gbs(8 * 4 * h["n"], fused_ms), 1),
+            "bytes": 5 * 4 * h["n"],
+            "GB/s": round(gbs(5 * 4 * h["n"], fused_ms), 1),
             "GElem/s": round(h["n"] / (fused_ms * 1e-3) / 1e9, 2),
             "speedup_vs_per_op_chain": round((ms / args.steps) / fused_ms, 3),
         },

@@ -666,6 +666,99 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
     }
 }
 
+// ---- one-launch backward -------------------------------------------------------
+
+// Backward in one launch (the shape of bn_fwd_coop_kernel): workgroup (f, k)
+// loads chunk k of channel f of y, delta, x_norm and x once, forms the four
+// f64 sums of bn_bwd_sums_kernel, posts them, waits at the channel barrier,
+// adds the channel's K partials, finalises exactly as the two-pass path
+// (workgroup k == 0 writing the updates, mean_delta and variance_delta) and
+// writes normalize_delta's result from the y, delta and x it holds: 20 bytes
+// an element instead of 32.
+#ifndef DKZ_BN_BWD_COOP_U
+#define DKZ_BN_BWD_COOP_U 4
+#endif
+constexpr int kBwdCoopU = DKZ_BN_BWD_COOP_U;
+constexpr uint32_t kBwdCoopChunk = kBlock * 4 * kBwdCoopU;
+
+template <int A, int H>
+__global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, float *delta, const float *x_norm,
+                                                             const float *x, BwdParams p, RedGeom g, BwdFin fin,
+                                                             double *partials, uint64_t *slots) {
+    constexpr bool kLin = A == kLinear;
+    constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtX = (H & 8) != 0;
+    constexpr bool kNtOut = (H & 16) != 0;
+    __shared__ double lds[4 * (kBlock / kWave)];
+    __shared__ BwdChan chan_sh;
+    const uint32_t f = fdiv(blockIdx.x, g.div_k);
+    const uint32_t k = blockIdx.x - f * g.K;
+    const uint32_t F = g.div_filters.d;
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const float m = p.mean[f], gam = p.scales[f];
+    // Held through the barrier: d2 = delta * gradient(y) * scale and x - mean,
+    // the two terms normalize_delta needs besides per-channel values, each
+    // formed exactly as bwd_elem forms it.
+    float4 d2[kBwdCoopU], xm[kBwdCoopU];
+    uint32_t at[kBwdCoopU];
+    double a[4] = {0.0, 0.0, 0.0, 0.0};
+    {
+        float4 vy[kBwdCoopU], vd[kBwdCoopU], vx[kBwdCoopU], vn[kBwdCoopU];
+#pragma unroll
+        for (int u = 0; u < kBwdCoopU; ++u) {
+            const uint32_t j = j0 + 4 * threadIdx.x + (uint32_t)u * (4 * kBlock);
+            at[u] = j < j1 ? chan_addr(fbase, j, g) >> 2 : 0xffffffffu;
+            if (j < j1) {
+                vd[u] = ld4<kNtD>(delta, at[u]);
+                if constexpr (!kLin) vy[u] = ld4<kNtY>(y, at[u]);
+                else vy[u] = vd[u];
+                vn[u] = ld4<kNtXn>(x_norm, at[u]);
+                vx[u] = ld4<kNtX>(x, at[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBwdCoopU; ++u) {
+            if (at[u] == 0xffffffffu) continue;
+            acc_bwd<A>(vy[u], vd[u], vn[u], vx[u], m, gam, a);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                lane(d2[u], l) = grad_delta<A>(lane(vd[u], l), lane(vy[u], l)) * gam;
+                lane(xm[u], l) = lane(vx[u], l) - m;
+            }
+        }
+    }
+    const Sums<4> r = block_sums<4, kBlock>(a, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        if (threadIdx.x == 0) {
+            float md, vdl;
+            fin.values(f, sums, md, vdl);
+            chan_sh = bwd_chan(p, f, md, vdl);
+            if (k == 0) fin.write(f, sums, md, vdl);
+        }
+    }
+    __syncthreads();
+    const BwdChan ch = chan_sh;
+#pragma unroll
+    for (int u = 0; u < kBwdCoopU; ++u) {
+        if (at[u] == 0xffffffffu) continue;
+        float4 o;
+#pragma unroll
+        for (int l = 0; l < 4; ++l)  // bwd_elem's expression on the held terms
+            lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
+        st4<kNtOut>(delta, at[u], o);
+    }
+}
+
 // ---- host ---------------------------------------------------------------------
 
 // The one-launch forward for channels of up to kCoopMaxChan elements (a
@@ -675,13 +768,38 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 #define DKZ_BN_FWD_COOP 1
 #endif
 constexpr uint64_t kCoopMaxChan = 256ull * kCoopChunk;
-// ... and at most this many workgroups in all, so that the whole grid is
-// resident at once (otherwise workgroups waiting at their barrier hold CUs
-// that later channels need: config 2's shape, 6272 workgroups, took 105 us
-// against 97 for the two passes).
+// ... and at most this many workgroups in all (and no more than the GPU
+// holds at once, resident_workgroups), so that the whole grid is resident at
+// once (otherwise workgroups waiting at their barrier hold CUs that later
+// channels need: config 2's shape, 6272 workgroups, took 105 us against 97
+// for the two passes; the backward with 2048 workgroups at 4 waves per SIMD
+// 38.6 against 27.8).
 #ifndef DKZ_BN_COOP_MAX_WGS
 #define DKZ_BN_COOP_MAX_WGS 2048
 #endif
+#ifndef DKZ_BN_BWD_COOP
+#define DKZ_BN_BWD_COOP 1
+#endif
+
+// Workgroups of `kernel` (kBlock threads) the GPU holds at once: HIP's
+// occupancy for the kernel's registers and LDS times the CU count, looked up
+// once per device. A one-launch pass runs only when its whole grid fits, so
+// no workgroup waits at its channel barrier for one that is not yet
+// resident.
+template <class Kernel>
+uint32_t resident_workgroups(Kernel kernel) {
+    static uint32_t cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    if (cache[dev] == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cache[dev] = (uint32_t)(per_cu > 0 ? per_cu : 0) * (uint32_t)(cus > 0 ? cus : 0);
+    }
+    return cache[dev];
+}
 
 struct Shape {
     uint32_t B, F, S, n;
@@ -760,7 +878,8 @@ int bn_forward_fused(const FwdArgs &a) {
     }
     if (DKZ_BN_FWD_COOP && L <= kCoopMaxChan && sh.F <= kScratchSlots / kCounterStride &&
         (uint64_t)sh.F * div_up(L, kCoopChunk) <= DKZ_BN_COOP_MAX_WGS &&
-        2ull * sh.F * div_up(L, kCoopChunk) * kPartialStride <= kScratchPartials) {
+        2ull * sh.F * div_up(L, kCoopChunk) * kPartialStride <= kScratchPartials &&
+        (uint64_t)sh.F * div_up(L, kCoopChunk) <= resident_workgroups(bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP>)) {
         // one launch: chunks of at most kCoopChunk elements, whole float4s
         const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, div_up(L, kCoopChunk), true);
         Scratch scc{nullptr};
@@ -790,6 +909,19 @@ int bn_backward_fused(const BwdArgs &a) {
     constexpr int H = DKZ_HINT_BN_BWD_APPLY;
     const Shape &sh = a.sh;
     const BwdFin fin{a.variance, a.bias_updates, a.scale_updates, a.mean_delta, a.variance_delta};
+    const uint64_t L = (uint64_t)sh.B * sh.S;
+    const uint64_t kb = div_up(L, kBwdCoopChunk);
+    if (DKZ_BN_BWD_COOP && kb <= 256 && (uint64_t)sh.F * kb <= DKZ_BN_COOP_MAX_WGS &&
+        sh.F <= kScratchSlots / kCounterStride && 4ull * sh.F * kb * kPartialStride <= kScratchPartials &&
+        (uint64_t)sh.F * kb <= resident_workgroups(bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>)) {
+        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)kb, true);
+        Scratch scc{nullptr};
+        DKZ_TRY(device_scratch(&scc));
+        const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
+                          (float)((uint64_t)sh.S * (uint64_t)sh.B)};
+        return launch("batchnorm_backward", bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>, dim3(sh.F * gc.K),
+                      dim3(kBlock), a.y, a.delta, a.x_norm, a.x, p, gc, fin, scc.partials, scc.slots);
+    }
     const RedGeom g = sums_geom<4>(sh, A == kLinear ? 3 : 4);
     const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;
