@@ -57,7 +57,9 @@ marker dispatches (after one untimed pass over all its rotations) and prints
 the rows, for rocprofv3 counter runs (READ_COUNTERS, WRITE_COUNTERS) and a
 kernel trace that attribute HBM traffic and kernel time to each row;
 --copy-calibration runs a known-size copy that checks the counter formula;
---traffic-table DIR prints the table (profiles/traffic_per_op.md) from them.
+--traffic-table DIR prints the table (profiles/traffic_per_op.md) from them;
+--sq-table DIR prints the instruction mix per row from two SQ counter runs of
+--per-op-traffic (SQ_COUNTERS; profiles/softmax_instruction_mix.md).
 """
 
 from __future__ import annotations
@@ -371,29 +373,40 @@ def gbs(nbytes: int, ms: float) -> float:
 # workgroups of 256, about 1 MB -- so that a profile (rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE, or a kernel trace) can attribute every dispatch to
 # its row from the dispatch order and grid sizes alone. Every rotation runs
-# once, untimed, before the begin marker: the traced passes then find their
-# pages mapped (as in a stream of such calls) but their data, at least
-# 512 MB back, out of the 256 MB Infinity Cache.
+# once, untimed, before the begin marker, so the traced passes find their
+# pages mapped (as in a stream of such calls); then a cached read of a
+# separate 512 MB buffer leaves the 256 MB Infinity Cache holding clean lines
+# of unrelated data. Each row thus starts from the same cache state, whatever
+# ran before it: its data out of the cache, and no dirty lines of another
+# row's writes for its own reads to evict.
 MARK_BASE = 1000
 TRAFFIC_PASSES = 3
+FLUSH_BYTES = 512 << 20
 
 
 def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     """The per-op table; with `traffic` (a list), no timing: each row's first
     TRAFFIC_PASSES launches (or call sequences) run once between markers and
-    the row is appended to `traffic`. `only`: time only rows whose config
-    name contains this string."""
+    the row is appended to `traffic`. `only`: run only rows whose full name
+    (config/op) contains one of these '|'-separated strings."""
     from darknet_zig_amd.activations import Activation
 
     rows = {}
 
-    def wanted(cfg):
-        return only is None or only in cfg
+    def wanted(cfg, name):
+        return only is None or any(o in f"{cfg}/{name}" for o in only.split("|"))
     if traffic is not None:
         mark_buf = gpu.alloc((MARK_BASE + 256) * 256 + 1)
+        flush_f = FLUSH_BYTES // 4 // 128
+        flush_buf, flush_out = gpu.alloc(flush_f * 128), gpu.alloc(128)
+        gpu.fill(flush_buf, flush_f * 128, 1.0)
 
     def marker(grid):
         gpu.fill(mark_buf.offset(1), grid * 256, 0.0)
+
+    def flush():
+        # a per-channel sum over 128 channels: cached loads, 512 B written
+        gpu.backwardBias(flush_out, flush_buf, 1, 128, flush_f)
 
     def traced(cfg, name, nbytes, seqs):
         i = len(traffic)
@@ -401,6 +414,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         for seq in seqs:
             for fn in seq:
                 fn()
+        flush()
         hip.sync()
         marker(MARK_BASE + 2 * i)
         for seq in seqs[:passes]:
@@ -431,7 +445,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         ~2 us of dispatch and completion). `hot`: also a row labelled
         [hot cache], the op replayed on one buffer set, whose data the 256 MB
         Infinity Cache then holds."""
-        if not wanted(cfg):
+        if not wanted(cfg, name):
             return
         if traffic is not None:
             return traced(cfg, name, nbytes, [[f] for f in fns])
@@ -445,7 +459,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         """A call sequence (or a multi-launch entry point) over rotated sets,
         graph-replayed back to back as a layer would issue it (`issued_us`:
         issued from Python); `hot` as in add()."""
-        if not wanted(cfg):
+        if not wanted(cfg, name):
             return
         if traffic is not None:
             return traced(cfg, name, nbytes, seqs)
@@ -736,7 +750,8 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         [lambda i=i, c=c: gpu.col2im(c, C2, H2, H2, K2, 1, 1, i) for i, c in zip(ims, cols)])
     dev.free()
     if traffic is not None:
-        gpu.free(mark_buf)
+        for b in (mark_buf, flush_buf, flush_out):
+            gpu.free(b)
     return rows
 
 
@@ -1158,6 +1173,55 @@ def counter_traffic(row: str):
     return None
 
 
+SQ_COUNTERS = ("SQ_WAVES SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR SQ_INSTS_LDS "
+               "SQ_WAIT_INST_ANY SQ_WAVE_CYCLES GRBM_GUI_ACTIVE",
+               "SQ_INSTS_VALU_TRANS_F32 SQ_INSTS_VALU_FMA_F32 SQ_INSTS_VALU_ADD_F32 SQ_INSTS_VALU_MUL_F32 "
+               "SQ_INSTS_VALU_FMA_F64 SQ_ACTIVE_INST_VALU SQ_BUSY_CYCLES SQ_WAIT_ANY")
+
+
+def sq_table(d: Path) -> str:
+    """Instruction mix per row (markdown) from the outputs under `d`:
+    rows.json (stdout of `bench.py --per-op-traffic --rows ...`) and sq_a/,
+    sq_b/ (rocprofv3 --pmc with the two SQ_COUNTERS groups over that
+    command). Per pass: waves, instructions per wave, VALU lane-operations
+    per element moved (instructions x 64 / (algorithmic bytes / 4)), and the
+    shares of a wave's cycles spent issuing VALU work and waiting."""
+    def last_json(path):
+        return json.loads([ln for ln in open(path) if ln.startswith("{")][-1])
+
+    meta = last_json(d / "rows.json")
+    rows, base = meta["per_op_traffic"], meta["mark_base"]
+    segs = [_segments([(n, b, c) for n, b, c in _dispatch_counters(d / sub)], base) for sub in ("sq_a", "sq_b")]
+    lines = [
+        "| row | waves | VALU / wave | SALU / wave | VMEM rd / wave | VMEM wr / wave | LDS / wave "
+        "| VALU lane-ops / elem | of which exp2 (trans) | f32 fma+add+mul | f64 fma | VALU-issue share "
+        "| wait share | GRBM_GUI_ACTIVE cycles |",
+        "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|",
+    ]
+    for i, r in enumerate(rows):
+        p = r["passes"]
+        c = {}
+        for seg in segs:
+            for _, vals in seg.get(i, []):
+                for k, v in vals.items():
+                    c[k] = c.get(k, 0.0) + v / p
+        if not c.get("SQ_WAVES"):
+            continue
+        w, elems = c["SQ_WAVES"], r["bytes"] / 4
+
+        def per_elem(k):
+            return 64 * c.get(k, 0.0) / elems
+        f32 = per_elem("SQ_INSTS_VALU_FMA_F32") + per_elem("SQ_INSTS_VALU_ADD_F32") + per_elem("SQ_INSTS_VALU_MUL_F32")
+        lines.append(
+            f"| {r['row']} | {w:.0f} | {c['SQ_INSTS_VALU'] / w:.1f} | {c['SQ_INSTS_SALU'] / w:.1f} | "
+            f"{c['SQ_INSTS_VMEM_RD'] / w:.1f} | {c['SQ_INSTS_VMEM_WR'] / w:.1f} | {c['SQ_INSTS_LDS'] / w:.1f} | "
+            f"{per_elem('SQ_INSTS_VALU'):.2f} | {per_elem('SQ_INSTS_VALU_TRANS_F32'):.2f} | {f32:.2f} | "
+            f"{per_elem('SQ_INSTS_VALU_FMA_F64'):.2f} | "
+            f"{c['SQ_ACTIVE_INST_VALU'] / c['SQ_WAVE_CYCLES']:.3f} | {c['SQ_WAIT_INST_ANY'] / c['SQ_WAVE_CYCLES']:.3f} | "
+            f"{c['GRBM_GUI_ACTIVE']:.0f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1175,7 +1239,11 @@ def main() -> int:
                     help="only run dkz_copy over MIB MiB (x4 launches, rotated): a known-size kernel that "
                          "checks the counter formula of the traffic table")
     ap.add_argument("--rows", default=None, metavar="SUBSTR",
-                    help="with --per-op-only: time only the per-op rows whose config contains SUBSTR")
+                    help="with --per-op-only or --per-op-traffic: only the per-op rows whose name "
+                         "(config/op) contains SUBSTR ('|'-separated alternatives)")
+    ap.add_argument("--sq-table", default=None, metavar="DIR",
+                    help="only print the instruction-mix table (markdown) from the rocprofv3 SQ counter outputs "
+                         "in DIR (see sq_table())")
     ap.add_argument("--traffic-table", default=None, metavar="DIR",
                     help="only print the per-op traffic table (markdown) from the rocprofv3 outputs in DIR "
                          "(see traffic_table())")
@@ -1187,6 +1255,9 @@ def main() -> int:
 
     if args.traffic_table:
         print(traffic_table(Path(args.traffic_table)))
+        return 0
+    if args.sq_table:
+        print(sq_table(Path(args.sq_table)))
         return 0
 
     from darknet_zig_amd import gpu
@@ -1209,7 +1280,7 @@ def main() -> int:
 
     if args.per_op_traffic:
         traffic = []
-        per_op_table(gpu, hip, stream, 1, traffic)
+        per_op_table(gpu, hip, stream, 1, traffic, only=args.rows)
         print(json.dumps({"per_op_traffic": traffic, "mark_base": MARK_BASE}), flush=True)
         return 0
 

@@ -34,6 +34,12 @@ namespace {
 #define DKZ_CHAN_UNROLL 4
 #endif
 constexpr int kUnroll = DKZ_CHAN_UNROLL;
+// Float4s in flight per lane for single-input sums. Measured on MI355X: 8 or
+// 16 instead of 4 took config 1's mean from 6.0 to 7.0 us and config 2's
+// backward_bias from 18.7 to 19.2 / 20.1 us, so single-input sums keep 4.
+#ifndef DKZ_CHAN_UNROLL1
+#define DKZ_CHAN_UNROLL1 DKZ_CHAN_UNROLL
+#endif
 #ifndef DKZ_CHAN_KMAJOR
 #define DKZ_CHAN_KMAJOR 1
 #endif
@@ -56,18 +62,19 @@ __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const f
     double acc0 = 0.0, acc1 = 0.0;
     if constexpr (VEC) {
         constexpr uint32_t kStep = 4 * BS;
+        constexpr int kU = TWO ? kUnroll : DKZ_CHAN_UNROLL1;
         uint32_t j = j0 + 4 * threadIdx.x;
-        for (; j + kStep * (kUnroll - 1) < j1; j += kStep * kUnroll) {
-            float4 a[kUnroll], b[kUnroll];
+        for (; j + kStep * (kU - 1) < j1; j += kStep * kU) {
+            float4 a[kU], b[kU];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < kU; ++u) {
                 const uint32_t v = chan_addr(fbase, j + u * kStep, g) >> 2;
                 a[u] = ld4<(H & 1) != 0>(p0, v);
                 if constexpr (TWO) b[u] = ld4<(H & 2) != 0>(p1, v);
                 else b[u] = a[u];
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; u += 2) {
+            for (int u = 0; u < kU; u += 2) {
                 acc0 += term4(term, a[u], b[u]);
                 acc1 += term4(term, a[u + 1], b[u + 1]);
             }
