@@ -38,14 +38,15 @@
  *     src/layers/pooling.zig: elementwise and broadcast ops bit-exact, the
  *     per-channel and per-row reductions and softmax within 1e-5 relative,
  *     maxpool indices bit-exact.
- *   - The library owns one scratch buffer per device (130 MiB), allocated and
- *     zeroed by dkz_init: the f64 partial sums of the split per-channel
+ *   - The library owns one scratch buffer per device (130.5 MiB), allocated
+ *     and zeroed by dkz_init: the f64 partial sums of the split per-channel
  *     reductions (2 MiB), the partial tiles of a split-K gemm or convolution
- *     weight gradient (128 MiB) and one 64-bit counter slot per channel
- *     (32 KiB) in which a split reduction's workgroups find the channel's
- *     last. Ops never allocate. Reductions or gemms issued concurrently on
- *     two streams of one device share that buffer and race; issue them on
- *     one stream (dkz_set_stream).
+ *     weight gradient (128 MiB) and 64-bit counter slots (512 KiB: one
+ *     256-byte line per channel's meeting slot, arrival counter or barrier)
+ *     through which a reduction's workgroups find the channel's last. Ops
+ *     never allocate, and leave the slots they use at zero. Reductions or
+ *     gemms issued concurrently on two streams of one device share that
+ *     buffer and race; issue them on one stream (dkz_set_stream).
  */
 #ifndef DKZ_OPS_H
 #define DKZ_OPS_H
@@ -428,7 +429,7 @@ int dkz_batchnorm_backward(int batch, int filters, int spatial, int activation, 
  * cannot allocate device memory (code under HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
  * results, bit for bit; its scratch is a static device array of 2 MiB of
- * partial sums + 32 KiB of counter slots per GPU (held until the process
+ * partial sums + 512 KiB of counter slots per GPU (held until the process
  * ends) instead of the library's allocated scratch, and it calls no
  * hipMalloc/hipFree. Limit: the ABI's 2^31-1 elements, beyond which it
  * returns hipErrorInvalidValue. Every call on one GPU shares that array:
