@@ -334,27 +334,45 @@ struct FinAccumulate {  // updates[f] += sum (blas.zig:79, 98)
     __device__ void operator()(uint32_t f, double s, float u) const { updates[f] = u + (float)s; }
 };
 
-// backward_bias with spatial == 1 (gpu.zig:540-543): one lane per filter walks
-// the batch in order, adding each row's one-element sum (0 + delta) to the
-// update exactly as blas.zig:73-82 does -- bit-exact, and coalesced across f.
-// A layer has few filters, so each lane keeps 32 rows' loads in flight
-// before their adds.
-__global__ __launch_bounds__(kBlock) void backward_bias_conn_kernel(float *updates, const float *delta,
-                                                                    uint32_t batch, uint32_t filters) {
-    constexpr uint32_t kRows = 32;
-    const uint32_t f = blockIdx.x * kBlock + threadIdx.x;
-    if (f >= filters) return;
-    float u = updates[f];
-    uint32_t b = 0;
-    for (; b + kRows <= batch; b += kRows) {
+// backward_bias with spatial == 1 (gpu.zig:540-543, a connected layer's
+// [batch, filters] delta): the twin adds the batch's rows into the update one
+// after another in f32 (blas.zig:73-82). Here a workgroup of kConnWaves
+// waves owns 64 consecutive filters (a wave's lanes read 256 contiguous
+// bytes of a row); wave w adds rows w, w + kConnWaves, ... in f64, eight
+// rows' loads in flight, and the first wave adds the waves' sums in wave
+// order and rounds u + sum once. Deterministic, and the correctly rounded
+// f32 of the update's exact value to within f64 rounding, so at least as
+// close to it as the twin's sequential sum.
+constexpr uint32_t kConnWaves = 16;
+__global__ __launch_bounds__(kConnWaves * kWave) void backward_bias_conn_kernel(float *updates, const float *delta,
+                                                                               uint32_t batch, uint32_t filters) {
+    constexpr uint32_t kRows = 8;
+    __shared__ double part[kConnWaves][kWave];
+    const uint32_t l = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const uint32_t f = blockIdx.x * kWave + l;
+    const bool live = f < filters;
+    // Lanes past the last filter read the last filter's column and drop it,
+    // so every load is unconditional and a lane's eight stay in flight
+    // together (a conditional load would be waited on before the next).
+    const uint32_t fc = live ? f : filters - 1;
+    double acc = 0.0;
+    uint32_t b = w;
+    for (; b + (kRows - 1) * kConnWaves < batch; b += kRows * kConnWaves) {
         float v[kRows];
 #pragma unroll
-        for (uint32_t k = 0; k < kRows; ++k) v[k] = delta[(b + k) * filters + f];
+        for (uint32_t k = 0; k < kRows; ++k) v[k] = delta[(b + k * kConnWaves) * filters + fc];
 #pragma unroll
-        for (uint32_t k = 0; k < kRows; ++k) u += 0.0f + v[k];
+        for (uint32_t k = 0; k < kRows; ++k) acc += (double)v[k];
     }
-    for (; b < batch; ++b) u += 0.0f + delta[b * filters + f];
-    updates[f] = u;
+    for (; b < batch; b += kConnWaves) acc += (double)delta[b * filters + fc];
+    part[w][l] = live ? acc : 0.0;
+    __syncthreads();
+    if (w == 0 && live) {
+        double s = part[0][l];
+#pragma unroll
+        for (uint32_t i = 1; i < kConnWaves; ++i) s += part[i][l];
+        updates[f] = (float)((double)updates[f] + s);
+    }
 }
 
 // ---- global average pooling forward: one wave per row ----------------------
@@ -444,8 +462,8 @@ int dkz_backward_bias(float *bias_updates, const float *delta, int batch, int fi
     DKZ_REQUIRE(bias_updates && (delta || spatial == 0));
     if (spatial == 1) {
         DKZ_REQUIRE((uint64_t)batch * (uint64_t)filters <= kMaxElems);
-        return launch("backward_bias_conn", backward_bias_conn_kernel, dim3(div_up((uint32_t)filters, kBlock)),
-                      dim3(kBlock), bias_updates, delta, (uint32_t)batch, (uint32_t)filters);
+        return launch("backward_bias_conn", backward_bias_conn_kernel, dim3(div_up((uint32_t)filters, kWave)),
+                      dim3(kConnWaves * kWave), bias_updates, delta, (uint32_t)batch, (uint32_t)filters);
     }
     return run_chan_reduce<DKZ_HINT_BACKWARD_BIAS, SumValue, FinAccumulate, false>("backward_bias", SumValue{},
                                                            FinAccumulate{bias_updates}, delta, nullptr, batch,

@@ -30,8 +30,9 @@
 // host-libm-identical expf_libm, and are bit-exact:
 //
 //  * side-by-side strided groups (group_offset 1) with n <= kTileMaxN: a
-//    workgroup stages 64 consecutive groups in LDS; all its lanes share the
-//    loads, exps and divides, and lane g < 64 takes group g's max and sum.
+//    workgroup stages T = 8..64 consecutive groups in LDS; all its lanes
+//    share the loads, exps and divides, and lane g < T takes group g's max
+//    and sum.
 //  * other strided groups, or n <= 32: one lane per group runs the twin's
 //    three loops, eight loads at a time.
 //
@@ -507,55 +508,94 @@ int softmax_contiguous(const float *input, float *output, const Groups &G, uint3
     return launch("softmax_big", softmax_big_kernel<false>, dim3(rows), dim3(kBigBlock), input, output, G, x);
 }
 
-constexpr uint32_t kTileRows = 64;
 constexpr uint32_t kTileMaxN = 128;
+// Workgroups a strided-softmax launch aims for: tiles of T = 64, 32, 16 or 8
+// rows, the widest that still gives this many (a [64,85,13,13] spatial
+// softmax has 10816 rows: 169 tiles of 64 leave most CUs idle).
+#ifndef DKZ_SOFTMAX_TILE_MIN_WGS
+#define DKZ_SOFTMAX_TILE_MIN_WGS 512
+#endif
 
-// Rows r0 .. r0+63 (group r = b*groups + g); tile[i*64 + l] holds element i of
-// row r0 + l.
+// Rows r0 .. r0+T-1 (group r = b*groups + g); tile[i*T + l] holds element i
+// of row r0 + l. Side-by-side groups make element i of the T rows T
+// consecutive floats, so the loads are T-float runs.
+template <uint32_t T>
 __global__ __launch_bounds__(kBlock) void softmax_tile_kernel(const float *in, float *out, Groups G, uint32_t rows) {
-    __shared__ float tile[kTileMaxN * kTileRows];
-    __shared__ uint32_t base_sh[kTileRows];
-    __shared__ float mt_sh[kTileRows], sum_sh[kTileRows];
-    const uint32_t r0 = blockIdx.x * kTileRows;
-    const uint32_t nr = rows - r0 < kTileRows ? rows - r0 : kTileRows;
-    const uint32_t n = G.n, st = G.stride, total = n * kTileRows;
+    __shared__ float tile[kTileMaxN * T];
+    __shared__ uint32_t base_sh[T];
+    __shared__ float mt_sh[T], sum_sh[T];
+    const uint32_t r0 = blockIdx.x * T;
+    const uint32_t nr = rows - r0 < T ? rows - r0 : T;
+    const uint32_t n = G.n, st = G.stride, total = n * T;
     const uint32_t t = threadIdx.x;
-    if (t < kTileRows) base_sh[t] = t < nr ? group_base(r0 + t, G) : 0u;
+    if (t < T) base_sh[t] = t < nr ? group_base(r0 + t, G) : 0u;
     __syncthreads();
-    // Eight loads per lane in flight: element i of row l for q = i*64 + l.
+    // Eight loads per lane in flight: element i of row l for q = i*T + l.
     for (uint32_t q0 = t; q0 < total; q0 += kBlock * 8) {
         float v[8];
 #pragma unroll
         for (uint32_t u = 0; u < 8; ++u) {
-            const uint32_t q = q0 + u * kBlock, l = q & (kTileRows - 1);
-            v[u] = q < total && l < nr ? in[base_sh[l] + (q / kTileRows) * st] : 0.0f;
+            const uint32_t q = q0 + u * kBlock, l = q & (T - 1);
+            v[u] = q < total && l < nr ? in[base_sh[l] + (q / T) * st] : 0.0f;
         }
 #pragma unroll
         for (uint32_t u = 0; u < 8; ++u)
             if (q0 + u * kBlock < total) tile[q0 + u * kBlock] = v[u];
     }
     __syncthreads();
+    // The row lanes' max and sum read eight LDS entries ahead of folding them
+    // (in element order), so each pass waits on LDS once per eight elements.
     if (t < nr) {
         float mx = -FLT_MAX;
-        for (uint32_t i = 0; i < n; ++i) mx = fmaxf(mx, tile[i * kTileRows + t]);
+        uint32_t i = 0;
+        for (; i + 8 <= n; i += 8) {
+            float v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) v[k] = tile[(i + k) * T + t];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) mx = fmaxf(mx, v[k]);
+        }
+        for (; i < n; ++i) mx = fmaxf(mx, tile[i * T + t]);
         mt_sh[t] = mx / G.temp;
     }
     __syncthreads();
     for (uint32_t q = t; q < total; q += kBlock) {
-        const uint32_t l = q & (kTileRows - 1);
+        const uint32_t l = q & (T - 1);
         if (l < nr) tile[q] = expf_libm(tile[q] / G.temp - mt_sh[l]);
     }
     __syncthreads();
     if (t < nr) {
         float s = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) s += tile[i * kTileRows + t];
+        uint32_t i = 0;
+        for (; i + 8 <= n; i += 8) {
+            float v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) v[k] = tile[(i + k) * T + t];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) s += v[k];
+        }
+        for (; i < n; ++i) s += tile[i * T + t];
         sum_sh[t] = s;
     }
     __syncthreads();
     for (uint32_t q = t; q < total; q += kBlock) {
-        const uint32_t l = q & (kTileRows - 1);
-        if (l < nr) out[base_sh[l] + (q / kTileRows) * st] = tile[q] / sum_sh[l];
+        const uint32_t l = q & (T - 1);
+        if (l < nr) out[base_sh[l] + (q / T) * st] = tile[q] / sum_sh[l];
     }
+}
+
+int softmax_tiles(const float *input, float *output, const Groups &G, uint32_t rows) {
+    if (div_up(rows, 64u) >= DKZ_SOFTMAX_TILE_MIN_WGS)
+        return launch("softmax_tile", softmax_tile_kernel<64>, dim3(div_up(rows, 64u)), dim3(kBlock), input, output,
+                      G, rows);
+    if (div_up(rows, 32u) >= DKZ_SOFTMAX_TILE_MIN_WGS)
+        return launch("softmax_tile", softmax_tile_kernel<32>, dim3(div_up(rows, 32u)), dim3(kBlock), input, output,
+                      G, rows);
+    if (div_up(rows, 16u) >= DKZ_SOFTMAX_TILE_MIN_WGS)
+        return launch("softmax_tile", softmax_tile_kernel<16>, dim3(div_up(rows, 16u)), dim3(kBlock), input, output,
+                      G, rows);
+    return launch("softmax_tile", softmax_tile_kernel<8>, dim3(div_up(rows, 8u)), dim3(kBlock), input, output, G,
+                  rows);
 }
 
 // One lane per group: blas.zig:213-223 verbatim.
@@ -623,9 +663,7 @@ int softmax_run(const float *input, int n, int batch, int batch_offset, int grou
                    (uint32_t)stride, temp,             make_fastdiv((uint32_t)groups)};
     if (!(stride == 1 && n > 32)) {
         DKZ_REQUIRE(xe == nullptr);
-        if (group_offset == 1 && stride > 1 && (uint32_t)n <= kTileMaxN)
-            return launch("softmax_tile", softmax_tile_kernel, dim3(div_up(rows, kTileRows)), dim3(kBlock), input,
-                          output, G, rows);
+        if (group_offset == 1 && stride > 1 && (uint32_t)n <= kTileMaxN) return softmax_tiles(input, output, G, rows);
         return launch("softmax_lane", softmax_lane_kernel, dim3(div_up(rows, kBlock)), dim3(kBlock), input, output,
                       G, rows);
     }

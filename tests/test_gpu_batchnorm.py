@@ -126,10 +126,7 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
         du = up(upd0)
         fn(du)
         got = down(du, upd0)
-        if name == "backward_bias" and S == 1:
-            assert_bitexact(got, cpu, f"{name} {shape} (spatial 1 path)")
-        else:
-            assert_r5(got, cpu, want64, f"{name} {shape}")
+        assert_r5(got, cpu, want64, f"{name} {shape}" + (" (spatial 1 path)" if S == 1 else ""))
         gpu.free(du)
 
     md_cpu, vd_cpu = np.empty(F, np.float32), np.empty(F, np.float32)
@@ -151,6 +148,35 @@ def test_backward_reductions_and_normalize_delta(dev, shape):
     gpu.normalizeDelta(dx, dm, dv, dmd_c, dvd_c, B, F, S, dd)
     assert_bitexact(down(dd, delta), cpu, f"normalize_delta {shape}")
     for b in (dx, dd, dxn, dm, dv, dmd, dvd, dmd_c, dvd_c):
+        gpu.free(b)
+
+
+@pytest.mark.parametrize("shape", [(256, 1000, 1), (1, 5, 1), (3, 70, 1), (129, 64, 1), (1000, 130, 1),
+                                   (4099, 33, 1), (17, 2000, 1)], ids=str)
+def test_backward_bias_connected(dev, shape):
+    """backward_bias with spatial 1 (a connected layer's [batch, filters]
+    delta, gpu.zig:540-543): the 1e-5 rule against the twin's sequential sum
+    and the exact f64 update, with large and cancelling updates (the twin's
+    update starts from a value the batch's deltas nearly cancel), and the
+    same bits on a repeat. Shapes cover filters off a multiple of 64, a batch
+    off a multiple of the 16 row-waves and of 8 rows a load round, one row,
+    and several load rounds per wave."""
+    B, F, S = shape
+    r = rng(777 + B + F)
+    delta = normal(r, B * F, 0, 1)
+    d64 = delta.astype(np.float64).reshape(B, F)
+    upd0 = normal(r, F, 0, 10)
+    upd0[::3] = (-d64.sum(axis=0)[::3]).astype(np.float32)  # near-cancelling updates
+    cpu = upd0.copy()
+    ref.backwardBias(cpu, delta, B, F, S)
+    dd, du = up(delta), up(upd0)
+    gpu.backwardBias(du, dd, B, F, S)
+    got = down(du, upd0)
+    assert_r5(got, cpu, upd0.astype(np.float64) + d64.sum(axis=0), f"backward_bias {shape}")
+    gpu.push(du, upd0)
+    gpu.backwardBias(du, dd, B, F, S)
+    assert_bitexact(down(du, upd0), got, f"backward_bias repeat {shape}")
+    for b in (dd, du):
         gpu.free(b)
 
 

@@ -116,12 +116,14 @@ def test_softmax_special_values(dev):
         assert np.all(got[~nan_c] >= 0)
 
 
-@pytest.mark.parametrize("b, c, s", [(2, 11, 49), (3, 85, 169), (2, 128, 65), (2, 130, 13), (1, 1, 7)])
+@pytest.mark.parametrize("b, c, s", [(2, 11, 49), (3, 85, 169), (2, 128, 65), (2, 130, 13), (1, 1, 7),
+                                     (64, 85, 169), (100, 20, 196), (256, 5, 169)])
 def test_softmax_spatial_groups(dev, b, c, s):
     # Spatial softmax: groups = positions, elements `spatial` apart
     # (n = channels, batch_offset = c*s, groups = s, group_offset = 1, stride = s).
-    # Up to 128 channels the groups go through the LDS tile kernel (64 groups
-    # per workgroup, the last tile partial); above, one lane per group.
+    # Up to 128 channels the groups go through the LDS tile kernel (8, 16, 32
+    # or 64 groups per workgroup by the group count: the last three cases take
+    # 16, 32 and 64; the last tile partial); above, one lane per group.
     x = normal(rng(11 + c + s), b * c * s, 0, 2.0)
     got, cpu = _softmax_case(x, c, b, c * s, s, 1, s, 1.0)
     assert_bitexact(got, cpu, f"spatial softmax {b}x{c}x{s}")
