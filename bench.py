@@ -544,7 +544,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
     sets = upload_config2(dev, h, 5)  # 5 x 102.8 MB of delta: backward_bias alone cycles 514 MB
     chains = [config2_chain_ops(gpu, d, h) for d in sets]
     for j, (name, nbytes, _) in enumerate(chains[0]):
-        add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains])
+        add("cfg2_bn_bwd[64,128,56,56]", name, nbytes, [c[j][2] for c in chains], hot=True)
     add_seq("fused", "cfg2 batchnorm_backward(leaky)", 5 * 4 * h["n"],
             [[lambda d=d: fused_backward(gpu, d, h)] for d in sets])
     # config 1's forward ops on the largest batch-norm tensor of the configs

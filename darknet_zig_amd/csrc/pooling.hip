@@ -64,6 +64,10 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 // against per-output kernels: [1,32,56,56] 4.9 / 9.7 against 2.9 / 4.4 us,
 // [1,128,56,56] 5.5 / 9.9 against 3.5 / 5.3, [1,64,104,104] forward 13.9
 // against 4.1.
+// The 3x3 stride-2 kernels (build-time switch, for measurement).
+#ifndef DKZ_POOL_3S2
+#define DKZ_POOL_3S2 1
+#endif
 #ifndef DKZ_POOL_PLANE_MIN
 #define DKZ_POOL_PLANE_MIN 256
 #endif
@@ -470,6 +474,138 @@ __global__ __launch_bounds__(kBlock) void maxpool2_bwd_kernel(const float *delta
     st4<(kHb & 4) != 0>(prev, r1 >> 2, b);
 }
 
+// ---- 3x3, stride 2, window offset -P0 (P0 = pad/2 = 0 or 1) -----------------
+//
+// For ow % 4 == 0 and w == 2*ow (darknet's size=3 stride=2 layer with pad 1
+// or 2 on a width that is a multiple of 8).
+//
+// Forward: a lane owns outputs x0..x0+3 (x0 = 4*xq) of output row y; their
+// windows span the 9 input columns 2*x0 - P0 .. 2*x0 - P0 + 8 of input rows
+// 2y - P0 .. 2y - P0 + 2, read per row as two aligned float4s (columns
+// 2*x0 .. 2*x0 + 7) and the one column beside them. Columns and rows outside
+// the input read a clamped in-range address and count as -FLT_MAX, which
+// strict '>' never takes: the twin's scan (rows outer, columns inner) and its
+// first-maximum index, bit for bit.
+template <int P0>
+__global__ __launch_bounds__(kBlock) void maxpool3s2_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g,
+                                                                FastDiv div_qw, uint32_t lanes) {
+    const uint32_t q = blockIdx.x * kBlock + threadIdx.x;
+    if (q >= lanes) return;
+    const uint32_t t = fdiv(q, div_qw);  // plane * oh + y
+    const uint32_t xq = q - t * (g.ow >> 2);
+    const uint32_t plane = fdiv(t, g.div_oh);
+    const uint32_t y = t - plane * g.oh;
+    const uint32_t c0 = 8 * xq;                      // first column of the float4 pair
+    const int ce = P0 == 1 ? (int)c0 - 1 : (int)c0 + 8;  // the column beside them
+    const bool ce_ok = ce >= 0 && ce < (int)g.w;
+    float v[3][9];
+    int rowi[3];
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+        const int r = 2 * (int)y - P0 + kh;
+        const bool r_ok = r >= 0 && r < (int)g.h;
+        const uint32_t rc = r_ok ? (uint32_t)r : 0u;
+        const uint32_t base = (plane * g.h + rc) * g.w;
+        rowi[kh] = (int)base;
+        const float4 a = ld4<(kHf & 1) != 0>(in, (base + c0) >> 2);
+        const float4 b = ld4<(kHf & 1) != 0>(in, (base + c0 + 4) >> 2);
+        const float e = in[base + (ce_ok ? (uint32_t)ce : c0)];
+        const float lo = -FLT_MAX;
+        // local column k is input column 2*x0 - P0 + k
+        float *row = v[kh];
+        if (P0 == 1) {
+            row[0] = r_ok && ce_ok ? e : lo;
+            row[1] = r_ok ? a.x : lo; row[2] = r_ok ? a.y : lo; row[3] = r_ok ? a.z : lo; row[4] = r_ok ? a.w : lo;
+            row[5] = r_ok ? b.x : lo; row[6] = r_ok ? b.y : lo; row[7] = r_ok ? b.z : lo; row[8] = r_ok ? b.w : lo;
+        } else {
+            row[0] = r_ok ? a.x : lo; row[1] = r_ok ? a.y : lo; row[2] = r_ok ? a.z : lo; row[3] = r_ok ? a.w : lo;
+            row[4] = r_ok ? b.x : lo; row[5] = r_ok ? b.y : lo; row[6] = r_ok ? b.z : lo; row[7] = r_ok ? b.w : lo;
+            row[8] = r_ok && ce_ok ? e : lo;
+        }
+    }
+    const int col0 = (int)c0 - P0;
+    float m[4];
+    int mi[4];
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        m[o] = -FLT_MAX;
+        mi[o] = -1;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) max_tap(v[kh][2 * o + kw], rowi[kh] + col0 + 2 * o + kw, m[o], mi[o]);
+    }
+    const uint32_t ov = (t * g.ow + 4 * xq) >> 2;
+    st4<(kHf & 2) != 0>(out, ov, make_float4(m[0], m[1], m[2], m[3]));
+    reinterpret_cast<int4 *>(idx)[ov] = make_int4(mi[0], mi[1], mi[2], mi[3]);
+}
+
+// Backward: a lane owns input columns 8*q8 .. 8*q8 + 7 of input row r. The
+// outputs whose windows can hold them are rows y_a <= y_b (the one or two
+// with 2y - P0 <= r <= 2y - P0 + 2) and columns 4*q8 - 1 + P0 .. 4*q8 + 3 + P0,
+// read as an aligned float4/int4 at column 4*q8 and one beside it. Each input
+// adds the deltas of the candidates naming it in ascending output order (row
+// y_a's columns ascending, then row y_b's): the twin's order, bit for bit.
+// Every input is written by its lane alone; those no output names keep their
+// value.
+template <int P0>
+__global__ __launch_bounds__(kBlock) void maxpool3s2_bwd_kernel(const float *delta, float *prev, const int *idx,
+                                                                PoolGeom g, FastDiv div_q8, uint32_t lanes) {
+    const uint32_t q = blockIdx.x * kBlock + threadIdx.x;
+    if (q >= lanes) return;
+    const uint32_t t = fdiv(q, div_q8);  // plane * h + r
+    const uint32_t q8 = q - t * (g.w >> 3);
+    const uint32_t plane = fdiv(t, g.div_h);
+    const int r = (int)(t - plane * g.h);
+    const uint32_t ib = t * g.w + 8 * q8;  // absolute index of the lane's first input
+    float4 pa = ld4<(kHb & 2) != 0>(prev, ib >> 2);
+    float4 pb = ld4<(kHb & 2) != 0>(prev, (ib >> 2) + 1);
+    // candidate output rows
+    const int yb = (r + P0) >> 1;
+    const int ya = r + P0 >= 1 ? (r + P0 - 1) >> 1 : 0;
+    const int oh = (int)g.oh, ow = (int)g.ow;
+    const int xe = P0 == 1 ? 4 * (int)q8 + 4 : 4 * (int)q8 - 1;  // the column beside the aligned four
+    const bool xe_ok = xe >= 0 && xe < ow;
+    float d[2][5];
+    int k[2][5];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int y = s == 0 ? ya : yb;
+        const bool y_ok = y < oh && (s == 0 || yb != ya);
+        const uint32_t orow = (plane * g.oh + (uint32_t)(y_ok ? y : 0)) * g.ow;
+        const uint32_t ov = (orow + 4 * q8) >> 2;
+        const float4 dd = ld4<(kHb & 1) != 0>(delta, ov);
+        const int4 kk = reinterpret_cast<const int4 *>(idx)[ov];
+        const float de = delta[orow + (xe_ok ? (uint32_t)xe : 4 * q8)];
+        const int ke = idx[orow + (xe_ok ? (uint32_t)xe : 4 * q8)];
+        // slot j is candidate column xe (P0 == 0: j = 0; P0 == 1: j = 4) or 4*q8 + (j - (1 - P0))
+        const int off = 1 - P0;
+        d[s][off + 0] = dd.x; d[s][off + 1] = dd.y; d[s][off + 2] = dd.z; d[s][off + 3] = dd.w;
+        k[s][off + 0] = y_ok ? kk.x : -1; k[s][off + 1] = y_ok ? kk.y : -1;
+        k[s][off + 2] = y_ok ? kk.z : -1; k[s][off + 3] = y_ok ? kk.w : -1;
+        d[s][P0 == 1 ? 4 : 0] = de;
+        k[s][P0 == 1 ? 4 : 0] = y_ok && xe_ok ? ke : -1;
+    }
+    float p[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int want = (int)ib + e;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int j = 0; j < 5; ++j) p[e] = add_if(p[e], want, k[s][j], d[s][j]);
+    }
+    st4<(kHb & 4) != 0>(prev, ib >> 2, make_float4(p[0], p[1], p[2], p[3]));
+    st4<(kHb & 4) != 0>(prev, (ib >> 2) + 1, make_float4(p[4], p[5], p[6], p[7]));
+}
+
+// Whether the 3x3/s2 kernels take a shape (see above); pad/2 is P0.
+bool pool3s2_shape(const PoolGeom &g, bool backward) {
+    (void)backward;  // w == 2*ow with ow % 4 == 0 makes w a multiple of 8, as both need
+    return g.size == 3 && g.stride == 2 && g.half_pad <= 1 && g.ow % 4 == 0 && 2 * g.ow == g.w && g.h > 0 &&
+           g.oh > 0;
+}
+
 // Validates the gpu.zig arguments and derives the geometry. `n` is out_n
 // (forward) or in_n (backward); the batch follows from it.
 int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, PoolGeom *g, uint64_t *planes,
@@ -522,6 +658,15 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
         return launch("forward_maxpool_2x2", maxpool2_fwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
                       input, output, indexes, g, pairs);
     }
+    if (DKZ_POOL_3S2 && pool3s2_shape(g, false) && aligned16(input) && aligned16(output) && aligned16(indexes)) {
+        const uint32_t lanes = (uint32_t)out_n / 4;
+        const FastDiv dq = make_fastdiv(g.ow / 4);
+        if (g.half_pad == 1)
+            return launch("forward_maxpool_3x3s2", maxpool3s2_fwd_kernel<1>, dim3(div_up(lanes, kBlock)), dim3(kBlock),
+                          input, output, indexes, g, dq, lanes);
+        return launch("forward_maxpool_3x3s2", maxpool3s2_fwd_kernel<0>, dim3(div_up(lanes, kBlock)), dim3(kBlock),
+                      input, output, indexes, g, dq, lanes);
+    }
     const uint64_t hw = (uint64_t)g.h * g.w;
     if (DKZ_POOL_PLANE && hw > 0 && hw <= kPlaneMaxFloats && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
@@ -559,6 +704,15 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
         const uint32_t pairs = (uint32_t)(planes * g.oh * g.ow / 2);
         return launch("backward_maxpool_2x2", maxpool2_bwd_kernel, dim3(div_up(pairs, kBlock)), dim3(kBlock),
                       delta, prev_delta, indexes, g, pairs);
+    }
+    if (DKZ_POOL_3S2 && pool3s2_shape(g, true) && aligned16(prev_delta) && aligned16(delta) && aligned16(indexes)) {
+        const uint32_t lanes = (uint32_t)(in_n / 8);
+        const FastDiv dq = make_fastdiv(g.w / 8);
+        if (g.half_pad == 1)
+            return launch("backward_maxpool_3x3s2", maxpool3s2_bwd_kernel<1>, dim3(div_up(lanes, kBlock)),
+                          dim3(kBlock), delta, prev_delta, indexes, g, dq, lanes);
+        return launch("backward_maxpool_3x3s2", maxpool3s2_bwd_kernel<0>, dim3(div_up(lanes, kBlock)), dim3(kBlock),
+                      delta, prev_delta, indexes, g, dq, lanes);
     }
     // Outputs whose window covers one input, per dimension: at most ceil(size / stride).
     const uint32_t per_dim = (g.size + g.stride - 1) / g.stride;

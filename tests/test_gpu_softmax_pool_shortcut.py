@@ -180,6 +180,15 @@ MAXPOOL_CASES = [
     (2, 3, 120, 120, 3, 2, 2),    # larger planes: one lane per output
     (2, 3, 78, 78, 3, 1, 2),
     (1, 2, 80, 80, 3, 1, 2),      # larger: one lane per input
+    # 3x3 stride 2 with w == 2*ow, ow % 4 == 0: four outputs a lane forward,
+    # eight inputs a lane backward, window offset -1 or 0
+    (64, 128, 56, 56, 3, 2, 2),   # the bench's generic pool shape
+    (2, 3, 16, 24, 3, 2, 1),      # offset 0
+    (3, 5, 10, 8, 3, 2, 2),       # one lane per output row
+    (2, 4, 7, 16, 3, 2, 2),       # odd height: the last window row clamped
+    (2, 2, 9, 8, 3, 2, 1),        # offset 0, odd height
+    (1, 1, 1, 8, 3, 2, 2),        # one input row: rows -1 and 1 outside
+    (2, 3, 8, 12, 3, 2, 2),       # ow = 6: not a multiple of 4, the generic kernels
 ]
 
 
@@ -239,14 +248,16 @@ def _shared_peaks(batch, c, h, w, size, stride, pad, seed):
 
 
 @pytest.mark.parametrize("case", [(2, 3, 11, 13, 3, 2, 2), (2, 2, 12, 12, 5, 3, 4), (1, 2, 9, 9, 3, 1, 2),
-                                  (2, 2, 10, 10, 4, 2, 2), (1, 2, 120, 120, 3, 2, 2), (86, 3, 11, 13, 3, 2, 2),
-                                  (64, 4, 12, 12, 5, 3, 4), (86, 3, 9, 9, 3, 1, 2)], ids=str)
+                                  (2, 2, 10, 10, 4, 2, 2), (1, 2, 122, 122, 3, 2, 2), (86, 3, 11, 13, 3, 2, 2),
+                                  (64, 4, 12, 12, 5, 3, 4), (86, 3, 9, 9, 3, 1, 2), (1, 2, 120, 120, 3, 2, 2),
+                                  (2, 3, 16, 16, 3, 2, 2), (1, 2, 12, 24, 3, 2, 1)], ids=str)
 def test_maxpool_shared_argmax(dev, case):
     """Inputs that are the argmax of several outputs: the backward pass must
     add their deltas in ascending output order -- the output-per-lane kernel
-    for stride >= 2 (few planes, or planes too large for LDS: 120x120), the
-    plane-in-LDS kernels for at least 256 planes, and the gather kernels for
-    stride 1."""
+    for stride >= 2 (few planes, or planes too large for LDS: 122x122), the
+    plane-in-LDS kernels for at least 256 planes, the gather kernels for
+    stride 1, and the eight-inputs-a-lane 3x3/s2 kernel (120x120, 16x16,
+    12x24 with offset 0)."""
     batch, c, h, w, size, stride, pad = case
     oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
     x = _shared_peaks(*case, seed=sum(case))
