@@ -1014,7 +1014,7 @@ def bn_gelem(table, bwd_chain_ms):
     c1, c2, c12 = "cfg1_bn_fwd[128,32,32,32]", "cfg2_bn_bwd[64,128,56,56]", "cfg1_ops_at_cfg2_shape[64,128,56,56]"
     e1, e2 = 128 * 32 * 1024, 64 * 128 * 3136
     fwd_sum = sum(table[f"{c1}/{k}"]["us"] for k in named)
-    bwd_sum = sum(v["us"] for k, v in table.items() if k.startswith(c2 + "/"))
+    bwd_sum = sum(v["us"] for k, v in table.items() if k.startswith(c2 + "/") and "[hot cache]" not in k)
     fwd1 = us(f"{c1}/chain: mean,variance,normalize,scale_bias,add_bias,leaky")
     bwd1 = us(f"{c1}/backward chain: gradient,backward_bias,backward_scale,scale_bias,mean_delta,variance_delta,"
               "normalize_delta")

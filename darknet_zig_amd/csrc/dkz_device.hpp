@@ -129,6 +129,17 @@ __device__ __forceinline__ void st1(float *p, uint32_t i, float x) {
     else p[i] = x;
 }
 
+// Workgroups are dispatched to the 8 XCDs in turn (workgroup b to XCD b % 8),
+// each with its own L2. xcd_run_block(b, grid, R) renumbers them so that the
+// logical blocks R*i .. R*i + R - 1 run on one XCD (physical blocks b,
+// b + 8, ..., b + 8(R-1)): neighbouring blocks whose data share 128-byte lines
+// then fetch each shared line once. A bijection on [0, grid); blocks past the
+// last whole group of 8R keep their index.
+__host__ __device__ __forceinline__ uint32_t xcd_run_block(uint32_t b, uint32_t grid, uint32_t R) {
+    if (b >= grid / (8 * R) * (8 * R)) return b;
+    return R * ((b / (8 * R)) * 8 + (b & 7)) + (b / 8) % R;
+}
+
 __device__ __forceinline__ float &lane(float4 &v, int k) {
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }

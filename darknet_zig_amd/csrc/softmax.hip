@@ -516,6 +516,9 @@ constexpr uint32_t kTileMaxN = 128;
 #define DKZ_SOFTMAX_TILE_MIN_WGS 512
 #endif
 
+// Runs of 128 / T consecutive tiles (512 bytes of each element row) go to
+// one XCD (xcd_run_block): a tile's runs rarely start on a 128-byte line, so
+// neighbouring tiles share lines, which that XCD's L2 then fetches once.
 // Rows r0 .. r0+T-1 (group r = b*groups + g); tile[i*T + l] holds element i
 // of row r0 + l. Side-by-side groups make element i of the T rows T
 // consecutive floats, so the loads are T-float runs.
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(kBlock) void softmax_tile_kernel(const float *in, f
     __shared__ float tile[kTileMaxN * T];
     __shared__ uint32_t base_sh[T];
     __shared__ float mt_sh[T], sum_sh[T];
-    const uint32_t r0 = blockIdx.x * T;
+    const uint32_t r0 = xcd_run_block(blockIdx.x, gridDim.x, T >= 128 ? 1u : 128u / T) * T;
     const uint32_t nr = rows - r0 < T ? rows - r0 : T;
     const uint32_t n = G.n, st = G.stride, total = n * T;
     const uint32_t t = threadIdx.x;

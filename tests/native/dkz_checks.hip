@@ -2,6 +2,8 @@
 // header (darknet_zig_amd/csrc/dkz_device.hpp) directly:
 //
 //   * chk_fastdiv: the launch-constant division, run on the host;
+//   * chk_xcd_run_block: the workgroup renumbering that keeps runs of
+//     logical blocks on one XCD, run on the host;
 //   * chk_exp2f_tab: the expf table entries, for the high-precision check;
 //   * chk_expf_host_mismatches: expf_libm compiled for the host, compared
 //     with the C library's expf over a range of float bit patterns;
@@ -139,6 +141,8 @@ __global__ void expf_hash_kernel(uint64_t lo, uint64_t hi, unsigned long long *o
 extern "C" {
 
 uint32_t chk_fastdiv(uint32_t n, uint32_t d) { return dkz::fdiv(n, dkz::make_fastdiv(d)); }
+
+uint32_t chk_xcd_run_block(uint32_t b, uint32_t grid, uint32_t r) { return dkz::xcd_run_block(b, grid, r); }
 
 uint64_t chk_exp2f_tab(uint32_t i) { return dkz::exp2f_tab(i); }
 

@@ -9,7 +9,9 @@ compiled for the host from the same source (tests/native/dkz_checks.hip):
 * expf_cw, softmax's exp, against exp in double over all 2^32 float inputs:
   within one ulp everywhere (its device build is checked bit for bit against
   this host build in tests/test_gpu_expf.py);
-* the launch-constant division against Python's integer division.
+* the launch-constant division against Python's integer division;
+* the workgroup renumbering that keeps runs of logical blocks on one XCD: a
+  bijection, with every run on one XCD under round-robin dispatch.
 """
 
 from __future__ import annotations
@@ -29,6 +31,8 @@ def lib():
     L = C.CDLL(str(native_build.LIB))
     L.chk_fastdiv.restype = C.c_uint32
     L.chk_fastdiv.argtypes = [C.c_uint32, C.c_uint32]
+    L.chk_xcd_run_block.restype = C.c_uint32
+    L.chk_xcd_run_block.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
     L.chk_exp2f_tab.restype = C.c_uint64
     L.chk_exp2f_tab.argtypes = [C.c_uint32]
     L.chk_expf_restated.restype = C.c_float
@@ -114,3 +118,20 @@ def test_fastdiv(d):
     for n in ns:
         if 0 <= n < (1 << 31):
             assert L.chk_fastdiv(n, d) == n // d, (n, d)
+
+
+@pytest.mark.parametrize("r", [1, 2, 4, 8, 16])
+def test_xcd_run_block(r):
+    """Logical blocks r*i .. r*i + r - 1 land on physical blocks b, b + 8, ...
+    (one XCD when block b goes to XCD b % 8), and the renumbering is a
+    permutation of [0, grid) for grids that are and are not multiples of 8r."""
+    L = lib()
+    for grid in list(range(1, 300)) + [676, 1352, 4096, 4099]:
+        phys = {}
+        for b in range(grid):
+            t = L.chk_xcd_run_block(b, grid, r)
+            assert 0 <= t < grid and t not in phys, (grid, r, b, t)
+            phys[t] = b
+        full = grid // (8 * r) * (8 * r)
+        for t0 in range(0, full, r):
+            assert len({phys[t0 + k] % 8 for k in range(r)}) == 1, (grid, r, t0)
