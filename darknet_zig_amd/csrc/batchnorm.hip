@@ -416,6 +416,11 @@ constexpr int kCoopU = DKZ_BN_COOP_U;
 #define DKZ_BN_COOP_X_LATE 0
 #endif
 constexpr uint32_t kCoopChunk = kBlock * 4 * kCoopU;
+// The register-resident variant: 512 threads (two waves a SIMD, up to 256
+// registers a lane) holding 49 float4s a lane, so one workgroup a CU covers
+// 100352 elements (half of a config-2 channel).
+constexpr int kRegBlock = 512, kRegU = 49;
+constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 
 // Forward (train) in one launch: workgroup (f, k) -- channel-major, k
 // fastest -- loads chunk k of channel f into registers once, adds its f64
@@ -423,14 +428,17 @@ constexpr uint32_t kCoopChunk = kBlock * 4 * kCoopU;
 // barrier, adds the channel's K partials, forms mean, variance (and, in
 // workgroup k == 0, the rolling averages) exactly as the split statistics
 // path does, and writes x, x_norm and the output from the registers. The
-// input is read once: 16 bytes an element instead of 20.
-template <int A, int H>
-__global__ __launch_bounds__(kBlock) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
-                                                             float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
-                                                             double *partials, uint64_t *slots) {
+// input is read once: 16 bytes an element instead of 20. BS threads a
+// workgroup, U float4s a lane: (kBlock, kCoopU) for small tensors, and
+// (kRegBlock, kRegU) -- one 512-thread workgroup a CU, 196 floats a lane --
+// for tensors that fill the register file (config 2's 103 MB over 256 CUs).
+template <int A, int H, int BS, int U>
+__global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
+                                                         float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
+                                                         double *partials, uint64_t *slots) {
     constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
     constexpr bool kXLate = DKZ_BN_COOP_X_LATE != 0;
-    __shared__ double lds[2 * (kBlock / kWave)];
+    __shared__ double lds[2 * (BS / kWave)];
     __shared__ FwdChan chan_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
@@ -439,24 +447,38 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_coop_kernel(const float *input,
     const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
     const uint32_t fbase = f * g.spatial;
     const double c = (double)input[fbase];
-    float4 v[kCoopU];
-    uint32_t at[kCoopU];
+    // float4 u of the lane is element jb + u*4*BS of the channel. Its
+    // address is recomputed in each phase from a copy of jb the compiler
+    // cannot see through, so it keeps no U addresses alive across phases
+    // (at U = 49 they would push the data out of registers).
+    const auto phase_base = [&]() {
+        uint32_t jb = j0 + 4 * threadIdx.x;
+        asm volatile("" : "+v"(jb));
+        return jb;
+    };
+    float4 v[U];
+    {
+        const uint32_t jb = phase_base();
 #pragma unroll
-    for (int u = 0; u < kCoopU; ++u) {
-        const uint32_t j = j0 + 4 * threadIdx.x + (uint32_t)u * (4 * kBlock);
-        at[u] = j < j1 ? chan_addr(fbase, j, g) >> 2 : 0xffffffffu;
-        if (j < j1) v[u] = ld4<kNtIn>(input, at[u]);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j < j1) v[u] = ld4<kNtIn>(input, chan_addr(fbase, j, g) >> 2);
+        }
     }
     double a[2] = {0.0, 0.0};
+    {
+        const uint32_t jb = phase_base();
 #pragma unroll
-    for (int u = 0; u < kCoopU; ++u) {
-        if (at[u] == 0xffffffffu) continue;
-        acc_shifted(v[u], c, a[0], a[1]);
-        // x (the input copy) needs no statistics: its stores drain while
-        // the channel meets
-        if constexpr (!kXLate) st4<kNtX>(x, at[u], v[u]);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j >= j1) continue;
+            acc_shifted(v[u], c, a[0], a[1]);
+            // x (the input copy) needs no statistics: its stores drain while
+            // the channel meets
+            if constexpr (!kXLate) st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, v[u]);
+        }
     }
-    const Sums<2> r = block_sums<2, kBlock>(a, lds);
+    const Sums<2> r = block_sums<2, BS>(a, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int q = 0; q < 2; ++q)
@@ -476,14 +498,17 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_coop_kernel(const float *input,
     }
     __syncthreads();
     const FwdChan ch = chan_sh;
+    const uint32_t jb = phase_base();
 #pragma unroll
-    for (int u = 0; u < kCoopU; ++u) {
-        if (at[u] == 0xffffffffu) continue;
+    for (int u = 0; u < U; ++u) {
+        const uint32_t j = jb + (uint32_t)u * (4 * BS);
+        if (j >= j1) continue;
+        const uint32_t at = chan_addr(fbase, j, g) >> 2;
         float4 xn, o;
         fwd_elem<A>(v[u], ch, xn, o);
-        if constexpr (kXLate) st4<kNtX>(x, at[u], v[u]);
-        st4<kNtXn>(x_norm, at[u], xn);
-        st4<kNtOut>(output, at[u], o);
+        if constexpr (kXLate) st4<kNtX>(x, at, v[u]);
+        st4<kNtXn>(x_norm, at, xn);
+        st4<kNtOut>(output, at, o);
     }
 }
 
@@ -780,25 +805,44 @@ constexpr uint64_t kCoopMaxChan = 256ull * kCoopChunk;
 #ifndef DKZ_BN_BWD_COOP
 #define DKZ_BN_BWD_COOP 1
 #endif
+#ifndef DKZ_BN_FWD_COOP_REG
+#define DKZ_BN_FWD_COOP_REG 1
+#endif
 
-// Workgroups of `kernel` (kBlock threads) the GPU holds at once: HIP's
-// occupancy for the kernel's registers and LDS times the CU count, looked up
-// once per device. A one-launch pass runs only when its whole grid fits, so
-// no workgroup waits at its channel barrier for one that is not yet
+// Workgroups of Kernel (BS threads) the GPU holds at once: HIP's occupancy
+// for the kernel's registers and LDS times the CU count, looked up once per
+// kernel and device. A one-launch pass runs only when its whole grid fits,
+// so no workgroup waits at its channel barrier for one that is not yet
 // resident.
-template <class Kernel>
-uint32_t resident_workgroups(Kernel kernel) {
+template <auto Kernel, int BS>
+uint32_t resident_workgroups() {
     static uint32_t cache[kMaxDevices];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
     if (cache[dev] == 0) {
         int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, BS, 0) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
         cache[dev] = (uint32_t)(per_cu > 0 ? per_cu : 0) * (uint32_t)(cus > 0 ? cus : 0);
     }
     return cache[dev];
+}
+
+// Whether Kernel keeps everything in registers (no private scratch), looked
+// up once: the register-resident pass is only worth it without spills (the
+// exp-based activations' tanh, for one, spills at 49 float4s a lane).
+template <auto Kernel>
+bool no_spills() {
+    static int cached = -1;  // -1 unknown, 0 spills, 1 none
+    if (cached < 0) {
+        hipFuncAttributes attr{};
+        cached = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(Kernel)) == hipSuccess &&
+                         attr.localSizeBytes == 0
+                     ? 1
+                     : 0;
+    }
+    return cached == 1;
 }
 
 struct Shape {
@@ -879,7 +923,8 @@ int bn_forward_fused(const FwdArgs &a) {
     if (DKZ_BN_FWD_COOP && L <= kCoopMaxChan && sh.F <= kScratchSlots / kCounterStride &&
         (uint64_t)sh.F * div_up(L, kCoopChunk) <= DKZ_BN_COOP_MAX_WGS &&
         2ull * sh.F * div_up(L, kCoopChunk) * kPartialStride <= kScratchPartials &&
-        (uint64_t)sh.F * div_up(L, kCoopChunk) <= resident_workgroups(bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP>)) {
+        (uint64_t)sh.F * div_up(L, kCoopChunk) <=
+            resident_workgroups<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kBlock, kCoopU>, kBlock>()) {
         // one launch: chunks of at most kCoopChunk elements, whole float4s
         const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, div_up(L, kCoopChunk), true);
         Scratch scc{nullptr};
@@ -887,8 +932,27 @@ int bn_forward_fused(const FwdArgs &a) {
         const FwdFin finc{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
                           (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
         const FwdParams p{a.mean, a.variance, a.scales, a.biases};
-        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP>, dim3(sh.F * gc.K),
-                      dim3(kBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc, scc.partials, scc.slots);
+        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kBlock, kCoopU>,
+                      dim3(sh.F * gc.K), dim3(kBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc, scc.partials,
+                      scc.slots);
+    }
+    // the same with one 512-thread workgroup a CU holding 196 floats a lane,
+    // for tensors that fill the register file
+    const uint64_t kr = div_up(L, kRegChunk);
+    if (DKZ_BN_FWD_COOP_REG && sh.F <= kScratchSlots / kCounterStride &&
+        2ull * sh.F * kr * kPartialStride <= kScratchPartials &&
+        no_spills<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>>() &&
+        (uint64_t)sh.F * kr <= resident_workgroups<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>,
+                                                   kRegBlock>()) {
+        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)kr, true);
+        Scratch scc{nullptr};
+        DKZ_TRY(device_scratch(&scc));
+        const FwdFin finc{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
+                          (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
+        const FwdParams p{a.mean, a.variance, a.scales, a.biases};
+        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>,
+                      dim3(sh.F * gc.K), dim3(kRegBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc,
+                      scc.partials, scc.slots);
     }
     const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;
@@ -913,7 +977,7 @@ int bn_backward_fused(const BwdArgs &a) {
     const uint64_t kb = div_up(L, kBwdCoopChunk);
     if (DKZ_BN_BWD_COOP && kb <= 256 && (uint64_t)sh.F * kb <= DKZ_BN_COOP_MAX_WGS &&
         sh.F <= kScratchSlots / kCounterStride && 4ull * sh.F * kb * kPartialStride <= kScratchPartials &&
-        (uint64_t)sh.F * kb <= resident_workgroups(bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>)) {
+        (uint64_t)sh.F * kb <= resident_workgroups<bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>, kBlock>()) {
         const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)kb, true);
         Scratch scc{nullptr};
         DKZ_TRY(device_scratch(&scc));

@@ -119,6 +119,26 @@ def test_forward_train(dev, shape):
     _forward_case(shape, Activation.leaky, True, inplace=True, seed=sum(shape))
 
 
+# Too many workgroups for the small one-launch forward, few enough for the
+# register-resident one (a 512-thread workgroup a CU, up to 100352 elements
+# of a channel each): config 2's shape (two per channel), one per channel
+# (K = 1), and four per channel with a ragged last chunk.
+REGISTER = [(64, 128, 3136), (32, 256, 3136), (100, 64, 4000)]
+
+
+@pytest.mark.parametrize("shape", REGISTER, ids=str)
+def test_forward_train_register_resident(dev, shape):
+    _forward_case(shape, Activation.leaky, True, inplace=True, seed=sum(shape) + 1)
+
+
+@pytest.mark.parametrize("act", [Activation.tanh, Activation.linear, Activation.logistic], ids=lambda a: a.name)
+def test_forward_register_resident_activations(dev, act):
+    """At config 2's shape an activation whose register-resident kernel would
+    spill (tanh) takes the two-pass path instead; either way the results are
+    the twins'."""
+    _forward_case(CONFIG2, act, True, inplace=True, seed=300 + int(act))
+
+
 @pytest.mark.parametrize("shape", [(4, 17, 52), (4, 17, 53)], ids=str)
 def test_forward_standalone_layer_copies_input(dev, shape):
     """input != output: the standalone batchnorm layer (batchnorm.zig:78)."""
@@ -293,22 +313,23 @@ def test_empty_batch_follows_the_sequence(dev):
     _free(d_m, d_v, d_rm, d_rv, d_s, d_b, d_bu, d_md, d_vd)
 
 
-def test_forward_back_to_back(dev):
+@pytest.mark.parametrize("shape, rounds", [((16, 24, 1024), 30), ((64, 128, 3136), 6)], ids=str)
+def test_forward_back_to_back(dev, shape, rounds):
     """Channels split over several workgroups meet at a per-channel barrier
-    inside one launch (the one-launch forward). 30 calls on different inputs
-    issued back to back with no synchronisation (sync-after-launch off): a
-    barrier counter not emptied, or partials read before they were visible,
-    would show in a later call's statistics."""
+    inside one launch (the one-launch forward: 4 workgroups a channel at
+    [16,24,1024], 2 register-resident ones at config 2's shape). Calls on
+    different inputs issued back to back with no synchronisation
+    (sync-after-launch off): a barrier counter not emptied, or partials read
+    before they were visible, would show in a later call's statistics."""
     from darknet_zig_amd import _lib
 
     lib = _lib.load()
     before = lib.dkz_get_sync_after_launch()
     lib.dkz_set_sync_after_launch(0)
     try:
-        B, F, S = 16, 24, 1024  # 16384 elements a channel: 4 workgroups per channel
+        B, F, S = shape
         n = B * F * S
         r = rng(123)
-        rounds = 30
         xs = [normal(r, n, 0.3 * k, 1.0 + 0.1 * k) for k in range(rounds)]
         scales, biases = uniform(r, F, 0.5, 1.5), normal(r, F, 0, 0.1)
         d_s, d_b = up(scales), up(biases)
