@@ -328,6 +328,8 @@ int dkz_copy(int n, const float *x, float *y) {
     if (n == 0) return 0;
     DKZ_REQUIRE(x != nullptr && y != nullptr);
     Streams<1, 1> s{{x}, {y}};
+    if ((uint64_t)n * sizeof(float) < DKZ_COPY_SMALL_BYTES)
+        return run_ew<DKZ_HINT_COPY_SMALL>("copy", CopyOp{}, s, n);
     return run_ew<DKZ_HINT_COPY>("copy", CopyOp{}, s, n);
 }
 
