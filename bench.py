@@ -117,6 +117,10 @@ class Hip:
         assert self.lib.hipEventCreate(C.byref(e)) == 0
         return e
 
+    def destroy(self, *events) -> None:
+        for e in events:
+            self.lib.hipEventDestroy(e)
+
     def record(self, e, stream) -> None:
         assert self.lib.hipEventRecord(e, stream) == 0
 
@@ -263,6 +267,7 @@ def time_chain(hip, stream, chains, steps, warmup):
     hip.record(b, stream)
     ms = hip.ms(a, b)
     hip.sync()
+    hip.destroy(a, b)
     return ms
 
 
@@ -282,6 +287,7 @@ def time_chain_per_kernel(hip, stream, chains, steps):
     per = [[] for _ in range(nops)]
     for j, (a, b) in enumerate(evs):
         per[j % nops].append(hip.ms(a, b))
+    hip.destroy(*(e for pair in evs for e in pair))
     return [statistics.mean(p) for p in per]
 
 
@@ -299,6 +305,7 @@ def time_seq(hip, stream, seqs, steps, warmup=3):
     hip.record(b, stream)
     ms = hip.ms(a, b)
     hip.sync()
+    hip.destroy(a, b)
     return ms / steps
 
 
@@ -313,16 +320,19 @@ def time_op(hip, stream, fns, launches, warmup=3):
         fns[k % len(fns)]()
         hip.record(evs[k][1], stream)
     hip.sync()
-    return statistics.mean(hip.ms(a, b) for a, b in evs)
+    ms = statistics.mean(hip.ms(a, b) for a, b in evs)
+    hip.destroy(*(e for pair in evs for e in pair))
+    return ms
 
 
-def time_graph(hip, seqs, launches, warmup=1):
-    """Mean time (ms) of one pass of an op sequence, cycling over rotated
-    sets, with `launches` passes captured into one HIP graph and replayed:
-    the kernels run back to back on the GPU as in a stream of such calls, and
-    the host's per-call issue time (ctypes, ~3 us a call) is not in the
-    figure. The library is pointed at the capture stream for the capture
-    and back at the null stream afterwards."""
+def time_graph(hip, seqs, launches, warmup=1, replays=5):
+    """Time (ms) of one pass of an op sequence, cycling over rotated sets,
+    with `launches` passes captured into one HIP graph: the median over
+    `replays` timed replays of the graph's mean per pass. The kernels run
+    back to back on the GPU as in a stream of such calls, and the host's
+    per-call issue time (ctypes, ~3 us a call) is not in the figure. The
+    library is pointed at the capture stream for the capture and back at the
+    null stream afterwards."""
     from darknet_zig_amd import _lib
 
     lib = _lib.load()
@@ -346,16 +356,21 @@ def time_graph(hip, seqs, launches, warmup=1):
         for _ in range(warmup):
             assert hip.lib.hipGraphLaunch(exe, s) == 0
         assert hip.lib.hipStreamSynchronize(s) == 0
+        times = []
         a, b = hip.event(), hip.event()
-        hip.record(a, s)
-        assert hip.lib.hipGraphLaunch(exe, s) == 0
-        hip.record(b, s)
-        ms = hip.ms(a, b)
-        assert hip.lib.hipStreamSynchronize(s) == 0
+        try:
+            for _ in range(replays):
+                hip.record(a, s)
+                assert hip.lib.hipGraphLaunch(exe, s) == 0
+                hip.record(b, s)
+                times.append(hip.ms(a, b))
+                assert hip.lib.hipStreamSynchronize(s) == 0
+        finally:
+            hip.destroy(a, b)
     finally:
         hip.lib.hipGraphExecDestroy(exe)
         hip.lib.hipGraphDestroy(graph)
-    return ms / launches
+    return statistics.median(times) / launches
 
 
 def gbs(nbytes: int, ms: float) -> float:
