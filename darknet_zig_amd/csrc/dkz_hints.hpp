@@ -136,8 +136,11 @@
 #ifndef DKZ_HINT_SOFTMAX
 #define DKZ_HINT_SOFTMAX 2
 #endif
+// The fused layer pass also reads the logits and the truth nontemporally
+// (each read once): [256,1000] 4.06 -> 3.82 us; the plain softmax keeps its
+// cached input load ([8192,1000] 12.6 against 12.8-13.0 us with it NT).
 #ifndef DKZ_HINT_SOFTMAX_XENT
-#define DKZ_HINT_SOFTMAX_XENT 10
+#define DKZ_HINT_SOFTMAX_XENT 15
 #endif
 // pooling.hip forward: bit 0 = input load, bit 1 = output store, bit 2 = index store
 #ifndef DKZ_HINT_MAXPOOL_FWD
