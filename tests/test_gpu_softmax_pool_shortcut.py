@@ -314,6 +314,12 @@ SHORTCUT_CASES = [
     (2, 7, 7, 6, 14, 14, 3, 1.0, -0.75),      # upsample: sample 2
     (2, 9, 9, 5, 4, 4, 5, 0.9, 1.1),          # w1/w2 = 2 with remainder
     (1, 5, 5, 3, 5, 5, 9, 2.0, 1.0),          # channel mismatch only
+    # the stride-2 pair path: pair counts off the 1024-pair workgroup tile,
+    # add with more channels than out, heights that do not halve exactly
+    (3, 16, 16, 8, 8, 8, 8, 0.5, 2.0),        # 768 pairs: one partial tile
+    (5, 12, 11, 7, 6, 5, 3, -1.0, 0.25),      # minc = c2, h1 = 2*h2 + 1
+    (7, 28, 28, 33, 14, 14, 40, 1.0, 1.0),    # 22638 pairs, ragged last tile
+    (1, 4, 4, 1, 2, 2, 1, 1.0, 1.0),          # a single pair
 ]
 
 
