@@ -560,13 +560,17 @@ uint32_t ref_hash_u32(uint32_t x) {
 }
 
 /* darknet_kernels.hip:177-183 (rand_uniform_kernel, gpu.zig:511 randUniform):
- * element i = top 24 bits of hash(seed ^ hash(i)) times 2^-24, in [0, 1). */
-void ref_rand_uniform(float *x, size_t n, uint32_t seed) {
+ * element i = top 24 bits of hash(seed ^ hash(i)) times 2^-24, in [0, 1).
+ * ref_rand_uniform_from writes elements first .. first+n-1 of that sequence
+ * (a window of a large buffer); ref_rand_uniform is the window at 0. */
+void ref_rand_uniform_from(float *x, size_t n, uint32_t seed, size_t first) {
     for (size_t i = 0; i < n; ++i) {
-        const uint32_t h = ref_hash_u32(seed ^ ref_hash_u32((uint32_t)i));
+        const uint32_t h = ref_hash_u32(seed ^ ref_hash_u32((uint32_t)(first + i)));
         x[i] = (float)(h >> 8) * (1.0f / 16777216.0f);
     }
 }
+
+void ref_rand_uniform(float *x, size_t n, uint32_t seed) { ref_rand_uniform_from(x, n, seed, 0); }
 
 /* layers/misc.zig:105-127 (forwardDropout's mask step given the uniform
  * draws, and backwardDropout): a draw below `prob` zeroes the element,

@@ -89,6 +89,7 @@ void ref_backward_avgpool(size_t batch, size_t w, size_t h, size_t c, const floa
 void ref_add_scalar(float alpha, float *x, size_t n);
 uint32_t ref_hash_u32(uint32_t x);
 void ref_rand_uniform(float *x, size_t n, uint32_t seed);
+void ref_rand_uniform_from(float *x, size_t n, uint32_t seed, size_t first);
 void ref_dropout(float *x, size_t n, const float *rand, float prob, float scale);
 void ref_adam_update(float *w, float *d, float *m, float *v, float b1, float b2, float eps,
                      float decay, float rate, size_t n, size_t batch, size_t t);

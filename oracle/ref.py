@@ -58,6 +58,7 @@ _SIGS = {
     "ref_add_scalar": (None, [_f, _P, _sz]),
     "ref_hash_u32": (C.c_uint32, [C.c_uint32]),
     "ref_rand_uniform": (None, [_P, _sz, C.c_uint32]),
+    "ref_rand_uniform_from": (None, [_P, _sz, C.c_uint32, _sz]),
     "ref_dropout": (None, [_P, _sz, _P, _f, _f]),
     "ref_adam_update": (None, [_P, _P, _P, _P, _f, _f, _f, _f, _f, _sz, _sz, _sz]),
     "ref_conv_out_dim": (_sz, [_sz, _sz, _sz, _sz]),
@@ -248,8 +249,12 @@ def hash_u32(x: int) -> int:
     return lib().ref_hash_u32(x & 0xFFFFFFFF)
 
 
-def randUniform(x: np.ndarray, seed: int) -> None:
-    lib().ref_rand_uniform(_ptr(x), x.size, seed & 0xFFFFFFFF)
+def randUniform(x: np.ndarray, seed: int, first: int = 0) -> None:
+    """x = elements first .. first + x.size - 1 of the seed's sequence."""
+    if first == 0:
+        lib().ref_rand_uniform(_ptr(x), x.size, seed & 0xFFFFFFFF)
+    else:
+        lib().ref_rand_uniform_from(_ptr(x), x.size, seed & 0xFFFFFFFF, first)
 
 
 def dropout(x: np.ndarray, rand: np.ndarray, prob: float, scale: float) -> None:

@@ -144,6 +144,14 @@ P = C.c_void_p(16)  # a non-null pointer value; never dereferenced in these call
         (lambda L: L.dkz_col2im(P, 3, 4, -4, 3, 1, 1, P), INVALID),
         (lambda L: L.dkz_col2im(P, 3, 4, 4, 3, 1, 1, None), INVALID),
         (lambda L: L.dkz_col2im(P, 65536, 256, 256, 3, 1, 1, P), INVALID),  # beyond 32-bit indexing
+        # shapes whose element count passes 2^31 - 1 (each argument fits an int)
+        (lambda L: L.dkz_mean(P, 65536, 65536, 1, P), INVALID),
+        (lambda L: L.dkz_backward_bias(P, P, 46341, 46341, 1), INVALID),
+        (lambda L: L.dkz_add_bias(P, P, 46341, 46341, 1), INVALID),
+        (lambda L: L.dkz_softmax(P, 1000, 2147484, 1000, 1, 1000, 1, 1.0, P), INVALID),  # last row ends past 2^31
+        (lambda L: L.dkz_forward_maxpool(1 << 29, 256, 256, 32768, 2, 2, 0, P, P, P), INVALID),  # 2^31 inputs
+        (lambda L: L.dkz_forward_avgpool(32768, 256, 256, 1, P, P), INVALID),
+        (lambda L: L.dkz_backward_avgpool(32768, 256, 256, 1, P, P), INVALID),
         (lambda L: L.dkz_gemm(0, 0, 0, 5, 5, 1.0, None, 5, None, 5, 0.0, None, 5), 0),  # m == 0
         (lambda L: L.dkz_gemm(0, 0, 4, 5, 3, 1.0, P, 2, P, 5, 0.0, P, 5), INVALID),  # lda < k
         (lambda L: L.dkz_gemm(1, 0, 4, 5, 3, 1.0, P, 3, P, 5, 0.0, P, 5), INVALID),  # lda < m (A transposed)

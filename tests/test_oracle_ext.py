@@ -112,6 +112,19 @@ def test_rand_uniform_distribution_and_prefix():
     assert np.mean(z == y) < 0.01
 
 
+def test_rand_uniform_window():
+    """A window starting at element `first` (how the maximum-size GPU tests
+    check the top of a 2^31-element buffer) is that slice of the whole
+    sequence, including one that crosses 2^24 (where a float index would
+    stop being exact)."""
+    full = np.empty((1 << 24) + 4096, f32)
+    ref.randUniform(full, 11)
+    for first, n in ((0, 100), (1, 4096), (9000, 1007), (5003, 1), ((1 << 24) - 2048, 4096)):
+        w = np.empty(n, f32)
+        ref.randUniform(w, 11, first)
+        np.testing.assert_array_equal(w, full[first:first + n])
+
+
 # ---------------------------------------------------------------------------
 # dropout (misc.zig:105-127)
 # ---------------------------------------------------------------------------
