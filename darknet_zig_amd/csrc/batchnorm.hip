@@ -403,19 +403,32 @@ __device__ __forceinline__ Sums<NS> wave_partials_coherent(const double *partial
     return r;
 }
 
-// Chunk of kCoopU float4s a lane: a workgroup owns at most kCoopChunk
-// elements of one channel. Measured at config 1 (cold / Infinity-Cache
-// resident): 4 float4s 17.6 / 13.3 us, 8 16.3 / 12.9, 16 18.0 / 15.6.
+// Workgroups of kCoopBS threads holding kCoopU float4s a lane: a workgroup
+// owns at most kCoopBS * 4 * kCoopU elements of one channel. Measured at
+// config 1 (graph replay, cold): 1024 x 4 (8 workgroups a channel, one a
+// CU) 15.2-15.3 us; 256 x 8 16.2-16.4; 512 x 4 / 512 x 8 15.5-15.7;
+// 1024 x 2 / x 3 / x 6 / x 8 15.8 / 17.7 / 16.3 / 17.6; 128 x 16 18.4;
+// 256 x 4 / x 16 17.6 / 18.0. Shapes whose grid at 1024 x 4 does not fit
+// the GPU at once try 256 x 8 (smaller workgroups fit more of them).
 // x, the input's copy, is stored as soon as it is loaded (x after the
-// barrier with the other two outputs: 16.4 / 13.3 us).
-#ifndef DKZ_BN_COOP_U
-#define DKZ_BN_COOP_U 8
+// barrier with the other two outputs: 16.4 against 16.3 us at 256 x 8).
+#ifndef DKZ_BN_COOP_BS
+#define DKZ_BN_COOP_BS 1024
 #endif
-constexpr int kCoopU = DKZ_BN_COOP_U;
+#ifndef DKZ_BN_COOP_U
+#define DKZ_BN_COOP_U 4
+#endif
+#ifndef DKZ_BN_COOP_BS2
+#define DKZ_BN_COOP_BS2 256
+#endif
+#ifndef DKZ_BN_COOP_U2
+#define DKZ_BN_COOP_U2 8
+#endif
+constexpr int kCoopBS = DKZ_BN_COOP_BS, kCoopU = DKZ_BN_COOP_U;
+constexpr int kCoopBS2 = DKZ_BN_COOP_BS2, kCoopU2 = DKZ_BN_COOP_U2;
 #ifndef DKZ_BN_COOP_X_LATE
 #define DKZ_BN_COOP_X_LATE 0
 #endif
-constexpr uint32_t kCoopChunk = kBlock * 4 * kCoopU;
 // The register-resident variant: 512 threads (two waves a SIMD, up to 256
 // registers a lane) holding 49 float4s a lane, so one workgroup a CU covers
 // 100352 elements (half of a config-2 channel).
@@ -429,7 +442,7 @@ constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 // workgroup k == 0, the rolling averages) exactly as the split statistics
 // path does, and writes x, x_norm and the output from the registers. The
 // input is read once: 16 bytes an element instead of 20. BS threads a
-// workgroup, U float4s a lane: (kBlock, kCoopU) for small tensors, and
+// workgroup, U float4s a lane: (kCoopBS, kCoopU) for small tensors, and
 // (kRegBlock, kRegU) -- one 512-thread workgroup a CU, 196 floats a lane --
 // for tensors that fill the register file (config 2's 103 MB over 256 CUs).
 template <int A, int H, int BS, int U>
@@ -786,13 +799,11 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, flo
 
 // ---- host ---------------------------------------------------------------------
 
-// The one-launch forward for channels of up to kCoopMaxChan elements (a
-// channel's workgroups must fit the GPU at once: 256 per channel at most,
-// each with a quarter of a CU's wave slots).
+// The one-launch forward, for channels split over at most 256 workgroups
+// (a channel's workgroups must fit the GPU at once).
 #ifndef DKZ_BN_FWD_COOP
 #define DKZ_BN_FWD_COOP 1
 #endif
-constexpr uint64_t kCoopMaxChan = 256ull * kCoopChunk;
 // ... and at most this many workgroups in all (and no more than the GPU
 // holds at once, resident_workgroups), so that the whole grid is resident at
 // once (otherwise workgroups waiting at their barrier hold CUs that later
@@ -901,6 +912,35 @@ int run_sums(const char *name, const RedGeom &g, const Shape &sh, const Fin &fin
                   (const double *)sc.partials, sh.F, g.K);
 }
 
+// The one-launch forward with BS-thread workgroups holding U float4s a
+// lane, when its whole grid fits the GPU at once (and, for CHECK_SPILLS,
+// when the kernel keeps its chunk in registers): launches it and returns
+// true with its status in *rc; otherwise returns false, launching nothing.
+template <int A, int BS, int U, bool CHECK_SPILLS>
+bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
+    constexpr auto kernel = bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, BS, U>;
+    constexpr uint64_t chunk = (uint64_t)BS * 4 * U;
+    const Shape &sh = a.sh;
+    const uint64_t K = div_up(L, chunk), wgs = (uint64_t)sh.F * K;
+    if (K > 256 || sh.F > kScratchSlots / kCounterStride || wgs > DKZ_BN_COOP_MAX_WGS ||
+        2ull * wgs * kPartialStride > kScratchPartials)
+        return false;
+    if constexpr (CHECK_SPILLS) {
+        if (!no_spills<kernel>()) return false;
+    }
+    if (wgs > resident_workgroups<kernel, BS>()) return false;
+    const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
+    Scratch sc{nullptr};
+    *rc = device_scratch(&sc);
+    if (*rc != 0) return true;
+    const FwdFin fin{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
+                     (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
+    const FwdParams p{a.mean, a.variance, a.scales, a.biases};
+    *rc = launch("batchnorm_forward", kernel, dim3(sh.F * gc.K), dim3(BS), a.input, a.output, a.x, a.x_norm, p, gc,
+                 fin, sc.partials, sc.slots);
+    return true;
+}
+
 template <int A>
 int bn_forward_fused(const FwdArgs &a) {
     constexpr int H = DKZ_HINT_BN_FWD_APPLY;
@@ -920,40 +960,13 @@ int bn_forward_fused(const FwdArgs &a) {
         return launch("batchnorm_forward_apply", bn_fwd_apply_kernel<A, false, H, false>, grid, block, a.input,
                       a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
     }
-    if (DKZ_BN_FWD_COOP && L <= kCoopMaxChan && sh.F <= kScratchSlots / kCounterStride &&
-        (uint64_t)sh.F * div_up(L, kCoopChunk) <= DKZ_BN_COOP_MAX_WGS &&
-        2ull * sh.F * div_up(L, kCoopChunk) * kPartialStride <= kScratchPartials &&
-        (uint64_t)sh.F * div_up(L, kCoopChunk) <=
-            resident_workgroups<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kBlock, kCoopU>, kBlock>()) {
-        // one launch: chunks of at most kCoopChunk elements, whole float4s
-        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, div_up(L, kCoopChunk), true);
-        Scratch scc{nullptr};
-        DKZ_TRY(device_scratch(&scc));
-        const FwdFin finc{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
-                          (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
-        const FwdParams p{a.mean, a.variance, a.scales, a.biases};
-        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kBlock, kCoopU>,
-                      dim3(sh.F * gc.K), dim3(kBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc, scc.partials,
-                      scc.slots);
-    }
+    int rc = 0;
+    if (DKZ_BN_FWD_COOP && (fwd_coop<A, kCoopBS, kCoopU, false>(a, L, &rc) ||
+                            fwd_coop<A, kCoopBS2, kCoopU2, false>(a, L, &rc)))
+        return rc;
     // the same with one 512-thread workgroup a CU holding 196 floats a lane,
     // for tensors that fill the register file
-    const uint64_t kr = div_up(L, kRegChunk);
-    if (DKZ_BN_FWD_COOP_REG && sh.F <= kScratchSlots / kCounterStride &&
-        2ull * sh.F * kr * kPartialStride <= kScratchPartials &&
-        no_spills<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>>() &&
-        (uint64_t)sh.F * kr <= resident_workgroups<bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>,
-                                                   kRegBlock>()) {
-        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)kr, true);
-        Scratch scc{nullptr};
-        DKZ_TRY(device_scratch(&scc));
-        const FwdFin finc{nullptr, a.mean, a.variance, a.rolling_mean, a.rolling_variance,
-                          (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
-        const FwdParams p{a.mean, a.variance, a.scales, a.biases};
-        return launch("batchnorm_forward", bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, kRegBlock, kRegU>,
-                      dim3(sh.F * gc.K), dim3(kRegBlock), a.input, a.output, a.x, a.x_norm, p, gc, finc,
-                      scc.partials, scc.slots);
-    }
+    if (DKZ_BN_FWD_COOP_REG && fwd_coop<A, kRegBlock, kRegU, true>(a, L, &rc)) return rc;
     const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;
     DKZ_TRY(run_sums<2>("batchnorm_forward_stats", g, sh, fin, defer, &partials,

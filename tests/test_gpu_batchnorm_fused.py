@@ -34,6 +34,7 @@ FAST = [
     (16, 5, 600),     # split; an apply tile spans up to 8 rows, channels repeat within it
     (8, 6, 1536),     # split; apply tiles finalise their own channels
     (128, 32, 1024),  # benchmark config 1
+    (8, 700, 1024),   # 700 channels: more 1024-thread workgroups than fit at once, so 256-thread ones
 ]
 FALLBACK = [
     (4, 17, 53),      # gputest's shape: spatial % 4 != 0
