@@ -116,10 +116,10 @@ __global__ __launch_bounds__(BS) void chan_reduce_kernel(T t, Fin fin, const flo
 // writes back and invalidates the whole L2 of the XCD. Nothing waits on
 // another workgroup, so any grid size is safe, and the sum's order is fixed
 // by the shape alone (deterministic).
-template <class T, class Fin, bool TWO, bool VEC, int H>
-__global__ __launch_bounds__(kBlock) void chan_split_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
-                                                            double *partials, uint64_t *counters) {
-    __shared__ double lds[kBlock / kWave];
+template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
+__global__ __launch_bounds__(BS) void chan_split_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
+                                                        double *partials, uint64_t *counters) {
+    __shared__ double lds[BS / kWave];
     __shared__ uint32_t last_sh;
     uint32_t f, k;
     if constexpr (DKZ_CHAN_KMAJOR != 0) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kBlock) void chan_split_kernel(T t, Fin fin, const 
         k = blockIdx.x - f * g.K;
     }
     const uint32_t slot = f * g.K + k;
-    const double total = chunk_sum<T, TWO, VEC, H, kBlock>(t, p0, p1, g, f, k, lds);
+    const double total = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, f, k, lds);
     if (threadIdx.x == 0) {
         __hip_atomic_store(&partials[(uint64_t)slot * kPartialStride], total, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -211,6 +211,13 @@ __global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float
 #ifndef DKZ_CHAN_MIN_CHUNK
 #define DKZ_CHAN_MIN_CHUNK 2048
 #endif
+// Threads a split workgroup. Measured at config 1 (mean / variance, graph
+// replay, cold): 256 threads with ~1024 workgroups 5.96 / 5.98 us; 512 x 512
+// 6.10 / 6.17, 512 x 256 6.23 / 6.35, 1024 x 256 6.45 / 6.40, 1024 x 512
+// 6.56 / 6.68, 256 x 256 7.00 / 7.13.
+#ifndef DKZ_CHAN_SPLIT_BS
+#define DKZ_CHAN_SPLIT_BS 256
+#endif
 // K > 1 only when filters < DKZ_CHAN_TARGET_WGS, so a padded counter per
 // channel always fits the scratch's slots.
 static_assert((uint64_t)DKZ_CHAN_TARGET_WGS * DKZ_SPLIT_CSTRIDE <= kScratchSlots, "one counter per split channel");
@@ -255,13 +262,14 @@ int run_chan_reduce(const char *name, const T &t, const Fin &fin, const float *p
         if (vec) return launch(name, chan_reduce_kernel<T, Fin, TWO, true, H, kBlock>, dim3(F), block, t, fin, p0, p1, g);
         return launch(name, chan_reduce_kernel<T, Fin, TWO, false, H, kBlock>, dim3(F), block, t, fin, p0, p1, g);
     }
-    const dim3 block(kBlock);
+    constexpr int BS = DKZ_CHAN_SPLIT_BS;
+    const dim3 block(BS);
     Scratch sc{nullptr};
     DKZ_TRY(device_scratch(&sc));
     if (vec)
-        return launch(name, chan_split_kernel<T, Fin, TWO, true, H>, dim3(F * K), block, t, fin, p0, p1, g,
+        return launch(name, chan_split_kernel<T, Fin, TWO, true, H, BS>, dim3(F * K), block, t, fin, p0, p1, g,
                       sc.partials, sc.slots);
-    return launch(name, chan_split_kernel<T, Fin, TWO, false, H>, dim3(F * K), block, t, fin, p0, p1, g,
+    return launch(name, chan_split_kernel<T, Fin, TWO, false, H, BS>, dim3(F * K), block, t, fin, p0, p1, g,
                   sc.partials, sc.slots);
 }
 
