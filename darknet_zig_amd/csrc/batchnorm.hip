@@ -713,20 +713,34 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 // (workgroup k == 0 writing the updates, mean_delta and variance_delta) and
 // writes normalize_delta's result from the y, delta and x it holds: 20 bytes
 // an element instead of 32.
+// BS threads a workgroup, U float4s of each input a lane. Measured at
+// config 1's shape (graph replay, cold): 1024 x 4 (8 workgroups a channel,
+// one a CU) 20.0 us; 512 x 4 20.4; 256 x 8 21.2; 256 x 4 22.3; 1024 x 2 and
+// 512 x 2 (grids that do not fit at once: two passes) 27.5. Shapes whose grid
+// at 1024 x 4 does not fit the GPU at once try 256 x 4.
+#ifndef DKZ_BN_BWD_COOP_BS
+#define DKZ_BN_BWD_COOP_BS 1024
+#endif
 #ifndef DKZ_BN_BWD_COOP_U
 #define DKZ_BN_BWD_COOP_U 4
 #endif
-constexpr int kBwdCoopU = DKZ_BN_BWD_COOP_U;
-constexpr uint32_t kBwdCoopChunk = kBlock * 4 * kBwdCoopU;
+#ifndef DKZ_BN_BWD_COOP_BS2
+#define DKZ_BN_BWD_COOP_BS2 256
+#endif
+#ifndef DKZ_BN_BWD_COOP_U2
+#define DKZ_BN_BWD_COOP_U2 4
+#endif
+constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
+constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2;
 
-template <int A, int H>
-__global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, float *delta, const float *x_norm,
-                                                             const float *x, BwdParams p, RedGeom g, BwdFin fin,
-                                                             double *partials, uint64_t *slots) {
+template <int A, int H, int BS, int U>
+__global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *delta, const float *x_norm,
+                                                         const float *x, BwdParams p, RedGeom g, BwdFin fin,
+                                                         double *partials, uint64_t *slots) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtX = (H & 8) != 0;
     constexpr bool kNtOut = (H & 16) != 0;
-    __shared__ double lds[4 * (kBlock / kWave)];
+    __shared__ double lds[4 * (BS / kWave)];
     __shared__ BwdChan chan_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
@@ -738,14 +752,14 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, flo
     // Held through the barrier: d2 = delta * gradient(y) * scale and x - mean,
     // the two terms normalize_delta needs besides per-channel values, each
     // formed exactly as bwd_elem forms it.
-    float4 d2[kBwdCoopU], xm[kBwdCoopU];
-    uint32_t at[kBwdCoopU];
+    float4 d2[U], xm[U];
+    uint32_t at[U];
     double a[4] = {0.0, 0.0, 0.0, 0.0};
     {
-        float4 vy[kBwdCoopU], vd[kBwdCoopU], vx[kBwdCoopU], vn[kBwdCoopU];
+        float4 vy[U], vd[U], vx[U], vn[U];
 #pragma unroll
-        for (int u = 0; u < kBwdCoopU; ++u) {
-            const uint32_t j = j0 + 4 * threadIdx.x + (uint32_t)u * (4 * kBlock);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = j0 + 4 * threadIdx.x + (uint32_t)u * (4 * BS);
             at[u] = j < j1 ? chan_addr(fbase, j, g) >> 2 : 0xffffffffu;
             if (j < j1) {
                 vd[u] = ld4<kNtD>(delta, at[u]);
@@ -756,7 +770,7 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, flo
             }
         }
 #pragma unroll
-        for (int u = 0; u < kBwdCoopU; ++u) {
+        for (int u = 0; u < U; ++u) {
             if (at[u] == 0xffffffffu) continue;
             acc_bwd<A>(vy[u], vd[u], vn[u], vx[u], m, gam, a);
 #pragma unroll
@@ -766,7 +780,7 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, flo
             }
         }
     }
-    const Sums<4> r = block_sums<4, kBlock>(a, lds);
+    const Sums<4> r = block_sums<4, BS>(a, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -787,7 +801,7 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_coop_kernel(const float *y, flo
     __syncthreads();
     const BwdChan ch = chan_sh;
 #pragma unroll
-    for (int u = 0; u < kBwdCoopU; ++u) {
+    for (int u = 0; u < U; ++u) {
         if (at[u] == 0xffffffffu) continue;
         float4 o;
 #pragma unroll
@@ -981,24 +995,39 @@ int bn_forward_fused(const FwdArgs &a) {
                   a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
 }
 
+// The one-launch backward with BS-thread workgroups holding U float4s of
+// each input a lane, when its whole grid fits the GPU at once: launches it
+// and returns true with its status in *rc; otherwise returns false,
+// launching nothing.
+template <int A, int BS, int U>
+bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
+    constexpr auto kernel = bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP, BS, U>;
+    const Shape &sh = a.sh;
+    const uint64_t K = div_up(L, (uint64_t)BS * 4 * U), wgs = (uint64_t)sh.F * K;
+    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
+        4ull * wgs * kPartialStride > kScratchPartials || wgs > resident_workgroups<kernel, BS>())
+        return false;
+    const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
+    Scratch sc{nullptr};
+    *rc = device_scratch(&sc);
+    if (*rc != 0) return true;
+    const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
+                      (float)((uint64_t)sh.S * (uint64_t)sh.B)};
+    *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(BS), a.y, a.delta, a.x_norm, a.x, p, gc, fin,
+                 sc.partials, sc.slots);
+    return true;
+}
+
 template <int A>
 int bn_backward_fused(const BwdArgs &a) {
     constexpr int H = DKZ_HINT_BN_BWD_APPLY;
     const Shape &sh = a.sh;
     const BwdFin fin{a.variance, a.bias_updates, a.scale_updates, a.mean_delta, a.variance_delta};
     const uint64_t L = (uint64_t)sh.B * sh.S;
-    const uint64_t kb = div_up(L, kBwdCoopChunk);
-    if (DKZ_BN_BWD_COOP && kb <= 256 && (uint64_t)sh.F * kb <= DKZ_BN_COOP_MAX_WGS &&
-        sh.F <= kScratchSlots / kCounterStride && 4ull * sh.F * kb * kPartialStride <= kScratchPartials &&
-        (uint64_t)sh.F * kb <= resident_workgroups<bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>, kBlock>()) {
-        const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)kb, true);
-        Scratch scc{nullptr};
-        DKZ_TRY(device_scratch(&scc));
-        const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
-                          (float)((uint64_t)sh.S * (uint64_t)sh.B)};
-        return launch("batchnorm_backward", bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP>, dim3(sh.F * gc.K),
-                      dim3(kBlock), a.y, a.delta, a.x_norm, a.x, p, gc, fin, scc.partials, scc.slots);
-    }
+    int rc = 0;
+    if (DKZ_BN_BWD_COOP && (bwd_coop<A, kBwdCoopBS, kBwdCoopU>(a, L, fin, &rc) ||
+                            bwd_coop<A, kBwdCoopBS2, kBwdCoopU2>(a, L, fin, &rc)))
+        return rc;
     const RedGeom g = sums_geom<4>(sh, A == kLinear ? 3 : 4);
     const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;

@@ -35,6 +35,7 @@ FAST = [
     (8, 6, 1536),     # split; apply tiles finalise their own channels
     (128, 32, 1024),  # benchmark config 1
     (8, 700, 1024),   # 700 channels: more 1024-thread workgroups than fit at once, so 256-thread ones
+    (4, 300, 1024),   # 300 one-workgroup channels: the backward's 1024-thread grid does not fit, 256 does
 ]
 FALLBACK = [
     (4, 17, 53),      # gputest's shape: spatial % 4 != 0
