@@ -25,6 +25,14 @@ namespace {
 #ifndef DKZ_BCAST_UNROLL_SMALL
 #define DKZ_BCAST_UNROLL_SMALL 4
 #endif
+// Threads a workgroup below the large-tensor threshold. Measured at config 1
+// (graph replay, cold): 512 threads took normalize / scale_bias / add_bias /
+// leaky 2-3% faster but the copy 3% slower and config 3's softmax_x_ent
+// 2.9 -> 3.5 us (half the workgroups); 1024 threads lost 3-8% on all and
+// doubled softmax_x_ent. 256 stays.
+#ifndef DKZ_BCAST_BS_SMALL
+#define DKZ_BCAST_BS_SMALL 256
+#endif
 #ifndef DKZ_BCAST_LARGE_FLOAT4S
 #define DKZ_BCAST_LARGE_FLOAT4S (1u << 22)  // 16 Mi elements
 #endif
@@ -49,26 +57,25 @@ __device__ __forceinline__ float4 bcast_vec(const Op &op, uint32_t v, float4 io,
 }
 
 // H: bit 0 = nontemporal io loads, bit 1 = io stores, bit 2 = loads of a.
-template <class Op, bool TWO, bool ROWWISE, bool S4, int H, int kUnroll>
-__global__ __launch_bounds__(kBlock) void bcast_vec_kernel(Op op, float *io, const float *a, ChanGeom g,
-                                                           uint32_t n) {
+template <class Op, bool TWO, bool ROWWISE, bool S4, int H, int kUnroll, int BS = kBlock>
+__global__ __launch_bounds__(BS) void bcast_vec_kernel(Op op, float *io, const float *a, ChanGeom g, uint32_t n) {
     constexpr bool kNtIo = (H & 1) != 0, kNtOut = (H & 2) != 0, kNtA = (H & 4) != 0;
     const uint32_t nv = n >> 2;
-    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
-    if (base + (kUnroll - 1) * kBlock < nv) {
+    const uint32_t base = blockIdx.x * (BS * kUnroll) + threadIdx.x;
+    if (base + (kUnroll - 1) * BS < nv) {
         float4 x[kUnroll], y[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            x[u] = ld4<kNtIo>(io, base + u * kBlock);
-            if constexpr (TWO) y[u] = ld4<kNtA>(a, base + u * kBlock);
+            x[u] = ld4<kNtIo>(io, base + u * BS);
+            if constexpr (TWO) y[u] = ld4<kNtA>(a, base + u * BS);
             else y[u] = x[u];
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
-            st4<kNtOut>(io, base + u * kBlock, bcast_vec<Op, TWO, ROWWISE, S4>(op, base + u * kBlock, x[u], y[u], g));
+            st4<kNtOut>(io, base + u * BS, bcast_vec<Op, TWO, ROWWISE, S4>(op, base + u * BS, x[u], y[u], g));
     } else {
         for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t v = base + u * kBlock;
+            const uint32_t v = base + u * BS;
             if (v < nv) {
                 const float4 x = ld4<kNtIo>(io, v);
                 const float4 y = TWO ? ld4<kNtA>(a, v) : x;
@@ -101,20 +108,21 @@ int run_bcast(const char *name, const Op &op, float *io, const float *a, int bat
     if (aligned16(io) && (!TWO || aligned16(a))) {
         const uint32_t nv = n >> 2;
         const bool large = nv >= DKZ_BCAST_LARGE_FLOAT4S;
-        const uint32_t u = large ? DKZ_BCAST_UNROLL_LARGE : DKZ_BCAST_UNROLL_SMALL;
-        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * u);
-        if (spatial % 4 == 0) {
-            if (large)
-                return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, DKZ_BCAST_UNROLL_LARGE>, dim3(grid),
-                              dim3(kBlock), op, io, a, g, n);
-            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, DKZ_BCAST_UNROLL_SMALL>, dim3(grid),
-                          dim3(kBlock), op, io, a, g, n);
+        constexpr int kU = DKZ_BCAST_UNROLL_LARGE, kUs = DKZ_BCAST_UNROLL_SMALL, kBs = DKZ_BCAST_BS_SMALL;
+        if (large) {
+            const dim3 grid(div_up(nv, (uint64_t)kBlock * kU));
+            if (spatial % 4 == 0)
+                return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, kU>, grid, dim3(kBlock), op, io, a,
+                              g, n);
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, kU>, grid, dim3(kBlock), op, io, a, g,
+                          n);
         }
-        if (large)
-            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, DKZ_BCAST_UNROLL_LARGE>, dim3(grid),
-                          dim3(kBlock), op, io, a, g, n);
-        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, DKZ_BCAST_UNROLL_SMALL>, dim3(grid),
-                      dim3(kBlock), op, io, a, g, n);
+        const dim3 grid(nv == 0 ? 1u : div_up(nv, (uint64_t)kBs * kUs));
+        if (spatial % 4 == 0)
+            return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, true, H, kUs, kBs>, grid, dim3(kBs), op, io, a, g,
+                          n);
+        return launch(name, bcast_vec_kernel<Op, TWO, ROWWISE, false, H, kUs, kBs>, grid, dim3(kBs), op, io, a, g,
+                      n);
     }
     const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
     return launch(name, bcast_scalar_kernel<Op, TWO, ROWWISE>, dim3(grid), dim3(kBlock), op, io, a, g, n);

@@ -27,6 +27,14 @@ namespace {
 #ifndef DKZ_EW_UNROLL_SMALL
 #define DKZ_EW_UNROLL_SMALL 4
 #endif
+// Threads a workgroup below the large-tensor threshold. Measured at config 1
+// (graph replay, cold): 512 threads took normalize / scale_bias / add_bias /
+// leaky 2-3% faster but the copy 3% slower and config 3's softmax_x_ent
+// 2.9 -> 3.5 us (half the workgroups); 1024 threads lost 3-8% on all and
+// doubled softmax_x_ent. 256 stays.
+#ifndef DKZ_EW_BS_SMALL
+#define DKZ_EW_BS_SMALL 256
+#endif
 #ifndef DKZ_EW_LARGE_FLOAT4S
 #define DKZ_EW_LARGE_FLOAT4S (1u << 22)  // 16 Mi elements
 #endif
@@ -74,22 +82,22 @@ __device__ __forceinline__ void apply_vec(const Op &op, const Streams<NI, NO> &s
     for (int k = 0; k < NO; ++k) st4<(H & 16) != 0>(s.out[k], v, out[k]);
 }
 
-template <int NI, int NO, int H, class Op, int kUnroll>
-__global__ __launch_bounds__(kBlock) void ew_vec_kernel(Op op, Streams<NI, NO> s, uint32_t n) {
+template <int NI, int NO, int H, class Op, int kUnroll, int BS = kBlock>
+__global__ __launch_bounds__(BS) void ew_vec_kernel(Op op, Streams<NI, NO> s, uint32_t n) {
     const uint32_t nv = n >> 2;
-    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
-    if (base + (kUnroll - 1) * kBlock < nv) {
+    const uint32_t base = blockIdx.x * (BS * kUnroll) + threadIdx.x;
+    if (base + (kUnroll - 1) * BS < nv) {
         // Whole tile in range: every load is issued before the first store.
         float4 in[kUnroll][NI > 0 ? NI : 1];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-            for (int k = 0; k < NI; ++k) in[u][k] = ld4_in<H>(k, s.in[k], base + u * kBlock);
+            for (int k = 0; k < NI; ++k) in[u][k] = ld4_in<H>(k, s.in[k], base + u * BS);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) apply_vec<NI, NO, H>(op, s, base + u * kBlock, in[u]);
+        for (int u = 0; u < kUnroll; ++u) apply_vec<NI, NO, H>(op, s, base + u * BS, in[u]);
     } else {
         for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t v = base + u * kBlock;
+            const uint32_t v = base + u * BS;
             if (v < nv) {
                 float4 in[NI > 0 ? NI : 1];
 #pragma unroll
@@ -119,8 +127,9 @@ int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
         if (nv >= DKZ_EW_LARGE_FLOAT4S)
             return launch(name, ew_vec_kernel<NI, NO, H, Op, DKZ_EW_UNROLL_LARGE>,
                           dim3(div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_LARGE)), dim3(kBlock), op, s, un);
-        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBlock * DKZ_EW_UNROLL_SMALL);
-        return launch(name, ew_vec_kernel<NI, NO, H, Op, DKZ_EW_UNROLL_SMALL>, dim3(grid), dim3(kBlock), op, s, un);
+        constexpr int kBs = DKZ_EW_BS_SMALL;
+        const uint32_t grid = nv == 0 ? 1u : div_up(nv, (uint64_t)kBs * DKZ_EW_UNROLL_SMALL);
+        return launch(name, ew_vec_kernel<NI, NO, H, Op, DKZ_EW_UNROLL_SMALL, kBs>, dim3(grid), dim3(kBs), op, s, un);
     }
     const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
     return launch(name, ew_scalar_kernel<NI, NO, Op>, dim3(grid), dim3(kBlock), op, s, un);
