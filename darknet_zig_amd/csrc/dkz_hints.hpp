@@ -164,10 +164,13 @@
 
 // batchnorm.hip, the fused layer passes. The statistics pass keeps its input
 // cached for the apply pass that re-reads it (at config 1 all of it fits the
-// Infinity Cache). The backward passes stream everything: at config 2 the
-// sums pass reads 411 MB, so nothing it caches survives to the apply pass
-// (nontemporal sums loads: 138 us per step against 146 us; walking the
-// apply tiles backwards made no difference).
+// Infinity Cache). The backward sums pass reads y and x cached -- two of the
+// three inputs the apply pass re-reads, 206 MB, within the 256 MB Infinity
+// Cache -- and delta and x_norm nontemporally; the apply pass streams. At
+// config 2 (graph replay, cold): 134.5 us with every sums load nontemporal,
+// 126.7 with y and x cached; y, delta and x cached 128.7, one of them 128.3-
+// 129.3, all four 137-146; walking the apply tiles backwards gained nothing, and
+// cached apply loads lost (137-158 us).
 // forward statistics: bit 0 = input load
 #ifndef DKZ_HINT_BN_STATS
 #define DKZ_HINT_BN_STATS 0
@@ -190,7 +193,7 @@
 #endif
 // backward sums: bit 0 = y, bit 1 = delta, bit 2 = x_norm, bit 3 = x loads
 #ifndef DKZ_HINT_BN_BWD_SUMS
-#define DKZ_HINT_BN_BWD_SUMS 15
+#define DKZ_HINT_BN_BWD_SUMS 6
 #endif
 // backward apply: bit 0 = y, bit 1 = delta, bit 2 = x loads, bit 3 = delta store
 // (all nontemporal: 135 us per config-2 step against 139 us with a cached
