@@ -99,6 +99,10 @@ __device__ __forceinline__ float col_tap(const float *__restrict__ im, const Col
     return im[(q.c * g.H + y) * g.W + x];
 }
 
+#ifndef DKZ_IM2COL_S1_CLAMP
+#define DKZ_IM2COL_S1_CLAMP 1
+#endif
+
 template <bool NT>
 __global__ __launch_bounds__(kBlock) void im2col_vec_kernel(const float *__restrict__ im, float *__restrict__ col,
                                                             ColGeom g, uint32_t n) {
@@ -154,6 +158,45 @@ __global__ __launch_bounds__(kBlock) void im2col_s1_kernel(const float *__restri
                                                            ColGeom g, uint32_t nv) {
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
     const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#if DKZ_IM2COL_S1_CLAMP
+    // Every load is issued before the first is used: a block outside its
+    // row (or a float4 past the column's end) loads an in-range block --
+    // the row clamped into the image, the block into the row -- and is then
+    // replaced by zeros, so no load waits on a branch.
+    float4 a[kUnroll], b[kUnroll];
+    uint32_t use[kUnroll];  // bit 0: a inside the row, bit 1: b, bits 2..3: x0 mod 4
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q4 = base + u * kBlock;
+        const ColPos q = col_pos((q4 < nv ? q4 : 0u) << 2, g);
+        const int y = (int)(q.h + q.kh) - (int)g.p;
+        const bool yin = y >= 0 && y < (int)g.H;
+        const int yc = y < 0 ? 0 : (y >= (int)g.H ? (int)g.H - 1 : y);
+        const int x0 = (int)(q.w + q.kw) - (int)g.p;
+        const int sh = x0 & 3;  // x0 mod 4, also for x0 < 0
+        const int xa = x0 - sh;  // aligned start of the first block
+        const int xb = xa + 4;
+        const int wl = (int)g.W - 4;  // last block start (W % 4 == 0, W > 0)
+        const bool ain = yin && xa >= 0 && xa <= wl;
+        const bool bin = yin && sh != 0 && xb >= 0 && xb <= wl;
+        const int xac = xa < 0 ? 0 : (xa > wl ? wl : xa);
+        const int xbc = sh == 0 ? xac : (xb < 0 ? 0 : (xb > wl ? wl : xb));
+        const uint32_t row4 = ((q.c * g.H + (uint32_t)yc) * g.W) >> 2;
+        a[u] = ld4<false>(im, row4 + (uint32_t)(xac >> 2));
+        b[u] = ld4<false>(im, row4 + (uint32_t)(xbc >> 2));
+        use[u] = (ain ? 1u : 0u) | (bin ? 2u : 0u) | ((uint32_t)sh << 2);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t q4 = base + u * kBlock;
+        if (q4 >= nv) continue;
+        const float4 va = (use[u] & 1u) ? a[u] : zero;
+        const float4 vb = (use[u] & 2u) ? b[u] : zero;
+        const int sh = (int)(use[u] >> 2);
+        st4<NT>(col, q4, make_float4(pick(va, vb, sh), pick(va, vb, sh + 1), pick(va, vb, sh + 2),
+                                     pick(va, vb, sh + 3)));
+    }
+#else
     float4 out[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -178,6 +221,7 @@ __global__ __launch_bounds__(kBlock) void im2col_s1_kernel(const float *__restri
         const uint32_t q4 = base + u * kBlock;
         if (q4 < nv) st4<NT>(col, q4, out[u]);
     }
+#endif
 }
 
 __global__ __launch_bounds__(kBlock) void im2col_scalar_kernel(const float *__restrict__ im, float *__restrict__ col,
