@@ -731,6 +731,22 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 #define DKZ_BN_BWD_COOP_U2 4
 #endif
 constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
+// bn_bwd_reg_kernel: 512 threads, UH held + UR re-read float4s a lane (one
+// workgroup a CU covers 100352 elements, half a config-2 channel), loading
+// G float4s of each input at once. Measured at config 2 (graph replay,
+// cold): two passes 128 us; UH 22 / 20 (G 2) 104.5 / 105.5 us, UH 16 / 12
+// (G 4) 110 / 113 us. UH 22 takes 252 registers a lane for every
+// activation, no scratch; a build that spilled would take the two passes.
+#ifndef DKZ_BN_BWD_REG
+#define DKZ_BN_BWD_REG 1
+#endif
+#ifndef DKZ_BN_BWD_REG_UH
+#define DKZ_BN_BWD_REG_UH 22
+#endif
+#ifndef DKZ_BN_BWD_REG_G
+#define DKZ_BN_BWD_REG_G 2
+#endif
+constexpr int kBwdRegBS = 512, kBwdRegUH = DKZ_BN_BWD_REG_UH, kBwdRegUR = 49 - DKZ_BN_BWD_REG_UH;
 constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2;
 
 template <int A, int H, int BS, int U>
@@ -808,6 +824,152 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
         for (int l = 0; l < 4; ++l)  // bwd_elem's expression on the held terms
             lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
         st4<kNtOut>(delta, at[u], o);
+    }
+}
+
+// The one-launch backward for tensors too large for bn_bwd_coop_kernel's
+// grid to fit the GPU at once (config 2's): one 512-thread workgroup a CU,
+// U = UH + UR float4s of each input a lane. The sums pass over the chunk
+// keeps, for its first UH float4s, the two terms normalize_delta needs
+// (d2 and x - mean, as bn_bwd_coop_kernel holds them) in registers; after
+// the channel barrier those are written from registers, and the last UR
+// float4s are read again (y, delta, x) and written as bn_bwd_apply_kernel
+// writes them. The sums pass reads that re-read part with ordinary loads, so
+// the second read finds it in the Infinity Cache, and the held part
+// nontemporally. Bytes: 16 an element read once, plus 12 for the re-read
+// part, plus 4 written -- instead of the two passes' 16 + 12 + 4 for every
+// element.
+template <int A, int H, int BS, int UH, int UR>
+__global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *delta, const float *x_norm,
+                                                        const float *x, BwdParams p, RedGeom g, BwdFin fin,
+                                                        double *partials, uint64_t *slots) {
+    constexpr bool kLin = A == kLinear;
+    constexpr bool kNtOut = (H & 16) != 0;
+    constexpr int G = DKZ_BN_BWD_REG_G;  // float4s of each input a lane loads at once
+    __shared__ double lds[4 * (BS / kWave)];
+    __shared__ BwdChan chan_sh;
+    const uint32_t f = fdiv(blockIdx.x, g.div_k);
+    const uint32_t k = blockIdx.x - f * g.K;
+    const uint32_t F = g.div_filters.d;
+    const uint32_t j0 = k * g.chunk;
+    const uint32_t j1 = min(j0 + g.chunk, g.chan_len);
+    const uint32_t fbase = f * g.spatial;
+    const float m = p.mean[f], gam = p.scales[f];
+    // float4 u of the lane is element jb + u*4*BS of the channel; jb is
+    // recomputed in each phase from a copy the compiler cannot see through,
+    // so no per-float4 address stays live across phases.
+    const auto phase_base = [&]() {
+        uint32_t jb = j0 + 4 * threadIdx.x;
+        asm volatile("" : "+v"(jb));
+        return jb;
+    };
+    float4 d2[UH], xm[UH];
+    double a[4] = {0.0, 0.0, 0.0, 0.0};
+    // sums over the held part, keeping d2 and x - m
+#pragma unroll
+    for (int u0 = 0; u0 < UH; u0 += G) {
+        const uint32_t jb = phase_base();
+        float4 vy[G], vd[G], vn[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<true>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
+                else vy[v] = vd[v];
+                vn[v] = ld4<true>(x_norm, at);
+                vx[v] = ld4<true>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j >= j1) continue;
+            acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                lane(d2[u0 + v], l) = grad_delta<A>(lane(vd[v], l), lane(vy[v], l)) * gam;
+                lane(xm[u0 + v], l) = lane(vx[v], l) - m;
+            }
+        }
+    }
+    // sums over the re-read part (y, delta, x cached for the second read)
+#pragma unroll
+    for (int u0 = UH; u0 < UH + UR; u0 += G) {
+        const uint32_t jb = phase_base();
+        float4 vy[G], vd[G], vn[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<false>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<false>(y, at);
+                else vy[v] = vd[v];
+                vn[v] = ld4<true>(x_norm, at);
+                vx[v] = ld4<false>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
+        }
+    }
+    const Sums<4> r = block_sums<4, BS>(a, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        if (threadIdx.x == 0) {
+            float md, vdl;
+            fin.values(f, sums, md, vdl);
+            chan_sh = bwd_chan(p, f, md, vdl);
+            if (k == 0) fin.write(f, sums, md, vdl);
+        }
+    }
+    __syncthreads();
+    const BwdChan ch = chan_sh;
+    {
+        const uint32_t jb = phase_base();
+#pragma unroll
+        for (int u = 0; u < UH; ++u) {
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j >= j1) continue;
+            float4 o;
+#pragma unroll
+            for (int l = 0; l < 4; ++l)  // bwd_elem's expression on the held terms
+                lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
+            st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
+        }
+    }
+#pragma unroll
+    for (int u0 = UH; u0 < UH + UR; u0 += G) {
+        const uint32_t jb = phase_base();
+        float4 vy[G], vd[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<true>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
+                else vy[v] = vd[v];
+                vx[v] = ld4<true>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
+        }
     }
 }
 
@@ -1018,6 +1180,28 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     return true;
 }
 
+// bn_bwd_reg_kernel under the same rules as bwd_coop, and only when the
+// kernel keeps its held part in registers (no scratch).
+template <int A>
+bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
+    constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegUH, kBwdRegUR>;
+    const Shape &sh = a.sh;
+    const uint64_t K = div_up(L, (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUR)), wgs = (uint64_t)sh.F * K;
+    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
+        4ull * wgs * kPartialStride > kScratchPartials || !no_spills<kernel>() ||
+        wgs > resident_workgroups<kernel, kBwdRegBS>())
+        return false;
+    const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
+    Scratch sc{nullptr};
+    *rc = device_scratch(&sc);
+    if (*rc != 0) return true;
+    const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
+                      (float)((uint64_t)sh.S * (uint64_t)sh.B)};
+    *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(kBwdRegBS), a.y, a.delta, a.x_norm, a.x, p,
+                 gc, fin, sc.partials, sc.slots);
+    return true;
+}
+
 template <int A>
 int bn_backward_fused(const BwdArgs &a) {
     constexpr int H = DKZ_HINT_BN_BWD_APPLY;
@@ -1028,6 +1212,7 @@ int bn_backward_fused(const BwdArgs &a) {
     if (DKZ_BN_BWD_COOP && (bwd_coop<A, kBwdCoopBS, kBwdCoopU>(a, L, fin, &rc) ||
                             bwd_coop<A, kBwdCoopBS2, kBwdCoopU2>(a, L, fin, &rc)))
         return rc;
+    if (DKZ_BN_BWD_REG && bwd_reg<A>(a, L, fin, &rc)) return rc;
     const RedGeom g = sums_geom<4>(sh, A == kLinear ? 3 : 4);
     const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && tile_fits_slots(sh.S);
     const double *partials = nullptr;

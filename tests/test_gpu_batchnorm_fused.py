@@ -243,6 +243,21 @@ def test_backward_every_activation(dev, act):
     _backward_case((8, 6, 1536), act, seed=250 + int(act))
 
 
+@pytest.mark.parametrize("shape", REGISTER, ids=str)
+def test_backward_register_holding(dev, shape):
+    """Grids too large for the one-launch kernel: one 512-thread workgroup a
+    CU holding part of its chunk's terms in registers and reading the rest
+    again after the channel barrier."""
+    g_d, c_d = _backward_case(shape, Activation.leaky, seed=60 + sum(shape))
+    np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("act", [Activation.tanh, Activation.linear, Activation.logistic, Activation.selu],
+                         ids=lambda a: a.name)
+def test_backward_register_holding_activations(dev, act):
+    _backward_case(CONFIG2, act, seed=350 + int(act))
+
+
 def test_backward_linear_needs_no_output(dev):
     _backward_case((4, 12, 64), Activation.linear, seed=300, with_y=False)
     _backward_case((4, 12, 63), Activation.linear, seed=301, with_y=False)
