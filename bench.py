@@ -38,10 +38,11 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                dkz_convolution_forward / _weight_gradient / _data_gradient),
                TFLOP/s
                against the 157.3 TFLOP/s fp32 matrix-core peak
-  fused_bwd    the same step through dkz_batchnorm_backward (at this size a
-               reduction pass and an apply pass: 32 B/elem moved instead of
-               the chain's 56; its algorithmic bytes, each tensor once, are
-               20 B/elem)
+  fused_bwd    the same step through dkz_batchnorm_backward (at this size one
+               launch that holds 22 of each lane's 49 float4s of terms in
+               registers and reads y, delta and x of the rest again: about
+               27 B/elem moved instead of the chain's 56; its algorithmic
+               bytes, each tensor once, are 20 B/elem)
   bn_act_gelem_s  batch-norm + activation elements per second: config 1's
                forward and config 2's backward (per op, the whole per-op layer
                forward, fused), and each config's layer forward + backward
@@ -225,9 +226,10 @@ def config2_chain_ops(gpu, d, h):
 
 
 def fused_backward(gpu, d, h):
-    """The same layer step through the fused entry point (one reduction pass
-    over y, delta, x_norm, x; one apply pass over y, delta, x): 32 B/elem
-    moved, 20 B/elem algorithmic."""
+    """The same layer step through the fused entry point (at config 2 one
+    launch: every element's y, delta, x_norm and x read once, 27 of each
+    lane's 49 float4s of y, delta and x read again after the channel
+    barrier, delta written: about 27 B/elem moved, 20 B/elem algorithmic)."""
     from darknet_zig_amd.activations import Activation
 
     gpu.batchnormBackward(h["B"], h["F"], h["S"], Activation.leaky, d["y"], d["delta"], d["x"], d["x_norm"],
@@ -1372,8 +1374,8 @@ def main() -> int:
         },
         "chain_kernels": chain_kernels,
         "fused_bwd": {
-            "entry": "dkz_batchnorm_backward (same step, same buffers; here one sums pass + one apply pass, "
-                     "32 B/elem moved; bytes below are algorithmic, 20 B/elem)",
+            "entry": "dkz_batchnorm_backward (same step, same buffers; here one launch holding part of each "
+                     "chunk in registers, about 27 B/elem moved; bytes below are algorithmic, 20 B/elem)",
             "us": round(fused_ms * 1e3, 2),
             "bytes": 5 * 4 * h["n"],
             "GB/s": round(gbs(5 * 4 * h["n"], fused_ms), 1),
