@@ -731,22 +731,29 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 #define DKZ_BN_BWD_COOP_U2 4
 #endif
 constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
-// bn_bwd_reg_kernel: 512 threads, UH held + UR re-read float4s a lane (one
-// workgroup a CU covers 100352 elements, half a config-2 channel), loading
-// G float4s of each input at once. Measured at config 2 (graph replay,
-// cold): two passes 128 us; UH 22 / 20 (G 2) 104.5 / 105.5 us, UH 16 / 12
-// (G 4) 110 / 113 us. UH 22 takes 252 registers a lane for every
-// activation, no scratch; a build that spilled would take the two passes.
+// bn_bwd_reg_kernel: 512 threads, UH float4s a lane whose terms stay in
+// registers, UL whose terms go to LDS (144 KiB of the CU's 160) and UR read
+// again, UH + UL + UR = 49 (one workgroup a CU covers 100352 elements, half
+// a config-2 channel), loading G float4s of each input at once. Measured at
+// config 2 (graph replay, cold): two passes 128 us; registers only, UH 22 /
+// 20 (G 2) 104.5 / 105.5 us, UH 16 / 12 (G 4) 110 / 113 us; UH 21 + UL 9
+// 97.4 us (UH 20 + UL 9 97.7). UH 21 takes up to 252 registers a lane
+// (every activation), no scratch; a build that spilled would take the two
+// passes.
 #ifndef DKZ_BN_BWD_REG
 #define DKZ_BN_BWD_REG 1
 #endif
 #ifndef DKZ_BN_BWD_REG_UH
-#define DKZ_BN_BWD_REG_UH 22
+#define DKZ_BN_BWD_REG_UH 21
 #endif
 #ifndef DKZ_BN_BWD_REG_G
 #define DKZ_BN_BWD_REG_G 2
 #endif
-constexpr int kBwdRegBS = 512, kBwdRegUH = DKZ_BN_BWD_REG_UH, kBwdRegUR = 49 - DKZ_BN_BWD_REG_UH;
+#ifndef DKZ_BN_BWD_REG_UL
+#define DKZ_BN_BWD_REG_UL 9
+#endif
+constexpr int kBwdRegBS = 512, kBwdRegUH = DKZ_BN_BWD_REG_UH, kBwdRegUL = DKZ_BN_BWD_REG_UL;
+constexpr int kBwdRegUR = 49 - kBwdRegUH - kBwdRegUL;
 constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2;
 
 template <int A, int H, int BS, int U>
@@ -829,24 +836,26 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
 
 // The one-launch backward for tensors too large for bn_bwd_coop_kernel's
 // grid to fit the GPU at once (config 2's): one 512-thread workgroup a CU,
-// U = UH + UR float4s of each input a lane. The sums pass over the chunk
-// keeps, for its first UH float4s, the two terms normalize_delta needs
-// (d2 and x - mean, as bn_bwd_coop_kernel holds them) in registers; after
-// the channel barrier those are written from registers, and the last UR
-// float4s are read again (y, delta, x) and written as bn_bwd_apply_kernel
-// writes them. The sums pass reads that re-read part with ordinary loads, so
-// the second read finds it in the Infinity Cache, and the held part
-// nontemporally. Bytes: 16 an element read once, plus 12 for the re-read
-// part, plus 4 written -- instead of the two passes' 16 + 12 + 4 for every
-// element.
-template <int A, int H, int BS, int UH, int UR>
+// UH + UL + UR float4s of each input a lane. The sums pass over the chunk
+// keeps the two terms normalize_delta needs (d2 and x - mean, as
+// bn_bwd_coop_kernel holds them) for its first UH float4s in registers and
+// for the next UL in LDS; after the channel barrier those are written from
+// there, and the last UR float4s are read again (y, delta, x) and written as
+// bn_bwd_apply_kernel writes them. The sums pass reads that re-read part
+// with ordinary loads, so the second read finds it in the Infinity Cache,
+// and the rest nontemporally. Bytes: 16 an element read once, plus 12 for
+// the re-read part, plus 4 written -- instead of the two passes' 16 + 12 + 4
+// for every element.
+template <int A, int H, int BS, int UH, int UL, int UR>
 __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *delta, const float *x_norm,
                                                         const float *x, BwdParams p, RedGeom g, BwdFin fin,
                                                         double *partials, uint64_t *slots) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtOut = (H & 16) != 0;
     constexpr int G = DKZ_BN_BWD_REG_G;  // float4s of each input a lane loads at once
+    constexpr int UL1 = UL > 0 ? UL : 1;
     __shared__ double lds[4 * (BS / kWave)];
+    __shared__ float4 held_d2[UL1 * BS], held_xm[UL1 * BS];  // float4 UH + i of lane t at [i * BS + t]
     __shared__ BwdChan chan_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
@@ -894,13 +903,45 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             }
         }
     }
-    // sums over the re-read part (y, delta, x cached for the second read)
+    // sums over the part whose terms go to LDS
 #pragma unroll
-    for (int u0 = UH; u0 < UH + UR; u0 += G) {
+    for (int u0 = UH; u0 < UH + UL; u0 += G) {
         const uint32_t jb = phase_base();
         float4 vy[G], vd[G], vn[G], vx[G];
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+        for (int v = 0; v < G && u0 + v < UH + UL; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<true>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
+                else vy[v] = vd[v];
+                vn[v] = ld4<true>(x_norm, at);
+                vx[v] = ld4<true>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UL; ++v) {
+            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j >= j1) continue;
+            acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
+            float4 t2, tm;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                lane(t2, l) = grad_delta<A>(lane(vd[v], l), lane(vy[v], l)) * gam;
+                lane(tm, l) = lane(vx[v], l) - m;
+            }
+            held_d2[(u0 + v - UH) * BS + threadIdx.x] = t2;
+            held_xm[(u0 + v - UH) * BS + threadIdx.x] = tm;
+        }
+    }
+    // sums over the re-read part (y, delta, x cached for the second read)
+#pragma unroll
+    for (int u0 = UH + UL; u0 < UH + UL + UR; u0 += G) {
+        const uint32_t jb = phase_base();
+        float4 vy[G], vd[G], vn[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
             if (j < j1) {
                 const uint32_t at = chan_addr(fbase, j, g) >> 2;
@@ -912,7 +953,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             }
         }
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
             if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
         }
@@ -949,13 +990,24 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
                 lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
             st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
         }
+#pragma unroll
+        for (int u = UH; u < UH + UL; ++u) {
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j >= j1) continue;
+            const float4 t2 = held_d2[(u - UH) * BS + threadIdx.x], tm = held_xm[(u - UH) * BS + threadIdx.x];
+            float4 o;
+#pragma unroll
+            for (int l = 0; l < 4; ++l)
+                lane(o, l) = (lane(t2, l) * ch.inv + (ch.vd2 * lane(tm, l)) / p.denom) + ch.mdn;
+            st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
+        }
     }
 #pragma unroll
-    for (int u0 = UH; u0 < UH + UR; u0 += G) {
+    for (int u0 = UH + UL; u0 < UH + UL + UR; u0 += G) {
         const uint32_t jb = phase_base();
         float4 vy[G], vd[G], vx[G];
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
             if (j < j1) {
                 const uint32_t at = chan_addr(fbase, j, g) >> 2;
@@ -966,7 +1018,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             }
         }
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UR; ++v) {
+        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
             if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
         }
@@ -1184,9 +1236,10 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
 // kernel keeps its held part in registers (no scratch).
 template <int A>
 bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
-    constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegUH, kBwdRegUR>;
+    constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegUH, kBwdRegUL, kBwdRegUR>;
     const Shape &sh = a.sh;
-    const uint64_t K = div_up(L, (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUR)), wgs = (uint64_t)sh.F * K;
+    const uint64_t K = div_up(L, (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUL + kBwdRegUR));
+    const uint64_t wgs = (uint64_t)sh.F * K;
     if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
         4ull * wgs * kPartialStride > kScratchPartials || !no_spills<kernel>() ||
         wgs > resident_workgroups<kernel, kBwdRegBS>())
