@@ -183,7 +183,9 @@
 #endif
 // one-launch backward: bits 0-3 = y, delta, x_norm, x loads, bit 4 = delta
 // store (all nontemporal: config 1's shape 28.7 us with delta cached, 22.9
-// all NT, against 27.8 for the two passes)
+// all NT, against 27.8 for the two passes). The register- and LDS-holding
+// variant (config 2) takes bit 4 only: its loads are nontemporal except the
+// first read of the part it reads twice, which stays cached for the second.
 #ifndef DKZ_HINT_BN_BWD_COOP
 #define DKZ_HINT_BN_BWD_COOP 31
 #endif
