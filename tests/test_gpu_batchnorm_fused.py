@@ -125,7 +125,9 @@ def test_forward_train(dev, shape):
 # register-resident one (a 512-thread workgroup a CU, up to 100352 elements
 # of a channel each): config 2's shape (two per channel), one per channel
 # (K = 1), and four per channel with a ragged last chunk.
-REGISTER = [(64, 128, 3136), (32, 256, 3136), (100, 64, 4000)]
+REGISTER = [(64, 128, 3136), (32, 256, 3136), (100, 64, 4000),
+            (4, 1, 6422528),   # one channel over all 256 workgroups
+            (2, 3, 1338368)]   # the backward's 27 workgroups a channel, the last chunk ragged
 
 
 @pytest.mark.parametrize("shape", REGISTER, ids=str)
