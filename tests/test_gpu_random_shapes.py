@@ -50,6 +50,19 @@ def _layer():
 LAYERS = sorted({_layer() for _ in range(14)})
 
 
+def _large_bn():
+    """[batch, filters, spatial] of 3 to 26 M elements: the one-launch
+    register-holding paths and, past what the GPU holds at once, the two
+    passes."""
+    f = int(_R.choice([1, 3, 17, 64, 128, 255]))
+    s = 4 * int(_R.integers(256, 4096)) + int(_R.choice([0, 0, 0, 2]))
+    b = max(1, int(_R.integers(3_000_000, 26_000_000)) // (f * s))
+    return b, f, s
+
+
+LARGE_BN = sorted({_large_bn() for _ in range(5)})
+
+
 @pytest.mark.parametrize("shape", CHANNEL_SHAPES, ids=str)
 def test_channel_ops(dev, shape):
     B, F, S = shape
@@ -121,6 +134,14 @@ def test_fused_batchnorm(dev, shape):
     act = list(Activation)[(B + F + S) % len(Activation)]
     m, v = _forward_case(shape, act, True, (B + S) % 2 == 0, seed=B * 7 + F * 3 + S)
     _backward_case(shape, act, seed=B * 11 + F + S * 5)
+
+
+@pytest.mark.parametrize("shape", LARGE_BN, ids=str)
+def test_fused_batchnorm_large(dev, shape):
+    B, F, S = shape
+    act = list(Activation)[(B + F + S) % len(Activation)]
+    _forward_case(shape, act, True, True, seed=B + F * 5 + S)
+    _backward_case(shape, act, seed=B * 3 + F + S)
 
 
 @pytest.mark.parametrize("n", EW_SIZES)
