@@ -35,6 +35,8 @@
 // The fast path needs spatial % 4 == 0, 16-byte aligned tensors and a
 // non-empty tensor; any other call runs the per-op sequence, which handles
 // every shape (and edge case) exactly as the individual entry points do.
+#include <cstdlib>
+
 #include "dkz_channel.hpp"
 #include "dkz_hints.hpp"
 
@@ -365,10 +367,21 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 // always has all its workgroups resident or about to be, and completes: no
 // deadlock for any grid size as long as K workgroups fit the GPU at once.
 // The wait is bounded anyway (kSpinMax sleeps of ~128 cycles, ~0.1 s), so
-// every wave ends even if that assumption failed.
+// every wave ends even if that assumption failed; the barrier then returns
+// false and the workgroup's results are NaN (poison_unless), not sums of
+// partials some of which were never posted. The late workgroups still
+// complete the protocol, leaving the slots ready for the next launch.
 constexpr uint32_t kSpinMax = 1u << 20;
 
-__device__ __forceinline__ void channel_barrier(uint64_t *count, uint64_t *gen, uint32_t K) {
+// The barrier's spin limit: kSpinMax, or $DKZ_BARRIER_SPIN_LIMIT, read at
+// each launch (a test sets 0 to force time-outs and check that they turn
+// into NaN results).
+inline uint32_t barrier_spin_limit() {
+    const char *e = getenv("DKZ_BARRIER_SPIN_LIMIT");
+    return e != nullptr && *e != '\0' ? (uint32_t)strtoul(e, nullptr, 10) : kSpinMax;
+}
+
+__device__ __forceinline__ bool channel_barrier(uint64_t *count, uint64_t *gen, uint32_t K, uint32_t spin) {
     const uint64_t g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const uint64_t before = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -376,11 +389,21 @@ __device__ __forceinline__ void channel_barrier(uint64_t *count, uint64_t *gen, 
         __hip_atomic_store(count, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __hip_atomic_fetch_add(gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+        return true;
     }
-    for (uint32_t it = 0; it < kSpinMax; ++it) {
-        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != g0) break;
+    for (uint32_t it = 0; it < spin; ++it) {
+        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != g0) return true;
         __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
+// The channel's sums as NaN when its barrier timed out (met == 0).
+template <int NS>
+__device__ __forceinline__ void poison_unless(uint32_t met, Sums<NS> &r) {
+    if (met == 0) {
+#pragma unroll
+        for (int q = 0; q < NS; ++q) r.s[q] = __builtin_nan("");
     }
 }
 
@@ -448,11 +471,12 @@ constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 template <int A, int H, int BS, int U>
 __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
                                                          float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
-                                                         double *partials, uint64_t *slots) {
+                                                         double *partials, uint64_t *slots, uint32_t spin) {
     constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
     constexpr bool kXLate = DKZ_BN_COOP_X_LATE != 0;
     __shared__ double lds[2 * (BS / kWave)];
     __shared__ FwdChan chan_sh;
+    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -497,11 +521,15 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
         for (int q = 0; q < 2; ++q)
             __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
+                                 spin)
+                     ? 1u
+                     : 0u;
     }
     __syncthreads();
     if (threadIdx.x < kWave) {
-        const Sums<2> sums = wave_partials_coherent<2>(partials, F, g.K, f);
+        Sums<2> sums = wave_partials_coherent<2>(partials, F, g.K, f);
+        poison_unless(met_sh, sums);
         if (threadIdx.x == 0) {
             float m, var;
             fin.stats(sums, c, m, var);
@@ -759,12 +787,13 @@ constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2
 template <int A, int H, int BS, int U>
 __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *delta, const float *x_norm,
                                                          const float *x, BwdParams p, RedGeom g, BwdFin fin,
-                                                         double *partials, uint64_t *slots) {
+                                                         double *partials, uint64_t *slots, uint32_t spin) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtX = (H & 8) != 0;
     constexpr bool kNtOut = (H & 16) != 0;
     __shared__ double lds[4 * (BS / kWave)];
     __shared__ BwdChan chan_sh;
+    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -809,11 +838,15 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
         for (int q = 0; q < 4; ++q)
             __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
+                                 spin)
+                     ? 1u
+                     : 0u;
     }
     __syncthreads();
     if (threadIdx.x < kWave) {
-        const Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        poison_unless(met_sh, sums);
         if (threadIdx.x == 0) {
             float md, vdl;
             fin.values(f, sums, md, vdl);
@@ -849,7 +882,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
 template <int A, int H, int BS, int UH, int UL, int UR>
 __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *delta, const float *x_norm,
                                                         const float *x, BwdParams p, RedGeom g, BwdFin fin,
-                                                        double *partials, uint64_t *slots) {
+                                                        double *partials, uint64_t *slots, uint32_t spin) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtOut = (H & 16) != 0;
     constexpr int G = DKZ_BN_BWD_REG_G;  // float4s of each input a lane loads at once
@@ -857,6 +890,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
     __shared__ double lds[4 * (BS / kWave)];
     __shared__ float4 held_d2[UL1 * BS], held_xm[UL1 * BS];  // float4 UH + i of lane t at [i * BS + t]
     __shared__ BwdChan chan_sh;
+    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -964,11 +998,15 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
         for (int q = 0; q < 4; ++q)
             __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K);
+        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
+                                 spin)
+                     ? 1u
+                     : 0u;
     }
     __syncthreads();
     if (threadIdx.x < kWave) {
-        const Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
+        poison_unless(met_sh, sums);
         if (threadIdx.x == 0) {
             float md, vdl;
             fin.values(f, sums, md, vdl);
@@ -1165,7 +1203,7 @@ bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
                      (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
     const FwdParams p{a.mean, a.variance, a.scales, a.biases};
     *rc = launch("batchnorm_forward", kernel, dim3(sh.F * gc.K), dim3(BS), a.input, a.output, a.x, a.x_norm, p, gc,
-                 fin, sc.partials, sc.slots);
+                 fin, sc.partials, sc.slots, barrier_spin_limit());
     return true;
 }
 
@@ -1228,7 +1266,7 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(BS), a.y, a.delta, a.x_norm, a.x, p, gc, fin,
-                 sc.partials, sc.slots);
+                 sc.partials, sc.slots, barrier_spin_limit());
     return true;
 }
 
@@ -1251,7 +1289,7 @@ bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(kBwdRegBS), a.y, a.delta, a.x_norm, a.x, p,
-                 gc, fin, sc.partials, sc.slots);
+                 gc, fin, sc.partials, sc.slots, barrier_spin_limit());
     return true;
 }
 

@@ -260,6 +260,44 @@ def test_backward_register_holding_activations(dev, act):
     _backward_case(CONFIG2, act, seed=350 + int(act))
 
 
+@pytest.mark.parametrize("bwd_shape", [(128, 32, 1024), CONFIG2], ids=str)
+def test_barrier_time_out_gives_nan(dev, monkeypatch, bwd_shape):
+    """The one-launch passes' channel barrier waits a bounded time. Forced to
+    give up at once (DKZ_BARRIER_SPIN_LIMIT=0, read at each launch), every
+    workgroup but the last of its channel finds the barrier unmet and writes
+    NaN rather than results from partial sums that were not all posted; the
+    barrier's slots are left ready, so the next call is right again. Every
+    kernel still exits normally: the spin limit only shortens its own wait."""
+    B, F, S = 128, 32, 1024  # config 1: the forward splits each channel 8 ways
+    n = B * F * S
+    r = rng(77)
+    x = normal(r, n)
+    d_in, d_out, d_x, d_xn = up(x), gpu.alloc(n), gpu.alloc(n), gpu.alloc(n)
+    d_m, d_v, d_rm, d_rv = gpu.alloc(F), gpu.alloc(F), up(np.zeros(F, np.float32)), up(np.ones(F, np.float32))
+    d_s, d_b = up(uniform(r, F, 0.5, 1.5)), up(normal(r, F, 0, 0.1))
+    monkeypatch.setenv("DKZ_BARRIER_SPIN_LIMIT", "0")
+    gpu.batchnormForward(B, F, S, Activation.leaky, True, d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    out = down(d_out, x)
+    _free(d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    assert np.isnan(out).any(), "a timed-out forward barrier left no NaN"
+
+    Bb, Fb, Sb = bwd_shape
+    nb = Bb * Fb * Sb
+    y, delta, xb, xn = normal(r, nb), normal(r, nb), normal(r, nb), normal(r, nb)
+    d_y, d_d, d_xb, d_xnb = up(y), up(delta), up(xb), up(xn)
+    d_m, d_v, d_s = up(normal(r, Fb, 0, 0.1)), up(uniform(r, Fb, 0.5, 1.5)), up(uniform(r, Fb, 0.5, 1.5))
+    d_bu, d_su, d_md, d_vd = gpu.alloc(Fb), gpu.alloc(Fb), gpu.alloc(Fb), gpu.alloc(Fb)
+    gpu.batchnormBackward(Bb, Fb, Sb, Activation.leaky, d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su, d_md,
+                          d_vd)
+    got = down(d_d, delta)
+    _free(d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su, d_md, d_vd)
+    assert np.isnan(got).any(), "a timed-out backward barrier left no NaN"
+
+    monkeypatch.delenv("DKZ_BARRIER_SPIN_LIMIT")
+    _forward_case((B, F, S), Activation.leaky, True, inplace=True, seed=78)
+    _backward_case(bwd_shape, Activation.leaky, seed=79)
+
+
 def test_backward_linear_needs_no_output(dev):
     _backward_case((4, 12, 64), Activation.linear, seed=300, with_y=False)
     _backward_case((4, 12, 63), Activation.linear, seed=301, with_y=False)
