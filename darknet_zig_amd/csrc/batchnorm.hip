@@ -255,6 +255,15 @@ __device__ __forceinline__ void fwd_elem(float4 v, const FwdChan &c, float4 &xn,
 #ifndef DKZ_BN_DEFER_BWD
 #define DKZ_BN_DEFER_BWD 1
 #endif
+// ... while a channel has at most this many partials: every apply workgroup
+// adds its channels' K partials itself, so with few channels split many
+// ways that is K loads per workgroup and the separate finalize launch is
+// cheaper. Measured (two passes, graph replay, backward / forward):
+// [2,1,60M] 1815 / 1233 us deferred (K 8192), 769 / 513 not; [4,3,12M]
+// 1253 / 675 against 788 / 552; [16,64,43264] (K 128) 231 against 220.
+#ifndef DKZ_BN_DEFER_MAX_K
+#define DKZ_BN_DEFER_MAX_K 16
+#endif
 // Elements of one apply workgroup, and how many channel rows it may span
 // and still finalise its channels itself.
 #ifndef DKZ_BN_APPLY_UNROLL
@@ -777,6 +786,12 @@ constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
 #ifndef DKZ_BN_BWD_REG_G
 #define DKZ_BN_BWD_REG_G 2
 #endif
+// Tensors larger than the GPU holds at once take this kernel while a
+// workgroup's chunk is at most this many times what it holds (its share of
+// re-read bytes grows with the chunk), two passes beyond.
+#ifndef DKZ_BN_BWD_REG_MAX_CHUNKS
+#define DKZ_BN_BWD_REG_MAX_CHUNKS 4
+#endif
 #ifndef DKZ_BN_BWD_REG_UL
 #define DKZ_BN_BWD_REG_UL 9
 #endif
@@ -992,6 +1007,30 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
         }
     }
+    // chunks longer than UH + UL + UR float4s a lane (tensors larger than the
+    // GPU holds at once): the rest is re-read as well
+    for (uint32_t u0 = UH + UL + UR;; u0 += G) {
+        const uint32_t jb = phase_base();
+        if (jb + u0 * (4 * BS) >= j1) break;
+        float4 vy[G], vd[G], vn[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G; ++v) {
+            const uint32_t j = jb + (u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<false>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<false>(y, at);
+                else vy[v] = vd[v];
+                vn[v] = ld4<true>(x_norm, at);
+                vx[v] = ld4<false>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G; ++v) {
+            const uint32_t j = jb + (u0 + v) * (4 * BS);
+            if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
+        }
+    }
     const Sums<4> r = block_sums<4, BS>(a, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
@@ -1058,6 +1097,27 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
 #pragma unroll
         for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
+            if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
+        }
+    }
+    for (uint32_t u0 = UH + UL + UR;; u0 += G) {
+        const uint32_t jb = phase_base();
+        if (jb + u0 * (4 * BS) >= j1) break;
+        float4 vy[G], vd[G], vx[G];
+#pragma unroll
+        for (int v = 0; v < G; ++v) {
+            const uint32_t j = jb + (u0 + v) * (4 * BS);
+            if (j < j1) {
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                vd[v] = ld4<true>(delta, at);
+                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
+                else vy[v] = vd[v];
+                vx[v] = ld4<true>(x, at);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < G; ++v) {
+            const uint32_t j = jb + (u0 + v) * (4 * BS);
             if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
         }
     }
@@ -1207,6 +1267,13 @@ bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
     return true;
 }
 
+// $DKZ_BN_TWO_PASS=1 (read at each call) skips the one-launch passes, so
+// the tests reach the two-pass path at any shape.
+inline bool two_pass_forced() {
+    const char *e = getenv("DKZ_BN_TWO_PASS");
+    return e != nullptr && e[0] == '1';
+}
+
 template <int A>
 int bn_forward_fused(const FwdArgs &a) {
     constexpr int H = DKZ_HINT_BN_FWD_APPLY;
@@ -1227,13 +1294,14 @@ int bn_forward_fused(const FwdArgs &a) {
                       a.output, a.x, a.x_norm, p, cg, sh.n, fin, (const double *)nullptr, 0u);
     }
     int rc = 0;
-    if (DKZ_BN_FWD_COOP && (fwd_coop<A, kCoopBS, kCoopU, false>(a, L, &rc) ||
-                            fwd_coop<A, kCoopBS2, kCoopU2, false>(a, L, &rc)))
+    const bool one_launch = !two_pass_forced();
+    if (DKZ_BN_FWD_COOP && one_launch && (fwd_coop<A, kCoopBS, kCoopU, false>(a, L, &rc) ||
+                                          fwd_coop<A, kCoopBS2, kCoopU2, false>(a, L, &rc)))
         return rc;
     // the same with one 512-thread workgroup a CU holding 196 floats a lane,
     // for tensors that fill the register file
-    if (DKZ_BN_FWD_COOP_REG && fwd_coop<A, kRegBlock, kRegU, true>(a, L, &rc)) return rc;
-    const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && tile_fits_slots(sh.S);
+    if (DKZ_BN_FWD_COOP_REG && one_launch && fwd_coop<A, kRegBlock, kRegU, true>(a, L, &rc)) return rc;
+    const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && g.K <= DKZ_BN_DEFER_MAX_K && tile_fits_slots(sh.S);
     const double *partials = nullptr;
     DKZ_TRY(run_sums<2>("batchnorm_forward_stats", g, sh, fin, defer, &partials,
                         bn_stats_kernel<DKZ_HINT_BN_STATS, kWideBlock, true>,
@@ -1276,11 +1344,20 @@ template <int A>
 bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegUH, kBwdRegUL, kBwdRegUR>;
     const Shape &sh = a.sh;
-    const uint64_t K = div_up(L, (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUL + kBwdRegUR));
+    constexpr uint64_t kCap = (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUL + kBwdRegUR);  // 100352
+    if (!no_spills<kernel>()) return false;
+    const uint64_t res = resident_workgroups<kernel, kBwdRegBS>();
+    uint64_t K = div_up(L, kCap);
+    if ((uint64_t)sh.F * K > res) {
+        // more than the GPU holds at once: as many workgroups a channel as
+        // fit, each re-reading what it cannot hold -- while that is at most
+        // DKZ_BN_BWD_REG_MAX_CHUNKS times what it holds
+        K = res / sh.F;
+        if (K == 0 || div_up(L, K) > (uint64_t)DKZ_BN_BWD_REG_MAX_CHUNKS * kCap) return false;
+    }
     const uint64_t wgs = (uint64_t)sh.F * K;
     if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
-        4ull * wgs * kPartialStride > kScratchPartials || !no_spills<kernel>() ||
-        wgs > resident_workgroups<kernel, kBwdRegBS>())
+        4ull * wgs * kPartialStride > kScratchPartials || wgs > res)
         return false;
     const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
     Scratch sc{nullptr};
@@ -1300,12 +1377,13 @@ int bn_backward_fused(const BwdArgs &a) {
     const BwdFin fin{a.variance, a.bias_updates, a.scale_updates, a.mean_delta, a.variance_delta};
     const uint64_t L = (uint64_t)sh.B * sh.S;
     int rc = 0;
-    if (DKZ_BN_BWD_COOP && (bwd_coop<A, kBwdCoopBS, kBwdCoopU>(a, L, fin, &rc) ||
-                            bwd_coop<A, kBwdCoopBS2, kBwdCoopU2>(a, L, fin, &rc)))
+    const bool one_launch = !two_pass_forced();
+    if (DKZ_BN_BWD_COOP && one_launch && (bwd_coop<A, kBwdCoopBS, kBwdCoopU>(a, L, fin, &rc) ||
+                                          bwd_coop<A, kBwdCoopBS2, kBwdCoopU2>(a, L, fin, &rc)))
         return rc;
-    if (DKZ_BN_BWD_REG && bwd_reg<A>(a, L, fin, &rc)) return rc;
+    if (DKZ_BN_BWD_REG && one_launch && bwd_reg<A>(a, L, fin, &rc)) return rc;
     const RedGeom g = sums_geom<4>(sh, A == kLinear ? 3 : 4);
-    const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && tile_fits_slots(sh.S);
+    const bool defer = DKZ_BN_DEFER_BWD && g.K > 1 && g.K <= DKZ_BN_DEFER_MAX_K && tile_fits_slots(sh.S);
     const double *partials = nullptr;
     constexpr int HS = DKZ_HINT_BN_BWD_SUMS;
     DKZ_TRY(run_sums<4>("batchnorm_backward_sums", g, sh, fin, defer, &partials,

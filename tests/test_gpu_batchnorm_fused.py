@@ -254,6 +254,16 @@ def test_backward_register_holding(dev, shape):
     np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("shape", [(16, 64, 43264), (4, 3, 6000000)], ids=str)
+def test_backward_register_holding_rereads(dev, shape):
+    """Tensors larger than the GPU holds at once: as many 512-thread
+    workgroups a channel as fit, each holding part of its chunk and reading
+    the rest again (a [16,64,208,208] layer: 1.7 times what a workgroup
+    holds; 3 channels of 24 M: 2.8 times)."""
+    g_d, c_d = _backward_case(shape, Activation.leaky, seed=70 + sum(shape))
+    np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
+
+
 @pytest.mark.parametrize("act", [Activation.tanh, Activation.linear, Activation.logistic, Activation.selu],
                          ids=lambda a: a.name)
 def test_backward_register_holding_activations(dev, act):
@@ -296,6 +306,19 @@ def test_barrier_time_out_gives_nan(dev, monkeypatch, bwd_shape):
     monkeypatch.delenv("DKZ_BARRIER_SPIN_LIMIT")
     _forward_case((B, F, S), Activation.leaky, True, inplace=True, seed=78)
     _backward_case(bwd_shape, Activation.leaky, seed=79)
+
+
+@pytest.mark.parametrize("shape", [(128, 32, 1024), (4, 17, 10000), (8, 512, 1024), CONFIG2, (2, 1, 1000000)],
+                         ids=str)
+def test_two_passes(dev, monkeypatch, shape):
+    """The two-pass forward and backward (what larger tensors take), forced
+    at shapes the one-launch kernels would otherwise run: channels split 32,
+    49 and 488 ways (their partials added by a separate finalize launch), 9
+    ways (added by each apply workgroup itself) and not at all."""
+    monkeypatch.setenv("DKZ_BN_TWO_PASS", "1")
+    _forward_case(shape, Activation.leaky, True, inplace=True, seed=90 + sum(shape))
+    g_d, c_d = _backward_case(shape, Activation.leaky, seed=91 + sum(shape))
+    np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
 
 
 def test_backward_linear_needs_no_output(dev):
