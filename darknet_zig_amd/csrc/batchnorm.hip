@@ -9,13 +9,19 @@
 //   backward:         gradient, backward_bias, backward_scale, scale_bias,
 //                     mean_delta, variance_delta, normalize_delta
 //                     = 56 bytes/element.
-// Here each direction is one reduction pass, a tiny per-channel finalise,
-// and one apply pass:
+// Here each direction is, in general, one reduction pass, a tiny
+// per-channel finalise, and one apply pass:
 //   forward:  stats (read input: 4 B/elem) -> finalise (mean, variance, EMA)
 //             -> apply (read input; write x, x_norm, output: 16 B/elem);
 //   backward: sums (read y, delta, x_norm, x: 16 B/elem) -> finalise
 //             (bias/scale updates, mean_delta, variance_delta) -> apply
 //             (read y, delta, x; write delta: 16 B/elem).
+// When every workgroup of the grid fits the GPU at once, each direction is
+// one launch instead (bn_fwd_coop_kernel, bn_bwd_coop_kernel,
+// bn_bwd_reg_kernel): a workgroup keeps its chunk (or, for the largest
+// tensors, part of it) in registers and LDS, the channel's workgroups meet
+// at a barrier, and the apply step runs on what they hold: 16 B/elem
+// forward, 20 backward (plus 12 for any part read again).
 // Element results are the per-op sequence's, bit for bit, given the same
 // per-channel values: every element expression below is the one of the
 // corresponding op (broadcast.hip, elementwise.hip), in the same order.
