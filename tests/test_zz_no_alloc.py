@@ -11,6 +11,10 @@ by each call).
     16 ways) count themselves in the slots;
   * [32,64,28,28]: the fused passes with each channel split over several
     workgroups, whose f64 partials go through the array.
+
+A second test runs config 2's shape, whose one-launch pass holds part of
+each chunk in registers and LDS and meets at per-channel barriers in the
+array's slots, then the smaller shape again.
 """
 
 from __future__ import annotations
@@ -71,6 +75,11 @@ def test_two_calls_second_smaller(dev):
     _check((8, 128, 4099), 1)  # per-op sequence, split channel reductions counting in the slots
     _check((32, 64, 28 * 28), 2)  # smaller: fused passes, split partials
     _check((8, 128, 4099), 3)  # the first shape again, after the array was reused
+
+
+def test_config2_register_holding_pass(dev):
+    _check((64, 128, 3136), 4)  # one launch: partials and barrier words in the array
+    _check((32, 64, 28 * 28), 5)  # smaller, after it
 
 
 def test_zero_filters_is_a_no_op(dev):
