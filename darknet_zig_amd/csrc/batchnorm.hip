@@ -471,6 +471,8 @@ constexpr int kCoopBS2 = DKZ_BN_COOP_BS2, kCoopU2 = DKZ_BN_COOP_U2;
 // registers a lane) holding 49 float4s a lane, so one workgroup a CU covers
 // 100352 elements (half of a config-2 channel).
 constexpr int kRegBlock = 512, kRegU = 49;
+// float4s of input a lane loads at once past its held chunk
+constexpr int kFwdExtraG = 4;
 constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 
 // Forward (train) in one launch: workgroup (f, k) -- channel-major, k
@@ -483,7 +485,7 @@ constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 // workgroup, U float4s a lane: (kCoopBS, kCoopU) for small tensors, and
 // (kRegBlock, kRegU) -- one 512-thread workgroup a CU, 196 floats a lane --
 // for tensors that fill the register file (config 2's 103 MB over 256 CUs).
-template <int A, int H, int BS, int U>
+template <int A, int H, int BS, int U, bool EXTRA = false>
 __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
                                                          float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
                                                          double *partials, uint64_t *slots, uint32_t spin) {
@@ -530,6 +532,28 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
             if constexpr (!kXLate) st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, v[u]);
         }
     }
+    if constexpr (EXTRA) {
+        // chunks longer than U float4s a lane (tensors larger than the GPU
+        // holds at once): the rest is read here, cached, and again after
+        // the barrier
+        for (uint32_t u0 = U;; u0 += kFwdExtraG) {
+            const uint32_t jb = phase_base();
+            if (jb + u0 * (4 * BS) >= j1) break;
+            float4 w[kFwdExtraG];
+#pragma unroll
+            for (int q = 0; q < kFwdExtraG; ++q) {
+                const uint32_t j = jb + (u0 + q) * (4 * BS);
+                if (j < j1) w[q] = ld4<false>(input, chan_addr(fbase, j, g) >> 2);
+            }
+#pragma unroll
+            for (int q = 0; q < kFwdExtraG; ++q) {
+                const uint32_t j = jb + (u0 + q) * (4 * BS);
+                if (j >= j1) continue;
+                acc_shifted(w[q], c, a[0], a[1]);
+                st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, w[q]);
+            }
+        }
+    }
     const Sums<2> r = block_sums<2, BS>(a, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
@@ -565,6 +589,28 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
         if constexpr (kXLate) st4<kNtX>(x, at, v[u]);
         st4<kNtXn>(x_norm, at, xn);
         st4<kNtOut>(output, at, o);
+    }
+    if constexpr (EXTRA) {
+        for (uint32_t u0 = U;; u0 += kFwdExtraG) {
+            const uint32_t jb2 = phase_base();
+            if (jb2 + u0 * (4 * BS) >= j1) break;
+            float4 w[kFwdExtraG];
+#pragma unroll
+            for (int q = 0; q < kFwdExtraG; ++q) {
+                const uint32_t j = jb2 + (u0 + q) * (4 * BS);
+                if (j < j1) w[q] = ld4<true>(input, chan_addr(fbase, j, g) >> 2);
+            }
+#pragma unroll
+            for (int q = 0; q < kFwdExtraG; ++q) {
+                const uint32_t j = jb2 + (u0 + q) * (4 * BS);
+                if (j >= j1) continue;
+                const uint32_t at = chan_addr(fbase, j, g) >> 2;
+                float4 xn, o;
+                fwd_elem<A>(w[q], ch, xn, o);
+                st4<kNtXn>(x_norm, at, xn);
+                st4<kNtOut>(output, at, o);
+            }
+        }
     }
 }
 
@@ -1151,6 +1197,13 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
 #ifndef DKZ_BN_FWD_COOP_REG
 #define DKZ_BN_FWD_COOP_REG 1
 #endif
+// ... and tensors larger than the register file: measured (graph replay),
+// [16,64,208,208] (1.7 times what a workgroup holds) 151.6 -> 131.4 us and
+// [32,128,112,112] (2.0) 178.4 -> 155.8 against two passes, [4,3,6M] (2.8)
+// 291 -> 303 and [2,1,50M] (3.9) 434 -> 478: up to twice.
+#ifndef DKZ_BN_FWD_REG_MAX_CHUNKS
+#define DKZ_BN_FWD_REG_MAX_CHUNKS 2
+#endif
 
 // Workgroups of Kernel (BS threads) the GPU holds at once: HIP's occupancy
 // for the kernel's registers and LDS times the CU count, looked up once per
@@ -1248,12 +1301,24 @@ int run_sums(const char *name, const RedGeom &g, const Shape &sh, const Fin &fin
 // lane, when its whole grid fits the GPU at once (and, for CHECK_SPILLS,
 // when the kernel keeps its chunk in registers): launches it and returns
 // true with its status in *rc; otherwise returns false, launching nothing.
-template <int A, int BS, int U, bool CHECK_SPILLS>
+template <int A, int BS, int U, bool CHECK_SPILLS, bool EXTRA = false>
 bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
-    constexpr auto kernel = bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, BS, U>;
+    constexpr auto kernel = bn_fwd_coop_kernel<A, DKZ_HINT_BN_FWD_COOP, BS, U, EXTRA>;
     constexpr uint64_t chunk = (uint64_t)BS * 4 * U;
     const Shape &sh = a.sh;
-    const uint64_t K = div_up(L, chunk), wgs = (uint64_t)sh.F * K;
+    uint64_t K = div_up(L, chunk);
+    if constexpr (EXTRA) {
+        // only for tensors whose held chunks do not all fit: as many
+        // workgroups a channel as fit, each reading again what it cannot
+        // hold, while that is at most DKZ_BN_FWD_REG_MAX_CHUNKS times what it
+        // holds
+        if (!no_spills<kernel>()) return false;
+        const uint64_t res = resident_workgroups<kernel, BS>();
+        if ((uint64_t)sh.F * K <= res) return false;
+        K = res / sh.F;
+        if (K == 0 || div_up(L, K) > (uint64_t)DKZ_BN_FWD_REG_MAX_CHUNKS * chunk) return false;
+    }
+    const uint64_t wgs = (uint64_t)sh.F * K;
     if (K > 256 || sh.F > kScratchSlots / kCounterStride || wgs > DKZ_BN_COOP_MAX_WGS ||
         2ull * wgs * kPartialStride > kScratchPartials)
         return false;
@@ -1306,7 +1371,9 @@ int bn_forward_fused(const FwdArgs &a) {
         return rc;
     // the same with one 512-thread workgroup a CU holding 196 floats a lane,
     // for tensors that fill the register file
-    if (DKZ_BN_FWD_COOP_REG && one_launch && fwd_coop<A, kRegBlock, kRegU, true>(a, L, &rc)) return rc;
+    if (DKZ_BN_FWD_COOP_REG && one_launch &&
+        (fwd_coop<A, kRegBlock, kRegU, true>(a, L, &rc) || fwd_coop<A, kRegBlock, kRegU, true, true>(a, L, &rc)))
+        return rc;
     const bool defer = DKZ_BN_DEFER_FWD && g.K > 1 && g.K <= DKZ_BN_DEFER_MAX_K && tile_fits_slots(sh.S);
     const double *partials = nullptr;
     DKZ_TRY(run_sums<2>("batchnorm_forward_stats", g, sh, fin, defer, &partials,

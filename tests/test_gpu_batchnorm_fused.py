@@ -255,11 +255,13 @@ def test_backward_register_holding(dev, shape):
 
 
 @pytest.mark.parametrize("shape", [(16, 64, 43264), (4, 3, 6000000)], ids=str)
-def test_backward_register_holding_rereads(dev, shape):
+def test_register_holding_rereads(dev, shape):
     """Tensors larger than the GPU holds at once: as many 512-thread
     workgroups a channel as fit, each holding part of its chunk and reading
     the rest again (a [16,64,208,208] layer: 1.7 times what a workgroup
-    holds; 3 channels of 24 M: 2.8 times)."""
+    holds, both directions; 3 channels of 24 M: 2.8 times, the backward --
+    the forward takes two passes there)."""
+    _forward_case(shape, Activation.leaky, True, inplace=True, seed=69 + sum(shape))
     g_d, c_d = _backward_case(shape, Activation.leaky, seed=70 + sum(shape))
     np.testing.assert_allclose(g_d, c_d, rtol=1e-4, atol=1e-5)
 
