@@ -1197,10 +1197,12 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
 #ifndef DKZ_BN_FWD_COOP_REG
 #define DKZ_BN_FWD_COOP_REG 1
 #endif
-// ... and tensors larger than the register file: measured (graph replay),
-// [16,64,208,208] (1.7 times what a workgroup holds) 151.6 -> 131.4 us and
-// [32,128,112,112] (2.0) 178.4 -> 155.8 against two passes, [4,3,6M] (2.8)
-// 291 -> 303 and [2,1,50M] (3.9) 434 -> 478: up to twice.
+// The register-resident forward also runs on tensors larger than the GPU
+// holds at once -- as many workgroups a channel as fit, each reading again
+// the part of its chunk it cannot hold -- while a chunk is at most this many
+// times what a workgroup holds. Measured against the two passes (graph
+// replay): [16,64,208,208] (1.7 times) 151.6 -> 131.4 us, [32,128,112,112]
+// (2.0) 178.4 -> 155.8; [4,3,6M] (2.8) 291 -> 303, [2,1,50M] (3.9) 434 -> 478.
 #ifndef DKZ_BN_FWD_REG_MAX_CHUNKS
 #define DKZ_BN_FWD_REG_MAX_CHUNKS 2
 #endif
