@@ -17,17 +17,24 @@
 // the result is bit-exact with no atomics. Elements with no contributor are
 // not written (0 + -0 would otherwise flip a sign).
 //
-// Planes that fit in 48 KiB of LDS take one workgroup each: the forward reads
-// the input plane into LDS once and scans every window from there, and the
-// stride-1 backward with windows wider than 2 stages the plane's indexes and
-// deltas the same way before its gather; with stride >= 2 the plane of
-// prev_delta joins them, is updated in LDS and written back whole.
+// From 256 planes the generic shapes go through LDS. Windows of 4 and more
+// take a separable forward, several planes a workgroup: a row pass keeps
+// each input row's first window maximum and its column, a column pass the
+// first of those over the window's rows (2*size taps an output instead of
+// size^2, the same first maximum). Smaller windows take one workgroup a
+// plane, every window scanned from the plane in LDS. The stride-1 backward
+// with windows wider than 2 stages the indexes and deltas of several planes
+// a workgroup before its gather; with stride >= 2 one workgroup a plane
+// stages the plane of prev_delta with them, updates it in LDS and writes it
+// back whole.
 //
 // Size 2, stride 2, offset 0 with in_w % 4 == 0 and even in_h -- the shape of
 // a darknet [maxpool] size=2 stride=2 layer -- has a fast path: each lane owns
 // two adjacent outputs and their 2x4 input patch, read and written as two
 // float4s (outputs and indexes as float2/int2), all with streaming hints.
 #include <float.h>
+
+#include <algorithm>
 
 #include "dkz_device.hpp"
 #include "dkz_hints.hpp"
@@ -73,6 +80,31 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #endif
 #ifndef DKZ_POOL_PLANE_UNROLL
 #define DKZ_POOL_PLANE_UNROLL 1
+#endif
+// The several-planes-a-workgroup kernels (build-time switches, for
+// measurement): the separable forward for windows of at least
+// DKZ_POOL_SEP_MIN_SIZE, the stride-1 gather backward for windows of 3 and
+// more. Measured on [64,512,19,19] stride 1, forward / backward us against
+// one workgroup a plane: size 5 120.6 / 162.8 -> 89.8 / 138.2, size 13
+// 461.9 / 544.6 -> 120.0 / 465.3; the separable forward lost on 2x2/s1
+// [64,512,26,26] (53.4 -> 90.5) and 3x3/s1 [64,128,56,56] (90.6 -> 120.1),
+// the gather on 2x2/s1 [64,256,13,13] (17.0 -> 20.3).
+#ifndef DKZ_POOL_SEP
+#define DKZ_POOL_SEP 1
+#endif
+#ifndef DKZ_POOL_SEP_MIN_SIZE
+#define DKZ_POOL_SEP_MIN_SIZE 4
+#endif
+#ifndef DKZ_POOL_S1_GATHER
+#define DKZ_POOL_S1_GATHER 1
+#endif
+// Elements (input plane elements) a workgroup of those kernels aims at, and
+// the fewest workgroups their grid keeps when there are enough planes.
+#ifndef DKZ_POOL_SEP_TARGET
+#define DKZ_POOL_SEP_TARGET 2048
+#endif
+#ifndef DKZ_POOL_SEP_MIN_GROUPS
+#define DKZ_POOL_SEP_MIN_GROUPS 512
 #endif
 
 // Candidate outputs of input (y, x) -- those whose window covers it: rows
@@ -135,6 +167,76 @@ __global__ __launch_bounds__(kBlock) void maxpool_fwd_kernel(const float *in, fl
 // from LDS in the twin's order.
 constexpr uint32_t kPlaneMaxFloats = DKZ_POOL_PLANE_MAX;
 
+// Copies n 4-byte elements from global memory into LDS, R vectors of four
+// (VEC: src and dst 16-byte aligned) or 4R elements a lane at a time: every
+// load of a batch (addresses clamped into the array) is issued before the
+// first LDS write, so that a workgroup waits out the memory latency once a
+// batch rather than once an element. Arrays of at most one element (or
+// vector) a lane take a single guarded load.
+template <typename T, typename T4, bool VEC, int BS, int R = 4>
+__device__ __forceinline__ void stage_to_lds(T *dst, const T *src, uint32_t n) {
+    if constexpr (VEC) {
+        const uint32_t n4 = n / 4;
+        const T4 *s4 = reinterpret_cast<const T4 *>(src);
+        T4 *d4 = reinterpret_cast<T4 *>(dst);
+        if (n4 <= BS) {
+            if (threadIdx.x < n4) d4[threadIdx.x] = s4[threadIdx.x];
+        } else {
+            for (uint32_t b = threadIdx.x; b < n4; b += R * BS) {
+                T4 t[R];
+#pragma unroll
+                for (int k = 0; k < R; ++k) t[k] = s4[min(b + (uint32_t)(k * BS), n4 - 1)];
+#pragma unroll
+                for (int k = 0; k < R; ++k)
+                    if (b + (uint32_t)(k * BS) < n4) d4[b + k * BS] = t[k];
+            }
+        }
+        for (uint32_t q = n4 * 4 + threadIdx.x; q < n; q += BS) dst[q] = src[q];
+    } else if (n <= BS) {
+        if (threadIdx.x < n) dst[threadIdx.x] = src[threadIdx.x];
+    } else {
+        for (uint32_t b = threadIdx.x; b < n; b += 4 * R * BS) {
+            T t[4 * R];
+#pragma unroll
+            for (int k = 0; k < 4 * R; ++k) t[k] = src[min(b + (uint32_t)(k * BS), n - 1)];
+#pragma unroll
+            for (int k = 0; k < 4 * R; ++k)
+                if (b + (uint32_t)(k * BS) < n) dst[b + k * BS] = t[k];
+        }
+    }
+}
+
+// The same for an output plane's indexes and deltas (n each), both arrays'
+// loads of a batch issued together.
+template <int BS, int R = 2>
+__device__ __forceinline__ void stage_pair_to_lds(int *il, float *dl, const int *idx, const float *delta,
+                                                  uint32_t n) {
+    if (n <= BS) {
+        if (threadIdx.x < n) {
+            il[threadIdx.x] = idx[threadIdx.x];
+            dl[threadIdx.x] = delta[threadIdx.x];
+        }
+        return;
+    }
+    for (uint32_t b = threadIdx.x; b < n; b += 4 * R * BS) {
+        int ti[4 * R];
+        float td[4 * R];
+#pragma unroll
+        for (int k = 0; k < 4 * R; ++k) {
+            const uint32_t q = min(b + (uint32_t)(k * BS), n - 1);
+            ti[k] = idx[q];
+            td[k] = delta[q];
+        }
+#pragma unroll
+        for (int k = 0; k < 4 * R; ++k) {
+            if (b + (uint32_t)(k * BS) < n) {
+                il[b + k * BS] = ti[k];
+                dl[b + k * BS] = td[k];
+            }
+        }
+    }
+}
+
 // S > 0: the window is S x S (its taps unrolled, all reads issued first);
 // S == 0: g.size.
 template <bool VEC, int S>
@@ -142,12 +244,7 @@ __global__ __launch_bounds__(kBlock) void maxpool_plane_fwd_kernel(const float *
     extern __shared__ float4 plane_lds4[];
     float *pl = reinterpret_cast<float *>(plane_lds4);
     const uint32_t plane = blockIdx.x, hw = g.h * g.w, ohw = g.oh * g.ow;
-    const float *src = in + (size_t)plane * hw;
-    if constexpr (VEC) {
-        for (uint32_t q = threadIdx.x; q < hw / 4; q += kBlock) plane_lds4[q] = reinterpret_cast<const float4 *>(src)[q];
-    } else {
-        for (uint32_t q = threadIdx.x; q < hw; q += kBlock) pl[q] = src[q];
-    }
+    stage_to_lds<float, float4, VEC, kBlock>(pl, in + (size_t)plane * hw, hw);
     __syncthreads();
     for (uint32_t o = threadIdx.x; o < ohw; o += kBlock) {
         const uint32_t i = fdiv(o, g.div_ow), j = o - i * g.ow;
@@ -256,10 +353,7 @@ __global__ __launch_bounds__(kBlock) void maxpool_plane_bwd_kernel(const float *
     const uint32_t plane = blockIdx.x, hw = g.h * g.w, ohw = g.oh * g.ow;
     int *il = reinterpret_cast<int *>(plane_lds4);
     float *dl = reinterpret_cast<float *>(plane_lds4) + ohw;
-    for (uint32_t q = threadIdx.x; q < ohw; q += kBlock) {
-        il[q] = idx[(size_t)plane * ohw + q];
-        dl[q] = delta[(size_t)plane * ohw + q];
-    }
+    stage_pair_to_lds<kBlock>(il, dl, idx + (size_t)plane * ohw, delta + (size_t)plane * ohw, ohw);
     __syncthreads();
     for (uint32_t el = threadIdx.x; el < hw; el += kBlock) {
         const uint32_t y = fdiv(el, g.div_w), x = el - y * g.w;
@@ -275,6 +369,152 @@ __global__ __launch_bounds__(kBlock) void maxpool_plane_bwd_kernel(const float *
                 if (!touched) v = prev[e];
                 touched = true;
                 v += dl[o];
+            }
+        }
+        if (touched) prev[e] = v;
+    }
+}
+
+// ---- several planes a workgroup ----------------------------------------------
+
+// The kernels below take P consecutive planes a workgroup (the last one may
+// take fewer), so that planes of a few hundred elements still give every
+// lane of a 256-lane workgroup several elements: the planes of one
+// workgroup are contiguous in memory, read and written as one run.
+constexpr uint32_t kSepBS = 256;
+
+// Separable forward. The workgroup's planes are read into LDS once. A row
+// pass takes, for every input row y and output column j, the first maximum
+// under strict '>' of the window's columns in that row (value and column;
+// -FLT_MAX and -1 when no tap beats -FLT_MAX); a column pass takes, for
+// every output, the first of those row maxima over the window's rows under
+// the same rule. The twin's scan (window rows, then columns, strict '>',
+// from -FLT_MAX) ends on the first tap in row-major order of the window's
+// largest values (NaNs never win; -0 and +0 tie), and that tap is the
+// first row whose row maximum is one of them, at that row's first column
+// holding one: the same value and index. h*ow + oh*ow window scans of
+// `size` taps each, against oh*ow scans of size^2. Taps are visited in
+// batches of 4 whose loads (clamped into the row) are all issued first.
+// VEC: the workgroups' first planes start 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(kSepBS) void maxpool_sep_fwd_kernel(const float *in, float *out, int *idx, PoolGeom g,
+                                                                 uint32_t planes, uint32_t P) {
+    extern __shared__ float4 plane_lds4[];
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow;
+    float *pl = reinterpret_cast<float *>(plane_lds4);
+    float *rmax = pl + P * hw;                               // [P*h][ow]
+    int *rarg = reinterpret_cast<int *>(rmax + P * g.h * g.ow);  // [P*h][ow]
+    stage_to_lds<float, float4, VEC, kSepBS>(pl, in + (size_t)plane0 * hw, np * hw);
+    __syncthreads();
+    const int sz = (int)g.size, w = (int)g.w, h = (int)g.h;
+    for (uint32_t r = threadIdx.x; r < np * g.h * g.ow; r += kSepBS) {
+        const uint32_t q = fdiv(r, g.div_ow), j = r - q * g.ow;  // q = p*h + y
+        const int c0 = (int)(j * g.stride) - (int)g.half_pad;
+        const int lo = max(c0, 0), n = min(c0 + sz, w) - lo;  // taps [lo, lo + n)
+        const float *row = pl + q * g.w;
+        float mx = -FLT_MAX;
+        int a = -1;
+        for (int m0 = 0; m0 < n; m0 += 4) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = row[lo + min(m0 + u, n - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (m0 + u < n && v[u] > mx) {
+                    mx = v[u];
+                    a = lo + m0 + u;
+                }
+            }
+        }
+        rmax[r] = mx;
+        rarg[r] = a;
+    }
+    __syncthreads();
+    const size_t out0 = (size_t)plane0 * ohw;
+    for (uint32_t o = threadIdx.x; o < np * ohw; o += kSepBS) {
+        const uint32_t q = fdiv(o, g.div_ow), j = o - q * g.ow;  // q = p*oh + i
+        const uint32_t p = fdiv(q, g.div_oh), i = q - p * g.oh;
+        const int r0 = (int)(i * g.stride) - (int)g.half_pad;
+        const int lo = max(r0, 0), n = min(r0 + sz, h) - lo;  // rows [lo, lo + n)
+        const float *col = rmax + p * g.h * g.ow + j;
+        float mx = -FLT_MAX;
+        int best = -1;
+        for (int m0 = 0; m0 < n; m0 += 4) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = col[(uint32_t)(lo + min(m0 + u, n - 1)) * g.ow];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (m0 + u < n && v[u] > mx) {
+                    mx = v[u];
+                    best = lo + m0 + u;
+                }
+            }
+        }
+        // a row maximum above -FLT_MAX has a column
+        const int a = best < 0 ? -1 : rarg[(p * g.h + (uint32_t)best) * g.ow + j];
+        out[out0 + o] = mx;
+        idx[out0 + o] = best < 0 ? -1 : (int)((plane0 + p) * hw + (uint32_t)best * g.w + (uint32_t)a);
+    }
+}
+
+// Backward with stride 1, P planes a workgroup: the planes' indexes and
+// deltas are read into LDS once, then each lane gathers for its inputs --
+// consecutive across lanes -- as maxpool_bwd_kernel does (candidate outputs
+// in ascending order, delta added whenever the index names the input), a
+// window row at a time, the indexes of 4 candidates loaded together.
+// prev_delta is read for every input, a lane's next 8 inputs' loads issued
+// together (the first batch before the barrier), and written only where
+// some output names the input.
+__global__ __launch_bounds__(kSepBS) void maxpool_s1_gather_kernel(const float *delta, float *prev, const int *idx,
+                                                                   PoolGeom g, uint32_t planes, uint32_t P) {
+    extern __shared__ float4 plane_lds4[];
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow;
+    int *il = reinterpret_cast<int *>(plane_lds4);  // [P][oh][ow]
+    float *dl = reinterpret_cast<float *>(plane_lds4) + P * ohw;
+    const size_t o0 = (size_t)plane0 * ohw;
+    stage_pair_to_lds<kSepBS>(il, dl, idx + o0, delta + o0, np * ohw);
+    const uint32_t e0 = plane0 * hw, n_el = np * hw;
+    // prev_delta of the lane's next kPrev inputs, loaded together; the
+    // first batch's loads are in flight across the barrier
+    constexpr int kPrev = 8;
+    float pv[kPrev];
+#pragma unroll
+    for (int k = 0; k < kPrev; ++k) pv[k] = prev[e0 + min(threadIdx.x + (uint32_t)(k * kSepBS), n_el - 1)];
+    __syncthreads();
+#pragma unroll 1
+    for (uint32_t el = threadIdx.x, k = 0; el < n_el; el += kSepBS) {
+        float v = pv[0];
+#pragma unroll
+        for (int u = 0; u + 1 < kPrev; ++u) pv[u] = pv[u + 1];
+        if (++k == kPrev) {
+            k = 0;
+#pragma unroll
+            for (int u = 0; u < kPrev; ++u)
+                pv[u] = prev[e0 + min(el + (uint32_t)((u + 1) * kSepBS), n_el - 1)];
+        }
+        const uint32_t q = fdiv(el, g.div_w), x = el - q * g.w;  // q = p*h + y
+        const uint32_t p = fdiv(q, g.div_h), y = q - p * g.h;
+        const int e = (int)(e0 + el);
+        int ilo, ihi, jlo, jhi;
+        pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
+        const int n = jhi - jlo + 1;
+        bool touched = false;
+        for (int ci = ilo; ci <= ihi; ++ci) {
+            const uint32_t rb = p * ohw + (uint32_t)ci * g.ow + (uint32_t)jlo;
+            for (int m0 = 0; m0 < n; m0 += 4) {
+                int ix[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) ix[u] = il[rb + (uint32_t)min(m0 + u, n - 1)];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (m0 + u < n && ix[u] == e) {
+                        v += dl[rb + (uint32_t)(m0 + u)];
+                        touched = true;
+                    }
+                }
             }
         }
         if (touched) prev[e] = v;
@@ -355,15 +595,8 @@ __global__ __launch_bounds__(kBlock) void maxpool_plane_bwd_out_kernel(const flo
     int *il = reinterpret_cast<int *>(pl + hw);
     float *dl = pl + hw + ohw;
     float *dst = prev + (size_t)plane * hw;
-    if constexpr (VEC) {
-        for (uint32_t q = threadIdx.x; q < hw / 4; q += kBlock) plane_lds4[q] = reinterpret_cast<const float4 *>(dst)[q];
-    } else {
-        for (uint32_t q = threadIdx.x; q < hw; q += kBlock) pl[q] = dst[q];
-    }
-    for (uint32_t q = threadIdx.x; q < ohw; q += kBlock) {
-        il[q] = idx[(size_t)plane * ohw + q];
-        dl[q] = delta[(size_t)plane * ohw + q];
-    }
+    stage_to_lds<float, float4, VEC, kBlock>(pl, dst, hw);
+    stage_pair_to_lds<kBlock>(il, dl, idx + (size_t)plane * ohw, delta + (size_t)plane * ohw, ohw);
     __syncthreads();
     const int base = (int)(plane * hw);
     for (uint32_t o = threadIdx.x; o < ohw; o += kBlock) {
@@ -606,6 +839,19 @@ bool pool3s2_shape(const PoolGeom &g, bool backward) {
            g.oh > 0;
 }
 
+// Planes a workgroup of the several-planes kernels takes: about
+// DKZ_POOL_SEP_TARGET input elements (hw each), at most what fits in
+// kPlaneMaxFloats of LDS (lds_floats each), and few enough to leave
+// DKZ_POOL_SEP_MIN_GROUPS workgroups where the planes allow. 0: a plane
+// alone does not fit.
+uint32_t sep_planes(uint64_t planes, uint64_t hw, uint64_t lds_floats) {
+    if (hw == 0 || lds_floats == 0 || lds_floats > kPlaneMaxFloats) return 0;
+    uint64_t p = std::max<uint64_t>(1, DKZ_POOL_SEP_TARGET / hw);
+    p = std::min<uint64_t>(p, kPlaneMaxFloats / lds_floats);
+    p = std::min<uint64_t>(p, std::max<uint64_t>(1, planes / DKZ_POOL_SEP_MIN_GROUPS));
+    return (uint32_t)p;
+}
+
 // Validates the gpu.zig arguments and derives the geometry. `n` is out_n
 // (forward) or in_n (backward); the batch follows from it.
 int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, PoolGeom *g, uint64_t *planes,
@@ -668,6 +914,19 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
                       input, output, indexes, g, dq, lanes);
     }
     const uint64_t hw = (uint64_t)g.h * g.w;
+    if (DKZ_POOL_SEP && g.size >= DKZ_POOL_SEP_MIN_SIZE && planes >= DKZ_POOL_PLANE_MIN) {
+        const uint64_t lds_floats = hw + 2ull * g.h * g.ow;
+        const uint32_t P = sep_planes(planes, hw, lds_floats);
+        if (P > 0) {
+            const dim3 grid((uint32_t)div_up(planes, (uint64_t)P)), block(kSepBS);
+            const bool vec = aligned16(input) && ((uint64_t)P * hw) % 4 == 0;
+            (void)hipGetLastError();
+            hipLaunchKernelGGL(vec ? maxpool_sep_fwd_kernel<true> : maxpool_sep_fwd_kernel<false>, grid, block,
+                               (size_t)(P * lds_floats * sizeof(float)), current_stream(), input, output, indexes, g,
+                               (uint32_t)planes, P);
+            return after_launch("forward_maxpool_separable", grid, block);
+        }
+    }
     if (DKZ_POOL_PLANE && hw > 0 && hw <= kPlaneMaxFloats && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
         const size_t lds = (size_t)hw * sizeof(float);
@@ -734,6 +993,16 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
                           indexes, g, out_n, (uint32_t)in_n);
         return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
                       indexes, g, out_n, (uint32_t)in_n);
+    }
+    if (DKZ_POOL_S1_GATHER && per_dim > 2 && planes >= DKZ_POOL_PLANE_MIN) {
+        const uint32_t P = sep_planes(planes, per_plane, 2 * ohw);
+        if (P > 0) {
+            const dim3 grid((uint32_t)div_up(planes, (uint64_t)P)), block(kSepBS);
+            (void)hipGetLastError();
+            hipLaunchKernelGGL(maxpool_s1_gather_kernel, grid, block, (size_t)(P * 2 * ohw * sizeof(float)),
+                               current_stream(), delta, prev_delta, indexes, g, (uint32_t)planes, P);
+            return after_launch("backward_maxpool_gather", grid, block);
+        }
     }
     // Through LDS when more than 2x2 outputs can cover an input (2x2 windows
     // measured faster with the batched loads of maxpool_bwd_kernel).

@@ -165,7 +165,8 @@ MAXPOOL_CASES = [
     (1, 2, 7, 7, 3, 1, 2),        # darknet size=3 stride=1 (default pad size-1)
     (2, 2, 6, 10, 5, 3, 4),
     (256, 512, 28, 28, 2, 2, 1),  # config 5
-    # one workgroup per plane (at least 256 planes) with the plane in LDS:
+    # at least 256 planes: planes in LDS -- the separable forward and the stride-1
+    # gather where a plane's rows fit, else one workgroup a plane:
     (8, 64, 56, 56, 3, 2, 2),     # generic forward, float4 loads
     (86, 3, 9, 9, 2, 1, 1),       # plane of 81 floats: element loads
     (86, 3, 9, 9, 3, 1, 2),       # stride-1 backward through LDS, odd plane
@@ -189,6 +190,17 @@ MAXPOOL_CASES = [
     (2, 2, 9, 8, 3, 2, 1),        # offset 0, odd height
     (1, 1, 1, 8, 3, 2, 2),        # one input row: rows -1 and 1 outside
     (2, 3, 8, 12, 3, 2, 2),       # ow = 6: not a multiple of 4, the generic kernels
+    # several planes a workgroup (separable forward for windows of 4 and more,
+    # stride-1 gather backward for windows of 3 and more); the last workgroup
+    # holds fewer planes
+    (19, 79, 13, 13, 5, 1, 4),    # 2 planes a workgroup, 751 workgroups
+    (37, 83, 9, 9, 5, 1, 4),      # 5 planes of 81 floats: element loads
+    (37, 83, 9, 9, 3, 1, 2),      # the gather alone
+    (3, 683, 13, 13, 4, 1, 3),    # 4 planes: float4 loads, the last plane's tail in elements
+    (16, 64, 6, 6, 4, 1, 11),     # windows wholly outside the input: index -1
+    (16, 64, 9, 11, 5, 2, 4),     # stride 2
+    (8, 512, 19, 19, 13, 1, 12),  # spatial pyramid pooling's 13x13 window, 5 planes a workgroup
+    (8, 512, 19, 19, 9, 1, 8),
 ]
 
 
@@ -250,13 +262,14 @@ def _shared_peaks(batch, c, h, w, size, stride, pad, seed):
 @pytest.mark.parametrize("case", [(2, 3, 11, 13, 3, 2, 2), (2, 2, 12, 12, 5, 3, 4), (1, 2, 9, 9, 3, 1, 2),
                                   (2, 2, 10, 10, 4, 2, 2), (1, 2, 122, 122, 3, 2, 2), (86, 3, 11, 13, 3, 2, 2),
                                   (64, 4, 12, 12, 5, 3, 4), (86, 3, 9, 9, 3, 1, 2), (1, 2, 120, 120, 3, 2, 2),
-                                  (2, 3, 16, 16, 3, 2, 2), (1, 2, 12, 24, 3, 2, 1)], ids=str)
+                                  (2, 3, 16, 16, 3, 2, 2), (1, 2, 12, 24, 3, 2, 1), (128, 9, 9, 9, 3, 1, 2),
+                                  (128, 9, 11, 11, 5, 1, 4), (41, 50, 7, 7, 4, 1, 3)], ids=str)
 def test_maxpool_shared_argmax(dev, case):
     """Inputs that are the argmax of several outputs: the backward pass must
     add their deltas in ascending output order -- the output-per-lane kernel
     for stride >= 2 (few planes, or planes too large for LDS: 122x122), the
     plane-in-LDS kernels for at least 256 planes, the gather kernels for
-    stride 1, and the eight-inputs-a-lane 3x3/s2 kernel (120x120, 16x16,
+    stride 1 (several planes a workgroup from 1024 planes), and the eight-inputs-a-lane 3x3/s2 kernel (120x120, 16x16,
     12x24 with offset 0)."""
     batch, c, h, w, size, stride, pad = case
     oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
