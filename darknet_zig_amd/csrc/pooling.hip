@@ -98,6 +98,16 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #ifndef DKZ_POOL_S1_GATHER
 #define DKZ_POOL_S1_GATHER 1
 #endif
+// Stride-1 windows of 4, 5, 9 and 13 through the separable forward with
+// runs of outputs a lane and the window size compiled in. Measured on
+// [64,512,19,19], us: size 4 54.0 -> 44.1, 5 89.6 -> 48.0, 9 94.4 -> 61.0,
+// 13 121.4 -> 73.7; runs of 2 or 8 outputs were 7-23% slower than 4. The
+// same kernel for 2x2 and 3x3 lost to one workgroup a plane except on
+// planes of a few hundred elements (3x3/s1 [64,512,19,19] 64.4 -> 40.7,
+// 2x2/s1 [64,512,26,26] 54.8 -> 68.3, 3x3/s1 [64,128,56,56] 90.2 -> 99.3).
+#ifndef DKZ_POOL_SEP_RUN
+#define DKZ_POOL_SEP_RUN 1
+#endif
 // Elements (input plane elements) a workgroup of those kernels aims at, and
 // the fewest workgroups their grid keeps when there are enough planes.
 #ifndef DKZ_POOL_SEP_TARGET
@@ -456,6 +466,97 @@ __global__ __launch_bounds__(kSepBS) void maxpool_sep_fwd_kernel(const float *in
         const int a = best < 0 ? -1 : rarg[(p * g.h + (uint32_t)best) * g.ow + j];
         out[out0 + o] = mx;
         idx[out0 + o] = best < 0 ? -1 : (int)((plane0 + p) * hw + (uint32_t)best * g.w + (uint32_t)a);
+    }
+}
+
+// The separable forward for stride 1 and an S x S window known at compile
+// time, each lane taking a run of kRun consecutive outputs: in the row pass
+// kRun outputs of one input row from the kRun + S - 1 input values they
+// span, in the column pass kRun outputs of one output column from the
+// kRun + S - 1 row maxima they span, each value read from LDS once a run
+// instead of once a window. Taps outside the input read as -FLT_MAX, which
+// never beats the -FLT_MAX start under strict '>' -- the same as skipping
+// them. Each output's window is scanned on its own in the twin's order, so
+// the results are those of maxpool_sep_fwd_kernel.
+constexpr int kRun = 4;
+
+template <bool VEC, int S>
+__global__ __launch_bounds__(kSepBS) void maxpool_sep_run_fwd_kernel(const float *in, float *out, int *idx,
+                                                                     PoolGeom g, uint32_t planes, uint32_t P,
+                                                                     FastDiv div_ow_runs, FastDiv div_oh_runs) {
+    extern __shared__ float4 plane_lds4[];
+    constexpr int T = kRun + S - 1;
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow;
+    const uint32_t ow_runs = (g.ow + kRun - 1) / kRun, oh_runs = (g.oh + kRun - 1) / kRun;
+    float *pl = reinterpret_cast<float *>(plane_lds4);
+    float *rmax = pl + P * hw;                                   // [P*h][ow]
+    int *rarg = reinterpret_cast<int *>(rmax + P * g.h * g.ow);  // [P*h][ow]
+    stage_to_lds<float, float4, VEC, kSepBS>(pl, in + (size_t)plane0 * hw, np * hw);
+    __syncthreads();
+    const int w = (int)g.w, h = (int)g.h, hp = (int)g.half_pad;
+    for (uint32_t r = threadIdx.x; r < np * g.h * ow_runs; r += kSepBS) {
+        const uint32_t q = fdiv(r, div_ow_runs), j0 = (r - q * ow_runs) * kRun;  // q = p*h + y
+        const int c0 = (int)j0 - hp;
+        const float *row = pl + q * g.w;
+        float v[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = c0 + t;
+            const float x = row[min(max(c, 0), w - 1)];
+            v[t] = c >= 0 && c < w ? x : -FLT_MAX;
+        }
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            float mx = -FLT_MAX;
+            int a = -1;
+#pragma unroll
+            for (int m = 0; m < S; ++m) {
+                if (v[k + m] > mx) {
+                    mx = v[k + m];
+                    a = k + m;
+                }
+            }
+            if (j0 + k < g.ow) {
+                rmax[q * g.ow + j0 + k] = mx;
+                rarg[q * g.ow + j0 + k] = a < 0 ? -1 : c0 + a;
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < np * oh_runs * g.ow; r += kSepBS) {
+        const uint32_t q = fdiv(r, g.div_ow), j = r - q * g.ow;  // q = p*oh_runs + run
+        const uint32_t p = fdiv(q, div_oh_runs), i0 = (q - p * oh_runs) * kRun;
+        const int r0 = (int)i0 - hp;
+        const float *col = rmax + p * g.h * g.ow + j;
+        float v[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int ch = r0 + t;
+            const float x = col[(uint32_t)min(max(ch, 0), h - 1) * g.ow];
+            v[t] = ch >= 0 && ch < h ? x : -FLT_MAX;
+        }
+        const size_t o_plane = (size_t)(plane0 + p) * ohw;
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            float mx = -FLT_MAX;
+            int best = -1;
+#pragma unroll
+            for (int m = 0; m < S; ++m) {
+                if (v[k + m] > mx) {
+                    mx = v[k + m];
+                    best = k + m;
+                }
+            }
+            if (i0 + k < g.oh) {
+                // a row that won is inside the input and has a column
+                const uint32_t ch = best < 0 ? 0u : (uint32_t)(r0 + best);
+                const int a = rarg[(p * g.h + ch) * g.ow + j];
+                out[o_plane + (i0 + k) * g.ow + j] = mx;
+                idx[o_plane + (i0 + k) * g.ow + j] =
+                    best < 0 ? -1 : (int)((plane0 + p) * hw + ch * g.w + (uint32_t)a);
+            }
+        }
     }
 }
 
@@ -914,15 +1015,27 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
                       input, output, indexes, g, dq, lanes);
     }
     const uint64_t hw = (uint64_t)g.h * g.w;
+    const bool runs = DKZ_POOL_SEP_RUN && g.stride == 1 && (g.size == 4 || g.size == 5 || g.size == 9 || g.size == 13);
     if (DKZ_POOL_SEP && g.size >= DKZ_POOL_SEP_MIN_SIZE && planes >= DKZ_POOL_PLANE_MIN) {
         const uint64_t lds_floats = hw + 2ull * g.h * g.ow;
         const uint32_t P = sep_planes(planes, hw, lds_floats);
         if (P > 0) {
             const dim3 grid((uint32_t)div_up(planes, (uint64_t)P)), block(kSepBS);
             const bool vec = aligned16(input) && ((uint64_t)P * hw) % 4 == 0;
+            const size_t lds = (size_t)(P * lds_floats * sizeof(float));
             (void)hipGetLastError();
+            if (runs) {
+                const FastDiv dor = make_fastdiv(div_up(g.ow, kRun)), dohr = make_fastdiv(div_up(g.oh, kRun));
+                auto k = vec ? maxpool_sep_run_fwd_kernel<true, 4> : maxpool_sep_run_fwd_kernel<false, 4>;
+                if (g.size == 5) k = vec ? maxpool_sep_run_fwd_kernel<true, 5> : maxpool_sep_run_fwd_kernel<false, 5>;
+                if (g.size == 9) k = vec ? maxpool_sep_run_fwd_kernel<true, 9> : maxpool_sep_run_fwd_kernel<false, 9>;
+                if (g.size == 13) k = vec ? maxpool_sep_run_fwd_kernel<true, 13> : maxpool_sep_run_fwd_kernel<false, 13>;
+                hipLaunchKernelGGL(k, grid, block, lds, current_stream(), input, output, indexes, g, (uint32_t)planes,
+                                   P, dor, dohr);
+                return after_launch("forward_maxpool_separable", grid, block);
+            }
             hipLaunchKernelGGL(vec ? maxpool_sep_fwd_kernel<true> : maxpool_sep_fwd_kernel<false>, grid, block,
-                               (size_t)(P * lds_floats * sizeof(float)), current_stream(), input, output, indexes, g,
+                               lds, current_stream(), input, output, indexes, g,
                                (uint32_t)planes, P);
             return after_launch("forward_maxpool_separable", grid, block);
         }

@@ -199,6 +199,7 @@ MAXPOOL_CASES = [
     (3, 683, 13, 13, 4, 1, 3),    # 4 planes: float4 loads, the last plane's tail in elements
     (16, 64, 6, 6, 4, 1, 11),     # windows wholly outside the input: index -1
     (16, 64, 9, 11, 5, 2, 4),     # stride 2
+    (32, 40, 11, 11, 7, 1, 6),    # a window size not compiled into the runs-a-lane kernel
     (8, 512, 19, 19, 13, 1, 12),  # spatial pyramid pooling's 13x13 window, 5 planes a workgroup
     (8, 512, 19, 19, 9, 1, 8),
 ]
