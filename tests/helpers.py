@@ -139,7 +139,8 @@ def softmax_f64(x: np.ndarray, n, batch, batch_offset, groups, group_offset, str
     v = x[idx].astype(np.float32)
     mx = np.maximum(np.max(v, axis=1, keepdims=True), np.float32(-np.finfo(np.float32).max))
     t = np.float32(temp)
-    a = (v / t - mx / t).astype(np.float32)
+    with np.errstate(invalid="ignore"):  # inf - inf in rows holding infinities, as in the twin
+        a = (v / t - mx / t).astype(np.float32)
     e = np.exp(a.astype(np.float64))
     out = np.full(x.shape, np.nan)
     out[idx] = e / e.sum(axis=1, keepdims=True)
