@@ -108,6 +108,19 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #ifndef DKZ_POOL_SEP_RUN
 #define DKZ_POOL_SEP_RUN 1
 #endif
+// The stride-1 gather from windows of DKZ_POOL_GATHER_MIN_DIM; windows of
+// 2, 3, 4, 5, 9 and 13 with runs of inputs a lane and the window size
+// compiled in. Measured, us: [64,512,19,19] size 5 137.1 -> 61.0, 9 283.8
+// -> 132.8, 13 463.5 -> 254.4, 3x3/s1 [64,128,56,56] 155.3 -> 100.6, and
+// for 2x2 against one lane an input over global memory [64,256,13,13] 16.7
+// -> 14.6, [64,512,26,26] 117.0 -> 66.7; runs of 2 or 8 inputs were
+// 2-63% slower than 4.
+#ifndef DKZ_POOL_GATHER_MIN_DIM
+#define DKZ_POOL_GATHER_MIN_DIM 2
+#endif
+#ifndef DKZ_POOL_RUN_GATHER
+#define DKZ_POOL_RUN_GATHER 1
+#endif
 // Elements (input plane elements) a workgroup of those kernels aims at, and
 // the fewest workgroups their grid keeps when there are enough planes.
 #ifndef DKZ_POOL_SEP_TARGET
@@ -622,6 +635,95 @@ __global__ __launch_bounds__(kSepBS) void maxpool_s1_gather_kernel(const float *
     }
 }
 
+// The stride-1 gather for an S x S window known at compile time, each lane
+// taking a run of kRunG consecutive inputs of one row: for each candidate
+// output row (ascending) the kRunG + S - 1 candidate columns' indexes and
+// deltas are read from LDS once for the run, and each input adds, in
+// ascending column order, the deltas whose index names it -- selected, not
+// branched on, so a candidate costs a compare, an add and a select. The
+// order of the adds is maxpool_s1_gather_kernel's (the twin's), and an
+// input is written only where some output names it. prev_delta of the
+// lane's next run is loaded while the current one gathers.
+constexpr int kRunG = 4;
+
+template <int S>
+__global__ __launch_bounds__(kSepBS) void maxpool_s1_run_gather_kernel(const float *delta, float *prev,
+                                                                       const int *idx, PoolGeom g, uint32_t planes,
+                                                                       uint32_t P, FastDiv div_w_runs) {
+    extern __shared__ float4 plane_lds4[];
+    constexpr int T = kRunG + S - 1;
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow, w_runs = (g.w + kRunG - 1) / kRunG;
+    int *il = reinterpret_cast<int *>(plane_lds4);  // [P][oh][ow]
+    float *dl = reinterpret_cast<float *>(plane_lds4) + P * ohw;
+    const size_t o0 = (size_t)plane0 * ohw;
+    stage_pair_to_lds<kSepBS>(il, dl, idx + o0, delta + o0, np * ohw);
+    const uint32_t e0 = plane0 * hw, n_el = np * hw, n_runs = np * g.h * w_runs;
+    const int hp = (int)g.half_pad, oh = (int)g.oh, ow = (int)g.ow;
+    // the lane's first run's prev_delta, in flight across the barrier
+    auto run_elems = [&](uint32_t r, uint32_t *el) {
+        const uint32_t q = fdiv(r, div_w_runs), x0 = (r - q * w_runs) * kRunG;  // q = p*h + y
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k) el[k] = q * g.w + x0 + k;  // x0 + k may pass the row's end
+    };
+    float pn[kRunG];
+    {
+        const uint32_t r = min(threadIdx.x, n_runs - 1);
+        uint32_t el[kRunG];
+        run_elems(r, el);
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k) pn[k] = prev[e0 + min(el[k], n_el - 1)];
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (uint32_t r = threadIdx.x; r < n_runs; r += kSepBS) {
+        float v[kRunG];
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k) v[k] = pn[k];
+        {
+            uint32_t el[kRunG];
+            run_elems(min(r + kSepBS, n_runs - 1), el);
+#pragma unroll
+            for (int k = 0; k < kRunG; ++k) pn[k] = prev[e0 + min(el[k], n_el - 1)];
+        }
+        const uint32_t q = fdiv(r, div_w_runs), x0 = (r - q * w_runs) * kRunG;
+        const uint32_t p = fdiv(q, g.div_h), y = q - p * g.h;
+        const int jb = (int)x0 + hp - S + 1;  // candidate column of t = 0
+        const int ilo = max((int)y + hp - S + 1, 0), ihi = min((int)y + hp, oh - 1);
+        int e[kRunG];
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k) e[k] = (int)(e0 + q * g.w + x0 + k);
+        bool touched[kRunG];
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k) touched[k] = false;
+        for (int ci = ilo; ci <= ihi; ++ci) {
+            const int *irow = il + p * ohw + (uint32_t)ci * g.ow;
+            const float *drow = dl + p * ohw + (uint32_t)ci * g.ow;
+            int ix[T];
+            float d[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int j = jb + t;
+                const uint32_t jc = (uint32_t)min(max(j, 0), ow - 1);
+                ix[t] = j >= 0 && j < ow ? irow[jc] : -1;  // -1 names no input
+                d[t] = drow[jc];
+            }
+#pragma unroll
+            for (int k = 0; k < kRunG; ++k) {
+#pragma unroll
+                for (int m = 0; m < S; ++m) {
+                    const bool hit = ix[k + m] == e[k];
+                    v[k] = hit ? v[k] + d[k + m] : v[k];
+                    touched[k] = touched[k] || hit;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kRunG; ++k)
+            if (touched[k] && x0 + k < g.w) prev[e[k]] = v[k];
+    }
+}
+
 // Backward, one lane per output (stride >= 2, where outputs are a quarter of
 // the inputs or fewer): output o names input t = idx[o]. Of the outputs that
 // name t, the lowest o -- the first to add into t in the twin's ascending
@@ -1107,18 +1209,33 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
         return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
                       indexes, g, out_n, (uint32_t)in_n);
     }
-    if (DKZ_POOL_S1_GATHER && per_dim > 2 && planes >= DKZ_POOL_PLANE_MIN) {
+    if (DKZ_POOL_S1_GATHER && per_dim >= DKZ_POOL_GATHER_MIN_DIM && planes >= DKZ_POOL_PLANE_MIN) {
         const uint32_t P = sep_planes(planes, per_plane, 2 * ohw);
         if (P > 0) {
             const dim3 grid((uint32_t)div_up(planes, (uint64_t)P)), block(kSepBS);
+            const size_t lds = (size_t)(P * 2 * ohw * sizeof(float));
             (void)hipGetLastError();
-            hipLaunchKernelGGL(maxpool_s1_gather_kernel, grid, block, (size_t)(P * 2 * ohw * sizeof(float)),
-                               current_stream(), delta, prev_delta, indexes, g, (uint32_t)planes, P);
+            if (DKZ_POOL_RUN_GATHER && (g.size == 2 || g.size == 3 || g.size == 4 || g.size == 5 || g.size == 9 ||
+                                        g.size == 13)) {
+                const FastDiv dwr = make_fastdiv(div_up(g.w, kRunG));
+                auto k = maxpool_s1_run_gather_kernel<3>;
+                if (g.size == 2) k = maxpool_s1_run_gather_kernel<2>;
+                if (g.size == 4) k = maxpool_s1_run_gather_kernel<4>;
+                if (g.size == 5) k = maxpool_s1_run_gather_kernel<5>;
+                if (g.size == 9) k = maxpool_s1_run_gather_kernel<9>;
+                if (g.size == 13) k = maxpool_s1_run_gather_kernel<13>;
+                hipLaunchKernelGGL(k, grid, block, lds, current_stream(), delta, prev_delta, indexes, g,
+                                   (uint32_t)planes, P, dwr);
+                return after_launch("backward_maxpool_gather", grid, block);
+            }
+            hipLaunchKernelGGL(maxpool_s1_gather_kernel, grid, block, lds, current_stream(), delta, prev_delta,
+                               indexes, g, (uint32_t)planes, P);
             return after_launch("backward_maxpool_gather", grid, block);
         }
     }
-    // Through LDS when more than 2x2 outputs can cover an input (2x2 windows
-    // measured faster with the batched loads of maxpool_bwd_kernel).
+    // Otherwise through LDS when more than 2x2 outputs can cover an input
+    // (2x2 windows measured faster with the batched loads of
+    // maxpool_bwd_kernel).
     if (DKZ_POOL_PLANE && per_dim > 2 && ohw <= kPlaneMaxFloats / 2 && planes >= DKZ_POOL_PLANE_MIN) {
         const dim3 pgrid((uint32_t)planes), block(kBlock);
         (void)hipGetLastError();

@@ -199,7 +199,9 @@ MAXPOOL_CASES = [
     (3, 683, 13, 13, 4, 1, 3),    # 4 planes: float4 loads, the last plane's tail in elements
     (16, 64, 6, 6, 4, 1, 11),     # windows wholly outside the input: index -1
     (16, 64, 9, 11, 5, 2, 4),     # stride 2
-    (32, 40, 11, 11, 7, 1, 6),    # a window size not compiled into the runs-a-lane kernel
+    (32, 40, 11, 11, 7, 1, 6),    # a window size not compiled into the runs-a-lane kernels
+    (4, 512, 13, 13, 2, 1, 1),    # a tiny-YOLO [maxpool] size=2 stride=1: the 2x2 gather, 4 planes a workgroup
+    (41, 50, 7, 7, 2, 1, 1),      # 2x2/s1 with the last workgroup's planes ragged
     (8, 512, 19, 19, 13, 1, 12),  # spatial pyramid pooling's 13x13 window, 5 planes a workgroup
     (8, 512, 19, 19, 9, 1, 8),
 ]
@@ -264,7 +266,8 @@ def _shared_peaks(batch, c, h, w, size, stride, pad, seed):
                                   (2, 2, 10, 10, 4, 2, 2), (1, 2, 122, 122, 3, 2, 2), (86, 3, 11, 13, 3, 2, 2),
                                   (64, 4, 12, 12, 5, 3, 4), (86, 3, 9, 9, 3, 1, 2), (1, 2, 120, 120, 3, 2, 2),
                                   (2, 3, 16, 16, 3, 2, 2), (1, 2, 12, 24, 3, 2, 1), (128, 9, 9, 9, 3, 1, 2),
-                                  (128, 9, 11, 11, 5, 1, 4), (41, 50, 7, 7, 4, 1, 3)], ids=str)
+                                  (128, 9, 11, 11, 5, 1, 4), (41, 50, 7, 7, 4, 1, 3), (64, 20, 12, 12, 7, 1, 6),
+                                  (41, 50, 7, 7, 2, 1, 1)], ids=str)
 def test_maxpool_shared_argmax(dev, case):
     """Inputs that are the argmax of several outputs: the backward pass must
     add their deltas in ascending output order -- the output-per-lane kernel
