@@ -724,6 +724,23 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         [lambda d=d, p=p, x=x: gpu.backwardMaxpool(gin, gh, gh, gc, gst, gsz, gpad, d, p, x)
          for d, p, x in zip(gouts, gins, gidx)])
     dev.free()
+    # spatial pyramid pooling's stride-1 windows (5 and 13, offset -(size-1)/2)
+    dev = Device(gpu)
+    qb, qc, qh = 64, 512, 19
+    qn = qb * qc * qh * qh
+    R = rotations(4 * 3 * qn)
+    qins = [dev.up(r.uniform(-1, 1, qn).astype(np.float32)) for _ in range(R)]
+    qouts = [dev.zeros(qn) for _ in range(R)]
+    qidx = [dev.zeros(qn) for _ in range(R)]
+    cfg = f"pool[{qb},{qc},{qh},{qh}]"
+    for qs in (5, 13):
+        add(cfg, f"maxpool_fwd {qs}x{qs}/s1", 4 * 3 * qn,
+            [lambda i=i, o=o, x=x, qs=qs: gpu.forwardMaxpool(qn, qh, qh, qc, 1, qs, qs - 1, i, o, x)
+             for i, o, x in zip(qins, qouts, qidx)])
+        add(cfg, f"maxpool_bwd {qs}x{qs}/s1", 4 * 4 * qn,
+            [lambda d=d, p=p, x=x, qs=qs: gpu.backwardMaxpool(qn, qh, qh, qc, 1, qs, qs - 1, d, p, x)
+             for d, p, x in zip(qouts, qins, qidx)])
+    dev.free()
     dev = Device(gpu)
     sb, sc, ss = 64, 85, 169
     sn = sb * sc * ss
