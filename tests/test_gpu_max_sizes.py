@@ -16,7 +16,8 @@ reductions against the oracle and f64 sums of the whole downloaded tensor
   * softmax over [2147483, 1000] (the grid-stride segment kernel);
   * 2x2/s2 max pooling forward and backward, global average pooling forward
     and backward at [63, 512, 256, 256] (2^31 - 2^25 inputs; argmax indexes
-    up to 2113929215).
+    up to 2113929215);
+  * stride-1 max pooling (sizes 13 and 7) at [11618, 512, 19, 19].
 """
 
 from __future__ import annotations
@@ -196,4 +197,39 @@ def test_pooling_at_max_elements(dev):
                       f"avgpool fwd plane {p}")
     finally:
         for b in (x, out, idx, d, prev, avg, od):
+            gpu.free(b)
+
+
+@pytest.mark.parametrize("size", [13, 7])
+def test_stride1_pooling_at_max_elements(dev, size):
+    """Spatial pyramid pooling's stride-1 windows at [11618, 512, 19, 19]
+    (2147378176 inputs): size 13 through the separable forward with runs
+    of outputs a lane and the gather with runs of inputs a lane, size 7
+    through the separable forward and the gather without them; the first
+    and last planes against the oracle, bit-exact."""
+    B, C, H, W = 11618, 512, 19, 19
+    pad = size - 1
+    planes, hw = B * C, H * W
+    ohw = ref.maxpool_out_dim(H, size, 1, pad) * ref.maxpool_out_dim(W, size, 1, pad)
+    n_in, n_out = planes * hw, planes * ohw
+    assert n_in <= N_MAX
+    print(f"stride-1 max pooling, size {size}, at [{B}, {C}, {H}, {W}]: {n_in} inputs", flush=True)
+    x, out, idx = gpu.alloc(n_in), gpu.alloc(n_out), gpu.allocInts(n_out)
+    d, prev = gpu.alloc(n_out), gpu.alloc(n_in)
+    try:
+        gpu.randUniform(n_in, x, 90 + size)
+        gpu.forwardMaxpool(n_out, H, W, C, 1, size, pad, x, out, idx)
+        gpu.randUniform(n_out, d, 91 + size)
+        gpu.backwardMaxpool(n_in, H, W, C, 1, size, pad, d, prev, idx)
+        for p in (0, 1, planes - 2, planes - 1):
+            xp = _pull(x, p * hw, hw)
+            o_c, i_c = np.empty(ohw, np.float32), np.empty(ohw, np.int32)
+            ref.forwardMaxpool(1, H, W, 1, size, 1, pad, xp, o_c, i_c)  # indexes within the plane
+            assert_bitexact(_pull(out, p * ohw, ohw), o_c, f"maxpool fwd plane {p}")
+            assert_bitexact(_pull(idx, p * ohw, ohw, np.int32), i_c + np.int32(p * hw), f"maxpool idx plane {p}")
+            prev_c = np.zeros(hw, np.float32)
+            ref.backwardMaxpool(i_c, _pull(d, p * ohw, ohw), prev_c)
+            assert_bitexact(_pull(prev, p * hw, hw), prev_c, f"maxpool bwd plane {p}")
+    finally:
+        for b in (x, out, idx, d, prev):
             gpu.free(b)
