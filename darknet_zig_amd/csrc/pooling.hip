@@ -23,8 +23,8 @@
 // first of those over the window's rows (2*size taps an output instead of
 // size^2, the same first maximum). Smaller windows take one workgroup a
 // plane, every window scanned from the plane in LDS. The stride-1 backward
-// with windows wider than 2 stages the indexes and deltas of several planes
-// a workgroup before its gather; with stride >= 2 one workgroup a plane
+// stages the indexes and deltas of several planes a workgroup before its
+// gather; with stride >= 2 one workgroup a plane
 // stages the plane of prev_delta with them, updates it in LDS and writes it
 // back whole.
 //
@@ -83,12 +83,13 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #endif
 // The several-planes-a-workgroup kernels (build-time switches, for
 // measurement): the separable forward for windows of at least
-// DKZ_POOL_SEP_MIN_SIZE, the stride-1 gather backward for windows of 3 and
-// more. Measured on [64,512,19,19] stride 1, forward / backward us against
-// one workgroup a plane: size 5 120.6 / 162.8 -> 89.8 / 138.2, size 13
-// 461.9 / 544.6 -> 120.0 / 465.3; the separable forward lost on 2x2/s1
-// [64,512,26,26] (53.4 -> 90.5) and 3x3/s1 [64,128,56,56] (90.6 -> 120.1),
-// the gather on 2x2/s1 [64,256,13,13] (17.0 -> 20.3).
+// DKZ_POOL_SEP_MIN_SIZE, the stride-1 gather backward for windows of at
+// least DKZ_POOL_GATHER_MIN_DIM. Measured on [64,512,19,19] stride 1,
+// forward / backward us against one workgroup a plane: size 5 120.6 / 162.8
+// -> 89.8 / 138.2, size 13 461.9 / 544.6 -> 120.0 / 465.3; the separable
+// forward lost on 2x2/s1 [64,512,26,26] (53.4 -> 90.5) and 3x3/s1
+// [64,128,56,56] (90.6 -> 120.1), the gather without runs (below) on 2x2/s1
+// [64,256,13,13] (17.0 -> 20.3).
 #ifndef DKZ_POOL_SEP
 #define DKZ_POOL_SEP 1
 #endif
