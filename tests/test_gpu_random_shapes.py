@@ -4,9 +4,9 @@ passes over random (batch, filters, spatial) -- every residue of spatial mod
 4, filters on both sides of the one-launch/split thresholds, ragged last
 chunks --, elementwise ops over random lengths and misaligned views, the
 convolution lowering over random geometries, the GEMM over random shapes,
-transposes and leading dimensions, and the whole-batch convolution forward,
+transposes and leading dimensions, the whole-batch convolution forward,
 weight gradient and data gradient over random layers (groups, ksize, stride,
-pad). The shapes are drawn once from a fixed seed, so a failure names a
+pad), and max pooling over random windows, strides, pads and plane counts. The shapes are drawn once from a fixed seed, so a failure names a
 reproducible case."""
 
 from __future__ import annotations
@@ -61,6 +61,28 @@ def _large_bn():
 
 
 LARGE_BN = sorted({_large_bn() for _ in range(5)})
+
+_P = np.random.default_rng(20261202)
+
+
+def _pool():
+    """batch, channels, height, width, size, stride, pad with the window
+    inside the padded input; planes below 256 (per-output and per-input
+    kernels), from 256 (planes in LDS, a plane a workgroup) and from 1024
+    (several planes a workgroup), under about 2 M inputs."""
+    while True:
+        size, stride = int(_P.choice([1, 2, 2, 3, 3, 4, 5, 6, 7, 9, 13])), int(_P.choice([1, 1, 1, 2, 3]))
+        h, w, pad = int(_P.integers(1, 41)), int(_P.integers(1, 41)), int(_P.integers(0, size + 3))
+        if h + pad < size or w + pad < size:
+            continue
+        planes = int(_P.choice([int(_P.integers(1, 256)), int(_P.integers(256, 1024)), int(_P.integers(1024, 5000))]))
+        if planes * h * w > 2_000_000:
+            continue
+        c = int(_P.choice([1, 3, 7, 16]))
+        return max(1, planes // c), c, h, w, size, stride, pad
+
+
+POOLS = sorted({_pool() for _ in range(28)})
 
 
 @pytest.mark.parametrize("shape", CHANNEL_SHAPES, ids=str)
@@ -171,6 +193,36 @@ def test_elementwise(dev, n):
     assert_bitexact(got[off:], cpu, "axpy")
     gpu.free(whole_a)
     gpu.free(whole_b)
+
+
+@pytest.mark.parametrize("case", POOLS, ids=str)
+def test_maxpool(dev, case):
+    """Max pooling over random geometries, bit-exact: inputs drawn from 16
+    levels (ties everywhere: the first maximum must win) with a NaN and a
+    -inf, and deltas over six decades so that adding an input's deltas in
+    another order changes the rounded result."""
+    batch, c, h, w, size, stride, pad = case
+    oh, ow = ref.maxpool_out_dim(h, size, stride, pad), ref.maxpool_out_dim(w, size, stride, pad)
+    r = rng(sum(case))
+    x = (np.floor(uniform(r, batch * c * h * w, 0, 16)) - 8).astype(np.float32)
+    x[min(5, x.size - 1)] = np.nan
+    x[min(11, x.size - 1)] = -np.inf
+    out_n = batch * c * oh * ow
+    out_c, idx_c = np.empty(out_n, np.float32), np.empty(out_n, np.int32)
+    ref.forwardMaxpool(batch, h, w, c, size, stride, pad, x, out_c, idx_c)
+    dx, dout, didx = up(x), gpu.alloc(out_n), gpu.allocInts(out_n)
+    gpu.forwardMaxpool(out_n, h, w, c, stride, size, pad, dx, dout, didx)
+    assert_bitexact(down(dout, out_c), out_c, f"maxpool fwd {case}")
+    assert_bitexact(down(didx, idx_c), idx_c, f"maxpool idx {case}")
+    delta = (normal(r, out_n) * np.float32(10.0) ** uniform(r, out_n, -3, 3)).astype(np.float32)
+    prev = normal(r, x.size)
+    prev_c = prev.copy()
+    ref.backwardMaxpool(idx_c, delta, prev_c)
+    dd, dprev = up(delta), up(prev)
+    gpu.backwardMaxpool(x.size, h, w, c, stride, size, pad, dd, dprev, didx)
+    assert_bitexact(down(dprev, prev), prev_c, f"maxpool bwd {case}")
+    for b in (dx, dout, didx, dd, dprev):
+        gpu.free(b)
 
 
 @pytest.mark.parametrize("C,H,W,k,s,p", CONV)
