@@ -122,6 +122,22 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #ifndef DKZ_POOL_RUN_GATHER
 #define DKZ_POOL_RUN_GATHER 1
 #endif
+// The stride-1 backward through its targets only (the inputs some output
+// names), from windows of DKZ_POOL_TARGETS_MIN_DIM. Measured against the
+// gather with runs, us: [64,512,19,19] size 5 61.3 -> 53.1, 9 133.9 ->
+// 80.2, 13 257.6 -> 121.4; it lost at size 4 (50.6 -> 53.1), 3 (42.1 ->
+// 48.2) and 2 ([64,512,26,26] 67.4 -> 93.0), where most inputs are targets.
+// Then a lane a target with consecutive targets on consecutive lanes and
+// the candidates' deltas loaded with their indexes (a select, no branch):
+// size 5 51.6-53.0, 9 66.8, 13 83.1; the targets spread over a workgroup's
+// four waves instead cost VALU issue (13: 106.3). From size 4 or 3 it tied
+// (48.2 against 49.3) and lost (46.3 against 41.7).
+#ifndef DKZ_POOL_S1_TARGETS
+#define DKZ_POOL_S1_TARGETS 1
+#endif
+#ifndef DKZ_POOL_TARGETS_MIN_DIM
+#define DKZ_POOL_TARGETS_MIN_DIM 5
+#endif
 // Elements (input plane elements) a workgroup of those kernels aims at, and
 // the fewest workgroups their grid keeps when there are enough planes.
 #ifndef DKZ_POOL_SEP_TARGET
@@ -633,6 +649,76 @@ __global__ __launch_bounds__(kSepBS) void maxpool_s1_gather_kernel(const float *
             }
         }
         if (touched) prev[e] = v;
+    }
+}
+
+// The stride-1 backward through the inputs that some output names ("targets"),
+// P planes a workgroup: the planes' indexes and deltas are staged in LDS,
+// each output marks its index in an LDS array of the planes' inputs (an
+// exchange, so that exactly one marker appends the input to a list of
+// targets), and a lane a target then gathers as maxpool_s1_gather_kernel
+// does -- candidate outputs in ascending order, each delta whose index
+// names the target added to its prev_delta. Inputs that no output names are
+// neither read nor written; with large windows they are nearly all of them
+// (a 13x13 window's maximum is shared by many outputs), so the size^2
+// candidate checks run for a few inputs a plane instead of every one. Which
+// lane takes which target varies from run to run; what each target receives,
+// and in which order, does not.
+// TB: candidates of a window row whose indexes and deltas are loaded
+// together (the host takes 4 or 8, whichever loads fewer for the window's
+// width, 8 on a tie).
+template <int TB>
+__global__ __launch_bounds__(kSepBS) void maxpool_s1_target_gather_kernel(const float *delta, float *prev,
+                                                                          const int *idx, PoolGeom g,
+                                                                          uint32_t planes, uint32_t P) {
+    extern __shared__ float4 plane_lds4[];
+    __shared__ uint32_t n_targets;
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow, n_el = np * hw, n_out = np * ohw;
+    int *il = reinterpret_cast<int *>(plane_lds4);                   // [P][oh][ow]
+    float *dl = reinterpret_cast<float *>(plane_lds4) + P * ohw;     // [P][oh][ow]
+    uint32_t *mark = reinterpret_cast<uint32_t *>(dl + P * ohw);     // [P][h][w]
+    uint32_t *list = mark + P * hw;                                  // the targets, plane-relative
+    const size_t o0 = (size_t)plane0 * ohw;
+    const uint32_t e0 = plane0 * hw;
+    for (uint32_t q = threadIdx.x; q < n_el; q += kSepBS) mark[q] = 0u;
+    if (threadIdx.x == 0) n_targets = 0u;
+    stage_pair_to_lds<kSepBS>(il, dl, idx + o0, delta + o0, n_out);
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < n_out; o += kSepBS) {
+        const int64_t t = (int64_t)il[o] - (int64_t)e0;  // -1 and other planes' inputs fall outside
+        if (t >= 0 && t < (int64_t)n_el && atomicExch(&mark[t], 1u) == 0u) list[atomicAdd(&n_targets, 1u)] = (uint32_t)t;
+    }
+    __syncthreads();
+    const uint32_t nt = n_targets;
+    // consecutive lanes take consecutive targets: a workgroup's few targets
+    // fill as few waves as they can, whose candidate scans then cost the
+    // least VALU issue
+    for (uint32_t k = threadIdx.x; k < nt; k += kSepBS) {
+        const uint32_t el = list[k];
+        const uint32_t q = fdiv(el, g.div_w), x = el - q * g.w;  // q = p*h + y
+        const uint32_t p = fdiv(q, g.div_h), y = q - p * g.h;
+        const int e = (int)(e0 + el);
+        float v = prev[e];
+        int ilo, ihi, jlo, jhi;
+        pool_candidates(y, x, g, ilo, ihi, jlo, jhi);
+        const int n = jhi - jlo + 1;
+        for (int ci = ilo; ci <= ihi; ++ci) {
+            const uint32_t rb = p * ohw + (uint32_t)ci * g.ow + (uint32_t)jlo;
+            for (int m0 = 0; m0 < n; m0 += TB) {
+                int ix[TB];
+                float d[TB];
+#pragma unroll
+                for (int u = 0; u < TB; ++u) {
+                    const uint32_t c = rb + (uint32_t)min(m0 + u, n - 1);
+                    ix[u] = il[c];
+                    d[u] = dl[c];
+                }
+#pragma unroll
+                for (int u = 0; u < TB; ++u) v = m0 + u < n && ix[u] == e ? v + d[u] : v;
+            }
+        }
+        prev[e] = v;  // a target: some output names it
     }
 }
 
@@ -1209,6 +1295,19 @@ int dkz_backward_maxpool(int in_n, int in_h, int in_w, int in_c, int stride, int
                           indexes, g, out_n, (uint32_t)in_n);
         return launch("backward_maxpool", maxpool_bwd_out_kernel<9>, ogrid, dim3(kBlock), delta, prev_delta,
                       indexes, g, out_n, (uint32_t)in_n);
+    }
+    if (DKZ_POOL_S1_TARGETS && per_dim >= DKZ_POOL_TARGETS_MIN_DIM && planes >= DKZ_POOL_PLANE_MIN) {
+        const uint32_t P = sep_planes(planes, per_plane, 2 * ohw + 2 * per_plane);
+        if (P > 0) {
+            const dim3 grid((uint32_t)div_up(planes, (uint64_t)P)), block(kSepBS);
+            (void)hipGetLastError();
+            const uint32_t w8 = div_up(g.size, 8) * 8, w4 = div_up(g.size, 4) * 4;
+            hipLaunchKernelGGL(w8 <= w4 ? maxpool_s1_target_gather_kernel<8> : maxpool_s1_target_gather_kernel<4>,
+                               grid, block,
+                               (size_t)(P * (2 * ohw + 2 * per_plane) * sizeof(float)), current_stream(), delta,
+                               prev_delta, indexes, g, (uint32_t)planes, P);
+            return after_launch("backward_maxpool_targets", grid, block);
+        }
     }
     if (DKZ_POOL_S1_GATHER && per_dim >= DKZ_POOL_GATHER_MIN_DIM && planes >= DKZ_POOL_PLANE_MIN) {
         const uint32_t P = sep_planes(planes, per_plane, 2 * ohw);
