@@ -201,6 +201,8 @@ MAXPOOL_CASES = [
     (16, 64, 9, 11, 5, 2, 4),     # stride 2
     (32, 40, 11, 11, 7, 1, 6),    # a window size not compiled into the runs-a-lane kernels
     (4, 512, 13, 13, 2, 1, 1),    # a tiny-YOLO [maxpool] size=2 stride=1: the 2x2 gather, 4 planes a workgroup
+    (2, 128, 60, 60, 7, 1, 6),    # planes too large for the targets-only backward: the gather without runs
+    (2, 128, 60, 60, 5, 1, 4),    # the same with runs of inputs a lane
     (41, 50, 7, 7, 2, 1, 1),      # 2x2/s1 with the last workgroup's planes ragged
     (8, 512, 19, 19, 13, 1, 12),  # spatial pyramid pooling's 13x13 window, 5 planes a workgroup
     (8, 512, 19, 19, 9, 1, 8),
