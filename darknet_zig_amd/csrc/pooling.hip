@@ -109,6 +109,13 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #ifndef DKZ_POOL_SEP_RUN
 #define DKZ_POOL_SEP_RUN 1
 #endif
+// Those windows through blocks of `size` outputs a lane with prefix and
+// suffix maxima instead of runs of 4. Measured on [64,512,19,19], us: size
+// 4 43.8 -> 42.3, 5 47.7 -> 43.7, 9 61.9 -> 61.2 (a 19-wide line is two
+// full blocks of 9 and one of 1), 13 76.3 -> 53.2.
+#ifndef DKZ_POOL_BLOCKS
+#define DKZ_POOL_BLOCKS 1
+#endif
 // The stride-1 gather from windows of DKZ_POOL_GATHER_MIN_DIM; windows of
 // 2, 3, 4, 5, 9 and 13 with runs of inputs a lane and the window size
 // compiled in. Measured, us: [64,512,19,19] size 5 137.1 -> 61.0, 9 283.8
@@ -583,6 +590,131 @@ __global__ __launch_bounds__(kSepBS) void maxpool_sep_run_fwd_kernel(const float
                 const uint32_t ch = best < 0 ? 0u : (uint32_t)(r0 + best);
                 const int a = rarg[(p * g.h + ch) * g.ow + j];
                 out[o_plane + (i0 + k) * g.ow + j] = mx;
+                idx[o_plane + (i0 + k) * g.ow + j] =
+                    best < 0 ? -1 : (int)((plane0 + p) * hw + ch * g.w + (uint32_t)a);
+            }
+        }
+    }
+}
+
+// The separable forward for stride 1 and an S x S window known at compile
+// time, each lane taking a block of S consecutive outputs of a line (an
+// input row in the row pass, an output column in the column pass) from the
+// 2S values from the block's first window start: the suffix maxima of the
+// first S values and the prefix maxima of the next S, so that the window
+// starting k into the block is the suffix from k joined with the prefix up
+// to k - 1 -- about three selects a value and three an output, whatever S
+// (van Herk's and Gil and Werman's sliding maximum). The twin's first
+// maximum is kept: the suffix scan (right to left) moves to an equal value
+// once it holds one, the prefix scan (left to right) only to a greater one,
+// and the join takes the prefix part, which lies after the suffix part,
+// only when it is greater. Taps outside the input read as -FLT_MAX, which
+// is never taken: the suffix scan moves to an equal value only once it holds
+// a tap, and NaNs compare false.
+template <int S>
+struct BlockMax {
+    float sv[S], pv[S];
+    int si[S], pi[S];  // offsets into the 2S values, -1 for none
+
+    __device__ __forceinline__ void scan(const float (&v)[2 * S]) {
+        float m = -FLT_MAX;
+        int a = -1;
+#pragma unroll
+        for (int k = S - 1; k >= 0; --k) {
+            if (v[k] > m || (v[k] == m && a >= 0)) {
+                m = v[k];
+                a = k;
+            }
+            sv[k] = m;
+            si[k] = a;
+        }
+        m = -FLT_MAX;
+        a = -1;
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            if (v[S + k] > m) {
+                m = v[S + k];
+                a = S + k;
+            }
+            pv[k] = m;
+            pi[k] = a;
+        }
+    }
+    // the window starting k into the block
+    __device__ __forceinline__ void window(int k, float &m, int &a) const {
+        m = sv[k];
+        a = si[k];
+        if (k >= 1 && pv[k - 1] > m) {
+            m = pv[k - 1];
+            a = pi[k - 1];
+        }
+    }
+};
+
+template <bool VEC, int S>
+__global__ __launch_bounds__(kSepBS) void maxpool_sep_block_fwd_kernel(const float *in, float *out, int *idx,
+                                                                       PoolGeom g, uint32_t planes, uint32_t P,
+                                                                       FastDiv div_ow_blocks, FastDiv div_oh_blocks) {
+    extern __shared__ float4 plane_lds4[];
+    const uint32_t plane0 = blockIdx.x * P, np = min(P, planes - plane0);
+    const uint32_t hw = g.h * g.w, ohw = g.oh * g.ow;
+    const uint32_t ow_blocks = (g.ow + S - 1) / S, oh_blocks = (g.oh + S - 1) / S;
+    float *pl = reinterpret_cast<float *>(plane_lds4);
+    float *rmax = pl + P * hw;                                   // [P*h][ow]
+    int *rarg = reinterpret_cast<int *>(rmax + P * g.h * g.ow);  // [P*h][ow]
+    stage_to_lds<float, float4, VEC, kSepBS>(pl, in + (size_t)plane0 * hw, np * hw);
+    __syncthreads();
+    const int w = (int)g.w, h = (int)g.h, hp = (int)g.half_pad;
+    for (uint32_t r = threadIdx.x; r < np * g.h * ow_blocks; r += kSepBS) {
+        const uint32_t q = fdiv(r, div_ow_blocks), j0 = (r - q * ow_blocks) * S;  // q = p*h + y
+        const int c0 = (int)j0 - hp;
+        const float *row = pl + q * g.w;
+        float v[2 * S];
+#pragma unroll
+        for (int t = 0; t < 2 * S; ++t) {
+            const int c = c0 + t;
+            const float x = row[min(max(c, 0), w - 1)];
+            v[t] = c >= 0 && c < w ? x : -FLT_MAX;
+        }
+        BlockMax<S> bm;
+        bm.scan(v);
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            if (j0 + k < g.ow) {
+                float m;
+                int a;
+                bm.window(k, m, a);
+                rmax[q * g.ow + j0 + k] = m;
+                rarg[q * g.ow + j0 + k] = a < 0 ? -1 : c0 + a;
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < np * oh_blocks * g.ow; r += kSepBS) {
+        const uint32_t q = fdiv(r, g.div_ow), j = r - q * g.ow;  // q = p*oh_blocks + block
+        const uint32_t p = fdiv(q, div_oh_blocks), i0 = (q - p * oh_blocks) * S;
+        const int r0 = (int)i0 - hp;
+        const float *col = rmax + p * g.h * g.ow + j;
+        float v[2 * S];
+#pragma unroll
+        for (int t = 0; t < 2 * S; ++t) {
+            const int ch = r0 + t;
+            const float x = col[(uint32_t)min(max(ch, 0), h - 1) * g.ow];
+            v[t] = ch >= 0 && ch < h ? x : -FLT_MAX;
+        }
+        BlockMax<S> bm;
+        bm.scan(v);
+        const size_t o_plane = (size_t)(plane0 + p) * ohw;
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            if (i0 + k < g.oh) {
+                float m;
+                int best;
+                bm.window(k, m, best);
+                // a row that won is inside the input and has a column
+                const uint32_t ch = best < 0 ? 0u : (uint32_t)(r0 + best);
+                const int a = rarg[(p * g.h + ch) * g.ow + j];
+                out[o_plane + (i0 + k) * g.ow + j] = m;
                 idx[o_plane + (i0 + k) * g.ow + j] =
                     best < 0 ? -1 : (int)((plane0 + p) * hw + ch * g.w + (uint32_t)a);
             }
@@ -1213,6 +1345,17 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
             const bool vec = aligned16(input) && ((uint64_t)P * hw) % 4 == 0;
             const size_t lds = (size_t)(P * lds_floats * sizeof(float));
             (void)hipGetLastError();
+            if (runs && DKZ_POOL_BLOCKS) {
+                const FastDiv dob = make_fastdiv(div_up(g.ow, g.size)), dohb = make_fastdiv(div_up(g.oh, g.size));
+                auto k = vec ? maxpool_sep_block_fwd_kernel<true, 4> : maxpool_sep_block_fwd_kernel<false, 4>;
+                if (g.size == 5) k = vec ? maxpool_sep_block_fwd_kernel<true, 5> : maxpool_sep_block_fwd_kernel<false, 5>;
+                if (g.size == 9) k = vec ? maxpool_sep_block_fwd_kernel<true, 9> : maxpool_sep_block_fwd_kernel<false, 9>;
+                if (g.size == 13)
+                    k = vec ? maxpool_sep_block_fwd_kernel<true, 13> : maxpool_sep_block_fwd_kernel<false, 13>;
+                hipLaunchKernelGGL(k, grid, block, lds, current_stream(), input, output, indexes, g, (uint32_t)planes,
+                                   P, dob, dohb);
+                return after_launch("forward_maxpool_separable", grid, block);
+            }
             if (runs) {
                 const FastDiv dor = make_fastdiv(div_up(g.ow, kRun)), dohr = make_fastdiv(div_up(g.oh, kRun));
                 auto k = vec ? maxpool_sep_run_fwd_kernel<true, 4> : maxpool_sep_run_fwd_kernel<false, 4>;
