@@ -818,7 +818,12 @@ __global__ __launch_bounds__(kSepBS) void maxpool_s1_target_gather_kernel(const 
     stage_pair_to_lds<kSepBS>(il, dl, idx + o0, delta + o0, n_out);
     __syncthreads();
     for (uint32_t o = threadIdx.x; o < n_out; o += kSepBS) {
-        const int64_t t = (int64_t)il[o] - (int64_t)e0;  // -1 and other planes' inputs fall outside
+        const int tv = il[o];
+        // consecutive outputs often name one input: the first of such a run
+        // marks it (fewer exchanges on one LDS word; [64,512,19,19] size 13
+        // 86.0 -> 77.0 us, 9 67.8 -> 62.6)
+        if (o > 0 && il[o - 1] == tv) continue;
+        const int64_t t = (int64_t)tv - (int64_t)e0;  // -1 and other planes' inputs fall outside
         if (t >= 0 && t < (int64_t)n_el && atomicExch(&mark[t], 1u) == 0u) list[atomicAdd(&n_targets, 1u)] = (uint32_t)t;
     }
     __syncthreads();
