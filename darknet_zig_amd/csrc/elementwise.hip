@@ -398,6 +398,8 @@ int dkz_dropout(float *input, int size, const float *rand, float prob, float sca
     if (size == 0) return 0;
     DKZ_REQUIRE(input != nullptr && rand != nullptr);
     Streams<2, 1> s{{input, rand}, {input}};
+    if ((uint64_t)size * sizeof(float) >= DKZ_DROPOUT_LARGE_BYTES)
+        return run_ew<DKZ_HINT_DROPOUT_LARGE>("dropout", DropoutOp{prob, scale}, s, size);
     return run_ew<DKZ_HINT_DROPOUT>("dropout", DropoutOp{prob, scale}, s, size);
 }
 

@@ -83,6 +83,26 @@ def test_dropout_forward_backward(dev, n, prob):
         gpu.free(b)
 
 
+def test_dropout_large_array(dev):
+    """Arrays of 128 MB and more take nontemporal loads and stores: the
+    same results. 2^25 + 4099 floats (134 MB), a ragged float4 tail."""
+    n = (1 << 25) + 4099
+    r = rng(7)
+    x = normal(r, n)
+    prob = 0.3
+    scale = float(np.float32(1.0) / (np.float32(1.0) - np.float32(prob)))
+    rand_cpu = np.empty(n, np.float32)
+    ref.randUniform(rand_cpu, 0x2468ACE)
+    x_cpu = x.copy()
+    ref.dropout(x_cpu, rand_cpu, prob, scale)
+    dx, drand = up(x), gpu.alloc(n)
+    gpu.randUniform(n, drand, 0x2468ACE)
+    gpu.dropout(dx, n, drand, prob, scale)
+    assert_bitexact(down(dx, x_cpu), x_cpu, f"dropout fwd n={n} p={prob}")
+    for b in (dx, drand):
+        gpu.free(b)
+
+
 def test_dropout_misaligned_and_boundary(dev):
     n = 1031
     r = rng(5)
