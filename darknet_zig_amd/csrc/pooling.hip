@@ -109,8 +109,8 @@ static_assert(DKZ_POOL_PLANE_MAX * sizeof(float) <= 65536, "a workgroup's dynami
 #ifndef DKZ_POOL_SEP_RUN
 #define DKZ_POOL_SEP_RUN 1
 #endif
-// Those windows through blocks of `size` outputs a lane with prefix and
-// suffix maxima instead of runs of 4. Measured on [64,512,19,19], us: size
+// Stride-1 windows of 4 to 13 through blocks of `size` outputs a lane with
+// prefix and suffix maxima (for 4, 5, 9 and 13 instead of runs of 4). Measured on [64,512,19,19], us: size
 // 4 43.8 -> 42.3, 5 47.7 -> 43.7, 9 61.9 -> 61.2 (a 19-wide line is two
 // full blocks of 9 and one of 1), 13 76.3 -> 53.2.
 #ifndef DKZ_POOL_BLOCKS
@@ -1279,6 +1279,23 @@ uint32_t sep_planes(uint64_t planes, uint64_t hw, uint64_t lds_floats) {
     return (uint32_t)p;
 }
 
+// maxpool_sep_block_fwd_kernel for a window size of 4 to 13.
+template <bool VEC>
+auto block_fwd_kernel(uint32_t size) -> decltype(&maxpool_sep_block_fwd_kernel<VEC, 4>) {
+    switch (size) {
+    case 4: return maxpool_sep_block_fwd_kernel<VEC, 4>;
+    case 5: return maxpool_sep_block_fwd_kernel<VEC, 5>;
+    case 6: return maxpool_sep_block_fwd_kernel<VEC, 6>;
+    case 7: return maxpool_sep_block_fwd_kernel<VEC, 7>;
+    case 8: return maxpool_sep_block_fwd_kernel<VEC, 8>;
+    case 9: return maxpool_sep_block_fwd_kernel<VEC, 9>;
+    case 10: return maxpool_sep_block_fwd_kernel<VEC, 10>;
+    case 11: return maxpool_sep_block_fwd_kernel<VEC, 11>;
+    case 12: return maxpool_sep_block_fwd_kernel<VEC, 12>;
+    default: return maxpool_sep_block_fwd_kernel<VEC, 13>;
+    }
+}
+
 // Validates the gpu.zig arguments and derives the geometry. `n` is out_n
 // (forward) or in_n (backward); the batch follows from it.
 int pool_geometry(int in_h, int in_w, int in_c, int stride, int size, int pad, PoolGeom *g, uint64_t *planes,
@@ -1342,6 +1359,7 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
     }
     const uint64_t hw = (uint64_t)g.h * g.w;
     const bool runs = DKZ_POOL_SEP_RUN && g.stride == 1 && (g.size == 4 || g.size == 5 || g.size == 9 || g.size == 13);
+    const bool blocks = DKZ_POOL_BLOCKS && g.stride == 1 && g.size >= 4 && g.size <= 13;
     if (DKZ_POOL_SEP && g.size >= DKZ_POOL_SEP_MIN_SIZE && planes >= DKZ_POOL_PLANE_MIN) {
         const uint64_t lds_floats = hw + 2ull * g.h * g.ow;
         const uint32_t P = sep_planes(planes, hw, lds_floats);
@@ -1350,13 +1368,9 @@ int dkz_forward_maxpool(int out_n, int in_h, int in_w, int in_c, int stride, int
             const bool vec = aligned16(input) && ((uint64_t)P * hw) % 4 == 0;
             const size_t lds = (size_t)(P * lds_floats * sizeof(float));
             (void)hipGetLastError();
-            if (runs && DKZ_POOL_BLOCKS) {
+            if (blocks) {
                 const FastDiv dob = make_fastdiv(div_up(g.ow, g.size)), dohb = make_fastdiv(div_up(g.oh, g.size));
-                auto k = vec ? maxpool_sep_block_fwd_kernel<true, 4> : maxpool_sep_block_fwd_kernel<false, 4>;
-                if (g.size == 5) k = vec ? maxpool_sep_block_fwd_kernel<true, 5> : maxpool_sep_block_fwd_kernel<false, 5>;
-                if (g.size == 9) k = vec ? maxpool_sep_block_fwd_kernel<true, 9> : maxpool_sep_block_fwd_kernel<false, 9>;
-                if (g.size == 13)
-                    k = vec ? maxpool_sep_block_fwd_kernel<true, 13> : maxpool_sep_block_fwd_kernel<false, 13>;
+                const auto k = vec ? block_fwd_kernel<true>(g.size) : block_fwd_kernel<false>(g.size);
                 hipLaunchKernelGGL(k, grid, block, lds, current_stream(), input, output, indexes, g, (uint32_t)planes,
                                    P, dob, dohb);
                 return after_launch("forward_maxpool_separable", grid, block);

@@ -200,6 +200,11 @@ MAXPOOL_CASES = [
     (16, 64, 6, 6, 4, 1, 11),     # windows wholly outside the input: index -1
     (16, 64, 9, 11, 5, 2, 4),     # stride 2
     (32, 40, 11, 11, 7, 1, 6),    # a window size not compiled into the runs-a-lane kernels
+    (16, 64, 15, 15, 6, 1, 5),    # the block forward at every compiled size: 6, 8, 10, 11, 12
+    (16, 64, 15, 15, 8, 1, 7),
+    (16, 64, 14, 14, 10, 1, 9),
+    (16, 64, 15, 15, 11, 1, 10),
+    (8, 64, 13, 13, 12, 1, 11),
     (4, 512, 13, 13, 2, 1, 1),    # a tiny-YOLO [maxpool] size=2 stride=1: the 2x2 gather, 4 planes a workgroup
     (2, 128, 60, 60, 7, 1, 6),    # planes too large for the targets-only backward: the gather without runs
     (2, 128, 60, 60, 5, 1, 4),    # the same with runs of inputs a lane
