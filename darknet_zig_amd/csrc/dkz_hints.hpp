@@ -166,6 +166,17 @@
 #ifndef DKZ_HINT_MAXPOOL_BWD
 #define DKZ_HINT_MAXPOOL_BWD 1
 #endif
+// The 3x3 stride-2 kernels' masks (same bits). Their backward lanes read
+// overlapping candidate outputs, which the caches share between them: at
+// [64,128,56,56] cold, backward masks 1 / 5 (NT delta and index loads)
+// 58.7-59.6 us, 0 54.6-54.9, 4 (NT prev store only) 54.3-54.4; forward 0
+// 30.9-31.2, 6 30.3-30.4, 1 / 7 48.7-49.2.
+#ifndef DKZ_HINT_MAXPOOL3_FWD
+#define DKZ_HINT_MAXPOOL3_FWD 0
+#endif
+#ifndef DKZ_HINT_MAXPOOL3_BWD
+#define DKZ_HINT_MAXPOOL3_BWD 4
+#endif
 // shortcut.hip: bit 0 = add load, bit 1 = out load, bit 2 = out store
 #ifndef DKZ_HINT_SHORTCUT
 #define DKZ_HINT_SHORTCUT 1

@@ -1073,6 +1073,7 @@ __device__ __forceinline__ void max_tap(float val, int index, float &mx, int &mi
 // q indexes output pairs; ow is even so a pair never straddles a row.
 // Nontemporal accesses per DKZ_HINT_MAXPOOL_FWD / _BWD (dkz_hints.hpp).
 constexpr int kHf = DKZ_HINT_MAXPOOL_FWD, kHb = DKZ_HINT_MAXPOOL_BWD;
+constexpr int kH3f = DKZ_HINT_MAXPOOL3_FWD, kH3b = DKZ_HINT_MAXPOOL3_BWD;
 
 __global__ __launch_bounds__(kBlock) void maxpool2_fwd_kernel(const float *in, float *out, int *idx,
                                                               PoolGeom g, uint32_t pairs) {
@@ -1167,8 +1168,8 @@ __global__ __launch_bounds__(kBlock) void maxpool3s2_fwd_kernel(const float *in,
         const uint32_t rc = r_ok ? (uint32_t)r : 0u;
         const uint32_t base = (plane * g.h + rc) * g.w;
         rowi[kh] = (int)base;
-        const float4 a = ld4<(kHf & 1) != 0>(in, (base + c0) >> 2);
-        const float4 b = ld4<(kHf & 1) != 0>(in, (base + c0 + 4) >> 2);
+        const float4 a = ld4<(kH3f & 1) != 0>(in, (base + c0) >> 2);
+        const float4 b = ld4<(kH3f & 1) != 0>(in, (base + c0 + 4) >> 2);
         const float e = in[base + (ce_ok ? (uint32_t)ce : c0)];
         const float lo = -FLT_MAX;
         // local column k is input column 2*x0 - P0 + k
@@ -1196,7 +1197,7 @@ __global__ __launch_bounds__(kBlock) void maxpool3s2_fwd_kernel(const float *in,
             for (int kw = 0; kw < 3; ++kw) max_tap(v[kh][2 * o + kw], rowi[kh] + col0 + 2 * o + kw, m[o], mi[o]);
     }
     const uint32_t ov = (t * g.ow + 4 * xq) >> 2;
-    st4<(kHf & 2) != 0>(out, ov, make_float4(m[0], m[1], m[2], m[3]));
+    st4<(kH3f & 2) != 0>(out, ov, make_float4(m[0], m[1], m[2], m[3]));
     reinterpret_cast<int4 *>(idx)[ov] = make_int4(mi[0], mi[1], mi[2], mi[3]);
 }
 
@@ -1218,8 +1219,8 @@ __global__ __launch_bounds__(kBlock) void maxpool3s2_bwd_kernel(const float *del
     const uint32_t plane = fdiv(t, g.div_h);
     const int r = (int)(t - plane * g.h);
     const uint32_t ib = t * g.w + 8 * q8;  // absolute index of the lane's first input
-    float4 pa = ld4<(kHb & 2) != 0>(prev, ib >> 2);
-    float4 pb = ld4<(kHb & 2) != 0>(prev, (ib >> 2) + 1);
+    float4 pa = ld4<(kH3b & 2) != 0>(prev, ib >> 2);
+    float4 pb = ld4<(kH3b & 2) != 0>(prev, (ib >> 2) + 1);
     // candidate output rows
     const int yb = (r + P0) >> 1;
     const int ya = r + P0 >= 1 ? (r + P0 - 1) >> 1 : 0;
@@ -1234,7 +1235,7 @@ __global__ __launch_bounds__(kBlock) void maxpool3s2_bwd_kernel(const float *del
         const bool y_ok = y < oh && (s == 0 || yb != ya);
         const uint32_t orow = (plane * g.oh + (uint32_t)(y_ok ? y : 0)) * g.ow;
         const uint32_t ov = (orow + 4 * q8) >> 2;
-        const float4 dd = ld4<(kHb & 1) != 0>(delta, ov);
+        const float4 dd = ld4<(kH3b & 1) != 0>(delta, ov);
         const int4 kk = reinterpret_cast<const int4 *>(idx)[ov];
         const float de = delta[orow + (xe_ok ? (uint32_t)xe : 4 * q8)];
         const int ke = idx[orow + (xe_ok ? (uint32_t)xe : 4 * q8)];
@@ -1255,8 +1256,8 @@ __global__ __launch_bounds__(kBlock) void maxpool3s2_bwd_kernel(const float *del
 #pragma unroll
             for (int j = 0; j < 5; ++j) p[e] = add_if(p[e], want, k[s][j], d[s][j]);
     }
-    st4<(kHb & 4) != 0>(prev, ib >> 2, make_float4(p[0], p[1], p[2], p[3]));
-    st4<(kHb & 4) != 0>(prev, (ib >> 2) + 1, make_float4(p[4], p[5], p[6], p[7]));
+    st4<(kH3b & 4) != 0>(prev, ib >> 2, make_float4(p[0], p[1], p[2], p[3]));
+    st4<(kH3b & 4) != 0>(prev, (ib >> 2) + 1, make_float4(p[4], p[5], p[6], p[7]));
 }
 
 // Whether the 3x3/s2 kernels take a shape (see above); pad/2 is P0.
