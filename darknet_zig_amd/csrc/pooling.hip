@@ -21,10 +21,12 @@
 // take a separable forward, several planes a workgroup: a row pass keeps
 // each input row's first window maximum and its column, a column pass the
 // first of those over the window's rows (2*size taps an output instead of
-// size^2, the same first maximum). Smaller windows take one workgroup a
-// plane, every window scanned from the plane in LDS. The stride-1 backward
-// stages the indexes and deltas of several planes a workgroup before its
-// gather; with stride >= 2 one workgroup a plane
+// size^2, the same first maximum; with stride 1 and sizes 4 to 13, prefix
+// and suffix maxima over blocks of `size` make it a few selects an output).
+// Smaller windows take one workgroup a plane, every window scanned from the
+// plane in LDS. The stride-1 backward stages the indexes and deltas of
+// several planes a workgroup before its gather (from windows of 5, for the
+// inputs some output names alone); with stride >= 2 one workgroup a plane
 // stages the plane of prev_delta with them, updates it in LDS and writes it
 // back whole.
 //
