@@ -67,6 +67,43 @@ def _p(b: Buf | None):
 # ---------------------------------------------------------------------------
 
 
+# gpu.zig:32, 39: this mirror always drives libdkz (GPU support compiled
+# in); the backend's label as the reference prints it.
+enabled = True
+backend_label = "HIP"
+# gpu.zig:141: -1 means "run on the CPU"; set by init, reset by deinit.
+device_index = -1
+
+
+def active() -> bool:  # gpu.zig:157-159
+    return enabled and device_index >= 0
+
+
+def deviceName() -> str:  # gpu.zig:147-151
+    return device_name(device_index) if active() else "CPU"
+
+
+def deviceMemoryMib() -> int:  # gpu.zig:153-155
+    return mem_info()[1] >> 20 if active() else 0
+
+
+def gemmPolicy() -> str:
+    """gpu.zig:104-108: the GEMM a run uses (the library's fp32 matrix-core
+    kernel), "cpu" when no device is active."""
+    return "dkz-mfma" if active() else "cpu"
+
+
+def gemmBlockMinTiles() -> int:
+    """gpu.zig:111-113: the tile threshold of the reference's blocked GEMM;
+    the library picks tiles from the shape alone, with no such gate: 0."""
+    return 0
+
+
+def deinit() -> None:  # gpu.zig:349-356
+    global device_index
+    device_index = -1
+
+
 def device_count() -> int:
     n = C.c_int(0)
     _must(_lib.load().dkz_device_count(C.byref(n)), "querying device count")
@@ -74,7 +111,9 @@ def device_count() -> int:
 
 
 def init(index: int = 0) -> None:
+    global device_index
     _must(_lib.load().dkz_init(index), "initialising the device")
+    device_index = index
 
 
 def device_name(index: int = 0) -> str:

@@ -42,7 +42,8 @@ class Error : public std::runtime_error {
     int code_;
 };
 
-inline constexpr const char *backend_label = "HIP (gfx950)";
+// gpu.zig:39: the backend's label as the reference prints it.
+inline constexpr const char *backend_label = "HIP";
 
 // gpu.zig:51-55 must(): a nonzero status ends the operation with a message.
 inline void must(int err, const char *what) {
@@ -77,9 +78,20 @@ struct Buf {
 
 // ---- device state (gpu.zig:141-183, 259-356) --------------------------------
 
+// gpu.zig:32: this mirror is always built against libdkz (GPU support
+// compiled in).
+inline constexpr bool enabled = true;
+
 inline int device_index = -1;
 
-inline bool active() { return device_index >= 0; }
+inline bool active() { return enabled && device_index >= 0; }
+
+// gpu.zig:104-113: the GEMM a run uses, for a benchmark record -- the
+// library's fp32 matrix-core kernel ("cpu" when no device is active) -- and
+// the tile threshold the reference's blocked kernel was gated on, which the
+// library does not have (0).
+inline const char *gemmPolicy() { return active() ? "dkz-mfma" : "cpu"; }
+inline unsigned long long gemmBlockMinTiles() { return 0; }
 
 inline void setSyncAfterLaunch(bool on) { dkz_set_sync_after_launch(on ? 1 : 0); }
 
@@ -99,12 +111,14 @@ inline void deinit() {  // gpu.zig:349-356
 }
 
 inline std::string deviceName() {  // gpu.zig:147-151
+    if (!active()) return "CPU";
     char buf[256];
-    must(dkz_device_name(device_index < 0 ? 0 : device_index, buf, (int)sizeof buf), "querying the device name");
+    must(dkz_device_name(device_index, buf, (int)sizeof buf), "querying the device name");
     return buf;
 }
 
 inline size_t deviceMemoryMib() {  // gpu.zig:153-155
+    if (!active()) return 0;
     size_t free_b = 0, total = 0;
     must(dkz_mem_info(&free_b, &total), "querying device memory");
     return total >> 20;

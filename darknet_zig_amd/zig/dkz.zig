@@ -58,8 +58,8 @@ pub extern fn dkz_softmax_cross_entropy(n: c_int, pred: ?*anyopaque, truth: ?*an
 pub extern fn dkz_l2(n: c_int, pred: ?*anyopaque, truth: ?*anyopaque, delta: ?*anyopaque, err: ?*anyopaque) Status;
 pub extern fn dkz_l1(n: c_int, pred: ?*anyopaque, truth: ?*anyopaque, delta: ?*anyopaque, err: ?*anyopaque) Status;
 pub extern fn dkz_smooth_l1(n: c_int, pred: ?*anyopaque, truth: ?*anyopaque, delta: ?*anyopaque, err: ?*anyopaque) Status;
-pub extern fn dkz_forward_maxpool(out_n: c_int, in_h: c_int, in_w: c_int, in_c: c_int, stride: c_int, size: c_int, pad: c_int, input: ?*anyopaque, output: ?*anyopaque, indexes: *c_int) Status;
-pub extern fn dkz_backward_maxpool(in_n: c_int, in_h: c_int, in_w: c_int, in_c: c_int, stride: c_int, size: c_int, pad: c_int, delta: ?*anyopaque, prev_delta: ?*anyopaque, indexes: *c_int) Status;
+pub extern fn dkz_forward_maxpool(out_n: c_int, in_h: c_int, in_w: c_int, in_c: c_int, stride: c_int, size: c_int, pad: c_int, input: ?*anyopaque, output: ?*anyopaque, indexes: ?*anyopaque) Status;
+pub extern fn dkz_backward_maxpool(in_n: c_int, in_h: c_int, in_w: c_int, in_c: c_int, stride: c_int, size: c_int, pad: c_int, delta: ?*anyopaque, prev_delta: ?*anyopaque, indexes: ?*anyopaque) Status;
 pub extern fn dkz_forward_avgpool(n: c_int, w: c_int, h: c_int, c: c_int, input: ?*anyopaque, output: ?*anyopaque) Status;
 pub extern fn dkz_backward_avgpool(n: c_int, w: c_int, h: c_int, c: c_int, in_delta: ?*anyopaque, out_delta: ?*anyopaque) Status;
 pub extern fn dkz_shortcut(batch: c_int, w1: c_int, h1: c_int, c1: c_int, add: ?*anyopaque, w2: c_int, h2: c_int, c2: c_int, s1: f32, s2: f32, out: ?*anyopaque) Status;

@@ -48,3 +48,28 @@ def test_cpp_mirror_matches_gpu_zig(tmp_path):
     proc = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", f"-I{ROOT / 'include'}",
                            f"-I{ROOT / 'darknet_zig_amd' / 'host'}", str(src)], capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr
+
+
+CALLERS = json.loads((Path(__file__).resolve().parent / "golden" / "gpu_zig_callers.json").read_text())["identifiers"]
+
+
+@pytest.mark.parametrize("name", sorted(CALLERS))
+def test_python_mirror_has_every_caller_identifier(name):
+    """Every gpu.<name> the reference's callers use (gpu_zig_callers.json)
+    exists in the Python mirror too, as a function where gpu.zig has one."""
+    assert hasattr(gpu, name), name
+    if CALLERS[name]["kind"] == "fn":
+        assert callable(getattr(gpu, name)), name
+
+
+def test_python_mirror_state_before_init():
+    """gpu.zig:104-160: with no device selected the state reads "CPU"."""
+    saved = gpu.device_index
+    try:
+        gpu.deinit()
+        assert gpu.enabled is True and gpu.backend_label == "HIP"
+        assert gpu.device_index == -1 and not gpu.active()
+        assert gpu.deviceName() == "CPU" and gpu.deviceMemoryMib() == 0
+        assert gpu.gemmPolicy() == "cpu" and gpu.gemmBlockMinTiles() == 0
+    finally:
+        gpu.device_index = saved

@@ -9,11 +9,22 @@
   src/gpu.zig:483-830 (tests/golden/gpu_zig_api.json) under the same name
   with the same parameter names, and each op's body is one call of a
   dkz_* function declared in dkz.zig with that function's number of
-  arguments.
+  arguments, every `<buf>.ptr` argument landing on a device-buffer
+  (?*anyopaque) parameter;
+* gpu.zig declares every identifier that the reference's callers use
+  (tests/golden/gpu_zig_callers.json: each `gpu.<name>` in src/**/*.zig
+  outside gpu.zig, 52 of them) as `pub`, of the same kind, with the same
+  parameter names and types and return type (Buf with the same fields and
+  methods; `enabled` the same build option), so the layers, network,
+  parser, main, benchmark and gputest compile against it unchanged;
+* every wrapper that reaches the library starts with the reference's
+  `if (!enabled) unreachable;` (or returns), so a build without GPU
+  support references no library symbol.
 """
 
 from __future__ import annotations
 
+import importlib.util
 import json
 import re
 from pathlib import Path
@@ -25,6 +36,20 @@ HEADER = ROOT / "include" / "dkz_ops.h"
 ZIG_DKZ = ROOT / "darknet_zig_amd" / "zig" / "dkz.zig"
 ZIG_GPU = ROOT / "darknet_zig_amd" / "zig" / "gpu.zig"
 API = json.loads((ROOT / "tests" / "golden" / "gpu_zig_api.json").read_text())["ops"]
+CALLERS = json.loads((ROOT / "tests" / "golden" / "gpu_zig_callers.json").read_text())["identifiers"]
+
+
+def _fixture_parser():
+    """The parser that wrote gpu_zig_callers.json, applied to the shim too,
+    so both sides are normalised the same way."""
+    spec = importlib.util.spec_from_file_location("make_gpu_zig_callers",
+                                                  ROOT / "tests" / "golden" / "make_gpu_zig_callers.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+PARSER = _fixture_parser()
 
 
 def header_decls():
@@ -142,3 +167,106 @@ def test_gpu_zig_keeps_the_host_api():
                  "setSyncAfterLaunch"):
         assert name in fns, name
     assert "pub const Buf = struct" in ZIG_GPU.read_text()
+
+
+def shim_declarations() -> dict:
+    return PARSER.declarations(ZIG_GPU.read_text())
+
+
+def test_caller_fixture_is_whole():
+    assert len(CALLERS) == 52
+    for name in ("active", "enabled", "backend_label", "deinit", "deviceName", "deviceMemoryMib", "gemmPolicy",
+                 "gemmBlockMinTiles", "init", "Buf"):
+        assert name in CALLERS, name
+
+
+@pytest.mark.parametrize("name", sorted(CALLERS))
+def test_gpu_zig_declares_what_callers_use(name):
+    want = CALLERS[name]
+    have = shim_declarations()
+    assert name in have, (name, want["callers"][:3])
+    got = have[name]
+    assert got["kind"] == want["kind"], (name, got["kind"], want["kind"])
+    if want["kind"] == "fn":
+        assert [tuple(p) for p in got["params"]] == [tuple(p) for p in want["params"]], name
+        assert got["returns"] == want["returns"], (name, got["returns"], want["returns"])
+    elif want.get("struct"):
+        members = PARSER.struct_members(ZIG_GPU.read_text(), name)
+        assert [tuple(f) for f in members["fields"]] == [tuple(f) for f in want["members"]["fields"]], name
+        for fn, sig in want["members"]["fns"].items():
+            assert fn in members["fns"], (name, fn)
+            assert [tuple(p) for p in members["fns"][fn]["params"]] == [tuple(p) for p in sig["params"]], fn
+            assert members["fns"][fn]["returns"] == sig["returns"], fn
+    elif name == "enabled":
+        assert got["value"] == want["value"] == "build_options.gpu"
+    elif name == "backend_label":
+        assert re.fullmatch(r'"[^"]+"', got["value"] or ""), got  # a string, as api.label is
+    else:
+        assert got.get("type") == want.get("type"), name
+
+
+def test_device_state_follows_the_reference():
+    """device_index (-1 = CPU) is set by init and reset by deinit, and
+    active() is `enabled and device_index >= 0` (gpu.zig:141-160, 349-356)."""
+    text = ZIG_GPU.read_text()
+    assert "pub var device_index: i32 = -1;" in text
+    fns = zig_pub_fns()
+    assert "return enabled and device_index >= 0;" in fns["active"][1]
+    assert "device_index = index;" in fns["init"][1]
+    assert "device_index = -1;" in fns["deinit"][1]
+    assert "dkz.dkz_device_name(" in fns["init"][1] and "device_total_mib = total_b >> 20;" in fns["init"][1]
+
+
+def test_ptr_arguments_land_on_device_buffer_params():
+    """A Buf crosses the ABI as its .ptr (?*anyopaque): every `<buf>.ptr`
+    argument of a dkz_* call in gpu.zig must meet a parameter of exactly
+    that type (a typed pointer such as *c_int would not accept it)."""
+    params = {z[0]: z[1] for z in zig_externs()}
+    decls = shim_declarations()
+    seen = 0
+    for name, (_, body) in zig_pub_fns().items():
+        bufs = {pn for pn, pt in decls[name]["params"] if pt == "Buf"}
+        for m in re.finditer(r"dkz\.(dkz_\w+)\(", body):
+            args = top_level_args(body, m.end() - 1)
+            for i, a in enumerate(args):
+                am = re.fullmatch(r"(\w+)\.ptr", a)
+                if am and am.group(1) in bufs:
+                    seen += 1
+                    assert params[m.group(1)][i][1] in ("?*anyopaque", "?*const anyopaque"), (name, m.group(1), i, a)
+    assert seen > 100
+
+
+def test_wrappers_reference_no_library_symbol_without_gpu():
+    """gpu.zig:363, 390, 432: a build with enabled == false reaches no GPU
+    symbol. Every pub fn that calls the library guards the call."""
+    for name, (_, body) in zig_pub_fns().items():
+        if "dkz.dkz_" not in body or name == "init":
+            continue
+        first = body.strip().split("\n", 1)[0].strip()
+        assert first in ("if (!enabled) unreachable;", "if (!enabled) return;"), (name, first)
+    init = zig_pub_fns()["init"][1]
+    assert init.index("if (!enabled)") < init.index("dkz.dkz_")
+
+
+def top_level_args(body: str, start: int) -> list[str]:
+    """The top-level arguments (text) of the call whose '(' is at body[start]."""
+    depth, i, cur, out = 0, start, "", []
+    while True:
+        c = body[i]
+        if c == "(":
+            depth += 1
+            if depth > 1:
+                cur += c
+        elif c == ")":
+            depth -= 1
+            if depth == 0:
+                if cur.strip():
+                    out.append(cur.strip())
+                return out
+            cur += c
+        elif c == "," and depth == 1:
+            out.append(cur.strip())
+            cur = ""
+        else:
+            cur += c
+        i += 1
