@@ -41,6 +41,7 @@
 // The fast path needs spatial % 4 == 0, 16-byte aligned tensors and a
 // non-empty tensor; any other call runs the per-op sequence, which handles
 // every shape (and edge case) exactly as the individual entry points do.
+#include <atomic>
 #include <cstdlib>
 
 #include "dkz_channel.hpp"
@@ -169,9 +170,13 @@ struct FwdFin {
         m2 = m2 > 0.0 ? m2 : 0.0;
         v = (float)(m2 + n * dm * dm) * var_scale;  // blas.zig:133
     }
-    __device__ void write(uint32_t f, float m, float v) const {
+    // met == false (a one-launch pass whose channel barrier gave up): the
+    // batch statistics are written (NaN) but the rolling averages, which
+    // carry over to the next call, are left as they were.
+    __device__ void write(uint32_t f, float m, float v, bool met = true) const {
         mean[f] = m;
         variance[f] = v;
+        if (!met) return;
         // batchnorm.zig:140-143: scal(0.99) then axpy(1 - 0.99) -- axpy is an fma (blas.zig:22)
         rolling_mean[f] = __builtin_fmaf(kAlpha, m, rolling_mean[f] * kMomentum);
         rolling_variance[f] = __builtin_fmaf(kAlpha, v, rolling_variance[f] * kMomentum);
@@ -384,9 +389,23 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 // The wait is bounded anyway (kSpinMax sleeps of ~128 cycles, ~0.1 s), so
 // every wave ends even if that assumption failed; the barrier then returns
 // false and the workgroup's results are NaN (poison_unless), not sums of
-// partials some of which were never posted. The late workgroups still
-// complete the protocol, leaving the slots ready for the next launch.
+// partials some of which were never posted. Such a workgroup adds nothing
+// to the state that outlives the call (rolling averages, bias and scale
+// updates) and records its kernel in barrier_timeout, which the host turns
+// into an error status (take_barrier_timeout: dkz_synchronize, or the op
+// itself under sync-after-launch). The late workgroups still complete the
+// protocol, leaving the slots ready for the next launch.
 constexpr uint32_t kSpinMax = 1u << 20;
+
+// Which one-launch pass last gave up at a channel barrier on this device
+// (0: none since the host last looked). Written by the kernels with a
+// vector atomic store, read and cleared by take_barrier_timeout.
+__device__ uint32_t barrier_timeout;
+enum : uint32_t { kTimeoutFwdCoop = 1, kTimeoutBwdCoop = 2, kTimeoutBwdReg = 3 };
+
+__device__ __forceinline__ void note_timeout(uint32_t met, uint32_t which) {
+    if (met == 0) __hip_atomic_store(&barrier_timeout, which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The barrier's spin limit: kSpinMax, or $DKZ_BARRIER_SPIN_LIMIT, read at
 // each launch (a test sets 0 to force time-outs and check that they turn
@@ -573,7 +592,8 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
             float m, var;
             fin.stats(sums, c, m, var);
             chan_sh = fwd_chan(m, var, p.scales[f], p.biases[f]);
-            if (k == 0) fin.write(f, m, var);
+            if (k == 0) fin.write(f, m, var, met_sh != 0);
+            note_timeout(met_sh, kTimeoutFwdCoop);
         }
     }
     __syncthreads();
@@ -627,9 +647,14 @@ struct BwdFin {
         md = (float)r.s[2] * (-1.0f / sqrtf(v + 1e-5f));            // blas.zig:155
         vd = ((float)r.s[3] * -0.5f) * pow_m1p5(v + 1e-5f);          // blas.zig:176
     }
-    __device__ void write(uint32_t f, const Sums<4> &r, float md, float vd) const {
-        bias_updates[f] = bias_updates[f] + (float)r.s[0];   // blas.zig:79
-        scale_updates[f] = scale_updates[f] + (float)r.s[1]; // blas.zig:98
+    // met == false (a one-launch pass whose channel barrier gave up):
+    // mean_delta and variance_delta are written (NaN), but nothing is added
+    // to the updates, which accumulate across calls.
+    __device__ void write(uint32_t f, const Sums<4> &r, float md, float vd, bool met = true) const {
+        if (met) {
+            bias_updates[f] = bias_updates[f] + (float)r.s[0];   // blas.zig:79
+            scale_updates[f] = scale_updates[f] + (float)r.s[1]; // blas.zig:98
+        }
         mean_delta[f] = md;
         variance_delta[f] = vd;
     }
@@ -918,7 +943,8 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
             float md, vdl;
             fin.values(f, sums, md, vdl);
             chan_sh = bwd_chan(p, f, md, vdl);
-            if (k == 0) fin.write(f, sums, md, vdl);
+            if (k == 0) fin.write(f, sums, md, vdl, met_sh != 0);
+            note_timeout(met_sh, kTimeoutBwdCoop);
         }
     }
     __syncthreads();
@@ -1102,7 +1128,8 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             float md, vdl;
             fin.values(f, sums, md, vdl);
             chan_sh = bwd_chan(p, f, md, vdl);
-            if (k == 0) fin.write(f, sums, md, vdl);
+            if (k == 0) fin.write(f, sums, md, vdl, met_sh != 0);
+            note_timeout(met_sh, kTimeoutBwdReg);
         }
     }
     __syncthreads();
@@ -1212,19 +1239,25 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
 // kernel and device. A one-launch pass runs only when its whole grid fits,
 // so no workgroup waits at its channel barrier for one that is not yet
 // resident.
+// The lookups are HIP queries, not stream work; dkz_init makes them all
+// once (batchnorm_prewarm) so that no op makes one for the first time inside
+// a graph capture. The caches are atomics: two host threads that race to
+// fill one store the same value.
 template <auto Kernel, int BS>
 uint32_t resident_workgroups() {
-    static uint32_t cache[kMaxDevices];
+    static std::atomic<uint32_t> cache[kMaxDevices];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-    if (cache[dev] == 0) {
+    uint32_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
         int per_cu = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, BS, 0) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        cache[dev] = (uint32_t)(per_cu > 0 ? per_cu : 0) * (uint32_t)(cus > 0 ? cus : 0);
+        v = (uint32_t)(per_cu > 0 ? per_cu : 0) * (uint32_t)(cus > 0 ? cus : 0);
+        cache[dev].store(v, std::memory_order_relaxed);
     }
-    return cache[dev];
+    return v;
 }
 
 // Whether Kernel keeps everything in registers (no private scratch), looked
@@ -1232,15 +1265,17 @@ uint32_t resident_workgroups() {
 // exp-based activations' tanh, for one, spills at 49 float4s a lane).
 template <auto Kernel>
 bool no_spills() {
-    static int cached = -1;  // -1 unknown, 0 spills, 1 none
-    if (cached < 0) {
+    static std::atomic<int> cached{-1};  // -1 unknown, 0 spills, 1 none
+    int v = cached.load(std::memory_order_relaxed);
+    if (v < 0) {
         hipFuncAttributes attr{};
-        cached = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(Kernel)) == hipSuccess &&
-                         attr.localSizeBytes == 0
-                     ? 1
-                     : 0;
+        v = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(Kernel)) == hipSuccess &&
+                    attr.localSizeBytes == 0
+                ? 1
+                : 0;
+        cached.store(v, std::memory_order_relaxed);
     }
-    return cached == 1;
+    return v == 1;
 }
 
 struct Shape {
@@ -1337,6 +1372,7 @@ bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
     const FwdParams p{a.mean, a.variance, a.scales, a.biases};
     *rc = launch("batchnorm_forward", kernel, dim3(sh.F * gc.K), dim3(BS), a.input, a.output, a.x, a.x_norm, p, gc,
                  fin, sc.partials, sc.slots, barrier_spin_limit());
+    if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }
 
@@ -1410,6 +1446,7 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(BS), a.y, a.delta, a.x_norm, a.x, p, gc, fin,
                  sc.partials, sc.slots, barrier_spin_limit());
+    if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }
 
@@ -1442,6 +1479,7 @@ bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(kBwdRegBS), a.y, a.delta, a.x_norm, a.x, p,
                  gc, fin, sc.partials, sc.slots, barrier_spin_limit());
+    if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }
 
@@ -1476,16 +1514,64 @@ int bn_backward_fused(const BwdArgs &a) {
                   cg, sh.n, fin, (const double *)nullptr, 0u);
 }
 
+// Every occupancy and attribute lookup the one-launch passes of activation
+// A make, made ahead (fwd_coop, bwd_coop and bwd_reg ask the same ones).
+template <int A>
+void prewarm() {
+    constexpr int HF = DKZ_HINT_BN_FWD_COOP, HB = DKZ_HINT_BN_BWD_COOP;
+    (void)resident_workgroups<bn_fwd_coop_kernel<A, HF, kCoopBS, kCoopU>, kCoopBS>();
+    (void)resident_workgroups<bn_fwd_coop_kernel<A, HF, kCoopBS2, kCoopU2>, kCoopBS2>();
+    (void)no_spills<bn_fwd_coop_kernel<A, HF, kRegBlock, kRegU>>();
+    (void)resident_workgroups<bn_fwd_coop_kernel<A, HF, kRegBlock, kRegU>, kRegBlock>();
+    (void)no_spills<bn_fwd_coop_kernel<A, HF, kRegBlock, kRegU, true>>();
+    (void)resident_workgroups<bn_fwd_coop_kernel<A, HF, kRegBlock, kRegU, true>, kRegBlock>();
+    (void)resident_workgroups<bn_bwd_coop_kernel<A, HB, kBwdCoopBS, kBwdCoopU>, kBwdCoopBS>();
+    (void)resident_workgroups<bn_bwd_coop_kernel<A, HB, kBwdCoopBS2, kBwdCoopU2>, kBwdCoopBS2>();
+    constexpr auto reg = bn_bwd_reg_kernel<A, HB, kBwdRegBS, kBwdRegUH, kBwdRegUL, kBwdRegUR>;
+    (void)no_spills<reg>();
+    (void)resident_workgroups<reg, kBwdRegBS>();
+}
+
 typedef int (*FwdFn)(const FwdArgs &);
 typedef int (*BwdFn)(const BwdArgs &);
+typedef void (*PrewarmFn)();
 template <int... As>
 struct BnTables {
     static constexpr FwdFn fwd[] = {bn_forward_fused<As>...};
     static constexpr BwdFn bwd[] = {bn_backward_fused<As>...};
+    static constexpr PrewarmFn prewarm[] = {dkz::prewarm<As>...};
 };
 using Tables = BnTables<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13>;
 
 }  // namespace
+
+void batchnorm_prewarm() {
+    for (const PrewarmFn fn : Tables::prewarm) fn();
+}
+
+int take_barrier_timeout() {
+    uint32_t which = 0;
+    hipError_t e = hipMemcpyFromSymbol(&which, HIP_SYMBOL(barrier_timeout), sizeof which, 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        set_error_context("reading the channel-barrier time-out flag");
+        return (int)e;
+    }
+    if (which == 0) return 0;
+    const uint32_t zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(barrier_timeout), &zero, sizeof zero, 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        set_error_context("clearing the channel-barrier time-out flag");
+        return (int)e;
+    }
+    static const char *const kernels[] = {"?", "batchnorm_forward (bn_fwd_coop_kernel)",
+                                          "batchnorm_backward (bn_bwd_coop_kernel)",
+                                          "batchnorm_backward (bn_bwd_reg_kernel)"};
+    set_error_context("HIP: %s: a channel barrier gave up waiting for the channel's other workgroups; those "
+                      "workgroups' outputs are NaN, rolling averages and bias/scale updates were left unchanged",
+                      kernels[which < 4 ? which : 0]);
+    return (int)hipErrorLaunchTimeOut;
+}
+
 }  // namespace dkz
 
 using namespace dkz;

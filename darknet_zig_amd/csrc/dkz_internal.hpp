@@ -21,6 +21,24 @@ void set_error_context(const char *fmt, ...);
 // launch shape go into the error context (gpu.zig:445-462).
 int after_launch(const char *name, dim3 grid, dim3 block);
 
+// Whether sync-after-launch is on (DARKNET_GPU_SYNC, dkz_set_sync_after_launch).
+bool sync_after_launch();
+
+// The one-launch batch-norm passes (batchnorm.hip) wait for the other
+// workgroups of their channel for a bounded time; one that gives up writes
+// NaN results, leaves the state that outlives the call alone and records its
+// kernel in a device word. take_barrier_timeout reads that word on the
+// current device (synchronously) and clears it: 0 when it was clear, else
+// hipErrorLaunchTimeOut with the kernel named in the error context.
+// Called by dkz_synchronize and dkz_copy_to_host (where the reference's
+// kernel faults surface) and, under sync-after-launch, right after the pass.
+int take_barrier_timeout();
+
+// Makes the batch-norm passes' occupancy and kernel-attribute lookups for
+// the current device now (dkz_init), so no op makes one for the first time
+// inside a graph capture.
+void batchnorm_prewarm();
+
 template <typename Kernel, typename... Args>
 inline int launch(const char *name, Kernel kernel, dim3 grid, dim3 block, Args... args) {
     (void)hipGetLastError();  // a stale error from the caller's own calls is not ours

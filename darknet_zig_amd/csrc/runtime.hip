@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "dkz_internal.hpp"
@@ -19,8 +20,11 @@ struct DeviceState {
 
 DeviceState g_devices[kMaxDevices];
 std::mutex g_mutex;
-hipStream_t g_stream = nullptr;
-bool g_sync_after_launch = false;
+// The stream and the sync-after-launch switch are process-wide, as gpu.zig's
+// are (gpu.zig:178, hip.zig:134); atomics, so that a host thread setting them
+// while another issues ops is a well-defined (if unordered) change.
+std::atomic<hipStream_t> g_stream{nullptr};
+std::atomic<bool> g_sync_after_launch{false};
 thread_local char g_context[512] = "";
 thread_local const Scratch *t_scratch_override = nullptr;
 
@@ -54,7 +58,9 @@ int ensure_scratch(int dev) {
 
 }  // namespace
 
-hipStream_t current_stream() { return g_stream; }
+hipStream_t current_stream() { return g_stream.load(std::memory_order_relaxed); }
+
+bool sync_after_launch() { return g_sync_after_launch.load(std::memory_order_relaxed); }
 
 void set_error_context(const char *fmt, ...) {
     va_list ap;
@@ -70,8 +76,8 @@ int after_launch(const char *name, dim3 grid, dim3 block) {
                           block.x, block.y, hipGetErrorString(e));
         return (int)e;
     }
-    if (g_sync_after_launch) {
-        e = hipStreamSynchronize(g_stream);
+    if (sync_after_launch()) {
+        e = hipStreamSynchronize(current_stream());
         if (e != hipSuccess) {
             set_error_context("HIP: %s <<<(%u,%u),(%u,%u)>>> faulted: %s", name, grid.x, grid.y,
                               block.x, block.y, hipGetErrorString(e));
@@ -131,7 +137,9 @@ int dkz_init(int device) {
     }
     if (env_flag("DARKNET_GPU_SYNC") || env_flag("DARKNET_HIP_SYNC")) g_sync_after_launch = true;
     DKZ_TRY(ensure_scratch(device));
-    return static_scratch_setup(device);
+    DKZ_TRY(static_scratch_setup(device));
+    batchnorm_prewarm();
+    return 0;
 }
 
 int dkz_device_name(int device, char *buf, int len) {
@@ -167,8 +175,8 @@ int dkz_malloc(void **ptr, size_t bytes) {
         *ptr = nullptr;
         return (int)e;
     }
-    e = hipMemsetAsync(*ptr, 0, bytes, g_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    e = hipMemsetAsync(*ptr, 0, bytes, current_stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(current_stream());
     if (e != hipSuccess) {
         set_error_context("zeroing device memory");
         (void)hipFree(*ptr);
@@ -185,14 +193,14 @@ int dkz_free(void *ptr) {
 int dkz_memset_zero(void *ptr, size_t bytes) {
     if (bytes == 0) return 0;
     DKZ_REQUIRE(ptr != nullptr);
-    return (int)hipMemsetAsync(ptr, 0, bytes, g_stream);
+    return (int)hipMemsetAsync(ptr, 0, bytes, current_stream());
 }
 
 int dkz_copy_to_device(void *dst, const void *src, size_t bytes) {
     if (bytes == 0) return 0;
     DKZ_REQUIRE(dst != nullptr && src != nullptr);
-    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, current_stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(current_stream());
     if (e != hipSuccess) set_error_context("copy host to device");
     return (int)e;
 }
@@ -200,32 +208,39 @@ int dkz_copy_to_device(void *dst, const void *src, size_t bytes) {
 int dkz_copy_to_host(void *dst, const void *src, size_t bytes) {
     if (bytes == 0) return 0;
     DKZ_REQUIRE(dst != nullptr && src != nullptr);
-    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-    if (e != hipSuccess) set_error_context("copy device to host");
-    return (int)e;
+    const hipStream_t s = current_stream();
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        set_error_context("copy device to host");
+        return (int)e;
+    }
+    return take_barrier_timeout();
 }
 
 int dkz_synchronize(void) {
-    hipError_t e = hipStreamSynchronize(g_stream);
+    hipError_t e = hipStreamSynchronize(current_stream());
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) set_error_context("device synchronise");
-    return (int)e;
+    if (e != hipSuccess) {
+        set_error_context("device synchronise");
+        return (int)e;
+    }
+    return take_barrier_timeout();
 }
 
 const char *dkz_error_string(int err) { return hipGetErrorString((hipError_t)err); }
 
-void dkz_set_sync_after_launch(int on) { g_sync_after_launch = on != 0; }
+void dkz_set_sync_after_launch(int on) { g_sync_after_launch.store(on != 0); }
 
-int dkz_get_sync_after_launch(void) { return g_sync_after_launch ? 1 : 0; }
+int dkz_get_sync_after_launch(void) { return sync_after_launch() ? 1 : 0; }
 
 const char *dkz_last_error_context(void) { return g_context; }
 
 int dkz_set_stream(void *stream) {
-    g_stream = static_cast<hipStream_t>(stream);
+    g_stream.store(static_cast<hipStream_t>(stream));
     return 0;
 }
 
-void *dkz_get_stream(void) { return g_stream; }
+void *dkz_get_stream(void) { return current_stream(); }
 
 }  // extern "C"

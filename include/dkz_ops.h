@@ -47,11 +47,27 @@
  *     never allocate, and leave the slots they use at zero. Reductions or
  *     gemms issued concurrently on two streams of one device share that
  *     buffer and race; issue them on one stream (dkz_set_stream).
+ *   - dkz_batchnorm_forward and dkz_batchnorm_backward may run as one launch
+ *     whose workgroups meet at per-channel barriers. A wait there is bounded
+ *     (~0.1 s); if it runs out (the GPU did not hold all of the launch's
+ *     workgroups at once, e.g. with other work on the device) the
+ *     workgroup's results are NaN and it adds nothing to rolling_mean,
+ *     rolling_variance, bias_updates or scale_updates. The next
+ *     dkz_synchronize or dkz_copy_to_host -- or the op itself under
+ *     sync-after-launch -- then returns hipErrorLaunchTimeOut (702), with the
+ *     kernel named by dkz_last_error_context, as a kernel fault would surface
+ *     in the reference (gpu.zig:51-55, 456-464).
+ *   - The library is built with hidden visibility: it exports exactly the
+ *     functions declared here.
  */
 #ifndef DKZ_OPS_H
 #define DKZ_OPS_H
 
 #include <stddef.h>
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -80,8 +96,10 @@ enum dkz_activation {
 /* ------------------------------------------------------------------------ */
 
 /* gpu.zig:259-347 init(): select `device`, read DARKNET_GPU_SYNC, allocate the
- * device's reduction scratch. Returns hipErrorInvalidDevice (101) when
- * `device` is out of range (gpu.zig:274-277 NoSuchDevice). */
+ * device's reduction scratch and make the occupancy lookups the batch-norm
+ * passes need (so that a later graph capture of any op makes no HIP query
+ * for the first time). Returns hipErrorInvalidDevice (101) when `device` is
+ * out of range (gpu.zig:274-277 NoSuchDevice). */
 int dkz_init(int device);
 
 /* hip.zig:69-71 deviceCount. */
@@ -107,10 +125,12 @@ int dkz_memset_zero(void *ptr, size_t bytes);
 int dkz_copy_to_device(void *dst, const void *src, size_t bytes);
 
 /* gpu.zig:395-405 pull()/pullInts() / hip.zig:103-105 copyToHost. Blocking,
- * after all earlier work on the current stream. */
+ * after all earlier work on the current stream. Also reports (and clears) a
+ * batch-norm channel-barrier time-out: hipErrorLaunchTimeOut after the copy. */
 int dkz_copy_to_host(void *dst, const void *src, size_t bytes);
 
-/* gpu.zig:407-410 sync() / hip.zig:107-109 synchronize. */
+/* gpu.zig:407-410 sync() / hip.zig:107-109 synchronize. Also reports (and
+ * clears) a batch-norm channel-barrier time-out: hipErrorLaunchTimeOut. */
 int dkz_synchronize(void);
 
 /* hip.zig:60-62 errorString. */
@@ -441,6 +461,10 @@ int dkz_batchnorm_backward_noalloc(int batch, int filters, int spatial, int acti
 
 #ifdef __cplusplus
 }
+#endif
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
 #endif
 
 #endif /* DKZ_OPS_H */

@@ -272,40 +272,109 @@ def test_backward_register_holding_activations(dev, act):
     _backward_case(CONFIG2, act, seed=350 + int(act))
 
 
+HIP_ERROR_LAUNCH_TIMEOUT = 702  # hipErrorLaunchTimeOut
+
+
+def _expect_timeout(kernel: str, sync_after_launch: bool, call):
+    """Runs `call` (one fused op) and returns once its barrier time-out has
+    been reported: by the op itself under sync-after-launch, else by the
+    next gpu.sync(). Either way the status is hipErrorLaunchTimeOut, the
+    context names `kernel`, and the report clears the flag (the next sync
+    is clean)."""
+    if sync_after_launch:
+        gpu.setSyncAfterLaunch(True)
+        try:
+            with pytest.raises(gpu.GpuError) as ei:
+                call()
+        finally:
+            gpu.setSyncAfterLaunch(False)
+    else:
+        call()
+        with pytest.raises(gpu.GpuError) as ei:
+            gpu.sync()
+    assert ei.value.code == HIP_ERROR_LAUNCH_TIMEOUT, ei.value
+    assert kernel in ei.value.context, ei.value.context
+    gpu.sync()  # reported once
+
+
+@pytest.mark.parametrize("sync_after_launch", [False, True], ids=["at_sync", "sync_after_launch"])
 @pytest.mark.parametrize("bwd_shape", [(128, 32, 1024), CONFIG2], ids=str)
-def test_barrier_time_out_gives_nan(dev, monkeypatch, bwd_shape):
+def test_barrier_time_out_gives_nan(dev, monkeypatch, bwd_shape, sync_after_launch):
     """The one-launch passes' channel barrier waits a bounded time. Forced to
     give up at once (DKZ_BARRIER_SPIN_LIMIT=0, read at each launch), every
     workgroup but the last of its channel finds the barrier unmet and writes
-    NaN rather than results from partial sums that were not all posted; the
-    barrier's slots are left ready, so the next call is right again. Every
-    kernel still exits normally: the spin limit only shortens its own wait."""
+    NaN rather than results from partial sums that were not all posted. The
+    call then surfaces as hipErrorLaunchTimeOut naming the kernel (the op's
+    own status under sync-after-launch, else the next sync), and the state
+    that outlives the call is never poisoned: each channel's rolling
+    averages and bias/scale updates are either left as they were (the
+    channel's finalising workgroup timed out) or hold the right update (it
+    met its channel), never NaN. The barrier's slots are left ready, so the
+    next call is right again. Every kernel still exits normally: the spin
+    limit only shortens its own wait."""
     B, F, S = 128, 32, 1024  # config 1: the forward splits each channel 8 ways
     n = B * F * S
     r = rng(77)
     x = normal(r, n)
-    d_in, d_out, d_x, d_xn = up(x), gpu.alloc(n), gpu.alloc(n), gpu.alloc(n)
-    d_m, d_v, d_rm, d_rv = gpu.alloc(F), gpu.alloc(F), up(np.zeros(F, np.float32)), up(np.ones(F, np.float32))
     d_s, d_b = up(uniform(r, F, 0.5, 1.5)), up(normal(r, F, 0, 0.1))
-    monkeypatch.setenv("DKZ_BARRIER_SPIN_LIMIT", "0")
-    gpu.batchnormForward(B, F, S, Activation.leaky, True, d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
-    out = down(d_out, x)
-    _free(d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv, d_s, d_b)
+    rm0, rv0 = normal(r, F, 0, 0.1), uniform(r, F, 0.5, 1.5)
+
+    def forward(spin_limit):
+        d_in, d_out, d_x, d_xn = up(x), gpu.alloc(n), gpu.alloc(n), gpu.alloc(n)
+        d_m, d_v, d_rm, d_rv = gpu.alloc(F), gpu.alloc(F), up(rm0), up(rv0)
+
+        def call():
+            gpu.batchnormForward(B, F, S, Activation.leaky, True, d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv,
+                                 d_s, d_b)
+        if spin_limit is None:
+            call()
+        else:
+            monkeypatch.setenv("DKZ_BARRIER_SPIN_LIMIT", spin_limit)
+            _expect_timeout("bn_fwd_coop_kernel", sync_after_launch, call)
+            monkeypatch.delenv("DKZ_BARRIER_SPIN_LIMIT")
+        got = down(d_out, x), down(d_rm, rm0), down(d_rv, rv0)
+        _free(d_in, d_out, d_x, d_xn, d_m, d_v, d_rm, d_rv)
+        return got
+
+    out, rm, rv = forward("0")
+    _, rm_ok, rv_ok = forward(None)
     assert np.isnan(out).any(), "a timed-out forward barrier left no NaN"
+    for got, before, right, what in ((rm, rm0, rm_ok, "rolling_mean"), (rv, rv0, rv_ok, "rolling_variance")):
+        assert np.isfinite(got).all(), what
+        assert np.all((got == before) | (got == right)), what
+    _free(d_s, d_b)
 
     Bb, Fb, Sb = bwd_shape
     nb = Bb * Fb * Sb
     y, delta, xb, xn = normal(r, nb), normal(r, nb), normal(r, nb), normal(r, nb)
-    d_y, d_d, d_xb, d_xnb = up(y), up(delta), up(xb), up(xn)
-    d_m, d_v, d_s = up(normal(r, Fb, 0, 0.1)), up(uniform(r, Fb, 0.5, 1.5)), up(uniform(r, Fb, 0.5, 1.5))
-    d_bu, d_su, d_md, d_vd = gpu.alloc(Fb), gpu.alloc(Fb), gpu.alloc(Fb), gpu.alloc(Fb)
-    gpu.batchnormBackward(Bb, Fb, Sb, Activation.leaky, d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su, d_md,
-                          d_vd)
-    got = down(d_d, delta)
-    _free(d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su, d_md, d_vd)
-    assert np.isnan(got).any(), "a timed-out backward barrier left no NaN"
+    m, v, s = normal(r, Fb, 0, 0.1), uniform(r, Fb, 0.5, 1.5), uniform(r, Fb, 0.5, 1.5)
+    bu0, su0 = normal(r, Fb), normal(r, Fb)
+    kernel = "bn_bwd_reg_kernel" if bwd_shape == CONFIG2 else "bn_bwd_coop_kernel"
 
-    monkeypatch.delenv("DKZ_BARRIER_SPIN_LIMIT")
+    def backward(spin_limit):
+        d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s = up(y), up(delta), up(xb), up(xn), up(m), up(v), up(s)
+        d_bu, d_su, d_md, d_vd = up(bu0), up(su0), gpu.alloc(Fb), gpu.alloc(Fb)
+
+        def call():
+            gpu.batchnormBackward(Bb, Fb, Sb, Activation.leaky, d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su,
+                                  d_md, d_vd)
+        if spin_limit is None:
+            call()
+        else:
+            monkeypatch.setenv("DKZ_BARRIER_SPIN_LIMIT", spin_limit)
+            _expect_timeout(kernel, sync_after_launch, call)
+            monkeypatch.delenv("DKZ_BARRIER_SPIN_LIMIT")
+        got = down(d_d, delta), down(d_bu, bu0), down(d_su, su0)
+        _free(d_y, d_d, d_xb, d_xnb, d_m, d_v, d_s, d_bu, d_su, d_md, d_vd)
+        return got
+
+    got, bu, su = backward("0")
+    _, bu_ok, su_ok = backward(None)
+    assert np.isnan(got).any(), "a timed-out backward barrier left no NaN"
+    for g, before, right, what in ((bu, bu0, bu_ok, "bias_updates"), (su, su0, su_ok, "scale_updates")):
+        assert np.isfinite(g).all(), what
+        assert np.all((g == before) | (g == right)), what
+
     _forward_case((B, F, S), Activation.leaky, True, inplace=True, seed=78)
     _backward_case(bwd_shape, Activation.leaky, seed=79)
 
