@@ -25,6 +25,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libdkz.so"
+VERSION_SCRIPT = PKG_DIR / "libdkz.map"  # exports dkz_* only
 
 ARCH = "gfx950"
 
@@ -44,6 +45,11 @@ HIPCC_FLAGS = [
     f"-I{CSRC}",
 ]
 
+# libdkz.so's host code: only what include/dkz_ops.h declares (visibility
+# pushed to default there) is exported; the device code objects keep their
+# kernels' own (protected) visibility.
+VISIBILITY_FLAGS = ["-Xarch_host", "-fvisibility=hidden", "-Xarch_host", "-fvisibility-inlines-hidden"]
+
 
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -58,7 +64,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *VISIBILITY_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
@@ -75,7 +81,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, srcs))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={VERSION_SCRIPT}",
+           *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"linking libdkz.so failed:\n{proc.stdout}\n{proc.stderr}")
