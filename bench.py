@@ -401,11 +401,13 @@ TRAFFIC_PASSES = 3
 FLUSH_BYTES = 512 << 20
 
 
-def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
+def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graphs=True):
     """The per-op table; with `traffic` (a list), no timing: each row's first
     TRAFFIC_PASSES launches (or call sequences) run once between markers and
     the row is appended to `traffic`. `only`: run only rows whose full name
-    (config/op) contains one of these '|'-separated strings."""
+    (config/op) contains one of these '|'-separated strings. `graphs` False:
+    no HIP graph is captured; `us` is then the issued-from-Python time (for
+    a kernel-trace profile, which times each kernel itself)."""
     from darknet_zig_amd.activations import Activation
 
     rows = {}
@@ -468,9 +470,12 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
             return traced(cfg, name, nbytes, [[f] for f in fns])
         k = max(launches, len(fns))
         seqs = [[f] for f in fns]
-        row(cfg, name, nbytes, time_graph(hip, seqs, k), time_op(hip, stream, fns, k), time_seq(hip, stream, seqs, k))
+        issued = time_seq(hip, stream, seqs, k)
+        row(cfg, name, nbytes, time_graph(hip, seqs, k) if graphs else issued, time_op(hip, stream, fns, k), issued)
         if hot:
-            row(cfg, name + " [hot cache]", nbytes, time_graph(hip, seqs[:1], max(launches, 64)))
+            hk = max(launches, 64)
+            row(cfg, name + " [hot cache]", nbytes,
+                time_graph(hip, seqs[:1], hk) if graphs else time_seq(hip, stream, seqs[:1], hk))
 
     def add_seq(cfg, name, nbytes, seqs, hot=False):
         """A call sequence (or a multi-launch entry point) over rotated sets,
@@ -481,9 +486,12 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None):
         if traffic is not None:
             return traced(cfg, name, nbytes, seqs)
         k = max(launches, len(seqs))
-        row(cfg, name, nbytes, time_graph(hip, seqs, k), issued_ms=time_seq(hip, stream, seqs, k))
+        issued = time_seq(hip, stream, seqs, k)
+        row(cfg, name, nbytes, time_graph(hip, seqs, k) if graphs else issued, issued_ms=issued)
         if hot:
-            row(cfg, name + " [hot cache]", nbytes, time_graph(hip, seqs[:1], max(launches, 64)))
+            hk = max(launches, 64)
+            row(cfg, name + " [hot cache]", nbytes,
+                time_graph(hip, seqs[:1], hk) if graphs else time_seq(hip, stream, seqs[:1], hk))
 
     # -- config 1: BN forward + leaky, [128,32,32,32], x~N(0,1), gamma~U(0.5,1.5), beta~N(0,0.1)
     dev = Device(gpu)
@@ -896,9 +904,8 @@ def cpu_baselines(h, repeats=5):
     """Each config's ops through the oracle's C restatement of the Zig CPU
     twins (blas.zig, activations.zig, pooling.zig), one host thread, median
     of `repeats` runs, as algorithmic GB/s (the GPU rows' byte counts). The
-    ops and inputs are the GPU rows'; config 5 runs on a sample of 32 of its
-    256 images (the same per-image work, so the same rate), the rest at full
-    size. About 10 s in all."""
+    ops and inputs are the GPU rows', every config at its stated size.
+    About 15 s in all."""
     from darknet_zig_amd.activations import Activation
     from oracle import ref
 
@@ -987,8 +994,8 @@ def cpu_baselines(h, repeats=5):
                    "config 4's SGD step (axpy, axpy, scal over 25e6 floats) and shortcut "
                    "[64,256,28,28] -> [64,512,14,14]")
 
-    # config 5: max pool 2x2/s2 fwd + bwd, global avg pool fwd + bwd, on 32 of the 256 images
-    pb, pc, ph = 32, 512, 28
+    # config 5: max pool 2x2/s2 fwd + bwd, global avg pool fwd + bwd on [256,512,28,28]
+    pb, pc, ph = 256, 512, 28
     nin = pb * pc * ph * ph
     oh = (ph + 1 - 2) // 2 + 1
     nout = pb * pc * oh * oh
@@ -1010,7 +1017,7 @@ def cpu_baselines(h, repeats=5):
     out["cfg5"] = (4 * (nin + 2 * nout) + 4 * (2 * nout + 2 * nin) + 4 * (nin + pb * pc) + 4 * (2 * nin + pb * pc),
                    _median_time(cfg5, repeats),
                    "config 5's max pool 2x2/s2 forward + backward and global avg pool forward + backward, "
-                   "[32,512,28,28] (32 of the 256 images)")
+                   "[256,512,28,28]")
 
     cores = os.cpu_count()
     model = _cpu_model()
@@ -1266,6 +1273,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--per-op-only", action="store_true",
                     help="only run the per-op table (for a kernel trace without the chain's launches)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="with --per-op-only: capture no HIP graph (per-op `us` is then the issued time); for "
+                         "rocprofv3 --kernel-trace, under which the graph-replay timing ended in a host "
+                         "segmentation fault")
     ap.add_argument("--per-op-traffic", action="store_true",
                     help="only run each per-op row's first launches once, between marker dispatches "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per row)")
@@ -1319,7 +1330,8 @@ def main() -> int:
         return 0
 
     if args.per_op_only:
-        res = {"per_op": per_op_table(gpu, hip, stream, args.op_launches, only=args.rows)}
+        res = {"per_op": per_op_table(gpu, hip, stream, args.op_launches, only=args.rows,
+                                      graphs=not args.no_graph)}
         if args.rows is None:
             res["gemm"] = gemm_table(gpu, hip, stream)
         print(json.dumps(res), flush=True)
