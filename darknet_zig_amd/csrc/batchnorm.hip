@@ -374,30 +374,51 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 
 // ---- one-launch forward --------------------------------------------------------
 
-// The K workgroups of one channel wait for each other here (thread 0 of
-// each; the caller's __syncthreads follow). count and gen are the channel's
-// two counter slots: every workgroup reads gen, counts itself in count, and
-// the last to arrive empties count (for the next launch) and advances gen,
-// which releases the others. This workgroup's partial sums were written with
-// coherent atomic stores before it arrives, and the s_waitcnt orders their
-// completion before the arrival, so whoever sees gen move sees them.
+// The K workgroups of one channel meet here: each posts its NS partial sums
+// and waits until all K have posted, then adds them (channel_meet, called
+// by wave 0 of the workgroup; the caller's __syncthreads follow).
+//   * Workgroup k's sums go to its own 128-byte line of the scratch's slots
+//     (line f*K + k after the F channel counters), as their bits XOR
+//     kMeetKey, so a posted value is never zero: kMeetKey is a NaN payload
+//     no sum produces (a NaN reaching a sum carries an f32 payload whose low
+//     29 bits are zero).
+//   * Wave 0 then reads the channel's other lines with coherent loads until
+//     every value is non-zero and adds the K partials of each sum in index
+//     order -- lane l adds lines l, l + 64, ..., then a wave sum -- so every
+//     workgroup of the channel gets the same bits. The workgroup's own line
+//     is taken from its registers.
+//   * The last workgroup to have read (a count in the channel's counter
+//     slot) clears the K lines and the count, so the next launch starts from
+//     zero.
+// The last workgroup to post pays one memory round trip (its poll) after
+// its sums are formed; the others see its post one round trip after it
+// lands. Measured at config 1 (per-workgroup s_memrealtime stamps), the
+// counter-and-generation barrier this replaces (arrive, release, observe,
+// then read the partials) took 2.7 us from the last arrival to the sums.
 //
 // A channel's workgroups have consecutive indices and the hardware
 // dispatches workgroups in index order, so the lowest channel not yet done
 // always has all its workgroups resident or about to be, and completes: no
 // deadlock for any grid size as long as K workgroups fit the GPU at once.
-// The wait is bounded anyway (kSpinMax sleeps of ~128 cycles, ~0.1 s), so
-// every wave ends even if that assumption failed; the barrier then returns
-// false and the workgroup's results are NaN (poison_unless), not sums of
+// The wait is bounded anyway (kSpinMax polls with a short sleep between
+// them), so every wave ends even if that assumption failed; the meeting
+// then returns false and the workgroup's results are NaN, not sums of
 // partials some of which were never posted. Such a workgroup adds nothing
 // to the state that outlives the call (rolling averages, bias and scale
 // updates) and records its kernel in barrier_timeout, which the host turns
 // into an error status (take_barrier_timeout: dkz_synchronize, or the op
-// itself under sync-after-launch). The late workgroups still complete the
-// protocol, leaving the slots ready for the next launch.
+// itself under sync-after-launch). It still counts itself as having read,
+// and the late workgroups find every partial posted and finish the
+// protocol, leaving the slots clear for the next launch.
 constexpr uint32_t kSpinMax = 1u << 20;
+constexpr uint64_t kMeetKey = 0xFFF8DEADBEEF0001ull;
+constexpr uint32_t kMeetLine = 16;  // 64-bit slots a posting line (128 bytes)
 
-// Which one-launch pass last gave up at a channel barrier on this device
+// Slots a one-launch pass over F channels of K workgroups needs: the
+// channel counters, then one posting line per workgroup.
+inline uint64_t meet_slots(uint64_t F, uint64_t K) { return F * kCounterStride + F * K * kMeetLine; }
+
+// Which one-launch pass last gave up at a channel meeting on this device
 // (0: none since the host last looked). Written by the kernels with a
 // vector atomic store, read and cleared by take_barrier_timeout.
 __device__ uint32_t barrier_timeout;
@@ -407,57 +428,87 @@ __device__ __forceinline__ void note_timeout(uint32_t met, uint32_t which) {
     if (met == 0) __hip_atomic_store(&barrier_timeout, which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The barrier's spin limit: kSpinMax, or $DKZ_BARRIER_SPIN_LIMIT, read at
+// The meeting's spin limit: kSpinMax, or $DKZ_BARRIER_SPIN_LIMIT, read at
 // each launch (a test sets 0 to force time-outs and check that they turn
-// into NaN results).
+// into NaN results and an error status).
 inline uint32_t barrier_spin_limit() {
     const char *e = getenv("DKZ_BARRIER_SPIN_LIMIT");
     return e != nullptr && *e != '\0' ? (uint32_t)strtoul(e, nullptr, 10) : kSpinMax;
 }
 
-__device__ __forceinline__ bool channel_barrier(uint64_t *count, uint64_t *gen, uint32_t K, uint32_t spin) {
-    const uint64_t g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const uint64_t before = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before == (uint64_t)(K - 1)) {
-        __hip_atomic_store(count, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __hip_atomic_fetch_add(gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return true;
-    }
-    for (uint32_t it = 0; it < spin; ++it) {
-        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != g0) return true;
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return false;
-}
-
-// The channel's sums as NaN when its barrier timed out (met == 0).
+// Called by all 64 lanes of wave 0 with this workgroup's sums in r (the
+// same in every lane, as block_sums leaves them); returns with the
+// channel's totals in r (NaN if the wait ran out) and whether it met. The
+// workgroup must call channel_leave once it no longer needs the lines.
 template <int NS>
-__device__ __forceinline__ void poison_unless(uint32_t met, Sums<NS> &r) {
-    if (met == 0) {
-#pragma unroll
-        for (int q = 0; q < NS; ++q) r.s[q] = __builtin_nan("");
-    }
-}
-
-// Channel f's K partials of each of NS sums (partials[((q*F + f)*K + k) *
-// kPartialStride]), read with coherent loads and added in index order over
-// one wave: every workgroup of the channel gets the same bits.
-template <int NS>
-__device__ __forceinline__ Sums<NS> wave_partials_coherent(const double *partials, uint32_t F, uint32_t K,
-                                                           uint32_t f) {
+__device__ __forceinline__ bool channel_meet(uint64_t *slots, uint32_t F, uint32_t K, uint32_t f, uint32_t k,
+                                             Sums<NS> &r, uint32_t spin) {
     const uint32_t l = threadIdx.x & (kWave - 1);
-    Sums<NS> r;
+    const uint64_t *const lines = slots + (uint64_t)F * kCounterStride + (uint64_t)f * K * kMeetLine;
+    uint64_t own[NS];
 #pragma unroll
-    for (int q = 0; q < NS; ++q) {
-        const double *p = partials + ((uint64_t)q * F + f) * K * kPartialStride;
-        double s = 0.0;
-        for (uint32_t i = l; i < K; i += kWave)
-            s += __hip_atomic_load(&p[(uint64_t)i * kPartialStride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        r.s[q] = wave_sum(s);
+    for (int q = 0; q < NS; ++q) own[q] = __builtin_bit_cast(uint64_t, r.s[q]) ^ kMeetKey;
+    if (l < (uint32_t)NS) {
+        uint64_t v = own[0];
+#pragma unroll
+        for (int q = 1; q < NS; ++q) v = l == (uint32_t)q ? own[q] : v;
+        __hip_atomic_store(const_cast<uint64_t *>(&lines[(uint64_t)k * kMeetLine + l]), v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
-    return r;
+    double acc[NS];
+    bool met = false;
+    for (uint32_t it = 0;; ++it) {
+        bool have = true;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) acc[q] = 0.0;
+        for (uint32_t i = l; i < K; i += kWave) {
+            // a lane's NS loads of one line are issued together
+            uint64_t u[NS];
+            if (i == k) {
+#pragma unroll
+                for (int q = 0; q < NS; ++q) u[q] = own[q];
+            } else {
+#pragma unroll
+                for (int q = 0; q < NS; ++q)
+                    u[q] = __hip_atomic_load(&lines[(uint64_t)i * kMeetLine + q], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int q = 0; q < NS; ++q) {
+                have = have && u[q] != 0;
+                acc[q] += __builtin_bit_cast(double, u[q] ^ kMeetKey);
+            }
+        }
+        if (__all(have)) {
+            met = true;
+            break;
+        }
+        if (it >= spin) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) r.s[q] = met ? wave_sum(acc[q]) : __builtin_nan("");
+    return met;
+}
+
+// Called by all 64 lanes of wave 0 at the end of the workgroup, after
+// channel_meet: counts the workgroup as done with the channel's lines; the
+// last of the K clears them and the count (off the path to the outputs:
+// the other waves' stores drain meanwhile).
+template <int NS>
+__device__ __forceinline__ void channel_leave(uint64_t *slots, uint32_t F, uint32_t K, uint32_t f) {
+    const uint32_t l = threadIdx.x & (kWave - 1);
+    uint64_t *const count = slots + (uint64_t)f * kCounterStride;
+    uint64_t *const lines = slots + (uint64_t)F * kCounterStride + (uint64_t)f * K * kMeetLine;
+    uint64_t before = 0;
+    if (l == 0) before = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    before = __shfl(before, 0);
+    if (before == (uint64_t)(K - 1)) {
+        for (uint32_t i = l; i < K * (uint32_t)NS; i += kWave)
+            __hip_atomic_store(&lines[(uint64_t)(i / NS) * kMeetLine + i % NS], 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (l == 0) __hip_atomic_store(count, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // Workgroups of kCoopBS threads holding kCoopU float4s a lane: a workgroup
@@ -492,7 +543,6 @@ constexpr int kCoopBS2 = DKZ_BN_COOP_BS2, kCoopU2 = DKZ_BN_COOP_U2;
 constexpr int kRegBlock = 512, kRegU = 49;
 // float4s of input a lane loads at once past its held chunk
 constexpr int kFwdExtraG = 4;
-constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 
 // Forward (train) in one launch: workgroup (f, k) -- channel-major, k
 // fastest -- loads chunk k of channel f into registers once, adds its f64
@@ -507,12 +557,11 @@ constexpr uint32_t kRegChunk = kRegBlock * 4 * kRegU;
 template <int A, int H, int BS, int U, bool EXTRA = false>
 __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, float *output, float *x,
                                                          float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
-                                                         double *partials, uint64_t *slots, uint32_t spin) {
+                                                         uint64_t *slots, uint32_t spin) {
     constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
     constexpr bool kXLate = DKZ_BN_COOP_X_LATE != 0;
     __shared__ double lds[2 * (BS / kWave)];
     __shared__ FwdChan chan_sh;
-    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -573,27 +622,15 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
             }
         }
     }
-    const Sums<2> r = block_sums<2, BS>(a, lds);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
-                                 spin)
-                     ? 1u
-                     : 0u;
-    }
-    __syncthreads();
+    Sums<2> sums = block_sums<2, BS>(a, lds);
     if (threadIdx.x < kWave) {
-        Sums<2> sums = wave_partials_coherent<2>(partials, F, g.K, f);
-        poison_unless(met_sh, sums);
+        const uint32_t met = channel_meet<2>(slots, F, g.K, f, k, sums, spin) ? 1u : 0u;
         if (threadIdx.x == 0) {
             float m, var;
             fin.stats(sums, c, m, var);
             chan_sh = fwd_chan(m, var, p.scales[f], p.biases[f]);
-            if (k == 0) fin.write(f, m, var, met_sh != 0);
-            note_timeout(met_sh, kTimeoutFwdCoop);
+            if (k == 0) fin.write(f, m, var, met != 0);
+            note_timeout(met, kTimeoutFwdCoop);
         }
     }
     __syncthreads();
@@ -632,6 +669,7 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
             }
         }
     }
+    if (threadIdx.x < kWave) channel_leave<2>(slots, F, g.K, f);
 }
 
 // ---- backward -----------------------------------------------------------------
@@ -879,13 +917,12 @@ constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2
 template <int A, int H, int BS, int U>
 __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *delta, const float *x_norm,
                                                          const float *x, BwdParams p, RedGeom g, BwdFin fin,
-                                                         double *partials, uint64_t *slots, uint32_t spin) {
+                                                         uint64_t *slots, uint32_t spin) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtY = (H & 1) != 0, kNtD = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtX = (H & 8) != 0;
     constexpr bool kNtOut = (H & 16) != 0;
     __shared__ double lds[4 * (BS / kWave)];
     __shared__ BwdChan chan_sh;
-    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -924,27 +961,15 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
             }
         }
     }
-    const Sums<4> r = block_sums<4, BS>(a, lds);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
-                                 spin)
-                     ? 1u
-                     : 0u;
-    }
-    __syncthreads();
+    Sums<4> sums = block_sums<4, BS>(a, lds);
     if (threadIdx.x < kWave) {
-        Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
-        poison_unless(met_sh, sums);
+        const uint32_t met = channel_meet<4>(slots, F, g.K, f, k, sums, spin) ? 1u : 0u;
         if (threadIdx.x == 0) {
             float md, vdl;
             fin.values(f, sums, md, vdl);
             chan_sh = bwd_chan(p, f, md, vdl);
-            if (k == 0) fin.write(f, sums, md, vdl, met_sh != 0);
-            note_timeout(met_sh, kTimeoutBwdCoop);
+            if (k == 0) fin.write(f, sums, md, vdl, met != 0);
+            note_timeout(met, kTimeoutBwdCoop);
         }
     }
     __syncthreads();
@@ -958,6 +983,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
             lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
         st4<kNtOut>(delta, at[u], o);
     }
+    if (threadIdx.x < kWave) channel_leave<4>(slots, F, g.K, f);
 }
 
 // The one-launch backward for tensors too large for bn_bwd_coop_kernel's
@@ -975,7 +1001,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
 template <int A, int H, int BS, int UH, int UL, int UR>
 __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *delta, const float *x_norm,
                                                         const float *x, BwdParams p, RedGeom g, BwdFin fin,
-                                                        double *partials, uint64_t *slots, uint32_t spin) {
+                                                        uint64_t *slots, uint32_t spin) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtOut = (H & 16) != 0;
     constexpr int G = DKZ_BN_BWD_REG_G;  // float4s of each input a lane loads at once
@@ -983,7 +1009,6 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
     __shared__ double lds[4 * (BS / kWave)];
     __shared__ float4 held_d2[UL1 * BS], held_xm[UL1 * BS];  // float4 UH + i of lane t at [i * BS + t]
     __shared__ BwdChan chan_sh;
-    __shared__ uint32_t met_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
     const uint32_t F = g.div_filters.d;
@@ -1109,27 +1134,15 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
         }
     }
-    const Sums<4> r = block_sums<4, BS>(a, lds);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __hip_atomic_store(&partials[(((uint64_t)q * F + f) * g.K + k) * kPartialStride], r.s[q],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        met_sh = channel_barrier(&slots[(uint64_t)f * kCounterStride], &slots[(uint64_t)f * kCounterStride + 1], g.K,
-                                 spin)
-                     ? 1u
-                     : 0u;
-    }
-    __syncthreads();
+    Sums<4> sums = block_sums<4, BS>(a, lds);
     if (threadIdx.x < kWave) {
-        Sums<4> sums = wave_partials_coherent<4>(partials, F, g.K, f);
-        poison_unless(met_sh, sums);
+        const uint32_t met = channel_meet<4>(slots, F, g.K, f, k, sums, spin) ? 1u : 0u;
         if (threadIdx.x == 0) {
             float md, vdl;
             fin.values(f, sums, md, vdl);
             chan_sh = bwd_chan(p, f, md, vdl);
-            if (k == 0) fin.write(f, sums, md, vdl, met_sh != 0);
-            note_timeout(met_sh, kTimeoutBwdReg);
+            if (k == 0) fin.write(f, sums, md, vdl, met != 0);
+            note_timeout(met, kTimeoutBwdReg);
         }
     }
     __syncthreads();
@@ -1200,6 +1213,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
         }
     }
+    if (threadIdx.x < kWave) channel_leave<4>(slots, F, g.K, f);
 }
 
 // ---- host ---------------------------------------------------------------------
@@ -1356,9 +1370,7 @@ bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
         if (K == 0 || div_up(L, K) > (uint64_t)DKZ_BN_FWD_REG_MAX_CHUNKS * chunk) return false;
     }
     const uint64_t wgs = (uint64_t)sh.F * K;
-    if (K > 256 || sh.F > kScratchSlots / kCounterStride || wgs > DKZ_BN_COOP_MAX_WGS ||
-        2ull * wgs * kPartialStride > kScratchPartials)
-        return false;
+    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || meet_slots(sh.F, K) > kScratchSlots) return false;
     if constexpr (CHECK_SPILLS) {
         if (!no_spills<kernel>()) return false;
     }
@@ -1371,7 +1383,7 @@ bool fwd_coop(const FwdArgs &a, uint64_t L, int *rc) {
                      (double)L, 1.0f / (float)L, 1.0f / (float)(L - 1u)};
     const FwdParams p{a.mean, a.variance, a.scales, a.biases};
     *rc = launch("batchnorm_forward", kernel, dim3(sh.F * gc.K), dim3(BS), a.input, a.output, a.x, a.x_norm, p, gc,
-                 fin, sc.partials, sc.slots, barrier_spin_limit());
+                 fin, sc.slots, barrier_spin_limit());
     if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }
@@ -1435,8 +1447,8 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     constexpr auto kernel = bn_bwd_coop_kernel<A, DKZ_HINT_BN_BWD_COOP, BS, U>;
     const Shape &sh = a.sh;
     const uint64_t K = div_up(L, (uint64_t)BS * 4 * U), wgs = (uint64_t)sh.F * K;
-    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
-        4ull * wgs * kPartialStride > kScratchPartials || wgs > resident_workgroups<kernel, BS>())
+    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || meet_slots(sh.F, K) > kScratchSlots ||
+        wgs > resident_workgroups<kernel, BS>())
         return false;
     const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
     Scratch sc{nullptr};
@@ -1445,7 +1457,7 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(BS), a.y, a.delta, a.x_norm, a.x, p, gc, fin,
-                 sc.partials, sc.slots, barrier_spin_limit());
+                 sc.slots, barrier_spin_limit());
     if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }
@@ -1468,9 +1480,7 @@ bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
         if (K == 0 || div_up(L, K) > (uint64_t)DKZ_BN_BWD_REG_MAX_CHUNKS * kCap) return false;
     }
     const uint64_t wgs = (uint64_t)sh.F * K;
-    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || sh.F > kScratchSlots / kCounterStride ||
-        4ull * wgs * kPartialStride > kScratchPartials || wgs > res)
-        return false;
+    if (K > 256 || wgs > DKZ_BN_COOP_MAX_WGS || meet_slots(sh.F, K) > kScratchSlots || wgs > res) return false;
     const RedGeom gc = make_red_geom(sh.F, sh.S, (uint32_t)L, (uint32_t)K, true);
     Scratch sc{nullptr};
     *rc = device_scratch(&sc);
@@ -1478,7 +1488,7 @@ bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
     const BwdParams p{a.mean, a.variance, a.mean_delta, a.variance_delta, a.scales,
                       (float)((uint64_t)sh.S * (uint64_t)sh.B)};
     *rc = launch("batchnorm_backward", kernel, dim3(sh.F * gc.K), dim3(kBwdRegBS), a.y, a.delta, a.x_norm, a.x, p,
-                 gc, fin, sc.partials, sc.slots, barrier_spin_limit());
+                 gc, fin, sc.slots, barrier_spin_limit());
     if (*rc == 0 && sync_after_launch()) *rc = take_barrier_timeout();
     return true;
 }

@@ -10,9 +10,11 @@
 //     the partials it then reads.
 //   * kScratchSlots 64-bit counter slots (512 KiB): the workgroups of a split
 //     channel reduction count themselves in their channel's slot to find the
-//     last one, so the slot must be zero when a call starts. Each call clears
-//     the slots of its channels first (a small kernel, not a memset, so the
-//     call can be captured in a graph).
+//     last one, and those of a one-launch pass post their sums on lines
+//     after the channel counters, so the slots must be zero when a call
+//     starts. Every kernel leaves them at zero; each call clears them all
+//     first anyway (a small kernel, not a memset, so the call can be captured
+//     in a graph).
 // Nothing here calls hipMalloc, hipFree or an allocating library routine.
 // Each GPU holds its own copy of the array until the process ends; every
 // call on a GPU shares it, so calls that overlap on one GPU (two streams,
@@ -88,10 +90,8 @@ int dkz_batchnorm_backward_noalloc(int batch, int filters, int spatial, int acti
     unsigned char *base = static_cast<unsigned char *>(g_scratch_ptr[dev]);
     const Scratch sc{reinterpret_cast<double *>(base), nullptr, 0,
                      reinterpret_cast<uint64_t *>(base + kPartialsBytes)};
-    const uint64_t want = (uint64_t)filters * kCounterStride;  // channel f's counter is slot f*kCounterStride
-    const uint32_t nslots = want < kScratchSlots ? (uint32_t)want : kScratchSlots;
-    DKZ_TRY(launch("batchnorm_backward_noalloc_zero_slots", zero_slots_kernel, dim3(div_up(nslots, kBlock)),
-                   dim3(kBlock), sc.slots, nslots));
+    DKZ_TRY(launch("batchnorm_backward_noalloc_zero_slots", zero_slots_kernel, dim3(div_up(kScratchSlots, kBlock)),
+                   dim3(kBlock), sc.slots, kScratchSlots));
     const ScratchOverride use(&sc);
     return dkz_batchnorm_backward(batch, filters, spatial, activation, output, delta, x, x_norm, mean, variance,
                                   scales, bias_updates, scale_updates, mean_delta, variance_delta);

@@ -18,7 +18,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from darknet_zig_amd import gpu
+from darknet_zig_amd import _lib, gpu
 from darknet_zig_amd.activations import Activation
 from oracle import ref
 from tests.helpers import assert_bitexact, assert_r5, down, normal, rng, uniform, up
@@ -281,17 +281,18 @@ def _expect_timeout(kernel: str, sync_after_launch: bool, call):
     next gpu.sync(). Either way the status is hipErrorLaunchTimeOut, the
     context names `kernel`, and the report clears the flag (the next sync
     is clean)."""
-    if sync_after_launch:
-        gpu.setSyncAfterLaunch(True)
-        try:
+    before = bool(_lib.load().dkz_get_sync_after_launch())
+    gpu.setSyncAfterLaunch(sync_after_launch)
+    try:
+        if sync_after_launch:
             with pytest.raises(gpu.GpuError) as ei:
                 call()
-        finally:
-            gpu.setSyncAfterLaunch(False)
-    else:
-        call()
-        with pytest.raises(gpu.GpuError) as ei:
-            gpu.sync()
+        else:
+            call()
+            with pytest.raises(gpu.GpuError) as ei:
+                gpu.sync()
+    finally:
+        gpu.setSyncAfterLaunch(before)
     assert ei.value.code == HIP_ERROR_LAUNCH_TIMEOUT, ei.value
     assert kernel in ei.value.context, ei.value.context
     gpu.sync()  # reported once
