@@ -96,13 +96,10 @@ __global__ __launch_bounds__(kBlock) void bcast_scalar_kernel(Op op, float *io, 
         io[e] = op(io[e], TWO ? a[e] : 0.0f, op.param(channel_of<ROWWISE>(e, g)));
 }
 
-// batch, filters, spatial already validated as non-negative ints.
+// filters, spatial already validated as non-negative ints; n64 the
+// element count (batch * filters * spatial), at most kMaxElems.
 template <int H, class Op, bool TWO, bool ROWWISE = false>
-int run_bcast(const char *name, const Op &op, float *io, const float *a, int batch, int filters,
-              int spatial) {
-    const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
-    if (n64 == 0) return 0;
-    DKZ_REQUIRE(n64 <= kMaxElems);
+int launch_bcast(const char *name, const Op &op, float *io, const float *a, int filters, int spatial, uint64_t n64) {
     const uint32_t n = (uint32_t)n64;
     const ChanGeom g{make_fastdiv((uint32_t)spatial), make_fastdiv((uint32_t)filters)};
     if (aligned16(io) && (!TWO || aligned16(a))) {
@@ -126,6 +123,18 @@ int run_bcast(const char *name, const Op &op, float *io, const float *a, int bat
     }
     const uint32_t grid = div_up(n, kBlock) < 65536u ? div_up(n, kBlock) : 65536u;
     return launch(name, bcast_scalar_kernel<Op, TWO, ROWWISE>, dim3(grid), dim3(kBlock), op, io, a, g, n);
+}
+
+// Launches the op and records what it wrote (note_output).
+template <int H, class Op, bool TWO, bool ROWWISE = false>
+int run_bcast(const char *name, const Op &op, float *io, const float *a, int batch, int filters,
+              int spatial) {
+    const uint64_t n64 = (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial;
+    if (n64 == 0) return 0;
+    DKZ_REQUIRE(n64 <= kMaxElems);
+    DKZ_TRY((launch_bcast<H, Op, TWO, ROWWISE>(name, op, io, a, filters, spatial, n64)));
+    note_output(io, 4 * n64);
+    return 0;
 }
 
 // ---- ops ------------------------------------------------------------------

@@ -120,14 +120,27 @@
 #ifndef DKZ_HINT_VARIANCE
 #define DKZ_HINT_VARIANCE 1        // x
 #endif
+// mean_delta and backward_bias read one tensor, delta, which in the layer's
+// backward step the op just before wrote (gradient_array, scale_bias):
+// then ordinary loads, which find it in the Infinity Cache and leave it
+// there for the ops after (nontemporal loads here cost the config-2 backward
+// chain 3.7%). Otherwise (recently_written false) nontemporal loads, which
+// stream cold data faster: measured on MI355X at config 2's shape, 18.6 ->
+// 17.7 us (0.69 -> 0.73 of 8 TB/s).
 #ifndef DKZ_HINT_MEAN_DELTA
-#define DKZ_HINT_MEAN_DELTA 0      // delta
+#define DKZ_HINT_MEAN_DELTA 0      // delta, just written
+#endif
+#ifndef DKZ_HINT_MEAN_DELTA_COLD
+#define DKZ_HINT_MEAN_DELTA_COLD 1 // delta, not written recently
 #endif
 #ifndef DKZ_HINT_VARIANCE_DELTA
 #define DKZ_HINT_VARIANCE_DELTA 2  // x; delta stays cached
 #endif
 #ifndef DKZ_HINT_BACKWARD_BIAS
-#define DKZ_HINT_BACKWARD_BIAS 0   // delta
+#define DKZ_HINT_BACKWARD_BIAS 0   // delta, just written
+#endif
+#ifndef DKZ_HINT_BACKWARD_BIAS_COLD
+#define DKZ_HINT_BACKWARD_BIAS_COLD 1  // delta, not written recently
 #endif
 #ifndef DKZ_HINT_BACKWARD_SCALE
 #define DKZ_HINT_BACKWARD_SCALE 2  // x_norm (read once); delta stays cached

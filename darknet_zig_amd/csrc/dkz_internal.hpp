@@ -34,6 +34,21 @@ bool sync_after_launch();
 // kernel faults surface) and, under sync-after-launch, right after the pass.
 int take_barrier_timeout();
 
+// Producer-to-consumer reuse of the 256 MB Infinity Cache. Every kernel
+// launch advances a count (after_launch); the elementwise and broadcast ops
+// record the range each launch wrote (note_output). recently_written(p, n)
+// tells whether [p, p + n) lies in a range written by one of the last
+// kRecentLaunches launches and is at most kRecentMaxBytes: the cache then
+// likely holds it, and a single-stream reduction reads it with ordinary
+// loads (which find it there and leave it for the op after); otherwise with
+// nontemporal loads, which stream data from HBM faster but leave the cache
+// without it. A hint only: results do not depend on it. Process-wide (the
+// reference drives one device from one host thread).
+constexpr uint64_t kRecentLaunches = 2;
+constexpr uint64_t kRecentMaxBytes = 192ull << 20;
+void note_output(const void *p, uint64_t bytes);
+bool recently_written(const void *p, uint64_t bytes);
+
 // Makes the batch-norm passes' occupancy and kernel-attribute lookups for
 // the current device now (dkz_init), so no op makes one for the first time
 // inside a graph capture.

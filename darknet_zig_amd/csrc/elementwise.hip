@@ -116,8 +116,7 @@ __global__ __launch_bounds__(kBlock) void ew_scalar_kernel(Op op, Streams<NI, NO
 }
 
 template <int H, int NI, int NO, class Op>
-int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
-    if (n == 0) return 0;
+int launch_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
     bool vec = true;
     for (int k = 0; k < NI; ++k) vec = vec && aligned16(s.in[k]);
     for (int k = 0; k < NO; ++k) vec = vec && aligned16(s.out[k]);
@@ -133,6 +132,15 @@ int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
     }
     const uint32_t grid = div_up(un, kBlock) < 65536u ? div_up(un, kBlock) : 65536u;
     return launch(name, ew_scalar_kernel<NI, NO, Op>, dim3(grid), dim3(kBlock), op, s, un);
+}
+
+// Launches the op and records what it wrote (note_output).
+template <int H, int NI, int NO, class Op>
+int run_ew(const char *name, const Op &op, const Streams<NI, NO> &s, int n) {
+    if (n == 0) return 0;
+    DKZ_TRY(launch_ew<H>(name, op, s, n));
+    for (int k = 0; k < NO; ++k) note_output(s.out[k], 4ull * (uint32_t)n);
+    return 0;
 }
 
 // ---- ops (CPU twins: blas.zig:13-46, activations.zig:107-143) -------------

@@ -448,9 +448,14 @@ int dkz_mean_delta(const float *delta, const float *variance, int batch, int fil
     DKZ_REQUIRE_SHAPE(batch, filters, spatial);
     if (filters == 0) return 0;
     DKZ_REQUIRE(out && variance && (delta || (uint64_t)batch * spatial == 0));
-    return run_chan_reduce<DKZ_HINT_MEAN_DELTA, SumValue, FinMeanDelta, false>("mean_delta", SumValue{},
-                                                          FinMeanDelta{out, variance}, delta, nullptr,
-                                                          batch, filters, spatial);
+    const FinMeanDelta fin{out, variance};
+    if (recently_written(delta, 4ull * (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial))
+        return run_chan_reduce<DKZ_HINT_MEAN_DELTA, SumValue, FinMeanDelta, false>("mean_delta", SumValue{}, fin,
+                                                                                   delta, nullptr, batch, filters,
+                                                                                   spatial);
+    return run_chan_reduce<DKZ_HINT_MEAN_DELTA_COLD, SumValue, FinMeanDelta, false>("mean_delta", SumValue{}, fin,
+                                                                                    delta, nullptr, batch, filters,
+                                                                                    spatial);
 }
 
 int dkz_variance_delta(const float *x, const float *delta, const float *mean, const float *variance,
@@ -473,9 +478,13 @@ int dkz_backward_bias(float *bias_updates, const float *delta, int batch, int fi
         return launch("backward_bias_conn", backward_bias_conn_kernel, dim3(div_up((uint32_t)filters, kWave)),
                       dim3(kConnWaves * kWave), bias_updates, delta, (uint32_t)batch, (uint32_t)filters);
     }
-    return run_chan_reduce<DKZ_HINT_BACKWARD_BIAS, SumValue, FinAccumulate, false>("backward_bias", SumValue{},
-                                                           FinAccumulate{bias_updates}, delta, nullptr, batch,
-                                                           filters, spatial);
+    const FinAccumulate fin{bias_updates};
+    if (recently_written(delta, 4ull * (uint64_t)batch * (uint64_t)filters * (uint64_t)spatial))
+        return run_chan_reduce<DKZ_HINT_BACKWARD_BIAS, SumValue, FinAccumulate, false>("backward_bias", SumValue{},
+                                                                                       fin, delta, nullptr, batch,
+                                                                                       filters, spatial);
+    return run_chan_reduce<DKZ_HINT_BACKWARD_BIAS_COLD, SumValue, FinAccumulate, false>(
+        "backward_bias", SumValue{}, fin, delta, nullptr, batch, filters, spatial);
 }
 
 int dkz_backward_scale(const float *x_norm, const float *delta, int batch, int filters, int spatial,

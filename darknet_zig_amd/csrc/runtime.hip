@@ -25,6 +25,16 @@ std::mutex g_mutex;
 // while another issues ops is a well-defined (if unordered) change.
 std::atomic<hipStream_t> g_stream{nullptr};
 std::atomic<bool> g_sync_after_launch{false};
+// note_output / recently_written: the last few written ranges, each with
+// the launch count just after the launch that wrote it.
+struct WrittenRange {
+    uintptr_t lo = 0, hi = 0;
+    uint64_t at = 0;
+};
+std::atomic<uint64_t> g_launches{0};
+std::mutex g_written_mutex;
+WrittenRange g_written[4];
+unsigned g_written_next = 0;
 thread_local char g_context[512] = "";
 thread_local const Scratch *t_scratch_override = nullptr;
 
@@ -69,7 +79,27 @@ void set_error_context(const char *fmt, ...) {
     va_end(ap);
 }
 
+void note_output(const void *p, uint64_t bytes) {
+    if (p == nullptr || bytes == 0) return;
+    std::lock_guard<std::mutex> lock(g_written_mutex);
+    WrittenRange &w = g_written[g_written_next++ % 4];
+    w.lo = (uintptr_t)p;
+    w.hi = (uintptr_t)p + bytes;
+    w.at = g_launches.load(std::memory_order_relaxed);
+}
+
+bool recently_written(const void *p, uint64_t bytes) {
+    if (p == nullptr || bytes == 0 || bytes > kRecentMaxBytes) return false;
+    const uintptr_t lo = (uintptr_t)p, hi = lo + bytes;
+    const uint64_t now = g_launches.load(std::memory_order_relaxed);
+    std::lock_guard<std::mutex> lock(g_written_mutex);
+    for (const WrittenRange &w : g_written)
+        if (w.hi > w.lo && lo >= w.lo && hi <= w.hi && now - w.at <= kRecentLaunches) return true;
+    return false;
+}
+
 int after_launch(const char *name, dim3 grid, dim3 block) {
+    g_launches.fetch_add(1, std::memory_order_relaxed);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error_context("HIP: launching %s <<<(%u,%u),(%u,%u)>>> failed: %s", name, grid.x, grid.y,
