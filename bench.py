@@ -39,10 +39,11 @@ over one batch; inputs are resident in HBM and rotate over three buffer sets
                TFLOP/s
                against the 157.3 TFLOP/s fp32 matrix-core peak
   fused_bwd    the same step through dkz_batchnorm_backward (at this size one
-               launch that holds 30 of each lane's 49 float4s of terms in
-               registers and LDS and reads y, delta and x of the rest again:
-               about 25 B/elem moved instead of the chain's 56; its
-               algorithmic bytes, each tensor once, are 20 B/elem)
+               launch that holds every element's delta * gradient * scale
+               in registers and LDS and x - mean for 11 of each lane's 49
+               float4s, and reads x of the other 38 again: about 23 B/elem
+               moved instead of the chain's 56; its algorithmic bytes, each
+               tensor once, are 20 B/elem)
   bn_act_gelem_s  batch-norm + activation elements per second: config 1's
                forward and config 2's backward (per op, the whole per-op layer
                forward, fused), and each config's layer forward + backward
@@ -227,9 +228,9 @@ def config2_chain_ops(gpu, d, h):
 
 def fused_backward(gpu, d, h):
     """The same layer step through the fused entry point (at config 2 one
-    launch: every element's y, delta, x_norm and x read once, 19 of each
-    lane's 49 float4s of y, delta and x read again after the channel
-    barrier, delta written: about 25 B/elem moved, 20 B/elem algorithmic)."""
+    launch: every element's y, delta, x_norm and x read once, x of 38 of
+    each lane's 49 float4s read again after the channel meeting, delta
+    written: about 23 B/elem moved, 20 B/elem algorithmic)."""
     from darknet_zig_amd.activations import Activation
 
     gpu.batchnormBackward(h["B"], h["F"], h["S"], Activation.leaky, d["y"], d["delta"], d["x"], d["x_norm"],
@@ -1403,8 +1404,9 @@ def main() -> int:
         },
         "chain_kernels": chain_kernels,
         "fused_bwd": {
-            "entry": "dkz_batchnorm_backward (same step, same buffers; here one launch holding part of each "
-                     "chunk in registers and LDS, about 25 B/elem moved; bytes below are algorithmic, 20 B/elem)",
+            "entry": "dkz_batchnorm_backward (same step, same buffers; here one launch holding each element's "
+                     "delta term in registers and LDS and reading x of most again, about 23 B/elem moved; bytes "
+                     "below are algorithmic, 20 B/elem)",
             "us": round(fused_ms * 1e3, 2),
             "bytes": 5 * 4 * h["n"],
             "GB/s": round(gbs(5 * 4 * h["n"], fused_ms), 1),

@@ -43,6 +43,7 @@
 // every shape (and edge case) exactly as the individual entry points do.
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
 
 #include "dkz_channel.hpp"
 #include "dkz_hints.hpp"
@@ -58,6 +59,17 @@ template <int NS>
 struct Sums {
     double s[NS];
 };
+
+// f(std::integral_constant<int, I>) for I = B, B + S, ... < E: a loop whose
+// index is a compile-time constant in each step (so arrays indexed by it
+// stay in registers, however long the body).
+template <int B, int E, int S, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + S, E, S>(f);
+    }
+}
 
 // Workgroup of a reduction pass: chunk k of channel f. KMAJOR: consecutive
 // workgroups take the same chunk of consecutive channels, so the grid
@@ -883,23 +895,36 @@ __global__ __launch_bounds__(kBlock) void bn_bwd_apply_kernel(const float *y, fl
 #define DKZ_BN_BWD_COOP_U2 4
 #endif
 constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
-// bn_bwd_reg_kernel: 512 threads, UH float4s a lane whose terms stay in
-// registers, UL whose terms go to LDS (144 KiB of the CU's 160) and UR read
-// again, UH + UL + UR = 49 (one workgroup a CU covers 100352 elements, half
-// a config-2 channel), loading G float4s of each input at once. Measured at
-// config 2 (graph replay, cold): two passes 128 us; registers only, UH 22 /
-// 20 (G 2) 104.5 / 105.5 us, UH 16 / 12 (G 4) 110 / 113 us; UH 21 + UL 9
-// 97.4 us (UH 20 + UL 9 97.7). UH 21 takes up to 252 registers a lane
-// (every activation), no scratch; a build that spilled would take the two
-// passes.
+// bn_bwd_reg_kernel: 512 threads (one workgroup a CU), 49 float4s of each
+// input a lane (a workgroup covers 100352 elements, half a config-2
+// channel), loading G float4s of each input at once. Of the two terms
+// normalize_delta needs, d2 (delta * gradient(y) * scale: two inputs) is
+// held for all 49 -- RD in registers, the other 49 - RD in LDS -- and
+// x - mean for the first LX in LDS; the other 49 - LX read x again after the
+// meeting (4 bytes an element instead of y, delta and x). LDS: (49 - RD +
+// LX) float4s a lane, 144 KiB of the CU's 160 at RD 42, LX 11. Measured at
+// config 2 (graph replay, cold): two passes 128 us; holding both terms of
+// 30 float4s (21 in registers, 9 in LDS) and reading y, delta and x of the
+// other 19 again 93.8-94.5 us; registers only, both terms, 22 / 20 / 16 /
+// 12 float4s 104.5 / 105.5 / 110 / 113 us; this layout 88.9 us with GX 8
+// x loads in flight after the meeting (GX 4 / 2: 89.6 / 91.7 us). RD 42
+// takes up to 240 registers a lane and no scratch with G 2 (G 4 spills, and
+// a build that spilled takes the two passes: 126 us).
 #ifndef DKZ_BN_BWD_REG
 #define DKZ_BN_BWD_REG 1
 #endif
-#ifndef DKZ_BN_BWD_REG_UH
-#define DKZ_BN_BWD_REG_UH 21
+#ifndef DKZ_BN_BWD_REG_RD
+#define DKZ_BN_BWD_REG_RD 42
+#endif
+#ifndef DKZ_BN_BWD_REG_LX
+#define DKZ_BN_BWD_REG_LX 11
 #endif
 #ifndef DKZ_BN_BWD_REG_G
 #define DKZ_BN_BWD_REG_G 2
+#endif
+// x loads in flight a lane after the meeting
+#ifndef DKZ_BN_BWD_REG_GX
+#define DKZ_BN_BWD_REG_GX 8
 #endif
 // Tensors larger than the GPU holds at once take this kernel while a
 // workgroup's chunk is at most this many times what it holds (its share of
@@ -907,11 +932,9 @@ constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
 #ifndef DKZ_BN_BWD_REG_MAX_CHUNKS
 #define DKZ_BN_BWD_REG_MAX_CHUNKS 4
 #endif
-#ifndef DKZ_BN_BWD_REG_UL
-#define DKZ_BN_BWD_REG_UL 9
-#endif
-constexpr int kBwdRegBS = 512, kBwdRegUH = DKZ_BN_BWD_REG_UH, kBwdRegUL = DKZ_BN_BWD_REG_UL;
-constexpr int kBwdRegUR = 49 - kBwdRegUH - kBwdRegUL;
+constexpr int kBwdRegBS = 512, kBwdRegU = 49, kBwdRegRD = DKZ_BN_BWD_REG_RD, kBwdRegLX = DKZ_BN_BWD_REG_LX;
+static_assert(kBwdRegRD <= kBwdRegU && kBwdRegLX <= kBwdRegU, "held float4s within the chunk");
+static_assert((size_t)(kBwdRegU - kBwdRegRD + kBwdRegLX) * kBwdRegBS * 16 <= 144 * 1024, "LDS of one CU");
 constexpr int kBwdCoopBS2 = DKZ_BN_BWD_COOP_BS2, kBwdCoopU2 = DKZ_BN_BWD_COOP_U2;
 
 template <int A, int H, int BS, int U>
@@ -988,26 +1011,27 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
 
 // The one-launch backward for tensors too large for bn_bwd_coop_kernel's
 // grid to fit the GPU at once (config 2's): one 512-thread workgroup a CU,
-// UH + UL + UR float4s of each input a lane. The sums pass over the chunk
-// keeps the two terms normalize_delta needs (d2 and x - mean, as
-// bn_bwd_coop_kernel holds them) for its first UH float4s in registers and
-// for the next UL in LDS; after the channel barrier those are written from
-// there, and the last UR float4s are read again (y, delta, x) and written as
-// bn_bwd_apply_kernel writes them. The sums pass reads that re-read part
-// with ordinary loads, so the second read finds it in the Infinity Cache,
-// and the rest nontemporally. Bytes: 16 an element read once, plus 12 for
-// the re-read part, plus 4 written -- instead of the two passes' 16 + 12 + 4
-// for every element.
-template <int A, int H, int BS, int UH, int UL, int UR>
+// U float4s of each input a lane. The sums pass over the chunk keeps d2 for
+// all U float4s (RD in registers, the rest in LDS) and x - mean for the
+// first LX (LDS); after the channel meeting the output is formed from those
+// and, past LX, from x read again. The sums pass reads that part of x with
+// ordinary loads, so the second read may find it in the Infinity Cache, and
+// everything else nontemporally. Bytes: 16 an element read once, 4 written,
+// plus 4 for x read again past LX -- instead of the two passes' 16 + 12 + 4
+// for every element. Chunks longer than U float4s a lane (tensors larger
+// than the GPU holds at once) read y, delta and x of the rest again.
+template <int A, int H, int BS, int U, int RD, int LX>
 __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *delta, const float *x_norm,
                                                         const float *x, BwdParams p, RedGeom g, BwdFin fin,
                                                         uint64_t *slots, uint32_t spin) {
     constexpr bool kLin = A == kLinear;
     constexpr bool kNtOut = (H & 16) != 0;
-    constexpr int G = DKZ_BN_BWD_REG_G;  // float4s of each input a lane loads at once
-    constexpr int UL1 = UL > 0 ? UL : 1;
+    constexpr int G = DKZ_BN_BWD_REG_G;   // float4s of each input a lane loads at once
+    constexpr int GX = DKZ_BN_BWD_REG_GX; // x loads in flight after the meeting
+    constexpr int LD = U - RD;            // d2 float4s held in LDS
     __shared__ double lds[4 * (BS / kWave)];
-    __shared__ float4 held_d2[UL1 * BS], held_xm[UL1 * BS];  // float4 UH + i of lane t at [i * BS + t]
+    __shared__ float4 held_d2[(LD > 0 ? LD : 1) * BS];  // float4 RD + i of lane t at [i * BS + t]
+    __shared__ float4 held_xm[(LX > 0 ? LX : 1) * BS];  // float4 i of lane t at [i * BS + t]
     __shared__ BwdChan chan_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
     const uint32_t k = blockIdx.x - f * g.K;
@@ -1024,15 +1048,18 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
         asm volatile("" : "+v"(jb));
         return jb;
     };
-    float4 d2[UH], xm[UH];
+    float4 d2[RD > 0 ? RD : 1];
     double a[4] = {0.0, 0.0, 0.0, 0.0};
-    // sums over the held part, keeping d2 and x - m
-#pragma unroll
-    for (int u0 = 0; u0 < UH; u0 += G) {
+    // sums over the held part, keeping d2 (and x - m for u < LX); the steps
+    // are generated at compile time, so every index into d2 is a constant
+    // and the array stays in registers
+    static_for<0, U, G>([&](auto step) {
+        constexpr int u0 = decltype(step)::value;
+        constexpr int n = U - u0 < G ? U - u0 : G;
         const uint32_t jb = phase_base();
         float4 vy[G], vd[G], vn[G], vx[G];
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH; ++v) {
+        for (int v = 0; v < n; ++v) {
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
             if (j < j1) {
                 const uint32_t at = chan_addr(fbase, j, g) >> 2;
@@ -1040,79 +1067,32 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
                 if constexpr (!kLin) vy[v] = ld4<true>(y, at);
                 else vy[v] = vd[v];
                 vn[v] = ld4<true>(x_norm, at);
-                vx[v] = ld4<true>(x, at);
+                // x past LX is read again after the meeting: cached
+                vx[v] = u0 + v < LX ? ld4<true>(x, at) : ld4<false>(x, at);
             }
         }
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j >= j1) continue;
+        static_for<0, n, 1>([&](auto vc) {
+            constexpr int v = decltype(vc)::value, u = u0 + v;
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j >= j1) return;
             acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
+            float4 t2;
 #pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                lane(d2[u0 + v], l) = grad_delta<A>(lane(vd[v], l), lane(vy[v], l)) * gam;
-                lane(xm[u0 + v], l) = lane(vx[v], l) - m;
+            for (int l = 0; l < 4; ++l) lane(t2, l) = grad_delta<A>(lane(vd[v], l), lane(vy[v], l)) * gam;
+            if constexpr (u < RD) d2[u] = t2;
+            else held_d2[(u - RD) * BS + threadIdx.x] = t2;
+            if constexpr (u < LX) {
+                float4 tm;
+#pragma unroll
+                for (int l = 0; l < 4; ++l) lane(tm, l) = lane(vx[v], l) - m;
+                held_xm[u * BS + threadIdx.x] = tm;
             }
-        }
-    }
-    // sums over the part whose terms go to LDS
-#pragma unroll
-    for (int u0 = UH; u0 < UH + UL; u0 += G) {
-        const uint32_t jb = phase_base();
-        float4 vy[G], vd[G], vn[G], vx[G];
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j < j1) {
-                const uint32_t at = chan_addr(fbase, j, g) >> 2;
-                vd[v] = ld4<true>(delta, at);
-                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
-                else vy[v] = vd[v];
-                vn[v] = ld4<true>(x_norm, at);
-                vx[v] = ld4<true>(x, at);
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j >= j1) continue;
-            acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
-            float4 t2, tm;
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                lane(t2, l) = grad_delta<A>(lane(vd[v], l), lane(vy[v], l)) * gam;
-                lane(tm, l) = lane(vx[v], l) - m;
-            }
-            held_d2[(u0 + v - UH) * BS + threadIdx.x] = t2;
-            held_xm[(u0 + v - UH) * BS + threadIdx.x] = tm;
-        }
-    }
-    // sums over the re-read part (y, delta, x cached for the second read)
-#pragma unroll
-    for (int u0 = UH + UL; u0 < UH + UL + UR; u0 += G) {
-        const uint32_t jb = phase_base();
-        float4 vy[G], vd[G], vn[G], vx[G];
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j < j1) {
-                const uint32_t at = chan_addr(fbase, j, g) >> 2;
-                vd[v] = ld4<false>(delta, at);
-                if constexpr (!kLin) vy[v] = ld4<false>(y, at);
-                else vy[v] = vd[v];
-                vn[v] = ld4<true>(x_norm, at);
-                vx[v] = ld4<false>(x, at);
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
-        }
-    }
-    // chunks longer than UH + UL + UR float4s a lane (tensors larger than the
-    // GPU holds at once): the rest is re-read as well
-    for (uint32_t u0 = UH + UL + UR;; u0 += G) {
+        });
+    });
+    // chunks longer than U float4s a lane (tensors larger than the GPU
+    // holds at once): the rest is read here, cached, and again after the
+    // meeting
+    for (uint32_t u0 = U;; u0 += G) {
         const uint32_t jb = phase_base();
         if (jb + u0 * (4 * BS) >= j1) break;
         float4 vy[G], vd[G], vn[G], vx[G];
@@ -1147,52 +1127,39 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
     }
     __syncthreads();
     const BwdChan ch = chan_sh;
-    {
+    // the held part: d2 from registers or LDS, x - m from LDS or x read again
+    static_for<0, U, GX>([&](auto step) {
+        constexpr int u0 = decltype(step)::value;
+        constexpr int n = U - u0 < GX ? U - u0 : GX;
         const uint32_t jb = phase_base();
-#pragma unroll
-        for (int u = 0; u < UH; ++u) {
-            const uint32_t j = jb + (uint32_t)u * (4 * BS);
-            if (j >= j1) continue;
-            float4 o;
-#pragma unroll
-            for (int l = 0; l < 4; ++l)  // bwd_elem's expression on the held terms
-                lane(o, l) = (lane(d2[u], l) * ch.inv + (ch.vd2 * lane(xm[u], l)) / p.denom) + ch.mdn;
-            st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
-        }
-#pragma unroll
-        for (int u = UH; u < UH + UL; ++u) {
-            const uint32_t j = jb + (uint32_t)u * (4 * BS);
-            if (j >= j1) continue;
-            const float4 t2 = held_d2[(u - UH) * BS + threadIdx.x], tm = held_xm[(u - UH) * BS + threadIdx.x];
-            float4 o;
-#pragma unroll
-            for (int l = 0; l < 4; ++l)
-                lane(o, l) = (lane(t2, l) * ch.inv + (ch.vd2 * lane(tm, l)) / p.denom) + ch.mdn;
-            st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
-        }
-    }
-#pragma unroll
-    for (int u0 = UH + UL; u0 < UH + UL + UR; u0 += G) {
-        const uint32_t jb = phase_base();
-        float4 vy[G], vd[G], vx[G];
-#pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
+        float4 vx[GX];
+        static_for<0, n, 1>([&](auto vc) {
+            constexpr int v = decltype(vc)::value;
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j < j1) {
-                const uint32_t at = chan_addr(fbase, j, g) >> 2;
-                vd[v] = ld4<true>(delta, at);
-                if constexpr (!kLin) vy[v] = ld4<true>(y, at);
-                else vy[v] = vd[v];
-                vx[v] = ld4<true>(x, at);
+            if constexpr (u0 + v >= LX) {
+                if (j < j1) vx[v] = ld4<true>(x, chan_addr(fbase, j, g) >> 2);
             }
-        }
+        });
+        static_for<0, n, 1>([&](auto vc) {
+            constexpr int v = decltype(vc)::value, u = u0 + v;
+            const uint32_t j = jb + (uint32_t)u * (4 * BS);
+            if (j >= j1) return;
+            float4 t2, tm;
+            if constexpr (u < RD) t2 = d2[u];
+            else t2 = held_d2[(u - RD) * BS + threadIdx.x];
+            if constexpr (u < LX) {
+                tm = held_xm[u * BS + threadIdx.x];
+            } else {
 #pragma unroll
-        for (int v = 0; v < G && u0 + v < UH + UL + UR; ++v) {
-            const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if (j < j1) st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, bwd_elem<A>(vy[v], vd[v], vx[v], ch, p.denom));
-        }
-    }
-    for (uint32_t u0 = UH + UL + UR;; u0 += G) {
+                for (int l = 0; l < 4; ++l) lane(tm, l) = lane(vx[v], l) - ch.m;
+            }
+            float4 o;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) lane(o, l) = (lane(t2, l) * ch.inv + (ch.vd2 * lane(tm, l)) / p.denom) + ch.mdn;
+            st4<kNtOut>(delta, chan_addr(fbase, j, g) >> 2, o);
+        });
+    });
+    for (uint32_t u0 = U;; u0 += G) {
         const uint32_t jb = phase_base();
         if (jb + u0 * (4 * BS) >= j1) break;
         float4 vy[G], vd[G], vx[G];
@@ -1466,9 +1433,9 @@ bool bwd_coop(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
 // kernel keeps its held part in registers (no scratch).
 template <int A>
 bool bwd_reg(const BwdArgs &a, uint64_t L, const BwdFin &fin, int *rc) {
-    constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegUH, kBwdRegUL, kBwdRegUR>;
+    constexpr auto kernel = bn_bwd_reg_kernel<A, DKZ_HINT_BN_BWD_COOP, kBwdRegBS, kBwdRegU, kBwdRegRD, kBwdRegLX>;
     const Shape &sh = a.sh;
-    constexpr uint64_t kCap = (uint64_t)kBwdRegBS * 4 * (kBwdRegUH + kBwdRegUL + kBwdRegUR);  // 100352
+    constexpr uint64_t kCap = (uint64_t)kBwdRegBS * 4 * kBwdRegU;  // 100352
     if (!no_spills<kernel>()) return false;
     const uint64_t res = resident_workgroups<kernel, kBwdRegBS>();
     uint64_t K = div_up(L, kCap);
@@ -1537,7 +1504,7 @@ void prewarm() {
     (void)resident_workgroups<bn_fwd_coop_kernel<A, HF, kRegBlock, kRegU, true>, kRegBlock>();
     (void)resident_workgroups<bn_bwd_coop_kernel<A, HB, kBwdCoopBS, kBwdCoopU>, kBwdCoopBS>();
     (void)resident_workgroups<bn_bwd_coop_kernel<A, HB, kBwdCoopBS2, kBwdCoopU2>, kBwdCoopBS2>();
-    constexpr auto reg = bn_bwd_reg_kernel<A, HB, kBwdRegBS, kBwdRegUH, kBwdRegUL, kBwdRegUR>;
+    constexpr auto reg = bn_bwd_reg_kernel<A, HB, kBwdRegBS, kBwdRegU, kBwdRegRD, kBwdRegLX>;
     (void)no_spills<reg>();
     (void)resident_workgroups<reg, kBwdRegBS>();
 }
