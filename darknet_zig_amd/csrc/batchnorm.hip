@@ -530,8 +530,6 @@ __device__ __forceinline__ void channel_leave(uint64_t *slots, uint32_t F, uint3
 // 1024 x 2 / x 3 / x 6 / x 8 15.8 / 17.7 / 16.3 / 17.6; 128 x 16 18.4;
 // 256 x 4 / x 16 17.6 / 18.0. Shapes whose grid at 1024 x 4 does not fit
 // the GPU at once try 256 x 8 (smaller workgroups fit more of them).
-// x, the input's copy, is stored as soon as it is loaded (x after the
-// barrier with the other two outputs: 16.4 against 16.3 us at 256 x 8).
 #ifndef DKZ_BN_COOP_BS
 #define DKZ_BN_COOP_BS 1024
 #endif
@@ -546,8 +544,15 @@ __device__ __forceinline__ void channel_leave(uint64_t *slots, uint32_t F, uint3
 #endif
 constexpr int kCoopBS = DKZ_BN_COOP_BS, kCoopU = DKZ_BN_COOP_U;
 constexpr int kCoopBS2 = DKZ_BN_COOP_BS2, kCoopU2 = DKZ_BN_COOP_U2;
-#ifndef DKZ_BN_COOP_X_LATE
-#define DKZ_BN_COOP_X_LATE 0
+// Where the one-launch forward with 1024- or 256-thread workgroups stores x
+// (the input's copy): 0 as each float4 arrives, 1 after the channel meeting
+// with x_norm and the output, 2 from the workgroup's other waves while its
+// first wave meets the channel (the first wave's own after the meeting).
+// Measured at config 1 (graph replay, cold): 13.8-13.9 / 14.0 / 13.2 us;
+// the register-holding variant (config 2's shape) stores x at once: there 2
+// took 70.6 to 74.4 us.
+#ifndef DKZ_BN_COOP_X_STORE
+#define DKZ_BN_COOP_X_STORE 2
 #endif
 // The register-resident variant: 512 threads (two waves a SIMD, up to 256
 // registers a lane) holding 49 float4s a lane, so one workgroup a CU covers
@@ -571,7 +576,7 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
                                                          float *x_norm, FwdParams p, RedGeom g, FwdFin fin,
                                                          uint64_t *slots, uint32_t spin) {
     constexpr bool kNtIn = (H & 1) != 0, kNtX = (H & 2) != 0, kNtXn = (H & 4) != 0, kNtOut = (H & 8) != 0;
-    constexpr bool kXLate = DKZ_BN_COOP_X_LATE != 0;
+    constexpr int kXMode = U > kCoopU2 ? 0 : DKZ_BN_COOP_X_STORE;  // the register-holding variant stores x at once
     __shared__ double lds[2 * (BS / kWave)];
     __shared__ FwdChan chan_sh;
     const uint32_t f = fdiv(blockIdx.x, g.div_k);
@@ -609,7 +614,7 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
             acc_shifted(v[u], c, a[0], a[1]);
             // x (the input copy) needs no statistics: its stores drain while
             // the channel meets
-            if constexpr (!kXLate) st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, v[u]);
+            if constexpr (kXMode == 0) st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, v[u]);
         }
     }
     if constexpr (EXTRA) {
@@ -635,6 +640,18 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
         }
     }
     Sums<2> sums = block_sums<2, BS>(a, lds);
+    if constexpr (kXMode == 2) {
+        // the other waves store x while wave 0 meets the channel (wave 0's
+        // stores would hold its polls back: they count in the same vmcnt)
+        if (threadIdx.x >= kWave) {
+            const uint32_t jb = phase_base();
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = jb + (uint32_t)u * (4 * BS);
+                if (j < j1) st4<kNtX>(x, chan_addr(fbase, j, g) >> 2, v[u]);
+            }
+        }
+    }
     if (threadIdx.x < kWave) {
         const uint32_t met = channel_meet<2>(slots, F, g.K, f, k, sums, spin) ? 1u : 0u;
         if (threadIdx.x == 0) {
@@ -655,7 +672,10 @@ __global__ __launch_bounds__(BS) void bn_fwd_coop_kernel(const float *input, flo
         const uint32_t at = chan_addr(fbase, j, g) >> 2;
         float4 xn, o;
         fwd_elem<A>(v[u], ch, xn, o);
-        if constexpr (kXLate) st4<kNtX>(x, at, v[u]);
+        if constexpr (kXMode == 1) st4<kNtX>(x, at, v[u]);
+        if constexpr (kXMode == 2) {
+            if (threadIdx.x < kWave) st4<kNtX>(x, at, v[u]);
+        }
         st4<kNtXn>(x_norm, at, xn);
         st4<kNtOut>(output, at, o);
     }
