@@ -389,11 +389,8 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 // The K workgroups of one channel meet here: each posts its NS partial sums
 // and waits until all K have posted, then adds them (channel_meet, called
 // by wave 0 of the workgroup; the caller's __syncthreads follow).
-//   * Workgroup k's sums go to its own 128-byte line of the scratch's slots
-//     (line f*K + k after the F channel counters), as their bits XOR
-//     kMeetKey, so a posted value is never zero: kMeetKey is a NaN payload
-//     no sum produces (a NaN reaching a sum carries an f32 payload whose low
-//     29 bits are zero).
+//   * Workgroup k's sums go to its own posting line (line f*K + k after the
+//     F channel counters; kMeetLine, kMeetKey: dkz_channel.hpp).
 //   * Wave 0 then reads the channel's other lines with coherent loads until
 //     every value is non-zero and adds the K partials of each sum in index
 //     order -- lane l adds lines l, l + 64, ..., then a wave sum -- so every
@@ -423,8 +420,6 @@ __global__ __launch_bounds__(kBlock) void bn_fwd_apply_kernel(const float *input
 // and the late workgroups find every partial posted and finish the
 // protocol, leaving the slots clear for the next launch.
 constexpr uint32_t kSpinMax = 1u << 20;
-constexpr uint64_t kMeetKey = 0xFFF8DEADBEEF0001ull;
-constexpr uint32_t kMeetLine = 16;  // 64-bit slots a posting line (128 bytes)
 
 // Slots a one-launch pass over F channels of K workgroups needs: the
 // channel counters, then one posting line per workgroup.
@@ -434,7 +429,6 @@ inline uint64_t meet_slots(uint64_t F, uint64_t K) { return F * kCounterStride +
 // (0: none since the host last looked). Written by the kernels with a
 // vector atomic store, read and cleared by take_barrier_timeout.
 __device__ uint32_t barrier_timeout;
-enum : uint32_t { kTimeoutFwdCoop = 1, kTimeoutBwdCoop = 2, kTimeoutBwdReg = 3 };
 
 __device__ __forceinline__ void note_timeout(uint32_t met, uint32_t which) {
     if (met == 0) __hip_atomic_store(&barrier_timeout, which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1563,7 +1557,7 @@ int take_barrier_timeout() {
     static const char *const kernels[] = {"?", "batchnorm_forward (bn_fwd_coop_kernel)",
                                           "batchnorm_backward (bn_bwd_coop_kernel)",
                                           "batchnorm_backward (bn_bwd_reg_kernel)"};
-    set_error_context("HIP: %s: a channel barrier gave up waiting for the channel's other workgroups; those "
+    set_error_context("HIP: %s: a channel meeting gave up waiting for the channel's other workgroups; those "
                       "workgroups' outputs are NaN, rolling averages and bias/scale updates were left unchanged",
                       kernels[which < 4 ? which : 0]);
     return (int)hipErrorLaunchTimeOut;

@@ -47,6 +47,21 @@ __device__ __forceinline__ uint32_t chan_addr(uint32_t fbase, uint32_t j, const 
 // Widest workgroup of a one-launch channel reduction.
 constexpr uint32_t kWideBlock = 1024;
 
+// One-launch reductions hand f64 partial sums between workgroups through
+// the scratch's slots as the bits XOR kMeetKey, so a posted value is never
+// zero (the slots are zero when a launch starts, and every kernel that
+// posts leaves them zero): kMeetKey is a NaN payload no sum produces (a NaN
+// reaching a sum carries an f32 payload whose low 29 bits are zero). The
+// batch-norm passes give each workgroup its own 128-byte posting line
+// (kMeetLine 64-bit slots).
+constexpr uint64_t kMeetKey = 0xFFF8DEADBEEF0001ull;
+constexpr uint32_t kMeetLine = 16;
+
+// What a one-launch batch-norm pass that gave up waiting for the other
+// workgroups of its channel writes to the device's time-out flag
+// (take_barrier_timeout names it).
+enum : uint32_t { kTimeoutFwdCoop = 1, kTimeoutBwdCoop = 2, kTimeoutBwdReg = 3 };
+
 // How a channel reduction is split, from the shape only (so a shape always
 // reduces in the same order on any GPU). A workgroup streams at most
 // ~43 GB/s, so one 1024-thread workgroup per channel reaches ~5.5 TB/s with

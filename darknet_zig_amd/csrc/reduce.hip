@@ -167,18 +167,14 @@ __global__ __launch_bounds__(BS) void chan_split_kernel(T t, Fin fin, const floa
 // split kernel's three (store and wait, count, read the partials). Config
 // 2, cold: backward_bias / mean_delta 19.9 -> 18.5 us, backward_scale /
 // variance_delta 34.4 / 33.8 -> 33.5 / 32.5 us, the backward chain 6584 ->
-// 6680 GB/s (nontemporal delta loads would take backward_bias to 17.4 us
-// alone but cost the chain 3%: delta stays cached). A partial travels as its bits XOR
-// kSlotKey -- a NaN payload no sum produces, since NaNs reaching it carry an
-// f32 payload whose low 29 bits are zero -- so a stored partial is never
-// zero.
+// 6680 GB/s. A partial travels as its bits XOR kMeetKey (dkz_channel.hpp),
+// so a stored partial is never zero.
 #ifndef DKZ_CHAN_PAIR
 #define DKZ_CHAN_PAIR 1
 #endif
 #ifndef DKZ_PAIR_MAX_BYTES
 #define DKZ_PAIR_MAX_BYTES 250000000ull
 #endif
-constexpr uint64_t kSlotKey = 0xFFF8DEADBEEF0001ull;
 
 template <class T, class Fin, bool TWO, bool VEC, int H, int BS>
 __global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float *p0, const float *p1, RedGeom g,
@@ -189,11 +185,11 @@ __global__ __launch_bounds__(BS) void chan_pair_kernel(T t, Fin fin, const float
     const double s = chunk_sum<T, TWO, VEC, H, BS>(t, p0, p1, g, f, k, lds);
     if (threadIdx.x == 0) {
         uint64_t *slot = &slots[(uint64_t)f * kCounterStride];
-        const uint64_t mine = __builtin_bit_cast(uint64_t, s) ^ kSlotKey;
+        const uint64_t mine = __builtin_bit_cast(uint64_t, s) ^ kMeetKey;
         const uint64_t held = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (held != 0) {
             __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            fin(f, s + __builtin_bit_cast(double, held ^ kSlotKey), pre);
+            fin(f, s + __builtin_bit_cast(double, held ^ kMeetKey), pre);
         }
     }
 }
