@@ -402,13 +402,16 @@ TRAFFIC_PASSES = 3
 FLUSH_BYTES = 512 << 20
 
 
-def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graphs=True):
+def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graphs=True, hot_traffic=False):
     """The per-op table; with `traffic` (a list), no timing: each row's first
     TRAFFIC_PASSES launches (or call sequences) run once between markers and
     the row is appended to `traffic`. `only`: run only rows whose full name
     (config/op) contains one of these '|'-separated strings. `graphs` False:
     no HIP graph is captured; `us` is then the issued-from-Python time (for
-    a kernel-trace profile, which times each kernel itself)."""
+    a kernel-trace profile, which times each kernel itself). `hot_traffic`:
+    in traffic mode, rows that have a [hot cache] timing also run hot
+    between markers (the first rotation twice untimed, so the Infinity Cache
+    holds its data, then its passes), for counters of cold against hot."""
     from darknet_zig_amd.activations import Activation
 
     rows = {}
@@ -428,7 +431,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graph
         # a per-channel sum over 128 channels: cached loads, 512 B written
         gpu.backwardBias(flush_out, flush_buf, 1, 128, flush_f)
 
-    def traced(cfg, name, nbytes, seqs):
+    def traced(cfg, name, nbytes, seqs, hot=False):
         i = len(traffic)
         passes = min(TRAFFIC_PASSES, len(seqs))
         for seq in seqs:
@@ -444,6 +447,21 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graph
         hip.sync()
         traffic.append({"row": f"{cfg}/{name}", "bytes": nbytes, "passes": passes, "begin_grid": MARK_BASE + 2 * i})
         print(f"traffic row {i}: {cfg}/{name}", file=sys.stderr, flush=True)
+        if hot and hot_traffic:
+            i = len(traffic)
+            for _ in range(2):
+                for fn in seqs[0]:
+                    fn()
+            hip.sync()
+            marker(MARK_BASE + 2 * i)
+            for _ in range(TRAFFIC_PASSES):
+                for fn in seqs[0]:
+                    fn()
+            marker(MARK_BASE + 2 * i + 1)
+            hip.sync()
+            traffic.append({"row": f"{cfg}/{name} [hot cache]", "bytes": nbytes, "passes": TRAFFIC_PASSES,
+                            "begin_grid": MARK_BASE + 2 * i})
+            print(f"traffic row {i}: {cfg}/{name} [hot cache]", file=sys.stderr, flush=True)
 
     def row(cfg, name, nbytes, ms, single_ms=None, issued_ms=None):
         g = gbs(nbytes, ms)
@@ -468,7 +486,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graph
         if not wanted(cfg, name):
             return
         if traffic is not None:
-            return traced(cfg, name, nbytes, [[f] for f in fns])
+            return traced(cfg, name, nbytes, [[f] for f in fns], hot)
         k = max(launches, len(fns))
         seqs = [[f] for f in fns]
         issued = time_seq(hip, stream, seqs, k)
@@ -485,7 +503,7 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graph
         if not wanted(cfg, name):
             return
         if traffic is not None:
-            return traced(cfg, name, nbytes, seqs)
+            return traced(cfg, name, nbytes, seqs, hot)
         k = max(launches, len(seqs))
         issued = time_seq(hip, stream, seqs, k)
         row(cfg, name, nbytes, time_graph(hip, seqs, k) if graphs else issued, issued_ms=issued)
@@ -1264,6 +1282,43 @@ def sq_table(d: Path) -> str:
     return "\n".join(lines)
 
 
+LATENCY_COUNTERS = "TCC_EA0_RDREQ_LEVEL_sum TCC_EA0_RDREQ_sum TCC_EA0_WRREQ_LEVEL_sum TCC_EA0_WRREQ_sum GRBM_GUI_ACTIVE"
+
+
+def latency_table(d: Path) -> str:
+    """Memory latency per row (markdown) from the outputs under `d`:
+    rows.json (stdout of `bench.py --per-op-traffic --hot --rows ...`) and
+    lat/ (rocprofv3 --pmc LATENCY_COUNTERS over that command). Per pass: the
+    average number of L2 read and write requests in flight to the fabric
+    (EA) and their average latency (in-flight sum / requests, in L2 clock
+    cycles), for a row run cold (its data in HBM) and hot (in the Infinity
+    Cache)."""
+    def last_json(path):
+        return json.loads([ln for ln in open(path) if ln.startswith("{")][-1])
+
+    meta = last_json(d / "rows.json")
+    rows, base = meta["per_op_traffic"], meta["mark_base"]
+    seg = _segments([(n, b, c) for n, b, c in _dispatch_counters(d / "lat")], base)
+    lines = [
+        "| row | EA read requests | avg read latency (cycles) | EA write requests | avg write latency (cycles) "
+        "| GRBM_GUI_ACTIVE cycles |",
+        "|---|---|---|---|---|---|",
+    ]
+    for i, r in enumerate(rows):
+        p = r["passes"]
+        c = {}
+        for _, vals in seg.get(i, []):
+            for k, v in vals.items():
+                c[k] = c.get(k, 0.0) + v / p
+        if not c:
+            continue
+        rq, wq = c.get("TCC_EA0_RDREQ_sum", 0.0), c.get("TCC_EA0_WRREQ_sum", 0.0)
+        rl = c.get("TCC_EA0_RDREQ_LEVEL_sum", 0.0) / rq if rq else float("nan")
+        wl = c.get("TCC_EA0_WRREQ_LEVEL_sum", 0.0) / wq if wq else float("nan")
+        lines.append(f"| {r['row']} | {rq:.0f} | {rl:.0f} | {wq:.0f} | {wl:.0f} | {c.get('GRBM_GUI_ACTIVE', 0):.0f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1274,6 +1329,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--per-op-only", action="store_true",
                     help="only run the per-op table (for a kernel trace without the chain's launches)")
+    ap.add_argument("--hot", action="store_true",
+                    help="with --per-op-traffic: also run each row that has a [hot cache] timing hot, between "
+                         "markers of its own")
     ap.add_argument("--no-graph", action="store_true",
                     help="with --per-op-only: capture no HIP graph (per-op `us` is then the issued time); for "
                          "rocprofv3 --kernel-trace, under which the graph-replay timing ended in a host "
@@ -1287,6 +1345,8 @@ def main() -> int:
     ap.add_argument("--rows", default=None, metavar="SUBSTR",
                     help="with --per-op-only or --per-op-traffic: only the per-op rows whose name "
                          "(config/op) contains SUBSTR ('|'-separated alternatives)")
+    ap.add_argument("--latency-table", default=None, metavar="DIR",
+                    help="print the memory-latency table (cold against hot rows) from DIR/rows.json and DIR/lat")
     ap.add_argument("--sq-table", default=None, metavar="DIR",
                     help="only print the instruction-mix table (markdown) from the rocprofv3 SQ counter outputs "
                          "in DIR (see sq_table())")
@@ -1304,6 +1364,9 @@ def main() -> int:
         return 0
     if args.sq_table:
         print(sq_table(Path(args.sq_table)))
+        return 0
+    if args.latency_table:
+        print(latency_table(Path(args.latency_table)))
         return 0
 
     from darknet_zig_amd import gpu
@@ -1326,7 +1389,7 @@ def main() -> int:
 
     if args.per_op_traffic:
         traffic = []
-        per_op_table(gpu, hip, stream, 1, traffic, only=args.rows)
+        per_op_table(gpu, hip, stream, 1, traffic, only=args.rows, hot_traffic=args.hot)
         print(json.dumps({"per_op_traffic": traffic, "mark_base": MARK_BASE}), flush=True)
         return 0
 
