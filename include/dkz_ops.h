@@ -41,15 +41,16 @@
  *   - The library owns one scratch buffer per device (130.5 MiB), allocated
  *     and zeroed by dkz_init: the f64 partial sums of the split per-channel
  *     reductions (2 MiB), the partial tiles of a split-K gemm or convolution
- *     weight gradient (128 MiB) and 64-bit counter slots (512 KiB: one
- *     256-byte line per channel's meeting slot, arrival counter or barrier)
- *     through which a reduction's workgroups find the channel's last. Ops
- *     never allocate, and leave the slots they use at zero. Reductions or
+ *     weight gradient (128 MiB) and 64-bit slots (512 KiB: one 256-byte
+ *     line per channel's meeting slot or arrival counter, and one 128-byte
+ *     posting line per workgroup of a one-launch batch-norm pass), through
+ *     which a reduction's workgroups hand each other their partial sums.
+ *     Ops never allocate, and leave the slots they use at zero. Reductions or
  *     gemms issued concurrently on two streams of one device share that
  *     buffer and race; issue them on one stream (dkz_set_stream).
  *   - dkz_batchnorm_forward and dkz_batchnorm_backward may run as one launch
- *     whose workgroups meet at per-channel barriers. A wait there is bounded
- *     (~0.1 s); if it runs out (the GPU did not hold all of the launch's
+ *     whose workgroups meet per channel. A wait there is bounded (about a
+ *     second); if it runs out (the GPU did not hold all of the launch's
  *     workgroups at once, e.g. with other work on the device) the
  *     workgroup's results are NaN and it adds nothing to rolling_mean,
  *     rolling_variance, bias_updates or scale_updates. The next
@@ -126,11 +127,11 @@ int dkz_copy_to_device(void *dst, const void *src, size_t bytes);
 
 /* gpu.zig:395-405 pull()/pullInts() / hip.zig:103-105 copyToHost. Blocking,
  * after all earlier work on the current stream. Also reports (and clears) a
- * batch-norm channel-barrier time-out: hipErrorLaunchTimeOut after the copy. */
+ * batch-norm channel-meeting time-out: hipErrorLaunchTimeOut after the copy. */
 int dkz_copy_to_host(void *dst, const void *src, size_t bytes);
 
 /* gpu.zig:407-410 sync() / hip.zig:107-109 synchronize. Also reports (and
- * clears) a batch-norm channel-barrier time-out: hipErrorLaunchTimeOut. */
+ * clears) a batch-norm channel-meeting time-out: hipErrorLaunchTimeOut. */
 int dkz_synchronize(void);
 
 /* hip.zig:60-62 errorString. */
