@@ -921,7 +921,8 @@ constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
 // 30 float4s (21 in registers, 9 in LDS) and reading y, delta and x of the
 // other 19 again 93.8-94.5 us; registers only, both terms, 22 / 20 / 16 /
 // 12 float4s 104.5 / 105.5 / 110 / 113 us; this layout 88.9 us with GX 8
-// x loads in flight after the meeting (GX 4 / 2: 89.6 / 91.7 us). RD 42
+// x loads in flight after the meeting (GX 4 / 2: 89.6 / 91.7 us), the
+// first PRE of them issued before the meeting (DKZ_BN_BWD_REG_PRE). RD 42
 // takes up to 240 registers a lane and no scratch with G 2 (G 4 spills, and
 // a build that spilled takes the two passes: 126 us).
 #ifndef DKZ_BN_BWD_REG
@@ -939,6 +940,12 @@ constexpr int kBwdCoopBS = DKZ_BN_BWD_COOP_BS, kBwdCoopU = DKZ_BN_BWD_COOP_U;
 // x loads in flight a lane after the meeting
 #ifndef DKZ_BN_BWD_REG_GX
 #define DKZ_BN_BWD_REG_GX 8
+#endif
+// x float4s a lane of the part read again that are loaded before the block's
+// sums and the meeting, so that they are in flight while the workgroup waits
+// (config 2, A/B on one box: 91.2 -> 90.5 us with 8, 90.6 with 4; 16 spills)
+#ifndef DKZ_BN_BWD_REG_PRE
+#define DKZ_BN_BWD_REG_PRE 8
 #endif
 // Tensors larger than the GPU holds at once take this kernel while a
 // workgroup's chunk is at most this many times what it holds (its share of
@@ -1043,6 +1050,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
     constexpr int G = DKZ_BN_BWD_REG_G;   // float4s of each input a lane loads at once
     constexpr int GX = DKZ_BN_BWD_REG_GX; // x loads in flight after the meeting
     constexpr int LD = U - RD;            // d2 float4s held in LDS
+    constexpr int PX = DKZ_BN_BWD_REG_PRE < U - LX ? DKZ_BN_BWD_REG_PRE : U - LX;  // x loaded before the meeting
     __shared__ double lds[4 * (BS / kWave)];
     __shared__ float4 held_d2[(LD > 0 ? LD : 1) * BS];  // float4 RD + i of lane t at [i * BS + t]
     __shared__ float4 held_xm[(LX > 0 ? LX : 1) * BS];  // float4 i of lane t at [i * BS + t]
@@ -1128,6 +1136,17 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             if (j < j1) acc_bwd<A>(vy[v], vd[v], vn[v], vx[v], m, gam, a);
         }
     }
+    // the first PX float4s of the x read again, loaded now so they are in
+    // flight during the block's sums and the meeting
+    float4 px[PX > 0 ? PX : 1];
+    {
+        const uint32_t jb = phase_base();
+        static_for<0, PX, 1>([&](auto vc) {
+            constexpr int v = decltype(vc)::value;
+            const uint32_t j = jb + (uint32_t)(LX + v) * (4 * BS);
+            if (j < j1) px[v] = ld4<true>(x, chan_addr(fbase, j, g) >> 2);
+        });
+    }
     Sums<4> sums = block_sums<4, BS>(a, lds);
     if (threadIdx.x < kWave) {
         const uint32_t met = channel_meet<4>(slots, F, g.K, f, k, sums, spin) ? 1u : 0u;
@@ -1150,7 +1169,7 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
         static_for<0, n, 1>([&](auto vc) {
             constexpr int v = decltype(vc)::value;
             const uint32_t j = jb + (uint32_t)(u0 + v) * (4 * BS);
-            if constexpr (u0 + v >= LX) {
+            if constexpr (u0 + v >= LX + PX) {
                 if (j < j1) vx[v] = ld4<true>(x, chan_addr(fbase, j, g) >> 2);
             }
         });
@@ -1163,6 +1182,9 @@ __global__ __launch_bounds__(BS) void bn_bwd_reg_kernel(const float *y, float *d
             else t2 = held_d2[(u - RD) * BS + threadIdx.x];
             if constexpr (u < LX) {
                 tm = held_xm[u * BS + threadIdx.x];
+            } else if constexpr (u < LX + PX) {
+#pragma unroll
+                for (int l = 0; l < 4; ++l) lane(tm, l) = lane(px[u - LX], l) - ch.m;
             } else {
 #pragma unroll
                 for (int l = 0; l < 4; ++l) lane(tm, l) = lane(vx[v], l) - ch.m;
