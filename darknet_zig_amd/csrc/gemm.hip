@@ -69,6 +69,14 @@ constexpr int kXcds = 8;
 #define DKZ_GEMM_FULL_SLABS 1
 #endif
 
+// Tiles wholly inside both operands take a loop without edge checks whose
+// slab loads stay in flight (build-time switch, for measurement). Config 2's
+// per-image convolution GEMMs 22.9 / 19.5 / 20.8 -> 21.0 / 18.3 / 19.8 us,
+// 4096^3 109 -> 111 TFLOP/s, 8192x8192x4096 122 -> 126.
+#ifndef DKZ_GEMM_FULL_TILES
+#define DKZ_GEMM_FULL_TILES 1
+#endif
+
 // Workgroups per CU that a split-K grid aims for (build-time tunable).
 #ifndef DKZ_GEMM_SPLIT_TARGET
 #define DKZ_GEMM_SPLIT_TARGET 2
@@ -197,11 +205,13 @@ struct Slab {
 
     // rows: tile rows available (m - m0 or n - n0); k0/kmax: the slab's first
     // k and the end of this split's range.
+    template <bool FULL = false>
     __device__ __forceinline__ void load(const float *p, uint32_t ld, uint32_t r0, uint32_t rows, uint32_t k0,
                                          uint32_t kend, bool vec, int tid) {
         // A whole slab inside the matrix (the usual case): every float4 is
-        // there, so no per-element checks (a branch the whole workgroup takes).
-        if (DKZ_GEMM_FULL_SLABS && vec && rows >= (uint32_t)R && kend - k0 >= (uint32_t)kBK) {
+        // there, so no per-element checks (a branch the whole workgroup
+        // takes). FULL: the caller has checked that for every slab of the tile.
+        if (FULL || (DKZ_GEMM_FULL_SLABS && vec && rows >= (uint32_t)R && kend - k0 >= (uint32_t)kBK)) {
 #pragma unroll
             for (int l = 0; l < kLoads; ++l) {
                 const int f = tid + l * kBlock;
@@ -506,13 +516,13 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
 
     std::conditional_t<kWg, SegSlab<BM>, Slab<BM, !TA>> sa[D];
     std::conditional_t<IM != kImNone, ConvSlab<BN, kWg, kMode, kSpanKind>, Slab<BN, TB>> sb[D];
-    auto load_a = [&](auto &slab, uint32_t k0) {
+    auto load_a = [&](auto &slab, uint32_t k0, auto full) {
         if constexpr (kWg) slab.load_seg(ga, cv, m0, rows_a, k0, kend, tid);
-        else slab.load(ga, lda, m0, rows_a, k0, kend, vec_a, tid);
+        else slab.template load<decltype(full)::value>(ga, lda, m0, rows_a, k0, kend, vec_a, tid);
     };
-    auto load_b = [&](auto &slab, uint32_t k0) {
+    auto load_b = [&](auto &slab, uint32_t k0, auto full) {
         if constexpr (IM != kImNone) slab.load_conv(gb, cv, n0, rows_b, k0, kend, tid);
-        else slab.load(gb, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
+        else slab.template load<decltype(full)::value>(gb, g.ldb, n0, rows_b, k0, kend, g.vec_b, tid);
     };
 
     f32x16 acc[NC][TM][TN];
@@ -526,64 +536,125 @@ __global__ __launch_bounds__(kBlock, 4) void gemm_mfma_kernel(GemmArgs g) {
                 for (int r = 0; r < 16; ++r) acc[c][ti][tj][r] = 0.0f;
 
     const uint32_t steps = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
+    // One slab's MFMAs out of LDS buffer `cur`.
+    auto compute = [&](int cur) {
+        float4 af[TM][2], bf[TN][2];
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        if ((uint32_t)d < steps) {
-            load_a(sa[d], kbeg + d * kBK);
-            load_b(sb[d], kbeg + d * kBK);
+        for (int ti = 0; ti < TM; ++ti) {
+            const float *p = As[cur] + (wm0 + ti * 32 + l32) * kPitch + 8 * half;
+            af[ti][0] = *reinterpret_cast<const float4 *>(p);
+            af[ti][1] = *reinterpret_cast<const float4 *>(p + 4);
         }
-    }
-    if (steps > 0) {
+#pragma unroll
+        for (int tj = 0; tj < TN; ++tj) {
+            const float *p = Bs[cur] + (wn0 + tj * 32 + l32) * kPitch + 8 * half;
+            bf[tj][0] = *reinterpret_cast<const float4 *>(p);
+            bf[tj][1] = *reinterpret_cast<const float4 *>(p + 4);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < TN; ++tj)
+                    acc[q % NC][ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        ::dkz::lane(af[ti][q >> 2], q & 3), ::dkz::lane(bf[tj][q >> 2], q & 3), acc[q % NC][ti][tj],
+                        0, 0, 0);
+    };
+    // A tile wholly inside both operands (aligned, whole tile rows, a K range
+    // of whole slabs) takes a loop without edge checks: every slab load is
+    // one 128-bit load a float4, issued on every step (past the last slab
+    // the last one again, unused), and the steady loop has no branch, so the
+    // compiler waits only for the slab it stores while the next D - 1 stay in
+    // flight. Other tiles check every element, and there the compiler waits
+    // for every load in flight before a store.
+    bool interior = false;
+    if constexpr (IM == kImNone && DKZ_GEMM_FULL_TILES)
+        interior = vec_a && g.vec_b && rows_a >= (uint32_t)BM && rows_b >= (uint32_t)BN && steps > 0 &&
+                   (kend - kbeg) % kBK == 0;
+    if (interior) {
+        const std::true_type full{};
+        const auto slab_k = [&](uint32_t x) { return kbeg + (x < steps ? x : steps - 1) * kBK; };
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load_a(sa[d], slab_k(d), full);
+            load_b(sb[d], slab_k(d), full);
+        }
         sa[0].store(As[0], tid);
         sb[0].store(Bs[0], tid);
-        // Slot 0 is free again: it takes slab D (slot X % D always holds slab X).
-        if ((uint32_t)D < steps) {
-            load_a(sa[0], kbeg + D * kBK);
-            load_b(sb[0], kbeg + D * kBK);
-        }
+        load_a(sa[0], slab_k(D), full);
+        load_b(sb[0], slab_k(D), full);
         __syncthreads();
-    }
-    for (uint32_t s0 = 0; s0 < steps; s0 += D) {
+        uint32_t s0 = 0;
+        // steady state: every step stores slab s + 1 and loads slab s + 1 + D
+        for (; s0 + D < steps; s0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const uint32_t s = s0 + j;
+                const int cur = s & 1;
+                compute(cur);
+                const int nx = (j + 1) % D;
+                sa[nx].store(As[cur ^ 1], tid);
+                sb[nx].store(Bs[cur ^ 1], tid);
+                load_a(sa[nx], slab_k(s + 1 + D), full);
+                load_b(sb[nx], slab_k(s + 1 + D), full);
+                __syncthreads();
+            }
+        }
+        // the last steps: every slab left is in its slot already
 #pragma unroll
         for (int j = 0; j < D; ++j) {
             const uint32_t s = s0 + j;
-            if (s >= steps) break;
-            const int cur = s & 1;
-            float4 af[TM][2], bf[TN][2];
-#pragma unroll
-            for (int ti = 0; ti < TM; ++ti) {
-                const float *p = As[cur] + (wm0 + ti * 32 + l32) * kPitch + 8 * half;
-                af[ti][0] = *reinterpret_cast<const float4 *>(p);
-                af[ti][1] = *reinterpret_cast<const float4 *>(p + 4);
-            }
-#pragma unroll
-            for (int tj = 0; tj < TN; ++tj) {
-                const float *p = Bs[cur] + (wn0 + tj * 32 + l32) * kPitch + 8 * half;
-                bf[tj][0] = *reinterpret_cast<const float4 *>(p);
-                bf[tj][1] = *reinterpret_cast<const float4 *>(p + 4);
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-#pragma unroll
-                for (int ti = 0; ti < TM; ++ti)
-#pragma unroll
-                    for (int tj = 0; tj < TN; ++tj)
-                        acc[q % NC][ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            ::dkz::lane(af[ti][q >> 2], q & 3), ::dkz::lane(bf[tj][q >> 2], q & 3), acc[q % NC][ti][tj],
-                            0, 0, 0);
-            // Slab s + 1 (ring slot (j + 1) % D) goes to the other LDS buffer,
-            // and its registers take the loads of slab s + 1 + D.
-            const int nx = (j + 1) % D;
-            if (s + 1 < steps) {
-                sa[nx].store(As[cur ^ 1], tid);
-                sb[nx].store(Bs[cur ^ 1], tid);
-                if (s + 1 + D < steps) {
-                    const uint32_t k0 = kbeg + (s + 1 + D) * kBK;
-                    load_a(sa[nx], k0);
-                    load_b(sb[nx], k0);
+            if (s < steps) {
+                const int cur = s & 1;
+                compute(cur);
+                if (s + 1 < steps) {
+                    const int nx = (j + 1) % D;
+                    sa[nx].store(As[cur ^ 1], tid);
+                    sb[nx].store(Bs[cur ^ 1], tid);
                 }
+                __syncthreads();
+            }
+        }
+    } else {
+        const std::false_type full{};
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if ((uint32_t)d < steps) {
+                load_a(sa[d], kbeg + d * kBK, full);
+                load_b(sb[d], kbeg + d * kBK, full);
+            }
+        }
+        if (steps > 0) {
+            sa[0].store(As[0], tid);
+            sb[0].store(Bs[0], tid);
+            // Slot 0 is free again: it takes slab D (slot X % D always holds slab X).
+            if ((uint32_t)D < steps) {
+                load_a(sa[0], kbeg + D * kBK, full);
+                load_b(sb[0], kbeg + D * kBK, full);
             }
             __syncthreads();
+        }
+        for (uint32_t s0 = 0; s0 < steps; s0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const uint32_t s = s0 + j;
+                if (s >= steps) break;
+                const int cur = s & 1;
+                compute(cur);
+                // Slab s + 1 (ring slot (j + 1) % D) goes to the other LDS buffer,
+                // and its registers take the loads of slab s + 1 + D.
+                const int nx = (j + 1) % D;
+                if (s + 1 < steps) {
+                    sa[nx].store(As[cur ^ 1], tid);
+                    sb[nx].store(Bs[cur ^ 1], tid);
+                    if (s + 1 + D < steps) {
+                        load_a(sa[nx], kbeg + (s + 1 + D) * kBK, full);
+                        load_b(sb[nx], kbeg + (s + 1 + D) * kBK, full);
+                    }
+                }
+                __syncthreads();
+            }
         }
     }
 
