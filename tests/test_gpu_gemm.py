@@ -122,6 +122,23 @@ def test_layer_shapes(dev, ta, tb, m, n, k):
     check(ta, tb, m, n, k, 1.0, 1.0 if not ta else 0.0, seed=k, scale=0.5)
 
 
+@pytest.mark.parametrize("ta,tb", VARIANTS)
+@pytest.mark.parametrize("m,n,k", [
+    (256, 192, 96),  # 64x64 tiles, one K range
+    (128, 256, 1024),  # 64x64 tiles, K split over several ranges (partials in the scratch)
+    (4096, 2048, 64),  # 128x128 tiles (512 of them)
+])
+def test_interior_tiles_match_the_checked_loop(dev, ta, tb, m, n, k):
+    """Tiles wholly inside aligned operands run a slab loop without edge
+    checks; the same product with every leading dimension one wider (no
+    operand aligned) runs the checked loop. Both feed the MFMAs the same
+    slabs in the same order, so the results agree bit for bit (and meet the
+    fp32 bound)."""
+    got_fast = check(ta, tb, m, n, k, 1.25, 0.5, seed=m + n + k)[0]
+    got_checked = check(ta, tb, m, n, k, 1.25, 0.5, seed=m + n + k, pad=(1, 1, 1))[0]
+    assert_bitexact(got_checked[:, :n], got_fast[:, :n], f"gemm {ta},{tb} {m}x{n}x{k}")
+
+
 def test_cpu_twin_meets_the_same_bound():
     """The oracle (the twin) satisfies the bound the GPU is held to."""
     m, n, k = 33, 17, 500
