@@ -62,6 +62,9 @@ kernel trace that attribute HBM traffic and kernel time to each row;
 --traffic-table DIR prints the table (profiles/traffic_per_op.md) from them;
 --sq-table DIR prints the instruction mix per row from two SQ counter runs of
 --per-op-traffic (SQ_COUNTERS; profiles/softmax_instruction_mix.md).
+--gemm-counters runs the GEMM table's products between markers, and
+--gemm-counter-table DIR prints their matrix-core use from two counter runs
+of it (MFMA_COUNTERS; profiles/gemm_mfma_counters.md).
 """
 
 from __future__ import annotations
@@ -819,19 +822,21 @@ def per_op_table(gpu, hip, stream, launches: int, traffic=None, only=None, graph
 GEMM_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
 
 
+GEMM_SHAPES = [("conv fwd NN 128x3136x1152", False, False, 128, 3136, 1152),
+               ("conv bwd-data TN 1152x3136x128", True, False, 1152, 3136, 128),
+               ("conv weight-grad NT 128x1152x3136", False, True, 128, 1152, 3136),
+               ("square NN 4096x4096x4096", False, False, 4096, 4096, 4096),
+               ("square NN 8192x8192x4096", False, False, 8192, 8192, 4096)]
+
+
 def gemm_table(gpu, hip, stream):
     """dkz_gemm at the shapes a convolutional layer issues for config 2's layer
     (forward, backward data, weight gradient; one image each, as
     convolutional.zig issues them) and at a large square size: TFLOP/s
     against the fp32 matrix-core peak."""
     rows = {}
-    shapes = [("conv fwd NN 128x3136x1152", False, False, 128, 3136, 1152),
-              ("conv bwd-data TN 1152x3136x128", True, False, 1152, 3136, 128),
-              ("conv weight-grad NT 128x1152x3136", False, True, 128, 1152, 3136),
-              ("square NN 4096x4096x4096", False, False, 4096, 4096, 4096),
-              ("square NN 8192x8192x4096", False, False, 8192, 8192, 4096)]
     r = gen(7)
-    for name, ta, tb, m, n, k in shapes:
+    for name, ta, tb, m, n, k in GEMM_SHAPES:
         dev = Device(gpu)
         a = dev.up(r.uniform(-1, 1, m * k).astype(np.float32))
         b = dev.up(r.uniform(-1, 1, k * n).astype(np.float32))
@@ -1319,6 +1324,82 @@ def latency_table(d: Path) -> str:
     return "\n".join(lines)
 
 
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_F32 SQ_WAVE_CYCLES SQ_WAIT_INST_ANY SQ_WAIT_INST_LDS "
+                 "GRBM_GUI_ACTIVE",
+                 "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS")
+GEMM_COUNTER_PASSES = 2
+
+
+def gemm_counters(gpu, hip):
+    """Counter mode of the GEMM table: each shape of GEMM_SHAPES runs once
+    untimed, then GEMM_COUNTER_PASSES times between two marker fills (as in
+    the traffic mode), so that rocprofv3 --pmc can attribute every dispatch
+    -- the product and, for split K, its reduction -- to its shape."""
+    mark_buf = gpu.alloc((MARK_BASE + 256) * 256 + 1)
+
+    def marker(grid):
+        gpu.fill(mark_buf.offset(1), grid * 256, 0.0)
+    out = []
+    r = gen(7)
+    for i, (name, ta, tb, m, n, k) in enumerate(GEMM_SHAPES):
+        dev = Device(gpu)
+        a = dev.up(r.uniform(-1, 1, m * k).astype(np.float32))
+        b = dev.up(r.uniform(-1, 1, k * n).astype(np.float32))
+        c = dev.zeros(m * n)
+        lda, ldb = (m if ta else k), (k if tb else n)
+        gpu.gemm(ta, tb, m, n, k, 1.0, a, lda, b, ldb, 1.0, c, n)
+        hip.sync()
+        marker(MARK_BASE + 2 * i)
+        for _ in range(GEMM_COUNTER_PASSES):
+            gpu.gemm(ta, tb, m, n, k, 1.0, a, lda, b, ldb, 1.0, c, n)
+        marker(MARK_BASE + 2 * i + 1)
+        hip.sync()
+        dev.free()
+        out.append({"row": name, "flops": 2 * m * n * k, "passes": GEMM_COUNTER_PASSES,
+                    "begin_grid": MARK_BASE + 2 * i})
+        print(f"gemm counter row {i}: {name}", file=sys.stderr, flush=True)
+    gpu.free(mark_buf)
+    return {"gemm_counters": out, "mark_base": MARK_BASE}
+
+
+def gemm_counter_table(d: Path) -> str:
+    """Matrix-core use per GEMM shape (markdown) from the outputs under `d`:
+    rows.json (stdout of `bench.py --gemm-counters`) and mfma_a/, mfma_b/
+    (rocprofv3 --pmc with the two MFMA_COUNTERS groups over that command).
+    Per product: fp32 MFMA instructions, the MFMA pipe's busy cycles per
+    instruction, the busy share of all SIMD cycles (GRBM_GUI_ACTIVE is summed
+    over the 8 XCDs, each of 32 CUs x 4 SIMDs), the share of the waves'
+    cycles spent waiting (all causes, and on LDS), and LDS bank conflicts as
+    a share of LDS-active cycles."""
+    def last_json(path):
+        return json.loads([ln for ln in open(path) if ln.startswith("{")][-1])
+
+    meta = last_json(d / "rows.json")
+    rows, base = meta["gemm_counters"], meta["mark_base"]
+    segs = [_segments([(n, b, c) for n, b, c in _dispatch_counters(d / sub)], base) for sub in ("mfma_a", "mfma_b")]
+    lines = [
+        "| product | MFMA instructions | MFMA-busy cycles / MFMA | MFMA-busy share of SIMD cycles | wait share "
+        "| LDS-wait share | LDS bank-conflict share | GPU-active cycles (per XCD) |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    for i, r in enumerate(rows):
+        p = r["passes"]
+        c = {}
+        for seg in segs:
+            for _, vals in seg.get(i, []):
+                for k, v in vals.items():
+                    c[k] = c.get(k, 0.0) + v / p
+        if not c.get("SQ_INSTS_VALU_MFMA_F32"):
+            continue
+        mf, busy = c["SQ_INSTS_VALU_MFMA_F32"], c["SQ_VALU_MFMA_BUSY_CYCLES"]
+        gui = c["GRBM_GUI_ACTIVE"] / 8
+        lines.append(
+            f"| {r['row']} | {mf:.0f} | {busy / mf:.1f} | {busy / (gui * 32 * 4 * 8):.3f} | "
+            f"{c['SQ_WAIT_INST_ANY'] / c['SQ_WAVE_CYCLES']:.3f} | {c['SQ_WAIT_INST_LDS'] / c['SQ_WAVE_CYCLES']:.3f} | "
+            f"{c['SQ_LDS_BANK_CONFLICT'] / max(c['SQ_LDS_IDX_ACTIVE'], 1.0):.3f} | {gui:.0f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1353,6 +1434,12 @@ def main() -> int:
     ap.add_argument("--traffic-table", default=None, metavar="DIR",
                     help="only print the per-op traffic table (markdown) from the rocprofv3 outputs in DIR "
                          "(see traffic_table())")
+    ap.add_argument("--gemm-counters", action="store_true",
+                    help="only run the GEMM table's products a few times each, between marker dispatches "
+                         "(for rocprofv3 --pmc with MFMA_COUNTERS)")
+    ap.add_argument("--gemm-counter-table", default=None, metavar="DIR",
+                    help="only print the matrix-core table (markdown) from the rocprofv3 outputs in DIR "
+                         "(see gemm_counter_table())")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -1367,6 +1454,9 @@ def main() -> int:
         return 0
     if args.latency_table:
         print(latency_table(Path(args.latency_table)))
+        return 0
+    if args.gemm_counter_table:
+        print(gemm_counter_table(Path(args.gemm_counter_table)))
         return 0
 
     from darknet_zig_amd import gpu
@@ -1385,6 +1475,10 @@ def main() -> int:
         dev.free()
         print(json.dumps({"copy_calibration": {"bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 4,
                                                "us": round(ms * 1e3, 2)}}), flush=True)
+        return 0
+
+    if args.gemm_counters:
+        print(json.dumps(gemm_counters(gpu, hip)), flush=True)
         return 0
 
     if args.per_op_traffic:
