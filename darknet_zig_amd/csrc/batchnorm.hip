@@ -1042,9 +1042,11 @@ __global__ __launch_bounds__(BS) void bn_bwd_coop_kernel(const float *y, float *
 // U float4s of each input a lane. The sums pass over the chunk keeps d2 for
 // all U float4s (RD in registers, the rest in LDS) and x - mean for the
 // first LX (LDS); after the channel meeting the output is formed from those
-// and, past LX, from x read again. The sums pass reads that part of x with
-// ordinary loads, so the second read may find it in the Infinity Cache, and
-// everything else nontemporally. Bytes: 16 an element read once, 4 written,
+// and, past LX, from x read again, last float4 first. The sums pass reads
+// that part of x with ordinary loads, so the second read -- newest first --
+// may find it in the Infinity Cache, and everything else nontemporally; the
+// first PRE float4s of the second read are issued before the meeting.
+// Bytes: 16 an element read once, 4 written,
 // plus 4 for x read again past LX -- instead of the two passes' 16 + 12 + 4
 // for every element. Chunks longer than U float4s a lane (tensors larger
 // than the GPU holds at once) read y, delta and x of the rest again.
