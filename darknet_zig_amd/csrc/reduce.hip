@@ -409,11 +409,51 @@ __global__ __launch_bounds__(kBlock) void avgpool_rows_kernel(const float *x, fl
             for (int u = 0; u < 4; ++u) acc += term4(Value{}, a[u], a[u]);
         }
     } else {
+        // the same, an element at a time: four loads a lane in flight, the
+        // masked ones adding +0.0, each lane's elements in index order
         const uint32_t e0 = row * S;
-        for (uint32_t i = l; i < S; i += kWave) acc += (double)x[e0 + i];
+        for (uint32_t i = l; i < S; i += 4 * kWave) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t iu = i + u * kWave;
+                v[u] = iu < S ? x[e0 + iu] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += (double)v[u];
+        }
     }
     acc = wave_sum(acc);
     if (l == 0) out[row] = (float)acc / denom;  // pooling.zig:155: sum / denom
+}
+
+// Rows of at most 4L elements (L = 4 .. 32): L lanes a row, 64 / L rows a
+// wave, each lane adding elements l, l + L, l + 2L, l + 3L of its row in
+// f64 (all four loads in flight, the ones past the row masked, adding
+// +0.0), then a butterfly over the row's L lanes; rounded once and divided
+// as avgpool_rows_kernel does. With a wave a row, a 7x7 plane left 15 of 64
+// lanes idle and paid a whole wave's reduction per 49 elements.
+template <int L>
+__global__ __launch_bounds__(kBlock) void avgpool_seg_kernel(const float *x, float *out, uint32_t rows, uint32_t S,
+                                                             float denom) {
+    const uint32_t lane = threadIdx.x & (kWave - 1), l = lane % L;
+    const uint32_t row = (blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave) * (kWave / L) + lane / L;
+    double acc = 0.0;
+    if (row < rows) {
+        const uint32_t e0 = row * S;
+        for (uint32_t i = l; i < S; i += 4 * L) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t iu = i + u * L;
+                v[u] = iu < S ? x[e0 + iu] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += (double)v[u];
+        }
+    }
+    acc = seg_sum<L>(acc);  // the whole wave: rows past the end add zeros
+    if (row < rows && l == 0) out[row] = (float)acc / denom;
 }
 
 }  // namespace
@@ -506,6 +546,15 @@ int dkz_forward_avgpool(int n, int w, int h, int c, const float *input, float *o
     DKZ_REQUIRE(output && (input || S == 0));
     const float denom = (float)S;  // pooling.zig:148
     const uint32_t rows = (uint32_t)n;
+    if (S <= 128) {  // short rows: L lanes a row, L the least of 4, 8, 16, 32 with 4L >= S
+        const uint32_t per_wg = (kBlock / kWave) * (kWave / (S <= 16 ? 4 : S <= 32 ? 8 : S <= 64 ? 16 : 32));
+        const dim3 g(div_up(rows, per_wg)), b(kBlock);
+        const uint32_t s = (uint32_t)S;
+        if (S <= 16) return launch("forward_avgpool", avgpool_seg_kernel<4>, g, b, input, output, rows, s, denom);
+        if (S <= 32) return launch("forward_avgpool", avgpool_seg_kernel<8>, g, b, input, output, rows, s, denom);
+        if (S <= 64) return launch("forward_avgpool", avgpool_seg_kernel<16>, g, b, input, output, rows, s, denom);
+        return launch("forward_avgpool", avgpool_seg_kernel<32>, g, b, input, output, rows, s, denom);
+    }
     const dim3 grid(div_up(rows, kBlock / kWave)), block(kBlock);
     if (S % 4 == 0 && aligned16(input))
         return launch("forward_avgpool", avgpool_rows_kernel<true>, grid, block, input, output, rows,

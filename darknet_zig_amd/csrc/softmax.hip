@@ -77,40 +77,6 @@ __device__ __forceinline__ void xent1(float p, float t, float &d, float &l) {
 
 __device__ __forceinline__ float xent_loss(float p, float t) { return (t != 0.0f) ? -logf(p) : 0.0f; }
 
-// ---------------------------------------------------------------------------
-// Reductions over a segment of L consecutive lanes (L = 4, 8, 16, 32, 64;
-// the whole wave active). Butterfly steps: DPP quad permutes and row mirrors
-// inside 16-lane rows, then lane swaps across rows. Partners combine the same
-// two operands, so every lane of the segment ends with the same bits.
-// ---------------------------------------------------------------------------
-template <int L>
-__device__ __forceinline__ float seg_max(float v) {
-    if constexpr (L == kWave) {
-        return wave_max(v);
-    } else {
-        v = fmaxf(v, dpp_f<kDppXor1>(v));
-        v = fmaxf(v, dpp_f<kDppXor2>(v));
-        if constexpr (L >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-        if constexpr (L >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
-        if constexpr (L >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-        return v;
-    }
-}
-
-template <int L>
-__device__ __forceinline__ double seg_sum(double v) {
-    if constexpr (L == kWave) {
-        return wave_sum(v);
-    } else {
-        v += dpp_d<kDppXor1>(v);
-        v += dpp_d<kDppXor2>(v);
-        if constexpr (L >= 8) v += dpp_d<kDppHalfMirror>(v);
-        if constexpr (L >= 16) v += dpp_d<kDppMirror>(v);
-        if constexpr (L >= 32) v += __shfl_xor(v, 16);
-        return v;
-    }
-}
-
 // A lane's share of one group, M = 4K floats held in registers. Slot m is
 // element at(m): with float4 access (V4) lane j of P lanes holds float4s
 // j, j+P, ..., otherwise elements j, j+P, j+2P, ...

@@ -307,7 +307,10 @@ def test_maxpool_shared_argmax(dev, case):
         gpu.free(b)
 
 
-@pytest.mark.parametrize("batch, c, h, w", [(3, 6, 14, 14), (2, 5, 7, 7), (4, 3, 1, 1), (256, 512, 28, 28)])
+# rows of 1, 30, 49, 110 elements take 4, 8, 16, 32 lanes a row; 169, 196, 323, 784 a wave a row
+@pytest.mark.parametrize("batch, c, h, w", [(3, 6, 14, 14), (2, 5, 7, 7), (4, 3, 1, 1), (8, 64, 13, 13),
+                                        (2, 3, 17, 19), (2, 4, 5, 6), (3, 10, 10, 11), (64, 1024, 7, 7),
+                                        (256, 512, 28, 28)])
 def test_avgpool(dev, batch, c, h, w):
     r = rng(batch * c + h)
     x = uniform(r, batch * c * h * w)
