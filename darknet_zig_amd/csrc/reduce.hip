@@ -43,6 +43,11 @@ constexpr int kUnroll = DKZ_CHAN_UNROLL;
 #ifndef DKZ_CHAN_KMAJOR
 #define DKZ_CHAN_KMAJOR 1
 #endif
+// Elements in flight per lane for channels whose spatial size is not a
+// multiple of 4 (read an element at a time).
+#ifndef DKZ_CHAN_SCALAR_W
+#define DKZ_CHAN_SCALAR_W 8
+#endif
 
 template <class Term>
 __device__ __forceinline__ double term4(const Term &t, float4 a, float4 b) {
@@ -86,9 +91,25 @@ __device__ __forceinline__ double chunk_sum(const T &t, const float *p0, const f
             acc0 += term4(term, a, b);
         }
     } else {
-        for (uint32_t j = j0 + threadIdx.x; j < j1; j += BS) {
-            const uint32_t e = chan_addr(fbase, j, g);
-            acc0 += (double)term(p0[e], TWO ? p1[e] : 0.0f);
+        // An element at a time (spatial not a multiple of 4), W a lane in
+        // flight: the loads past the chunk read the lane's first element
+        // again and are not added, so each lane still adds its elements in
+        // index order. With one load a round trip [64,1024,13,13]'s mean took
+        // 22.9 us, with 4 a lane 11.5, with 8 11.0 ([64,256,19,19] 15.4 /
+        // 8.4 / 7.6; 16 no better).
+        constexpr int W = DKZ_CHAN_SCALAR_W;
+        for (uint32_t j = j0 + threadIdx.x; j < j1; j += W * BS) {
+            float a[W], b[W];
+#pragma unroll
+            for (int u = 0; u < W; ++u) {
+                const uint32_t ju = j + u * BS;
+                const uint32_t e = chan_addr(fbase, ju < j1 ? ju : j, g);
+                a[u] = p0[e];
+                b[u] = TWO ? p1[e] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < W; ++u)
+                if (j + u * BS < j1) acc0 += (double)term(a[u], b[u]);
         }
     }
     return block_sum<BS>(acc0 + acc1, lds);

@@ -29,6 +29,7 @@ SHAPES = [
     (7, 1, 13),
     (5, 33, 196),     # spatial % 4 == 0, filters not a power of two
     (16, 64, 3136),   # K > 1 split path
+    (8, 1024, 169),   # 13x13 planes: spatial % 4 != 0, one workgroup a channel
 ]
 CONFIG1 = (128, 32, 1024)
 CONFIG2 = (64, 128, 3136)
